@@ -1,0 +1,252 @@
+/*
+ * jmodels_attn — MI355X (gfx950) grouped-query attention and KV-cache library, C ABI.
+ *
+ * Drop-in for backend-java's attention/KV-cache path of integrallis/models. Reference paths
+ * (relative to /root/reference):
+ *   BJ/ = backend-java/src/main/java/com/integrallis/models/backend/purejava/
+ *   RS  = backend-native/src/main/rust/model-kernels/src/lib.rs   (C-ABI conventions followed)
+ *   BN/ = backend-native/src/main/java/com/integrallis/models/backend/nativekernel/
+ *
+ * Conventions (after RS:58-82, 469-584):
+ *   - every export is extern "C", takes plain pointers, u32 dims and u64 element counts, and
+ *     returns an int32 status (0 = OK); nothing unwinds across the boundary (C++ try/catch at
+ *     every export, like the Rust catch_unwind wrappers at RS:497-537);
+ *   - a context is created per GPU and used by one caller at a time (the single-caller contract
+ *     of API/InferenceBackend.java:20-28); it owns one HIP stream;
+ *   - host-buffer calls are synchronous: they return once outputs are visible to the host;
+ *   - *_device calls take device pointers and are asynchronous on the context stream; errors
+ *     detected by kernels are reported by jmodels_attn_context_synchronize;
+ *   - outputs must not alias inputs (RS:535-539).
+ *
+ * Ownership change vs the reference: the library owns the KV cache, resident in HBM and
+ * appended in place; Java holds an opaque handle instead of float[] buffers.
+ */
+#ifndef JMODELS_ATTN_H
+#define JMODELS_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JMODELS_ATTN_ABI_VERSION 1u
+
+#if defined(__GNUC__)
+#define JMODELS_ATTN_API __attribute__((visibility("default")))
+#else
+#define JMODELS_ATTN_API
+#endif
+
+/* Status codes. 0-4 keep the meaning of RS:78-82. */
+#define JMODELS_ATTN_OK 0
+#define JMODELS_ATTN_NULL_POINTER 1
+#define JMODELS_ATTN_INVALID_SHAPE 2     /* dims/counts inconsistent or unsupported */
+#define JMODELS_ATTN_BUFFER_TOO_SMALL 3  /* an element count is below what the shape needs */
+#define JMODELS_ATTN_PANIC 4             /* C++ exception caught at the boundary */
+#define JMODELS_ATTN_DEVICE_ERROR 5      /* HIP runtime failure */
+#define JMODELS_ATTN_OUT_OF_RANGE 6      /* layer/position/sequence out of range (the reference's
+                                            IllegalArgumentException, BJ/cache/KvCache.java:237-244) */
+#define JMODELS_ATTN_UNAVAILABLE 7       /* position not populated or overwritten (the reference's
+                                            IllegalStateException, BJ/cache/KvCache.java:232-235,
+                                            BJ/cache/LayeredKvCache.java:192-197) */
+#define JMODELS_ATTN_NON_FINITE 8        /* an attention score was NaN or +inf; TensorOps.softmax
+                                            rejects those (BJ/ops/TensorOps.java:1256-1269) */
+
+/* Capability bits (RS:59-77 style). */
+#define JMODELS_ATTN_CAP_DECODE_F32 (1ull << 0)      /* f32 KV split-K decode */
+#define JMODELS_ATTN_CAP_DECODE_F16 (1ull << 1)      /* f16 KV split-K decode */
+#define JMODELS_ATTN_CAP_PREFILL_MFMA (1ull << 2)    /* causal / sliding-window f16 MFMA prefill */
+#define JMODELS_ATTN_CAP_RAGGED_DECODE (1ull << 3)   /* many sessions, ragged lengths, one launch */
+#define JMODELS_ATTN_CAP_SLIDING_WINDOW (1ull << 4)  /* causal window max(0, p - w + 1) */
+#define JMODELS_ATTN_CAP_RING_LAYERS (1ull << 5)     /* LayeredKvCache RING retention */
+#define JMODELS_ATTN_CAP_DEVICE_POINTERS (1ull << 6) /* *_device entry points */
+
+/* KV storage element types. F16 stores IEEE binary16 (round to nearest even), which widens to
+ * exactly Float.float16ToFloat(Float.floatToFloat16(x)) — the reference's half-precision KV
+ * (BJ/cache/KvCache.java:84-100). */
+#define JMODELS_ATTN_KV_F32 0u
+#define JMODELS_ATTN_KV_F16 1u
+
+typedef struct jmodels_attn_context jmodels_attn_context;
+typedef struct jmodels_attn_kv jmodels_attn_kv;
+typedef struct jmodels_attn_rope jmodels_attn_rope;
+
+/* One attention layer's parameters for a call.
+ *   layer           zero-based layer of the KV cache
+ *   num_heads       query heads; must be a multiple of the cache's num_kv_heads; query head h
+ *                   reads KV head h / (num_heads / num_kv_heads) (BJ/llama/LlamaForwardPass.java:1563)
+ *   sliding_window  0 = global; else causal window, first position max(0, p - w + 1)
+ *                   (LlamaConfig.attentionStartPosition, BJ/llama/LlamaConfig.java:184-195)
+ *   neox            1 = split-half RoPE pairs (i, i + pairs), 0 = interleaved (2i, 2i+1)
+ *                   (TensorOps.ropeNeox / rope, BJ/ops/TensorOps.java:1336-1390)
+ *   scale           score multiplier; 0 selects (float)(1 / sqrt(key_length))
+ *                   (BJ/llama/LlamaForwardPass.java:1559); Gemma 4 passes 1.0
+ *   rope            NULL = this layer applies no RoPE (LlamaConfig.usesRope false) */
+typedef struct jmodels_attn_layer {
+  uint32_t layer;
+  uint32_t num_heads;
+  uint32_t sliding_window;
+  uint32_t neox;
+  float scale;
+  uint32_t reserved;
+  const jmodels_attn_rope* rope;
+} jmodels_attn_layer;
+
+/* ---------------------------------------------------------------- library and context */
+
+/* jmodels_kernels_abi_version analogue (RS:469-472). */
+JMODELS_ATTN_API uint32_t jmodels_attn_abi_version(void);
+/* jmodels_kernels_capabilities analogue (RS:474-495). */
+JMODELS_ATTN_API uint64_t jmodels_attn_capabilities(void);
+/* Upper-case name of a status code ("OK", "INVALID_SHAPE", ...), like
+ * NativeKernelLibrary.statusName (BN/NativeKernelLibrary.java:771-779). */
+JMODELS_ATTN_API const char* jmodels_attn_status_name(int32_t status);
+/* Detail message of the last failing call on this thread ("" if none). */
+JMODELS_ATTN_API const char* jmodels_attn_last_error(void);
+
+/* jmodels_kernels_context_create analogue (RS:496-520): NULL on failure (no such device, not a
+ * gfx950, HIP error). */
+JMODELS_ATTN_API jmodels_attn_context* jmodels_attn_context_create(int32_t device);
+/* RS:521-537 analogue; NULL_POINTER for NULL. Destroys nothing else: KV caches and RoPE tables
+ * must be destroyed first. */
+JMODELS_ATTN_API int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx);
+/* Waits for the context stream and reports errors recorded by kernels since the last call. */
+JMODELS_ATTN_API int32_t jmodels_attn_context_synchronize(jmodels_attn_context* ctx);
+/* The context's hipStream_t, for callers that order their own work (events, copies) with it. */
+JMODELS_ATTN_API int32_t jmodels_attn_context_stream(jmodels_attn_context* ctx, void** stream_out);
+
+/* ---------------------------------------------------------------- RoPE tables */
+
+/* RotaryTable (BJ/ops/RotaryTable.java:48-75, 177-186): cos/sin for positions
+ * [0, max_positions) computed on the host exactly as fillFactors does (frequency in double pow,
+ * angle in float, cos/sin in double rounded to float) and kept in HBM. frequency_factors may be
+ * NULL; otherwise factor_count == rotary_dim / 2 finite positive divisors. */
+JMODELS_ATTN_API int32_t jmodels_attn_rope_create(jmodels_attn_context* ctx, uint32_t rotary_dim, float theta,
+                                 float frequency_scale, const float* frequency_factors,
+                                 uint32_t factor_count, uint32_t max_positions,
+                                 jmodels_attn_rope** rope_out);
+JMODELS_ATTN_API int32_t jmodels_attn_rope_destroy(jmodels_attn_rope* rope);
+
+/* ---------------------------------------------------------------- KV cache */
+
+/* A device-resident KV cache for `sequences` independent sessions of one shape (each session is
+ * one backend-java KvCache, BJ/llama/LlamaForwardPass.java:412-416). Allocated at max_seq_len up
+ * front (no growth copies; BJ/cache/KvCache.java:284-322 grows lazily instead).
+ * ring_capacity: NULL, or num_layers entries where 0 = LINEAR and c > 0 = RING of c slots
+ * (BJ/cache/LayeredKvCache.java:41-64); c must be a multiple of 32 and is capped at max_seq_len. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_create(jmodels_attn_context* ctx, uint32_t sequences, uint32_t num_layers,
+                               uint32_t max_seq_len, uint32_t num_kv_heads, uint32_t key_length,
+                               uint32_t value_length, uint32_t dtype,
+                               const uint32_t* ring_capacity, jmodels_attn_kv** kv_out);
+JMODELS_ATTN_API int32_t jmodels_attn_kv_destroy(jmodels_attn_kv* kv);
+/* KvCache.clear (BJ/cache/KvCache.java:156-158) for one sequence, or all when sequence < 0. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_clear(jmodels_attn_kv* kv, int32_t sequence);
+/* KvCache.discardFrom / LayeredKvCache.discardFrom (BJ/cache/KvCache.java:161-173,
+ * BJ/cache/LayeredKvCache.java:212-223): position in [0, max_seq_len]. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_discard_from(jmodels_attn_kv* kv, uint32_t sequence, uint32_t position);
+/* LayeredKvCache.contains (BJ/cache/LayeredKvCache.java:172-175): *out = 1 if available. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_contains(const jmodels_attn_kv* kv, uint32_t sequence, uint32_t layer,
+                                 uint32_t position, int32_t* out);
+/* KvCache.store without RoPE (BJ/cache/KvCache.java:51-73): host vectors of key_dim/value_dim. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_store(jmodels_attn_context* ctx, jmodels_attn_kv* kv, uint32_t sequence,
+                              uint32_t layer, uint32_t position, const float* key,
+                              uint64_t key_elements, const float* value, uint64_t value_elements);
+/* keySlice/valueSlice (BJ/cache/KvCache.java:105-115, 208-230): rows [from, to) in the
+ * reference's [position][kv_head * head_dim] f32 layout; either output may be NULL. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_read(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                             uint32_t sequence, uint32_t layer, uint32_t from, uint32_t to,
+                             float* keys, uint64_t key_elements, float* values,
+                             uint64_t value_elements);
+/* Device bytes held by the cache's K and V storage. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_bytes(const jmodels_attn_kv* kv, uint64_t* bytes_out);
+
+/* ---------------------------------------------------------------- attention */
+
+/* RoPE + KV append for `count` rows (kernel 1). Row i belongs to sequence sequences[i] at
+ * position positions[i]. q [count][num_heads*key_length] and k [count][num_kv_heads*key_length]
+ * are rotated with the layer's RoPE (RotaryTable.apply, BJ/llama/LlamaForwardPass.java:1070-1083);
+ * the rotated q is written to q_rotated (may be NULL); the rotated k and v
+ * [count][num_kv_heads*value_length] are stored at (sequence, layer, position)
+ * (KvCache.store, :1086). Rows must not repeat a (sequence, position). */
+JMODELS_ATTN_API int32_t jmodels_attn_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, const float* k, uint64_t k_elements,
+                            const float* v, uint64_t v_elements, float* q_rotated,
+                            uint64_t q_rotated_elements);
+
+/* Grouped-query attention of `count` already-rotated query rows over their cached positions
+ * [first, position] (groupedQueryAttention, BJ/llama/LlamaForwardPass.java:1543-1670):
+ * split-K flash-decoding (kernel 2) plus the cross-split reduction (kernel 4).
+ * out [count][num_heads*value_length] f32. */
+JMODELS_ATTN_API int32_t jmodels_attn_attend(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, float* out, uint64_t out_elements);
+
+/* One decode token for `count` sessions: append then attend (the per-layer attention block of
+ * LlamaForwardPass.forwardSequenceInternal :1069-1128 for count == 1, and
+ * attendIndependentSessions :793-839 for count > 1). */
+JMODELS_ATTN_API int32_t jmodels_attn_decode(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, const float* k, uint64_t k_elements,
+                            const float* v, uint64_t v_elements, float* out,
+                            uint64_t out_elements);
+
+/* Causal prefill of n consecutive tokens of one sequence at start .. start+n-1
+ * (prepareBatchedAttention + computeBatchedAttention, BJ/llama/LlamaForwardPass.java:1479-1541):
+ * RoPE + append every row (one kernel-1 launch), then jmodels_attn_attend_causal: f16 caches run
+ * the MFMA kernel (kernel 3) with f16 queries; f32 caches run the split-K decode kernel per row. */
+JMODELS_ATTN_API int32_t jmodels_attn_prefill(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                             const jmodels_attn_layer* layer, uint32_t sequence, uint32_t start,
+                             uint32_t n, const float* q, uint64_t q_elements, const float* k,
+                             uint64_t k_elements, const float* v, uint64_t v_elements,
+                             float* out, uint64_t out_elements);
+
+/* Causal attention of rows start .. start+n-1 of one sequence whose K/V are already cached and
+ * whose rotated queries are q [n][num_heads*key_length] (computeBatchedAttention,
+ * BJ/llama/LlamaForwardPass.java:1515-1541): row b attends [first(start+b), start+b]. This is the
+ * attention half of jmodels_attn_prefill (kernel 3 on f16 caches). */
+JMODELS_ATTN_API int32_t jmodels_attn_attend_causal(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t sequence,
+                                   uint32_t start, uint32_t n, const float* q,
+                                   uint64_t q_elements, float* out, uint64_t out_elements);
+
+/* Device-pointer variants of the five calls above: q/k/v/q_rotated/out are device pointers
+ * (sequences/positions stay host arrays: they size the launch). Asynchronous on the context
+ * stream; call jmodels_attn_context_synchronize before reading results or to collect errors. */
+JMODELS_ATTN_API int32_t jmodels_attn_append_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t count,
+                                   const uint32_t* sequences, const uint32_t* positions,
+                                   const float* q, uint64_t q_elements, const float* k,
+                                   uint64_t k_elements, const float* v, uint64_t v_elements,
+                                   float* q_rotated, uint64_t q_rotated_elements);
+JMODELS_ATTN_API int32_t jmodels_attn_attend_device(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t count,
+                                   const uint32_t* sequences, const uint32_t* positions,
+                                   const float* q, uint64_t q_elements, float* out,
+                                   uint64_t out_elements);
+JMODELS_ATTN_API int32_t jmodels_attn_decode_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t count,
+                                   const uint32_t* sequences, const uint32_t* positions,
+                                   const float* q, uint64_t q_elements, const float* k,
+                                   uint64_t k_elements, const float* v, uint64_t v_elements,
+                                   float* out, uint64_t out_elements);
+JMODELS_ATTN_API int32_t jmodels_attn_attend_causal_device(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                                          const jmodels_attn_layer* layer, uint32_t sequence,
+                                          uint32_t start, uint32_t n, const float* q,
+                                          uint64_t q_elements, float* out,
+                                          uint64_t out_elements);
+JMODELS_ATTN_API int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                    const jmodels_attn_layer* layer, uint32_t sequence,
+                                    uint32_t start, uint32_t n, const float* q,
+                                    uint64_t q_elements, const float* k, uint64_t k_elements,
+                                    const float* v, uint64_t v_elements, float* out,
+                                    uint64_t out_elements);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

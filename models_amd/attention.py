@@ -1,0 +1,509 @@
+"""Python mirror of backend-java's attention/KV-cache contract over ``libjmodels_attn.so``.
+
+This is the host side above the C ABI (``include/jmodels_attn.h``). Names follow the reference
+(paths relative to ``backend-java/src/main/java/com/integrallis/models/backend/purejava/``):
+
+* :class:`HipAttentionLibrary` — ``NativeKernelLibrary.open`` (backend-native
+  ``NativeKernelLibrary.java:126-191``): load the library, check the ABI version and the
+  required capabilities, create a context; ``close`` is idempotent.
+* :class:`HipRotaryTable` — ``ops/RotaryTable.java`` (factors resident in HBM).
+* :class:`HipKvCache` — ``cache/KvCache.java`` / ``cache/LayeredKvCache.java`` resident in HBM:
+  ``store``, ``key_slice``/``value_slice``, ``contains``, ``discard_from``, ``clear``.
+* :class:`AttentionLayer` — the per-layer flags ``LlamaConfig`` supplies (heads, window, NeoX,
+  scale, RoPE table).
+* ``decode`` / ``attend`` / ``append`` / ``prefill`` — the attention block of
+  ``llama/LlamaForwardPass.java`` (:1069-1128, :1479-1541, :793-839).
+
+Shape errors raise ``ValueError`` before crossing the boundary (as the reference validates before
+the downcall, ``NativeKernelLibrary.java:552-578``); a non-zero native status raises
+:class:`AttentionStatusError` (the reference's ``IllegalStateException`` mapping, :771-779).
+There is no CPU fallback: without the HIP library and a gfx950 GPU every call fails loudly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+ABI_VERSION = 1
+
+OK = 0
+NULL_POINTER = 1
+INVALID_SHAPE = 2
+BUFFER_TOO_SMALL = 3
+PANIC = 4
+DEVICE_ERROR = 5
+OUT_OF_RANGE = 6
+UNAVAILABLE = 7
+NON_FINITE = 8
+
+CAP_DECODE_F32 = 1 << 0
+CAP_DECODE_F16 = 1 << 1
+CAP_PREFILL_MFMA = 1 << 2
+CAP_RAGGED_DECODE = 1 << 3
+CAP_SLIDING_WINDOW = 1 << 4
+CAP_RING_LAYERS = 1 << 5
+CAP_DEVICE_POINTERS = 1 << 6
+
+KV_F32 = 0
+KV_F16 = 1
+
+EXPORTS = (
+    "jmodels_attn_abi_version", "jmodels_attn_capabilities", "jmodels_attn_status_name",
+    "jmodels_attn_last_error", "jmodels_attn_context_create", "jmodels_attn_context_destroy",
+    "jmodels_attn_context_synchronize", "jmodels_attn_context_stream", "jmodels_attn_rope_create",
+    "jmodels_attn_rope_destroy", "jmodels_attn_kv_create", "jmodels_attn_kv_destroy",
+    "jmodels_attn_kv_clear", "jmodels_attn_kv_discard_from", "jmodels_attn_kv_contains",
+    "jmodels_attn_kv_store", "jmodels_attn_kv_read", "jmodels_attn_kv_bytes",
+    "jmodels_attn_append", "jmodels_attn_attend", "jmodels_attn_decode", "jmodels_attn_prefill",
+    "jmodels_attn_append_device", "jmodels_attn_attend_device", "jmodels_attn_decode_device",
+    "jmodels_attn_prefill_device", "jmodels_attn_attend_causal",
+    "jmodels_attn_attend_causal_device",
+)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_LIBRARY = os.path.join(_HERE, "libjmodels_attn.so")
+LIBRARY_PROPERTY = "MODELS_HIP_ATTENTION_LIBRARY"
+
+
+class AttentionStatusError(RuntimeError):
+    """A native call returned a non-zero status."""
+
+    def __init__(self, status: int, name: str, detail: str, call: str):
+        super().__init__(f"{call} failed with {name} ({status}): {detail}")
+        self.status = status
+        self.status_name = name
+        self.detail = detail
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [
+        ("layer", ctypes.c_uint32),
+        ("num_heads", ctypes.c_uint32),
+        ("sliding_window", ctypes.c_uint32),
+        ("neox", ctypes.c_uint32),
+        ("scale", ctypes.c_float),
+        ("reserved", ctypes.c_uint32),
+        ("rope", ctypes.c_void_p),
+    ]
+
+
+_u32, _u64, _i32, _cf = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_float
+_vp = ctypes.c_void_p
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_LP = ctypes.POINTER(_Layer)
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    sig = {
+        "jmodels_attn_abi_version": (_u32, []),
+        "jmodels_attn_capabilities": (_u64, []),
+        "jmodels_attn_status_name": (ctypes.c_char_p, [_i32]),
+        "jmodels_attn_last_error": (ctypes.c_char_p, []),
+        "jmodels_attn_context_create": (_vp, [_i32]),
+        "jmodels_attn_context_destroy": (_i32, [_vp]),
+        "jmodels_attn_context_synchronize": (_i32, [_vp]),
+        "jmodels_attn_context_stream": (_i32, [_vp, ctypes.POINTER(_vp)]),
+        "jmodels_attn_rope_create": (_i32, [_vp, _u32, _cf, _cf, _vp, _u32, _u32,
+                                            ctypes.POINTER(_vp)]),
+        "jmodels_attn_rope_destroy": (_i32, [_vp]),
+        "jmodels_attn_kv_create": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp,
+                                          ctypes.POINTER(_vp)]),
+        "jmodels_attn_kv_destroy": (_i32, [_vp]),
+        "jmodels_attn_kv_clear": (_i32, [_vp, _i32]),
+        "jmodels_attn_kv_discard_from": (_i32, [_vp, _u32, _u32]),
+        "jmodels_attn_kv_contains": (_i32, [_vp, _u32, _u32, _u32, ctypes.POINTER(_i32)]),
+        "jmodels_attn_kv_store": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp, _u64, _vp, _u64]),
+        "jmodels_attn_kv_read": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u64, _vp, _u64]),
+        "jmodels_attn_kv_bytes": (_i32, [_vp, ctypes.POINTER(_u64)]),
+    }
+    rows = [_vp, _vp, _LP, _u32, _u32p, _u32p]
+    for name in ("jmodels_attn_append", "jmodels_attn_append_device"):
+        sig[name] = (_i32, rows + [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _u64])
+    for name in ("jmodels_attn_attend", "jmodels_attn_attend_device"):
+        sig[name] = (_i32, rows + [_vp, _u64, _vp, _u64])
+    for name in ("jmodels_attn_decode", "jmodels_attn_decode_device"):
+        sig[name] = (_i32, rows + [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _u64])
+    for name in ("jmodels_attn_attend_causal", "jmodels_attn_attend_causal_device"):
+        sig[name] = (_i32, [_vp, _vp, _LP, _u32, _u32, _u32, _vp, _u64, _vp, _u64])
+    for name in ("jmodels_attn_prefill", "jmodels_attn_prefill_device"):
+        sig[name] = (_i32, [_vp, _vp, _LP, _u32, _u32, _u32, _vp, _u64, _vp, _u64, _vp, _u64,
+                            _vp, _u64])
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+_LIBS: dict = {}
+
+
+def load_library(path: Optional[str] = None) -> ctypes.CDLL:
+    """dlopen the HIP library (``MODELS_HIP_ATTENTION_LIBRARY`` overrides the in-tree path) and
+    verify every export of ``include/jmodels_attn.h`` and the ABI version; no GPU is touched."""
+    path = path or os.environ.get(LIBRARY_PROPERTY) or DEFAULT_LIBRARY
+    path = os.path.abspath(path)
+    if path in _LIBS:
+        return _LIBS[path]
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"HIP attention library not found at {path}; build it with `python -m models_amd.build`")
+    lib = ctypes.CDLL(path)
+    missing = [name for name in EXPORTS if not hasattr(lib, name)]
+    if missing:
+        raise RuntimeError(f"{path} lacks exports: {missing}")
+    _declare(lib)
+    version = lib.jmodels_attn_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"ABI version mismatch: library {version}, binding {ABI_VERSION}")
+    _LIBS[path] = lib
+    return lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def uses_sliding_window(layer: int, pattern: int, sliding_window: int) -> bool:
+    """LlamaConfig.usesSlidingWindow for the Gemma family (llama/LlamaConfig.java:157-162)."""
+    return sliding_window > 0 and layer % pattern < pattern - 1
+
+
+def attention_start_position(position: int, sliding_window: int) -> int:
+    """LlamaConfig.attentionStartPosition, causal branch (llama/LlamaConfig.java:184-195)."""
+    if position < 0:
+        raise ValueError("position must be >= 0")
+    if sliding_window <= 0:
+        return 0
+    return max(0, position - sliding_window + 1)
+
+
+class HipAttentionLibrary:
+    """Loaded library + one context on one GPU (NativeKernelLibrary analogue)."""
+
+    def __init__(self, device: int = 0, path: Optional[str] = None,
+                 required_capabilities: int = 0):
+        self.lib = load_library(path)
+        caps = self.lib.jmodels_attn_capabilities()
+        if caps & required_capabilities != required_capabilities:
+            raise RuntimeError(f"library lacks capabilities {required_capabilities & ~caps:#x}")
+        self.capabilities = caps
+        ctx = self.lib.jmodels_attn_context_create(device)
+        if not ctx:
+            raise AttentionStatusError(
+                -1, "CONTEXT_CREATE_FAILED",
+                self.lib.jmodels_attn_last_error().decode(), "jmodels_attn_context_create")
+        self.ctx = ctx
+        self.device = device
+
+    # ---- plumbing
+
+    def check(self, status: int, call: str) -> None:
+        if status != OK:
+            name = self.lib.jmodels_attn_status_name(status).decode()
+            detail = self.lib.jmodels_attn_last_error().decode()
+            raise AttentionStatusError(status, name, detail, call)
+
+    def synchronize(self) -> None:
+        self.check(self.lib.jmodels_attn_context_synchronize(self.ctx), "synchronize")
+
+    def stream(self) -> int:
+        out = _vp()
+        self.check(self.lib.jmodels_attn_context_stream(self.ctx, ctypes.byref(out)), "stream")
+        return out.value or 0
+
+    def close(self) -> None:
+        if getattr(self, "ctx", None):
+            self.check(self.lib.jmodels_attn_context_destroy(self.ctx), "context_destroy")
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- factories
+
+    def rotary_table(self, rotary_dim: int, theta: float, frequency_scale: float = 1.0,
+                     max_positions: int = 4096, frequency_factors=None) -> "HipRotaryTable":
+        return HipRotaryTable(self, rotary_dim, theta, frequency_scale, max_positions,
+                              frequency_factors)
+
+    def kv_cache(self, num_layers: int, max_seq_len: int, num_kv_heads: int, key_length: int,
+                 value_length: int, half_precision: bool = True, sequences: int = 1,
+                 ring_capacity: Optional[Sequence[int]] = None) -> "HipKvCache":
+        return HipKvCache(self, num_layers, max_seq_len, num_kv_heads, key_length, value_length,
+                          half_precision, sequences, ring_capacity)
+
+
+class HipRotaryTable:
+    """RotaryTable (ops/RotaryTable.java:48-186) with factors for [0, max_positions) in HBM."""
+
+    def __init__(self, owner: HipAttentionLibrary, rotary_dim: int, theta: float,
+                 frequency_scale: float, max_positions: int, frequency_factors=None):
+        self.owner = owner
+        if rotary_dim <= 0 or rotary_dim % 2:
+            raise ValueError(f"rotaryDim must be positive and even: {rotary_dim}")
+        factors = None
+        fp, fc = None, 0
+        if frequency_factors is not None:
+            factors = _f32(frequency_factors)
+            fp, fc = _ptr(factors), factors.size
+        out = _vp()
+        owner.check(owner.lib.jmodels_attn_rope_create(owner.ctx, rotary_dim, theta,
+                                                       frequency_scale, fp, fc, max_positions,
+                                                       ctypes.byref(out)), "rope_create")
+        self.handle = out.value
+        self.rotary_dim = rotary_dim
+        self.max_positions = max_positions
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.owner.check(self.owner.lib.jmodels_attn_rope_destroy(self.handle), "rope_destroy")
+            self.handle = None
+
+
+@dataclass
+class AttentionLayer:
+    """Per-layer attention parameters (LlamaConfig flags for one layer)."""
+
+    layer: int
+    num_heads: int
+    sliding_window: int = 0
+    neox: bool = False
+    scale: float = 0.0  # 0 -> (float)(1/sqrt(key_length))
+    rope: Optional[HipRotaryTable] = None
+
+    def struct(self) -> _Layer:
+        return _Layer(self.layer, self.num_heads, self.sliding_window, int(bool(self.neox)),
+                      self.scale, 0, self.rope.handle if self.rope is not None else None)
+
+
+class HipKvCache:
+    """Device-resident KV cache for ``sequences`` independent sessions (KvCache / LayeredKvCache)."""
+
+    def __init__(self, owner: HipAttentionLibrary, num_layers: int, max_seq_len: int,
+                 num_kv_heads: int, key_length: int, value_length: int, half_precision: bool,
+                 sequences: int, ring_capacity: Optional[Sequence[int]]):
+        self.owner = owner
+        self.num_layers, self.max_seq_len = num_layers, max_seq_len
+        self.num_kv_heads, self.key_length, self.value_length = num_kv_heads, key_length, value_length
+        self.key_dim = num_kv_heads * key_length
+        self.value_dim = num_kv_heads * value_length
+        self.sequences = sequences
+        self.half_precision = half_precision
+        ring = None
+        if ring_capacity is not None:
+            if len(ring_capacity) != num_layers:
+                raise ValueError("ring_capacity needs one entry per layer")
+            ring = (ctypes.c_uint32 * num_layers)(*ring_capacity)
+        out = _vp()
+        owner.check(owner.lib.jmodels_attn_kv_create(
+            owner.ctx, sequences, num_layers, max_seq_len, num_kv_heads, key_length, value_length,
+            KV_F16 if half_precision else KV_F32, ring, ctypes.byref(out)), "kv_create")
+        self.handle = out.value
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.owner.check(self.owner.lib.jmodels_attn_kv_destroy(self.handle), "kv_destroy")
+            self.handle = None
+
+    # ---- KvCache API
+
+    def store(self, layer: int, position: int, key, value, sequence: int = 0) -> None:
+        k = _f32(key)
+        v = _f32(value)
+        if k.size != self.key_dim:
+            raise ValueError(f"key.length must equal {self.key_dim}: {k.size}")
+        if v.size != self.value_dim:
+            raise ValueError(f"value.length must equal {self.value_dim}: {v.size}")
+        o = self.owner
+        o.check(o.lib.jmodels_attn_kv_store(o.ctx, self.handle, sequence, layer, position,
+                                            _ptr(k), k.size, _ptr(v), v.size), "kv_store")
+
+    def read(self, layer: int, frm: int, to: int, sequence: int = 0):
+        n = max(to - frm, 0)
+        keys = np.empty(n * self.key_dim, np.float32)
+        values = np.empty(n * self.value_dim, np.float32)
+        o = self.owner
+        o.check(o.lib.jmodels_attn_kv_read(o.ctx, self.handle, sequence, layer, frm, to,
+                                           _ptr(keys), keys.size, _ptr(values), values.size),
+                "kv_read")
+        return keys, values
+
+    def key_slice(self, layer: int, frm: int, to: int, sequence: int = 0) -> np.ndarray:
+        return self.read(layer, frm, to, sequence)[0]
+
+    def value_slice(self, layer: int, frm: int, to: int, sequence: int = 0) -> np.ndarray:
+        return self.read(layer, frm, to, sequence)[1]
+
+    def contains(self, layer: int, position: int, sequence: int = 0) -> bool:
+        out = ctypes.c_int32()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_kv_contains(self.handle, sequence, layer, position,
+                                               ctypes.byref(out)), "kv_contains")
+        return bool(out.value)
+
+    def discard_from(self, position: int, sequence: int = 0) -> None:
+        o = self.owner
+        o.check(o.lib.jmodels_attn_kv_discard_from(self.handle, sequence, position),
+                "kv_discard_from")
+
+    def clear(self, sequence: int = -1) -> None:
+        o = self.owner
+        o.check(o.lib.jmodels_attn_kv_clear(self.handle, sequence), "kv_clear")
+
+    def device_bytes(self) -> int:
+        out = ctypes.c_uint64()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_kv_bytes(self.handle, ctypes.byref(out)), "kv_bytes")
+        return out.value
+
+    # ---- attention (host buffers, synchronous)
+
+    def _rows(self, sequences, positions):
+        seq = np.ascontiguousarray(sequences, dtype=np.uint32).reshape(-1)
+        pos = np.ascontiguousarray(positions, dtype=np.uint32).reshape(-1)
+        if seq.size != pos.size or seq.size == 0:
+            raise ValueError("sequences and positions must be non-empty and of equal length")
+        return seq, pos
+
+    def _check_heads(self, layer: AttentionLayer):
+        if layer.num_heads <= 0 or layer.num_heads % self.num_kv_heads:
+            raise ValueError("numHeads must be divisible by numKvHeads")
+
+    def append(self, layer: AttentionLayer, positions, q, k, v, sequences=None):
+        """RoPE + store; returns the rotated queries."""
+        self._check_heads(layer)
+        seq, pos = self._rows(np.zeros(np.size(positions)) if sequences is None else sequences,
+                              positions)
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        qr = np.empty_like(q)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_append(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), _ptr(q), q.size, _ptr(k), k.size, _ptr(v), v.size,
+            _ptr(qr), qr.size), "append")
+        return qr
+
+    def attend(self, layer: AttentionLayer, positions, q, sequences=None) -> np.ndarray:
+        """groupedQueryAttention for already-rotated queries."""
+        self._check_heads(layer)
+        seq, pos = self._rows(np.zeros(np.size(positions)) if sequences is None else sequences,
+                              positions)
+        q = _f32(q)
+        out = np.empty(seq.size * layer.num_heads * self.value_length, np.float32)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_attend(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), _ptr(q), q.size, _ptr(out), out.size), "attend")
+        return out
+
+    def decode(self, layer: AttentionLayer, positions, q, k, v, sequences=None) -> np.ndarray:
+        """One token per session: RoPE, append, attend."""
+        self._check_heads(layer)
+        seq, pos = self._rows(np.zeros(np.size(positions)) if sequences is None else sequences,
+                              positions)
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        out = np.empty(seq.size * layer.num_heads * self.value_length, np.float32)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_decode(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), _ptr(q), q.size, _ptr(k), k.size, _ptr(v), v.size,
+            _ptr(out), out.size), "decode")
+        return out
+
+    def prefill(self, layer: AttentionLayer, start: int, q, k, v, sequence: int = 0) -> np.ndarray:
+        """Causal prefill of consecutive rows start .. start+n-1."""
+        self._check_heads(layer)
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        n = q.size // (layer.num_heads * self.key_length)
+        out = np.empty(n * layer.num_heads * self.value_length, np.float32)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_prefill(
+            o.ctx, self.handle, ctypes.byref(st), sequence, start, n, _ptr(q), q.size, _ptr(k),
+            k.size, _ptr(v), v.size, _ptr(out), out.size), "prefill")
+        return out
+
+    def attend_causal(self, layer: AttentionLayer, start: int, q, sequence: int = 0) -> np.ndarray:
+        """computeBatchedAttention: causal attention of cached rows start .. start+n-1."""
+        self._check_heads(layer)
+        q = _f32(q)
+        n = q.size // (layer.num_heads * self.key_length)
+        out = np.empty(n * layer.num_heads * self.value_length, np.float32)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_attend_causal(
+            o.ctx, self.handle, ctypes.byref(st), sequence, start, n, _ptr(q), q.size, _ptr(out),
+            out.size), "attend_causal")
+        return out
+
+    # ---- attention (device pointers, asynchronous on the context stream)
+
+    def attend_causal_device(self, layer: AttentionLayer, sequence: int, start: int, n: int,
+                             q_ptr: int, q_elems: int, out_ptr: int, out_elems: int) -> None:
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_attend_causal_device(
+            o.ctx, self.handle, ctypes.byref(st), sequence, start, n, q_ptr, q_elems, out_ptr,
+            out_elems), "attend_causal_device")
+
+
+    def decode_device(self, layer: AttentionLayer, sequences, positions, q_ptr: int, q_elems: int,
+                      k_ptr: int, k_elems: int, v_ptr: int, v_elems: int, out_ptr: int,
+                      out_elems: int) -> None:
+        seq, pos = self._rows(sequences, positions)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_decode_device(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), q_ptr, q_elems, k_ptr, k_elems, v_ptr, v_elems, out_ptr,
+            out_elems), "decode_device")
+
+    def attend_device(self, layer: AttentionLayer, sequences, positions, q_ptr: int,
+                      q_elems: int, out_ptr: int, out_elems: int) -> None:
+        seq, pos = self._rows(sequences, positions)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_attend_device(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), q_ptr, q_elems, out_ptr, out_elems), "attend_device")
+
+    def append_device(self, layer: AttentionLayer, sequences, positions, q_ptr: int,
+                      q_elems: int, k_ptr: int, k_elems: int, v_ptr: int, v_elems: int,
+                      qrot_ptr: int = 0, qrot_elems: int = 0) -> None:
+        seq, pos = self._rows(sequences, positions)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_append_device(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), q_ptr, q_elems, k_ptr, k_elems, v_ptr, v_elems,
+            qrot_ptr or None, qrot_elems), "append_device")
+
+    def prefill_device(self, layer: AttentionLayer, sequence: int, start: int, n: int,
+                       q_ptr: int, q_elems: int, k_ptr: int, k_elems: int, v_ptr: int,
+                       v_elems: int, out_ptr: int, out_elems: int) -> None:
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_prefill_device(
+            o.ctx, self.handle, ctypes.byref(st), sequence, start, n, q_ptr, q_elems, k_ptr,
+            k_elems, v_ptr, v_elems, out_ptr, out_elems), "prefill_device")
+
+
+def default_scale(key_length: int) -> float:
+    """(float)(1.0 / Math.sqrt(keyLength)) (llama/LlamaForwardPass.java:1559)."""
+    return float(np.float32(1.0 / math.sqrt(key_length)))

@@ -1,0 +1,104 @@
+// Internal interface between the C-ABI runtime (jma_runtime.cpp) and the gfx950 kernels
+// (jma_kernels.hip). Not part of the public ABI; include/jmodels_attn.h is.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jma {
+
+// Rows handled by one launch when their (sequence, position) pairs are passed as kernel
+// arguments; larger batches are split into several launches by the runtime.
+constexpr int kMaxRows = 128;
+// Waves per decode workgroup: the waves of one workgroup share a split and combine in LDS.
+constexpr int kDecodeWaves = 4;
+// Most splits one decode row may be cut into; the cross-split reduction loads them all at once.
+constexpr int kMaxSplits = 32;
+
+// Where one layer's K and V live. K: [sequence][layer][kv head][slot][key_length] row-major.
+// V: [sequence][layer][kv head][slot / B][value_length][B] (B = 32 for f16, 16 for f32), the
+// transposed block layout the PV matrix cores read directly; f16 blocks store slot r at
+// index 8*((r%16)/4) + 4*(r/16) + r%4 (see perm32 in jma_kernels.hip).
+struct KvView {
+  void* k;
+  void* v;
+  uint64_t seq_stride_k, seq_stride_v;  // elements per sequence
+  uint64_t layer_off_k, layer_off_v;    // elements from a sequence's base to this layer
+  uint32_t cap;                         // physical slots per (sequence, layer, kv head)
+  uint32_t ring;                        // 1: slot = position % cap, else slot = position
+};
+
+// Rows of one launch. Contiguous rows (one sequence, consecutive positions) have no count limit;
+// listed rows are at most kMaxRows.
+struct RowList {
+  uint32_t count;
+  uint32_t contiguous;  // 1: row i is (seq0, start + i); else (seq[i], pos[i])
+  uint32_t seq0, start;
+  uint32_t seq[kMaxRows];
+  uint32_t pos[kMaxRows];
+};
+
+// Kernel arguments keep their scalars first so a kernel's opening scalar loads touch a few cache
+// lines; the row tables come last and are read only when rows are listed.
+struct AppendArgs {
+  const float* q;       // [count][num_heads * dk]
+  const float* k;       // [count][num_kv_heads * dk]
+  const float* v;       // [count][num_kv_heads * dv]
+  float* q_out;         // rotated q, f32, nullable
+  const float* cos_t;   // [max_positions][pairs], nullable = no RoPE
+  const float* sin_t;
+  KvView kv;
+  uint32_t pairs, neox, num_heads, num_kv_heads, dk, dv;
+  uint32_t blocks_per_row;  // 256-thread blocks per row; one thread per element pair
+  RowList rows;
+};
+
+struct DecodeArgs {
+  const float* q;       // [count][num_heads * dk]; rotated unless rope_q
+  float* out;           // [count][num_heads * dv]
+  float* part_acc;      // [items][16][dv]
+  float* part_ml;       // [items][16][2]  (running max in log2 units, sum)
+  uint32_t* counters;   // [rows][kv heads][head groups] arrival counts, zero between launches;
+                        // null = reduce_kernel combines the splits
+  const float* k_new;   // [count][num_kv_heads * dk] raw keys to rotate and append; null = none
+  const float* v_new;   // [count][num_kv_heads * dv]
+  const float* cos_t;   // RoPE factors [max_positions][pairs]; null = no RoPE
+  const float* sin_t;
+  int* err;             // bit 0: non-finite score seen
+  KvView kv;
+  float qscale;         // score scale * log2(e), folded into q
+  uint32_t num_heads, group, hgroups, window;
+  uint32_t pairs, neox, rope_q;  // rope_q: q is raw and the kernel rotates it
+  uint32_t tiles_per_split;
+  uint32_t total_items;
+  uint32_t ns_uniform;  // > 0: every row has this many splits, rows located arithmetically
+  RowList rows;
+  uint32_t item_start[kMaxRows + 1];
+  uint32_t nsplit[kMaxRows];
+};
+
+struct PrefillArgs {
+  KvView kv;
+  const float* q;       // [n][num_heads][dk], rotated
+  float qscale;         // score scale * log2(e)
+  float* out;           // [n][num_heads][dv]
+  int* err;
+  uint32_t n, start, seq, window;
+  uint32_t num_heads, group;
+  uint32_t heads_per_block;  // query heads of one kv head handled by a workgroup
+  uint32_t rows_per_block;   // query rows per workgroup (multiple of 16)
+  uint32_t q_tiles;
+};
+
+// Storage block (slots) of the transposed V layout.
+inline int v_block(bool f16) { return f16 ? 32 : 16; }
+
+bool decode_supported(bool f16, int dk, int dv);
+bool prefill_supported(int dk, int dv);
+
+hipError_t launch_append(const AppendArgs& a, bool f16, hipStream_t stream);
+hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStream_t stream);
+hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream);
+hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stream);
+
+}  // namespace jma

@@ -1,0 +1,1268 @@
+// Host runtime behind the C ABI declared in include/jmodels_attn.h.
+//
+// Owns the per-GPU context (stream, error word, scratch), the RoPE tables and the HBM-resident
+// KV caches with the reference's bookkeeping: the populated bitmap of KvCache
+// (backend-java/src/main/java/com/integrallis/models/backend/purejava/cache/KvCache.java:33, 72,
+// 161-173) for LINEAR layers and the positions[] array of LayeredKvCache
+// (cache/LayeredKvCache.java:124, 168, 192-197, 212-223) for RING layers. Every export catches
+// C++ exceptions and turns them into status codes, like the Rust exports' catch_unwind
+// (backend-native/src/main/rust/model-kernels/src/lib.rs:497-584).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/jmodels_attn.h"
+#include "jma_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Failure {
+  int32_t status;
+  std::string message;
+};
+
+[[noreturn]] void fail(int32_t status, const std::string& message) {
+  throw Failure{status, message};
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(JMODELS_ATTN_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <typename F>
+int32_t guard(F&& body) {
+  try {
+    body();
+    return JMODELS_ATTN_OK;
+  } catch (const Failure& f) {
+    g_last_error = f.message;
+    return f.status;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return JMODELS_ATTN_PANIC;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return JMODELS_ATTN_PANIC;
+  } catch (...) {
+    g_last_error = "unknown exception";
+    return JMODELS_ATTN_PANIC;
+  }
+}
+
+uint64_t round_up(uint64_t x, uint64_t m) { return (x + m - 1) / m * m; }
+
+// Grow-only device buffer owned by a context.
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  // Regrowth waits for `stream` so no queued kernel still reads the old allocation.
+  void reserve(size_t need, hipStream_t stream) {
+    if (need <= bytes) return;
+    if (ptr) {
+      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      hip_check(hipFree(ptr), "hipFree");
+    }
+    ptr = nullptr;
+    bytes = 0;
+    size_t grow = std::max(need, (size_t)1 << 16);
+    hip_check(hipMalloc(&ptr, grow), "hipMalloc scratch");
+    bytes = grow;
+  }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+};
+
+int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return fallback;
+  return std::atoi(v);
+}
+
+}  // namespace
+
+struct jmodels_attn_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int* d_err = nullptr;
+  DeviceBuffer part_acc, part_ml, counters, qrot, stage_q, stage_k, stage_v, stage_out;
+  int decode_target_blocks = 256;   // workgroups a decode launch aims for (256 CUs)
+  int tiles_per_wave = 2;           // minimum tiles each decode wave streams
+  bool unfused = false;             // JMA_UNFUSED=1: separate append and reduce kernels
+};
+
+struct jmodels_attn_rope {
+  jmodels_attn_context* ctx = nullptr;
+  uint32_t rotary_dim = 0, pairs = 0, max_positions = 0;
+  float* d_cos = nullptr;
+  float* d_sin = nullptr;
+};
+
+struct jmodels_attn_kv {
+  jmodels_attn_context* ctx = nullptr;
+  uint32_t sequences = 0, layers = 0, max_seq_len = 0, hkv = 0, dk = 0, dv = 0, dtype = 0;
+  std::vector<uint32_t> ring;      // logical ring capacity per layer, 0 = linear
+  std::vector<uint32_t> cap;       // physical slots per layer
+  std::vector<uint64_t> layer_off_k, layer_off_v;
+  uint64_t seq_stride_k = 0, seq_stride_v = 0;
+  void* d_k = nullptr;
+  void* d_v = nullptr;
+  uint64_t bytes = 0;
+  // host bookkeeping, indexed [sequence * layers + layer]
+  std::vector<std::vector<uint64_t>> populated;  // linear layers: bitmap over positions
+  std::vector<uint32_t> contiguous_end;          // linear: positions [0, end) all populated
+  std::vector<std::vector<int32_t>> positions;   // ring layers: position held by each slot
+
+  bool f16() const { return dtype == JMODELS_ATTN_KV_F16; }
+  size_t elem() const { return f16() ? 2 : 4; }
+  size_t idx(uint32_t s, uint32_t l) const { return (size_t)s * layers + l; }
+
+  jma::KvView view(uint32_t layer) const {
+    jma::KvView v{};
+    v.k = d_k;
+    v.v = d_v;
+    v.seq_stride_k = seq_stride_k;
+    v.seq_stride_v = seq_stride_v;
+    v.layer_off_k = layer_off_k[layer];
+    v.layer_off_v = layer_off_v[layer];
+    v.cap = cap[layer];
+    v.ring = ring[layer] != 0 ? 1u : 0u;
+    return v;
+  }
+
+  bool available(uint32_t s, uint32_t l, uint32_t p) const {
+    if (ring[l]) {
+      const auto& pos = positions[idx(s, l)];
+      return pos[p % ring[l]] == (int32_t)p;
+    }
+    const auto& bits = populated[idx(s, l)];
+    return (bits[p >> 6] >> (p & 63)) & 1u;
+  }
+
+  void mark(uint32_t s, uint32_t l, uint32_t p) {
+    if (ring[l]) {
+      positions[idx(s, l)][p % ring[l]] = (int32_t)p;
+      return;
+    }
+    auto& bits = populated[idx(s, l)];
+    bits[p >> 6] |= 1ull << (p & 63);
+    uint32_t& end = contiguous_end[idx(s, l)];
+    while (end < max_seq_len && ((bits[end >> 6] >> (end & 63)) & 1u)) ++end;
+  }
+
+  // The reference's checks for reading positions [from, to] of a layer: KvCache.slice /
+  // LayeredKvCache.attentionView (cache/KvCache.java:208-230, cache/LayeredKvCache.java:178-197).
+  void require_range(uint32_t s, uint32_t l, uint32_t from, uint32_t to_inclusive) const {
+    if (ring[l] && to_inclusive - from + 1 > ring[l]) {
+      fail(JMODELS_ATTN_OUT_OF_RANGE, "attention range length " +
+                                          std::to_string(to_inclusive - from + 1) +
+                                          " exceeds ring capacity " + std::to_string(ring[l]));
+    }
+    if (!ring[l] && to_inclusive < contiguous_end[idx(s, l)]) return;
+    for (uint32_t p = from; p <= to_inclusive; ++p) {
+      if (!available(s, l, p)) {
+        fail(JMODELS_ATTN_UNAVAILABLE, "cache position " + std::to_string(p) + " for layer " +
+                                           std::to_string(l) + " of sequence " +
+                                           std::to_string(s) + " is not populated");
+      }
+    }
+  }
+};
+
+namespace {
+
+void require(bool ok, int32_t status, const std::string& msg) {
+  if (!ok) fail(status, msg);
+}
+
+void check_ctx(const jmodels_attn_context* ctx) {
+  require(ctx != nullptr, JMODELS_ATTN_NULL_POINTER, "context is null");
+}
+
+struct LayerCall {
+  uint32_t layer, num_heads, group, window, neox;
+  float scale;
+  const jmodels_attn_rope* rope;
+};
+
+LayerCall resolve_layer(const jmodels_attn_kv* kv, const jmodels_attn_layer* p) {
+  require(p != nullptr, JMODELS_ATTN_NULL_POINTER, "layer parameters are null");
+  require(p->layer < kv->layers, JMODELS_ATTN_OUT_OF_RANGE,
+          "layer out of range: " + std::to_string(p->layer));
+  require(p->num_heads > 0 && p->num_heads % kv->hkv == 0, JMODELS_ATTN_INVALID_SHAPE,
+          "num_heads must be a positive multiple of num_kv_heads");
+  LayerCall c{};
+  c.layer = p->layer;
+  c.num_heads = p->num_heads;
+  c.group = p->num_heads / kv->hkv;
+  c.window = p->sliding_window;
+  c.neox = p->neox ? 1u : 0u;
+  // LlamaForwardPass: scale = (float)(1.0 / Math.sqrt(keyLength)) (llama/LlamaForwardPass.java:1559)
+  c.scale = p->scale != 0.0f ? p->scale : (float)(1.0 / sqrt((double)kv->dk));
+  require(isfinite(c.scale) && c.scale > 0.0f, JMODELS_ATTN_INVALID_SHAPE, "scale must be finite and > 0");
+  c.rope = p->rope;
+  if (c.rope) {
+    require(c.rope->ctx == kv->ctx, JMODELS_ATTN_INVALID_SHAPE, "rope table belongs to another context");
+    require(c.rope->rotary_dim <= kv->dk, JMODELS_ATTN_INVALID_SHAPE, "rotary_dim exceeds key_length");
+  }
+  return c;
+}
+
+uint32_t first_visible(uint32_t position, uint32_t window) {
+  return (window == 0 || position + 1 <= window) ? 0u : position + 1 - window;
+}
+
+void check_rows(const jmodels_attn_kv* kv, const LayerCall& lc, uint32_t count,
+                const uint32_t* sequences, const uint32_t* positions) {
+  require(count > 0, JMODELS_ATTN_INVALID_SHAPE, "count must be > 0");
+  require(sequences && positions, JMODELS_ATTN_NULL_POINTER, "sequences/positions are null");
+  for (uint32_t i = 0; i < count; ++i) {
+    require(sequences[i] < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE,
+            "sequence out of range: " + std::to_string(sequences[i]));
+    require(positions[i] < kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "position out of range: " + std::to_string(positions[i]));
+    if (lc.rope) {
+      require(positions[i] < lc.rope->max_positions, JMODELS_ATTN_OUT_OF_RANGE,
+              "position beyond the rope table: " + std::to_string(positions[i]));
+    }
+  }
+  std::vector<uint64_t> keys(count);
+  for (uint32_t i = 0; i < count; ++i) keys[i] = ((uint64_t)sequences[i] << 32) | positions[i];
+  std::sort(keys.begin(), keys.end());
+  require(std::adjacent_find(keys.begin(), keys.end()) == keys.end(), JMODELS_ATTN_INVALID_SHAPE,
+          "rows repeat a (sequence, position)");
+}
+
+void check_elems(uint64_t have, uint64_t need, const char* what) {
+  require(have >= need, JMODELS_ATTN_BUFFER_TOO_SMALL,
+          std::string(what) + " holds " + std::to_string(have) + " elements, needs " +
+              std::to_string(need));
+}
+
+// Rows of one launch. Consecutive positions of one sequence (a single decode row included) use the
+// contiguous form, which kernels resolve without reading the row tables.
+jma::RowList make_rows(uint32_t count, const uint32_t* sequences, const uint32_t* positions) {
+  jma::RowList r{};
+  r.count = count;
+  bool consecutive = true;
+  for (uint32_t i = 1; i < count && consecutive; ++i)
+    consecutive = sequences[i] == sequences[0] && positions[i] == positions[0] + i;
+  r.contiguous = consecutive ? 1u : 0u;
+  r.seq0 = sequences[0];
+  r.start = positions[0];
+  for (uint32_t i = 0; i < count; ++i) {
+    r.seq[i] = sequences[i];
+    r.pos[i] = positions[i];
+  }
+  return r;
+}
+
+uint32_t append_blocks_per_row(uint32_t num_heads, const jmodels_attn_kv* kv) {
+  const uint32_t pairs = num_heads * kv->dk / 2 + kv->hkv * kv->dk / 2 + kv->hkv * kv->dv / 2;
+  return (pairs + 255) / 256;
+}
+
+// ---------------------------------------------------------------- launches
+
+void run_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall& lc,
+                const jma::RowList& rows, const float* q, const float* k, const float* v,
+                float* q_out) {
+  jma::AppendArgs a{};
+  a.kv = kv->view(lc.layer);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_out = q_out;
+  if (lc.rope) {
+    a.cos_t = lc.rope->d_cos;
+    a.sin_t = lc.rope->d_sin;
+    a.pairs = lc.rope->pairs;
+  }
+  a.neox = lc.neox;
+  a.num_heads = lc.num_heads;
+  a.num_kv_heads = kv->hkv;
+  a.dk = kv->dk;
+  a.dv = kv->dv;
+  a.blocks_per_row = append_blocks_per_row(lc.num_heads, kv);
+  a.rows = rows;
+  hip_check(jma::launch_append(a, kv->f16(), ctx->stream), "rope_append launch");
+}
+
+// Split planning for one launch of <= kMaxRows rows. Every workgroup of the launch streams
+// tiles_per_split tiles: at least tiles_per_wave per wave, raised until the launch is near the
+// workgroup target, and high enough that no row needs more than kMaxSplits splits.
+// New rows handed to the decode kernel to rotate and append itself (all null: rows are cached).
+struct FusedAppend {
+  const float* k = nullptr;
+  const float* v = nullptr;
+  bool rope_q = false;  // q is raw: the kernel applies the layer's RoPE
+};
+
+void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
+                     const jma::RowList& rows, const float* q, float* out,
+                     const FusedAppend& fa = FusedAppend()) {
+  const uint32_t blk = (uint32_t)jma::v_block(kv->f16());
+  jma::DecodeArgs a{};
+  a.kv = kv->view(lc.layer);
+  a.q = q;
+  a.out = out;
+  a.err = ctx->d_err;
+  a.qscale = lc.scale * 1.4426950408889634f;
+  a.num_heads = lc.num_heads;
+  a.group = lc.group;
+  a.hgroups = (lc.group + 15) / 16;
+  a.window = lc.window;
+  a.rows = rows;
+  a.k_new = fa.k;
+  a.v_new = fa.v;
+  a.rope_q = fa.rope_q ? 1u : 0u;
+  if (lc.rope && (fa.k || fa.rope_q)) {
+    a.cos_t = lc.rope->d_cos;
+    a.sin_t = lc.rope->d_sin;
+    a.pairs = lc.rope->pairs;
+  }
+  a.neox = lc.neox;
+  std::vector<uint32_t> ntiles(rows.count);
+  uint64_t units = 0;
+  uint32_t max_tiles = 0;
+  for (uint32_t i = 0; i < rows.count; ++i) {
+    const uint32_t pos = rows.pos[i];
+    const uint32_t first = first_visible(pos, lc.window);
+    ntiles[i] = pos / blk - first / blk + 1;
+    max_tiles = std::max(max_tiles, ntiles[i]);
+    units += (uint64_t)ntiles[i] * kv->hkv * a.hgroups;
+  }
+  const uint64_t target = (uint64_t)ctx->decode_target_blocks;
+  uint64_t tps = (uint64_t)jma::kDecodeWaves * ctx->tiles_per_wave;
+  tps = std::max<uint64_t>(tps, (units + target - 1) / target);
+  tps = std::max<uint64_t>(tps, (max_tiles + jma::kMaxSplits - 1) / jma::kMaxSplits);
+  a.tiles_per_split = (uint32_t)tps;
+  uint32_t items = 0;
+  bool any_split = false;
+  bool uniform = true;
+  for (uint32_t i = 0; i < rows.count; ++i) {
+    a.item_start[i] = items;
+    a.nsplit[i] = (uint32_t)((ntiles[i] + tps - 1) / tps);
+    any_split |= a.nsplit[i] > 1;
+    uniform &= a.nsplit[i] == a.nsplit[0];
+    items += a.nsplit[i] * kv->hkv * a.hgroups;
+  }
+  a.item_start[rows.count] = items;
+  a.total_items = items;
+  a.ns_uniform = uniform ? a.nsplit[0] : 0u;
+  if (any_split) {
+    ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream);
+    ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream);
+    a.part_acc = (float*)ctx->part_acc.ptr;
+    a.part_ml = (float*)ctx->part_ml.ptr;
+    if (!ctx->unfused) {
+      // Arrival counters start at zero and the reducing workgroup resets its own, so they are
+      // zeroed only when (re)allocated, never inside a launch sequence a caller may capture.
+      const size_t need = (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t);
+      if (need > ctx->counters.bytes) {
+        ctx->counters.reserve(need, ctx->stream);
+        hip_check(hipMemsetAsync(ctx->counters.ptr, 0, ctx->counters.bytes, ctx->stream),
+                  "zero counters");
+      }
+      a.counters = (uint32_t*)ctx->counters.ptr;
+    }
+  }
+  hip_check(jma::launch_decode(a, kv->f16(), kv->dk, kv->dv, ctx->stream), "decode launch");
+  if (any_split && a.counters == nullptr)
+    hip_check(jma::launch_reduce(a, kv->dv, ctx->stream), "reduce launch");
+}
+
+// The decode kernel rotates q and appends the new rows itself when its RoPE chunks line up with
+// the rotary pairs (a multiple of 8 pairs) and the context does not ask for separate kernels.
+bool can_fuse_decode(const jmodels_attn_context* ctx, const LayerCall& lc) {
+  if (ctx->unfused) return false;
+  return lc.rope == nullptr || lc.rope->pairs % 8 == 0;
+}
+
+void run_attend(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
+                uint32_t count, const uint32_t* sequences, const uint32_t* positions,
+                const float* q, float* out) {
+  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
+  const uint64_t odim = (uint64_t)lc.num_heads * kv->dv;
+  for (uint32_t base = 0; base < count; base += jma::kMaxRows) {
+    const uint32_t n = std::min<uint32_t>(jma::kMaxRows, count - base);
+    jma::RowList rows = make_rows(n, sequences + base, positions + base);
+    run_attend_rows(ctx, kv, lc, rows, q + base * qdim, out + base * odim);
+  }
+}
+
+void validate_attend_ranges(const jmodels_attn_kv* kv, const LayerCall& lc, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions) {
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint32_t p = positions[i];
+    kv->require_range(sequences[i], lc.layer, first_visible(p, lc.window), p);
+  }
+}
+
+void append_rows(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall& lc,
+                 uint32_t count, const uint32_t* sequences, const uint32_t* positions,
+                 const float* q, const float* k, const float* v, float* q_out) {
+  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
+  const uint64_t kdim = (uint64_t)kv->hkv * kv->dk;
+  const uint64_t vdim = (uint64_t)kv->hkv * kv->dv;
+  // One launch takes up to kMaxRows rows. On a RING layer two rows of one sequence may map to
+  // the same slot; such rows go to separate launches in row order, so the later store wins as
+  // with sequential KvCache.store calls.
+  const uint32_t ring = kv->ring[lc.layer];
+  std::vector<uint64_t> slots_in_launch;
+  uint32_t base = 0;
+  while (base < count) {
+    uint32_t n = 0;
+    slots_in_launch.clear();
+    while (base + n < count && n < (uint32_t)jma::kMaxRows) {
+      if (ring) {
+        const uint64_t key = ((uint64_t)sequences[base + n] << 32) | (positions[base + n] % ring);
+        if (std::find(slots_in_launch.begin(), slots_in_launch.end(), key) != slots_in_launch.end())
+          break;
+        slots_in_launch.push_back(key);
+      }
+      ++n;
+    }
+    jma::RowList rows = make_rows(n, sequences + base, positions + base);
+    run_append(ctx, kv, lc, rows, q + base * qdim, k + base * kdim, v + base * vdim,
+               q_out ? q_out + base * qdim : nullptr);
+    base += n;
+  }
+  for (uint32_t i = 0; i < count; ++i) kv->mark(sequences[i], lc.layer, positions[i]);
+}
+
+void check_decode_shape(const jmodels_attn_kv* kv) {
+  require(jma::decode_supported(kv->f16(), (int)kv->dk, (int)kv->dv), JMODELS_ATTN_INVALID_SHAPE,
+          "unsupported head dims for decode: key_length " + std::to_string(kv->dk) +
+              ", value_length " + std::to_string(kv->dv));
+}
+
+// Causal attention of rows start .. start+n-1 whose K/V are cached and whose rotated queries are
+// q (computeBatchedAttention, llama/LlamaForwardPass.java:1515-1541): row b attends
+// [first(start+b), start+b]. f16 caches run the MFMA prefill kernel; f32 caches run the split-K
+// decode kernel over chunks of listed rows.
+void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
+                        uint32_t sequence, uint32_t start, uint32_t n, const float* q, float* out) {
+  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
+  const uint64_t odim = (uint64_t)lc.num_heads * kv->dv;
+  if (kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv)) {
+    jma::PrefillArgs a{};
+    a.kv = kv->view(lc.layer);
+    a.q = q;
+    a.qscale = lc.scale * 1.4426950408889634f;
+    a.out = out;
+    a.err = ctx->d_err;
+    a.n = n;
+    a.start = start;
+    a.seq = sequence;
+    a.window = lc.window;
+    a.num_heads = lc.num_heads;
+    a.group = lc.group;
+    a.heads_per_block = std::min<uint32_t>(lc.group, 16);
+    a.rows_per_block = a.heads_per_block <= 4 ? 64 : (a.heads_per_block <= 8 ? 32 : 16);
+    a.q_tiles = (n + a.rows_per_block - 1) / a.rows_per_block;
+    hip_check(jma::launch_prefill(a, (int)kv->dk, (int)kv->dv, ctx->stream), "prefill launch");
+    return;
+  }
+  check_decode_shape(kv);
+  for (uint32_t base = 0; base < n; base += jma::kMaxRows) {
+    const uint32_t m = std::min<uint32_t>(jma::kMaxRows, n - base);
+    jma::RowList rows{};
+    rows.count = m;
+    rows.contiguous = 0;
+    for (uint32_t i = 0; i < m; ++i) {
+      rows.seq[i] = sequence;
+      rows.pos[i] = start + base + i;
+    }
+    run_attend_rows(ctx, kv, lc, rows, q + base * qdim, out + base * odim);
+  }
+}
+
+// The reference's checks before a causal block of rows reads the cache: every position rows
+// start .. start+n-1 see must be available, and a RING layer must hold them all at once.
+void validate_causal(const jmodels_attn_kv* kv, const LayerCall& lc, uint32_t sequence,
+                     uint32_t start, uint32_t n, bool rows_cached) {
+  const uint32_t first = first_visible(start, lc.window);
+  if (kv->ring[lc.layer]) {
+    // Gemma4KvCache sizes rings as window + prefill chunk (gemma4/Gemma4KvCache.java:39).
+    require(start + n - first <= kv->ring[lc.layer], JMODELS_ATTN_OUT_OF_RANGE,
+            "prefill chunk plus window exceeds ring capacity " + std::to_string(kv->ring[lc.layer]));
+  }
+  if (rows_cached) kv->require_range(sequence, lc.layer, first, start + n - 1);
+  else if (first < start) kv->require_range(sequence, lc.layer, first, start - 1);
+}
+
+void prefill_impl(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall& lc,
+                  uint32_t sequence, uint32_t start, uint32_t n, const float* q, const float* k,
+                  const float* v, float* out) {
+  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
+  if (!(kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv))) check_decode_shape(kv);
+  validate_causal(kv, lc, sequence, start, n, false);
+  ctx->qrot.reserve((size_t)n * qdim * sizeof(float), ctx->stream);
+  // One launch appends every row: consecutive positions of one sequence need no row table.
+  jma::RowList rows{};
+  rows.count = n;
+  rows.contiguous = 1;
+  rows.seq0 = sequence;
+  rows.start = start;
+  run_append(ctx, kv, lc, rows, q, k, v, (float*)ctx->qrot.ptr);
+  for (uint32_t i = 0; i < n; ++i) kv->mark(sequence, lc.layer, start + i);
+  attend_causal_impl(ctx, kv, lc, sequence, start, n, (const float*)ctx->qrot.ptr, out);
+}
+
+int32_t collect_errors(jmodels_attn_context* ctx) {
+  hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  int err = 0;
+  hip_check(hipMemcpy(&err, ctx->d_err, sizeof(int), hipMemcpyDeviceToHost), "read error word");
+  if (err != 0) {
+    int zero = 0;
+    hip_check(hipMemcpy(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "reset error word");
+    fail(JMODELS_ATTN_NON_FINITE, "softmax input contains NaN or positive infinity");
+  }
+  return JMODELS_ATTN_OK;
+}
+
+void set_device(const jmodels_attn_context* ctx) { hip_check(hipSetDevice(ctx->device), "hipSetDevice"); }
+
+template <typename T>
+T* stage(DeviceBuffer& buf, const T* host, uint64_t elems, hipStream_t stream) {
+  buf.reserve(elems * sizeof(T), stream);
+  if (host)
+    hip_check(hipMemcpyAsync(buf.ptr, host, elems * sizeof(T), hipMemcpyHostToDevice, stream),
+              "copy to device");
+  return (T*)buf.ptr;
+}
+
+}  // namespace
+
+// ================================================================ exports
+
+extern "C" {
+
+uint32_t jmodels_attn_abi_version(void) { return JMODELS_ATTN_ABI_VERSION; }
+
+uint64_t jmodels_attn_capabilities(void) {
+  return JMODELS_ATTN_CAP_DECODE_F32 | JMODELS_ATTN_CAP_DECODE_F16 | JMODELS_ATTN_CAP_PREFILL_MFMA |
+         JMODELS_ATTN_CAP_RAGGED_DECODE | JMODELS_ATTN_CAP_SLIDING_WINDOW |
+         JMODELS_ATTN_CAP_RING_LAYERS | JMODELS_ATTN_CAP_DEVICE_POINTERS;
+}
+
+const char* jmodels_attn_status_name(int32_t status) {
+  switch (status) {
+    case JMODELS_ATTN_OK: return "OK";
+    case JMODELS_ATTN_NULL_POINTER: return "NULL_POINTER";
+    case JMODELS_ATTN_INVALID_SHAPE: return "INVALID_SHAPE";
+    case JMODELS_ATTN_BUFFER_TOO_SMALL: return "BUFFER_TOO_SMALL";
+    case JMODELS_ATTN_PANIC: return "PANIC";
+    case JMODELS_ATTN_DEVICE_ERROR: return "DEVICE_ERROR";
+    case JMODELS_ATTN_OUT_OF_RANGE: return "OUT_OF_RANGE";
+    case JMODELS_ATTN_UNAVAILABLE: return "UNAVAILABLE";
+    case JMODELS_ATTN_NON_FINITE: return "NON_FINITE";
+    default: return "UNKNOWN";
+  }
+}
+
+const char* jmodels_attn_last_error(void) { return g_last_error.c_str(); }
+
+jmodels_attn_context* jmodels_attn_context_create(int32_t device) {
+  jmodels_attn_context* out = nullptr;
+  int32_t st = guard([&] {
+    int n = 0;
+    hip_check(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    require(device >= 0 && device < n, JMODELS_ATTN_OUT_OF_RANGE, "no such device");
+    hipDeviceProp_t prop;
+    hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    require(strncmp(prop.gcnArchName, "gfx950", 6) == 0, JMODELS_ATTN_INVALID_SHAPE,
+            std::string("device is not gfx950: ") + prop.gcnArchName);
+    hip_check(hipSetDevice(device), "hipSetDevice");
+    auto* ctx = new jmodels_attn_context();
+    ctx->device = device;
+    ctx->decode_target_blocks = std::max(1, env_int("JMA_DECODE_TARGET_BLOCKS", 256));
+    ctx->tiles_per_wave = std::max(1, env_int("JMA_DECODE_TILES_PER_WAVE", 2));
+    ctx->unfused = env_int("JMA_UNFUSED", 0) != 0;
+    try {
+      hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
+      hip_check(hipMalloc(&ctx->d_err, sizeof(int)), "hipMalloc error word");
+      hip_check(hipMemset(ctx->d_err, 0, sizeof(int)), "hipMemset error word");
+    } catch (...) {
+      if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+      if (ctx->d_err) (void)hipFree(ctx->d_err);
+      delete ctx;
+      throw;
+    }
+    out = ctx;
+  });
+  return st == JMODELS_ATTN_OK ? out : nullptr;
+}
+
+int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx) {
+  if (!ctx) return JMODELS_ATTN_NULL_POINTER;
+  return guard([&] {
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->counters, &ctx->qrot, &ctx->stage_q,
+                            &ctx->stage_k, &ctx->stage_v, &ctx->stage_out})
+      b->release();
+    (void)hipFree(ctx->d_err);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+  });
+}
+
+int32_t jmodels_attn_context_synchronize(jmodels_attn_context* ctx) {
+  return guard([&] {
+    check_ctx(ctx);
+    set_device(ctx);
+    collect_errors(ctx);
+  });
+}
+
+int32_t jmodels_attn_context_stream(jmodels_attn_context* ctx, void** stream_out) {
+  return guard([&] {
+    check_ctx(ctx);
+    require(stream_out != nullptr, JMODELS_ATTN_NULL_POINTER, "stream_out is null");
+    *stream_out = (void*)ctx->stream;
+  });
+}
+
+int32_t jmodels_attn_rope_create(jmodels_attn_context* ctx, uint32_t rotary_dim, float theta,
+                                 float frequency_scale, const float* frequency_factors,
+                                 uint32_t factor_count, uint32_t max_positions,
+                                 jmodels_attn_rope** rope_out) {
+  return guard([&] {
+    check_ctx(ctx);
+    require(rope_out != nullptr, JMODELS_ATTN_NULL_POINTER, "rope_out is null");
+    *rope_out = nullptr;
+    // RotaryTable ctor validation (ops/RotaryTable.java:48-66, 188-192).
+    require(rotary_dim > 0 && (rotary_dim & 1) == 0, JMODELS_ATTN_INVALID_SHAPE,
+            "rotaryDim must be positive and even: " + std::to_string(rotary_dim));
+    require(theta > 0.0f && isfinite(theta), JMODELS_ATTN_INVALID_SHAPE, "theta must be finite and > 0");
+    require(frequency_scale > 0.0f && isfinite(frequency_scale), JMODELS_ATTN_INVALID_SHAPE,
+            "frequencyScale must be finite and > 0");
+    require(max_positions > 0, JMODELS_ATTN_INVALID_SHAPE, "max_positions must be > 0");
+    const uint32_t pairs = rotary_dim / 2;
+    if (frequency_factors) {
+      require(factor_count == pairs, JMODELS_ATTN_INVALID_SHAPE,
+              "frequencyFactors must contain " + std::to_string(pairs) + " entries");
+      for (uint32_t i = 0; i < pairs; ++i)
+        require(frequency_factors[i] > 0.0f && isfinite(frequency_factors[i]),
+                JMODELS_ATTN_INVALID_SHAPE, "frequencyFactors must be finite and > 0");
+    }
+    // RotaryTable: frequencies in double pow (:69-72); fillFactors (:177-186): angle in float,
+    // cos/sin in double rounded to float.
+    std::vector<float> freq(pairs);
+    for (uint32_t p = 0; p < pairs; ++p)
+      freq[p] = (float)(1.0 / pow((double)theta, (double)(p * 2) / (double)rotary_dim));
+    std::vector<float> cs((size_t)max_positions * pairs), sn((size_t)max_positions * pairs);
+    for (uint32_t pos = 0; pos < max_positions; ++pos) {
+      const float scaled = (float)pos * frequency_scale;
+      for (uint32_t p = 0; p < pairs; ++p) {
+        const float divisor = frequency_factors ? frequency_factors[p] : 1.0f;
+        const float angle = scaled * freq[p] / divisor;
+        cs[(size_t)pos * pairs + p] = (float)cos((double)angle);
+        sn[(size_t)pos * pairs + p] = (float)sin((double)angle);
+      }
+    }
+    set_device(ctx);
+    auto* rope = new jmodels_attn_rope();
+    rope->ctx = ctx;
+    rope->rotary_dim = rotary_dim;
+    rope->pairs = pairs;
+    rope->max_positions = max_positions;
+    try {
+      const size_t bytes = cs.size() * sizeof(float);
+      hip_check(hipMalloc(&rope->d_cos, bytes), "hipMalloc rope");
+      hip_check(hipMalloc(&rope->d_sin, bytes), "hipMalloc rope");
+      hip_check(hipMemcpy(rope->d_cos, cs.data(), bytes, hipMemcpyHostToDevice), "upload rope");
+      hip_check(hipMemcpy(rope->d_sin, sn.data(), bytes, hipMemcpyHostToDevice), "upload rope");
+    } catch (...) {
+      if (rope->d_cos) (void)hipFree(rope->d_cos);
+      if (rope->d_sin) (void)hipFree(rope->d_sin);
+      delete rope;
+      throw;
+    }
+    *rope_out = rope;
+  });
+}
+
+int32_t jmodels_attn_rope_destroy(jmodels_attn_rope* rope) {
+  if (!rope) return JMODELS_ATTN_NULL_POINTER;
+  return guard([&] {
+    (void)hipSetDevice(rope->ctx->device);
+    (void)hipStreamSynchronize(rope->ctx->stream);
+    (void)hipFree(rope->d_cos);
+    (void)hipFree(rope->d_sin);
+    delete rope;
+  });
+}
+
+int32_t jmodels_attn_kv_create(jmodels_attn_context* ctx, uint32_t sequences, uint32_t num_layers,
+                               uint32_t max_seq_len, uint32_t num_kv_heads, uint32_t key_length,
+                               uint32_t value_length, uint32_t dtype,
+                               const uint32_t* ring_capacity, jmodels_attn_kv** kv_out) {
+  return guard([&] {
+    check_ctx(ctx);
+    require(kv_out != nullptr, JMODELS_ATTN_NULL_POINTER, "kv_out is null");
+    *kv_out = nullptr;
+    require(sequences > 0 && num_layers > 0 && max_seq_len > 0 && num_kv_heads > 0 &&
+                key_length > 0 && value_length > 0,
+            JMODELS_ATTN_INVALID_SHAPE, "cache dimensions must be > 0");
+    require(dtype == JMODELS_ATTN_KV_F32 || dtype == JMODELS_ATTN_KV_F16, JMODELS_ATTN_INVALID_SHAPE,
+            "dtype must be JMODELS_ATTN_KV_F32 or JMODELS_ATTN_KV_F16");
+    require(key_length % 16 == 0 && value_length % 16 == 0, JMODELS_ATTN_INVALID_SHAPE,
+            "key_length and value_length must be multiples of 16");
+    auto kv = std::make_unique<jmodels_attn_kv>();
+    kv->ctx = ctx;
+    kv->sequences = sequences;
+    kv->layers = num_layers;
+    kv->max_seq_len = max_seq_len;
+    kv->hkv = num_kv_heads;
+    kv->dk = key_length;
+    kv->dv = value_length;
+    kv->dtype = dtype;
+    const uint32_t blk = (uint32_t)jma::v_block(dtype == JMODELS_ATTN_KV_F16);
+    kv->ring.assign(num_layers, 0);
+    kv->cap.assign(num_layers, 0);
+    kv->layer_off_k.assign(num_layers, 0);
+    kv->layer_off_v.assign(num_layers, 0);
+    uint64_t off_k = 0, off_v = 0;
+    for (uint32_t l = 0; l < num_layers; ++l) {
+      uint32_t r = ring_capacity ? ring_capacity[l] : 0;
+      // LayeredKvCache physicalLimit = min(ringCapacity, maxSeqLen) (cache/LayeredKvCache.java:128-129);
+      // a ring at least as long as the context never wraps, so it is stored linearly.
+      if (r >= max_seq_len) r = 0;
+      require(r % 32 == 0, JMODELS_ATTN_INVALID_SHAPE,
+              "ring capacity must be a multiple of 32: " + std::to_string(r));
+      kv->ring[l] = r;
+      kv->cap[l] = r ? r : (uint32_t)round_up(max_seq_len, 32);
+      (void)blk;
+      kv->layer_off_k[l] = off_k;
+      kv->layer_off_v[l] = off_v;
+      off_k += (uint64_t)num_kv_heads * kv->cap[l] * key_length;
+      off_v += (uint64_t)num_kv_heads * kv->cap[l] * value_length;
+    }
+    kv->seq_stride_k = off_k;
+    kv->seq_stride_v = off_v;
+    const uint64_t kbytes = off_k * sequences * kv->elem();
+    const uint64_t vbytes = off_v * sequences * kv->elem();
+    kv->bytes = kbytes + vbytes;
+    set_device(ctx);
+    hip_check(hipMalloc(&kv->d_k, kbytes), "hipMalloc K cache");
+    if (hipMalloc(&kv->d_v, vbytes) != hipSuccess) {
+      (void)hipFree(kv->d_k);
+      fail(JMODELS_ATTN_DEVICE_ERROR, "hipMalloc V cache failed");
+    }
+    // Zero fill: rows past a sequence's end are masked, and zeros keep 0 * V finite.
+    hip_check(hipMemsetAsync(kv->d_k, 0, kbytes, ctx->stream), "zero K cache");
+    hip_check(hipMemsetAsync(kv->d_v, 0, vbytes, ctx->stream), "zero V cache");
+    hip_check(hipStreamSynchronize(ctx->stream), "zero cache");
+    const size_t n = (size_t)sequences * num_layers;
+    kv->populated.resize(n);
+    kv->positions.resize(n);
+    kv->contiguous_end.assign(n, 0);
+    for (uint32_t s = 0; s < sequences; ++s)
+      for (uint32_t l = 0; l < num_layers; ++l) {
+        if (kv->ring[l]) kv->positions[kv->idx(s, l)].assign(kv->ring[l], -1);
+        else kv->populated[kv->idx(s, l)].assign((max_seq_len + 63) / 64, 0);
+      }
+    *kv_out = kv.release();
+  });
+}
+
+int32_t jmodels_attn_kv_destroy(jmodels_attn_kv* kv) {
+  if (!kv) return JMODELS_ATTN_NULL_POINTER;
+  return guard([&] {
+    (void)hipSetDevice(kv->ctx->device);
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    (void)hipFree(kv->d_k);
+    (void)hipFree(kv->d_v);
+    delete kv;
+  });
+}
+
+int32_t jmodels_attn_kv_clear(jmodels_attn_kv* kv, int32_t sequence) {
+  return guard([&] {
+    require(kv != nullptr, JMODELS_ATTN_NULL_POINTER, "kv is null");
+    require(sequence < (int32_t)kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    for (uint32_t s = 0; s < kv->sequences; ++s) {
+      if (sequence >= 0 && (uint32_t)sequence != s) continue;
+      for (uint32_t l = 0; l < kv->layers; ++l) {
+        const size_t i = kv->idx(s, l);
+        if (kv->ring[l]) std::fill(kv->positions[i].begin(), kv->positions[i].end(), -1);
+        else std::fill(kv->populated[i].begin(), kv->populated[i].end(), 0);
+        kv->contiguous_end[i] = 0;
+      }
+    }
+  });
+}
+
+int32_t jmodels_attn_kv_discard_from(jmodels_attn_kv* kv, uint32_t sequence, uint32_t position) {
+  return guard([&] {
+    require(kv != nullptr, JMODELS_ATTN_NULL_POINTER, "kv is null");
+    require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    require(position <= kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "position out of range: " + std::to_string(position));
+    for (uint32_t l = 0; l < kv->layers; ++l) {
+      const size_t i = kv->idx(sequence, l);
+      if (kv->ring[l]) {
+        for (auto& p : kv->positions[i])
+          if (p >= (int32_t)position) p = -1;
+        continue;
+      }
+      auto& bits = kv->populated[i];
+      for (uint32_t p = position; p < kv->max_seq_len; ++p) {
+        if ((p & 63) == 0 && p + 64 <= kv->max_seq_len) {
+          bits[p >> 6] = 0;
+          p += 63;
+          continue;
+        }
+        bits[p >> 6] &= ~(1ull << (p & 63));
+      }
+      kv->contiguous_end[i] = std::min(kv->contiguous_end[i], position);
+    }
+  });
+}
+
+int32_t jmodels_attn_kv_contains(const jmodels_attn_kv* kv, uint32_t sequence, uint32_t layer,
+                                 uint32_t position, int32_t* out) {
+  return guard([&] {
+    require(kv != nullptr && out != nullptr, JMODELS_ATTN_NULL_POINTER, "null argument");
+    require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    require(layer < kv->layers, JMODELS_ATTN_OUT_OF_RANGE, "layer out of range: " + std::to_string(layer));
+    require(position < kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "position out of range: " + std::to_string(position));
+    *out = kv->available(sequence, layer, position) ? 1 : 0;
+  });
+}
+
+int32_t jmodels_attn_kv_store(jmodels_attn_context* ctx, jmodels_attn_kv* kv, uint32_t sequence,
+                              uint32_t layer, uint32_t position, const float* key,
+                              uint64_t key_elements, const float* value, uint64_t value_elements) {
+  return guard([&] {
+    check_ctx(ctx);
+    require(kv != nullptr && key != nullptr && value != nullptr, JMODELS_ATTN_NULL_POINTER, "null argument");
+    require(kv->ctx == ctx, JMODELS_ATTN_INVALID_SHAPE, "cache belongs to another context");
+    require(layer < kv->layers, JMODELS_ATTN_OUT_OF_RANGE, "layer out of range: " + std::to_string(layer));
+    require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    require(position < kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "position out of range: " + std::to_string(position));
+    const uint64_t kdim = (uint64_t)kv->hkv * kv->dk, vdim = (uint64_t)kv->hkv * kv->dv;
+    check_elems(key_elements, kdim, "key");
+    check_elems(value_elements, vdim, "value");
+    set_device(ctx);
+    LayerCall lc{};
+    lc.layer = layer;
+    lc.num_heads = kv->hkv;
+    lc.group = 1;
+    lc.rope = nullptr;
+    float* dk = stage(ctx->stage_k, key, kdim, ctx->stream);
+    float* dv = stage(ctx->stage_v, value, vdim, ctx->stream);
+    // q is unused by a store: point it at k with zero query heads' worth of work.
+    jma::RowList rows = make_rows(1, &sequence, &position);
+    jma::AppendArgs a{};
+    a.kv = kv->view(layer);
+    a.q = dk;
+    a.k = dk;
+    a.v = dv;
+    a.num_heads = 0;
+    a.num_kv_heads = kv->hkv;
+    a.dk = kv->dk;
+    a.dv = kv->dv;
+    a.blocks_per_row = append_blocks_per_row(0, kv);
+    a.rows = rows;
+    hip_check(jma::launch_append(a, kv->f16(), ctx->stream), "store launch");
+    hip_check(hipStreamSynchronize(ctx->stream), "store");
+    kv->mark(sequence, layer, position);
+  });
+}
+
+int32_t jmodels_attn_kv_read(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                             uint32_t sequence, uint32_t layer, uint32_t from, uint32_t to,
+                             float* keys, uint64_t key_elements, float* values,
+                             uint64_t value_elements) {
+  return guard([&] {
+    check_ctx(ctx);
+    require(kv != nullptr, JMODELS_ATTN_NULL_POINTER, "kv is null");
+    require(layer < kv->layers, JMODELS_ATTN_OUT_OF_RANGE, "layer out of range: " + std::to_string(layer));
+    require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    require(from <= to && to <= kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "invalid position range: [" + std::to_string(from) + ", " + std::to_string(to) + ")");
+    const uint32_t n = to - from;
+    const uint64_t kdim = (uint64_t)kv->hkv * kv->dk, vdim = (uint64_t)kv->hkv * kv->dv;
+    if (keys) check_elems(key_elements, n * kdim, "keys");
+    if (values) check_elems(value_elements, n * vdim, "values");
+    if (n == 0) return;
+    for (uint32_t p = from; p < to; ++p) {
+      if (!kv->available(sequence, layer, p))
+        fail(JMODELS_ATTN_UNAVAILABLE, "cache position " + std::to_string(p) + " for layer " +
+                                           std::to_string(layer) + " is not populated");
+    }
+    set_device(ctx);
+    hip_check(hipStreamSynchronize(ctx->stream), "read");
+    const size_t es = kv->elem();
+    const uint32_t cap = kv->cap[layer];
+    const uint32_t blk = (uint32_t)jma::v_block(kv->f16());
+    const uint64_t kl = (uint64_t)kv->hkv * cap * kv->dk, vl = (uint64_t)kv->hkv * cap * kv->dv;
+    std::vector<unsigned char> hk(kl * es), hv(vl * es);
+    const unsigned char* kbase = (const unsigned char*)kv->d_k +
+                                 (sequence * kv->seq_stride_k + kv->layer_off_k[layer]) * es;
+    const unsigned char* vbase = (const unsigned char*)kv->d_v +
+                                 (sequence * kv->seq_stride_v + kv->layer_off_v[layer]) * es;
+    hip_check(hipMemcpy(hk.data(), kbase, hk.size(), hipMemcpyDeviceToHost), "read K");
+    hip_check(hipMemcpy(hv.data(), vbase, hv.size(), hipMemcpyDeviceToHost), "read V");
+    auto widen = [&](const unsigned char* src, uint64_t index) -> float {
+      if (kv->f16()) {
+        _Float16 h;
+        memcpy(&h, src + index * 2, 2);
+        return (float)h;
+      }
+      float f;
+      memcpy(&f, src + index * 4, 4);
+      return f;
+    };
+    for (uint32_t p = from; p < to; ++p) {
+      const uint32_t slot = kv->ring[layer] ? p % cap : p;
+      const uint32_t r = slot % blk, b = slot / blk;
+      const uint32_t s = kv->f16() ? 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u) : r;
+      for (uint32_t h = 0; h < kv->hkv; ++h) {
+        if (keys)
+          for (uint32_t d = 0; d < kv->dk; ++d)
+            keys[(uint64_t)(p - from) * kdim + h * kv->dk + d] =
+                widen(hk.data(), ((uint64_t)h * cap + slot) * kv->dk + d);
+        if (values)
+          for (uint32_t d = 0; d < kv->dv; ++d)
+            values[(uint64_t)(p - from) * vdim + h * kv->dv + d] =
+                widen(hv.data(), (uint64_t)h * cap * kv->dv + ((uint64_t)b * kv->dv + d) * blk + s);
+      }
+    }
+  });
+}
+
+int32_t jmodels_attn_kv_bytes(const jmodels_attn_kv* kv, uint64_t* bytes_out) {
+  return guard([&] {
+    require(kv != nullptr && bytes_out != nullptr, JMODELS_ATTN_NULL_POINTER, "null argument");
+    *bytes_out = kv->bytes;
+  });
+}
+
+// ---------------------------------------------------------------- attention entry points
+
+static void common_checks(jmodels_attn_context* ctx, const jmodels_attn_kv* kv) {
+  check_ctx(ctx);
+  require(kv != nullptr, JMODELS_ATTN_NULL_POINTER, "kv is null");
+  require(kv->ctx == ctx, JMODELS_ATTN_INVALID_SHAPE, "cache belongs to another context");
+}
+
+static int32_t append_entry(bool device, jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, const float* k, uint64_t k_elements,
+                            const float* v, uint64_t v_elements, float* q_rotated,
+                            uint64_t q_rotated_elements) {
+  return guard([&] {
+    common_checks(ctx, kv);
+    const LayerCall lc = resolve_layer(kv, layer);
+    check_rows(kv, lc, count, sequences, positions);
+    require(q && k && v, JMODELS_ATTN_NULL_POINTER, "q/k/v are null");
+    const uint64_t qn = (uint64_t)count * lc.num_heads * kv->dk;
+    check_elems(q_elements, qn, "q");
+    check_elems(k_elements, (uint64_t)count * kv->hkv * kv->dk, "k");
+    check_elems(v_elements, (uint64_t)count * kv->hkv * kv->dv, "v");
+    if (q_rotated) check_elems(q_rotated_elements, qn, "q_rotated");
+    set_device(ctx);
+    if (device) {
+      append_rows(ctx, kv, lc, count, sequences, positions, q, k, v, q_rotated);
+      return;
+    }
+    const float* dq = stage(ctx->stage_q, q, qn, ctx->stream);
+    const float* dk = stage(ctx->stage_k, k, (uint64_t)count * kv->hkv * kv->dk, ctx->stream);
+    const float* dv = stage(ctx->stage_v, v, (uint64_t)count * kv->hkv * kv->dv, ctx->stream);
+    float* dqo = q_rotated ? stage<float>(ctx->stage_out, nullptr, qn, ctx->stream) : nullptr;
+    append_rows(ctx, kv, lc, count, sequences, positions, dq, dk, dv, dqo);
+    if (q_rotated)
+      hip_check(hipMemcpyAsync(q_rotated, dqo, qn * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                "copy q_rotated");
+    collect_errors(ctx);
+  });
+}
+
+static int32_t attend_entry(bool device, jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, float* out, uint64_t out_elements) {
+  return guard([&] {
+    common_checks(ctx, kv);
+    check_decode_shape(kv);
+    const LayerCall lc = resolve_layer(kv, layer);
+    check_rows(kv, lc, count, sequences, positions);
+    require(q && out, JMODELS_ATTN_NULL_POINTER, "q/out are null");
+    const uint64_t qn = (uint64_t)count * lc.num_heads * kv->dk;
+    const uint64_t on = (uint64_t)count * lc.num_heads * kv->dv;
+    check_elems(q_elements, qn, "q");
+    check_elems(out_elements, on, "out");
+    validate_attend_ranges(kv, lc, count, sequences, positions);
+    set_device(ctx);
+    if (device) {
+      run_attend(ctx, kv, lc, count, sequences, positions, q, out);
+      return;
+    }
+    const float* dq = stage(ctx->stage_q, q, qn, ctx->stream);
+    float* dout = stage<float>(ctx->stage_out, nullptr, on, ctx->stream);
+    run_attend(ctx, kv, lc, count, sequences, positions, dq, dout);
+    hip_check(hipMemcpyAsync(out, dout, on * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "copy out");
+    collect_errors(ctx);
+  });
+}
+
+static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, const float* k, uint64_t k_elements,
+                            const float* v, uint64_t v_elements, float* out,
+                            uint64_t out_elements) {
+  return guard([&] {
+    common_checks(ctx, kv);
+    check_decode_shape(kv);
+    const LayerCall lc = resolve_layer(kv, layer);
+    check_rows(kv, lc, count, sequences, positions);
+    require(q && k && v && out, JMODELS_ATTN_NULL_POINTER, "q/k/v/out are null");
+    const uint64_t qn = (uint64_t)count * lc.num_heads * kv->dk;
+    const uint64_t kn = (uint64_t)count * kv->hkv * kv->dk;
+    const uint64_t vn = (uint64_t)count * kv->hkv * kv->dv;
+    const uint64_t on = (uint64_t)count * lc.num_heads * kv->dv;
+    check_elems(q_elements, qn, "q");
+    check_elems(k_elements, kn, "k");
+    check_elems(v_elements, vn, "v");
+    check_elems(out_elements, on, "out");
+    // Sessions of one batch must be distinct (LlamaForwardPass.validateSessionBatch,
+    // llama/LlamaForwardPass.java:933-960).
+    for (uint32_t i = 0; i < count; ++i)
+      for (uint32_t j = 0; j < i; ++j)
+        require(sequences[i] != sequences[j], JMODELS_ATTN_INVALID_SHAPE, "sessions must be distinct");
+    // Everything the new rows will read, except the rows themselves, must already be cached.
+    for (uint32_t i = 0; i < count; ++i) {
+      const uint32_t p = positions[i];
+      const uint32_t first = first_visible(p, lc.window);
+      if (kv->ring[lc.layer] && p - first + 1 > kv->ring[lc.layer])
+        fail(JMODELS_ATTN_OUT_OF_RANGE, "attention range exceeds ring capacity " +
+                                            std::to_string(kv->ring[lc.layer]));
+      if (first < p) kv->require_range(sequences[i], lc.layer, first, p - 1);
+    }
+    set_device(ctx);
+    const float* dq = q;
+    const float* dk = k;
+    const float* dv = v;
+    float* dout = out;
+    if (!device) {
+      dq = stage(ctx->stage_q, q, qn, ctx->stream);
+      dk = stage(ctx->stage_k, k, kn, ctx->stream);
+      dv = stage(ctx->stage_v, v, vn, ctx->stream);
+      dout = stage<float>(ctx->stage_out, nullptr, on, ctx->stream);
+    }
+    if (can_fuse_decode(ctx, lc)) {
+      // One launch per chunk of rows: RoPE, append, attention and the split reduction.
+      const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk, kdim = (uint64_t)kv->hkv * kv->dk;
+      const uint64_t vdim = (uint64_t)kv->hkv * kv->dv, odim = (uint64_t)lc.num_heads * kv->dv;
+      for (uint32_t base = 0; base < count; base += jma::kMaxRows) {
+        const uint32_t n = std::min<uint32_t>(jma::kMaxRows, count - base);
+        jma::RowList rows = make_rows(n, sequences + base, positions + base);
+        FusedAppend fa;
+        fa.k = dk + base * kdim;
+        fa.v = dv + base * vdim;
+        fa.rope_q = lc.rope != nullptr;
+        run_attend_rows(ctx, kv, lc, rows, dq + base * qdim, dout + base * odim, fa);
+      }
+      for (uint32_t i = 0; i < count; ++i) kv->mark(sequences[i], lc.layer, positions[i]);
+    } else {
+      ctx->qrot.reserve(qn * sizeof(float), ctx->stream);
+      float* qrot = (float*)ctx->qrot.ptr;
+      append_rows(ctx, kv, lc, count, sequences, positions, dq, dk, dv, qrot);
+      run_attend(ctx, kv, lc, count, sequences, positions, qrot, dout);
+    }
+    if (device) return;
+    hip_check(hipMemcpyAsync(out, dout, on * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "copy out");
+    collect_errors(ctx);
+  });
+}
+
+static int32_t prefill_entry(bool device, jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                             const jmodels_attn_layer* layer, uint32_t sequence, uint32_t start,
+                             uint32_t n, const float* q, uint64_t q_elements, const float* k,
+                             uint64_t k_elements, const float* v, uint64_t v_elements,
+                             float* out, uint64_t out_elements) {
+  return guard([&] {
+    common_checks(ctx, kv);
+    const LayerCall lc = resolve_layer(kv, layer);
+    require(n > 0, JMODELS_ATTN_INVALID_SHAPE, "n must be > 0");
+    require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    require((uint64_t)start + n <= kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "position out of range: " + std::to_string((uint64_t)start + n - 1));
+    if (lc.rope)
+      require((uint64_t)start + n <= lc.rope->max_positions, JMODELS_ATTN_OUT_OF_RANGE,
+              "positions beyond the rope table");
+    require(q && k && v && out, JMODELS_ATTN_NULL_POINTER, "q/k/v/out are null");
+    const uint64_t qn = (uint64_t)n * lc.num_heads * kv->dk;
+    const uint64_t kn = (uint64_t)n * kv->hkv * kv->dk;
+    const uint64_t vn = (uint64_t)n * kv->hkv * kv->dv;
+    const uint64_t on = (uint64_t)n * lc.num_heads * kv->dv;
+    check_elems(q_elements, qn, "q");
+    check_elems(k_elements, kn, "k");
+    check_elems(v_elements, vn, "v");
+    check_elems(out_elements, on, "out");
+    set_device(ctx);
+    if (device) {
+      prefill_impl(ctx, kv, lc, sequence, start, n, q, k, v, out);
+      return;
+    }
+    const float* dq = stage(ctx->stage_q, q, qn, ctx->stream);
+    const float* dk = stage(ctx->stage_k, k, kn, ctx->stream);
+    const float* dv = stage(ctx->stage_v, v, vn, ctx->stream);
+    float* dout = stage<float>(ctx->stage_out, nullptr, on, ctx->stream);
+    prefill_impl(ctx, kv, lc, sequence, start, n, dq, dk, dv, dout);
+    hip_check(hipMemcpyAsync(out, dout, on * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "copy out");
+    collect_errors(ctx);
+  });
+}
+
+static int32_t attend_causal_entry(bool device, jmodels_attn_context* ctx,
+                                   const jmodels_attn_kv* kv, const jmodels_attn_layer* layer,
+                                   uint32_t sequence, uint32_t start, uint32_t n, const float* q,
+                                   uint64_t q_elements, float* out, uint64_t out_elements) {
+  return guard([&] {
+    common_checks(ctx, kv);
+    const LayerCall lc = resolve_layer(kv, layer);
+    require(n > 0, JMODELS_ATTN_INVALID_SHAPE, "n must be > 0");
+    require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
+    require((uint64_t)start + n <= kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
+            "position out of range: " + std::to_string((uint64_t)start + n - 1));
+    require(q && out, JMODELS_ATTN_NULL_POINTER, "q/out are null");
+    const uint64_t qn = (uint64_t)n * lc.num_heads * kv->dk;
+    const uint64_t on = (uint64_t)n * lc.num_heads * kv->dv;
+    check_elems(q_elements, qn, "q");
+    check_elems(out_elements, on, "out");
+    if (!(kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv))) check_decode_shape(kv);
+    validate_causal(kv, lc, sequence, start, n, true);
+    set_device(ctx);
+    if (device) {
+      attend_causal_impl(ctx, kv, lc, sequence, start, n, q, out);
+      return;
+    }
+    const float* dq = stage(ctx->stage_q, q, qn, ctx->stream);
+    float* dout = stage<float>(ctx->stage_out, nullptr, on, ctx->stream);
+    attend_causal_impl(ctx, kv, lc, sequence, start, n, dq, dout);
+    hip_check(hipMemcpyAsync(out, dout, on * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "copy out");
+    collect_errors(ctx);
+  });
+}
+
+int32_t jmodels_attn_attend_causal(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t sequence,
+                                   uint32_t start, uint32_t n, const float* q,
+                                   uint64_t q_elements, float* out, uint64_t out_elements) {
+  return attend_causal_entry(false, ctx, kv, layer, sequence, start, n, q, q_elements, out,
+                             out_elements);
+}
+
+int32_t jmodels_attn_attend_causal_device(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                                          const jmodels_attn_layer* layer, uint32_t sequence,
+                                          uint32_t start, uint32_t n, const float* q,
+                                          uint64_t q_elements, float* out,
+                                          uint64_t out_elements) {
+  return attend_causal_entry(true, ctx, kv, layer, sequence, start, n, q, q_elements, out,
+                             out_elements);
+}
+
+int32_t jmodels_attn_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, const float* k, uint64_t k_elements,
+                            const float* v, uint64_t v_elements, float* q_rotated,
+                            uint64_t q_rotated_elements) {
+  return append_entry(false, ctx, kv, layer, count, sequences, positions, q, q_elements, k,
+                      k_elements, v, v_elements, q_rotated, q_rotated_elements);
+}
+
+int32_t jmodels_attn_attend(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, float* out, uint64_t out_elements) {
+  return attend_entry(false, ctx, kv, layer, count, sequences, positions, q, q_elements, out,
+                      out_elements);
+}
+
+int32_t jmodels_attn_decode(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                            const jmodels_attn_layer* layer, uint32_t count,
+                            const uint32_t* sequences, const uint32_t* positions, const float* q,
+                            uint64_t q_elements, const float* k, uint64_t k_elements,
+                            const float* v, uint64_t v_elements, float* out,
+                            uint64_t out_elements) {
+  return decode_entry(false, ctx, kv, layer, count, sequences, positions, q, q_elements, k,
+                      k_elements, v, v_elements, out, out_elements);
+}
+
+int32_t jmodels_attn_prefill(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                             const jmodels_attn_layer* layer, uint32_t sequence, uint32_t start,
+                             uint32_t n, const float* q, uint64_t q_elements, const float* k,
+                             uint64_t k_elements, const float* v, uint64_t v_elements,
+                             float* out, uint64_t out_elements) {
+  return prefill_entry(false, ctx, kv, layer, sequence, start, n, q, q_elements, k, k_elements, v,
+                       v_elements, out, out_elements);
+}
+
+int32_t jmodels_attn_append_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t count,
+                                   const uint32_t* sequences, const uint32_t* positions,
+                                   const float* q, uint64_t q_elements, const float* k,
+                                   uint64_t k_elements, const float* v, uint64_t v_elements,
+                                   float* q_rotated, uint64_t q_rotated_elements) {
+  return append_entry(true, ctx, kv, layer, count, sequences, positions, q, q_elements, k,
+                      k_elements, v, v_elements, q_rotated, q_rotated_elements);
+}
+
+int32_t jmodels_attn_attend_device(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t count,
+                                   const uint32_t* sequences, const uint32_t* positions,
+                                   const float* q, uint64_t q_elements, float* out,
+                                   uint64_t out_elements) {
+  return attend_entry(true, ctx, kv, layer, count, sequences, positions, q, q_elements, out,
+                      out_elements);
+}
+
+int32_t jmodels_attn_decode_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                   const jmodels_attn_layer* layer, uint32_t count,
+                                   const uint32_t* sequences, const uint32_t* positions,
+                                   const float* q, uint64_t q_elements, const float* k,
+                                   uint64_t k_elements, const float* v, uint64_t v_elements,
+                                   float* out, uint64_t out_elements) {
+  return decode_entry(true, ctx, kv, layer, count, sequences, positions, q, q_elements, k,
+                      k_elements, v, v_elements, out, out_elements);
+}
+
+int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                    const jmodels_attn_layer* layer, uint32_t sequence,
+                                    uint32_t start, uint32_t n, const float* q,
+                                    uint64_t q_elements, const float* k, uint64_t k_elements,
+                                    const float* v, uint64_t v_elements, float* out,
+                                    uint64_t out_elements) {
+  return prefill_entry(true, ctx, kv, layer, sequence, start, n, q, q_elements, k, k_elements, v,
+                       v_elements, out, out_elements);
+}
+
+}  // extern "C"

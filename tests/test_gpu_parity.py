@@ -1,0 +1,642 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle on identical seeded inputs.
+
+Bars (from the path's contract): KV-cache contents, RoPE outputs, window bounds and positions are
+bit-exact; attention outputs are within max-abs 1e-3 with f32 KV and normwise relative 2e-2 with
+f16 KV. Configs C1-C5 are the five BASELINE workloads; sizes the oracle cannot finish in seconds
+are reduced, and the full sizes are covered by spot checks and size-independent properties."""
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from gpu_support import (assert_f16_close, assert_f32_close, normal, rope_rows)
+from models_amd import attention as A
+from models_amd import synth
+from oracle import oracle
+from oracle.oracle import KvCache as OracleKv
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def hip():
+    lib = A.HipAttentionLibrary(0)
+    yield lib
+    lib.close()
+
+
+# ------------------------------------------------------------------ KV cache semantics
+
+def _pad(vec, width):
+    out = np.zeros(width, np.float32)
+    out[:len(vec)] = vec
+    return out
+
+
+def test_kv_cache_known_answers_on_device(hip, known_answers):
+    """Replays backend-java's KvCacheTest cases (tests/golden) on the device cache. Head widths are
+    padded to 16 (the device minimum); the observable semantics — stored values, null for
+    unpopulated positions, slices, discardFrom, clear, range errors — must match exactly."""
+    for case in known_answers["kv_cache"]:
+        _say(f"kv case {case['name']}")
+        layers, max_seq, kd, vd = case["ctor"]
+        kv = hip.kv_cache(layers, max_seq, 1, 16, 16, half_precision=case.get("half_precision", False))
+        try:
+            def run(ops):
+                for op in ops:
+                    if op[0] == "store":
+                        kv.store(op[1], op[2], _pad(op[3], 16), _pad(op[4], 16))
+                    elif op[0] == "clear":
+                        kv.clear()
+                    elif op[0] == "discard":
+                        kv.discard_from(op[1])
+                    elif op[0] == "reserve":
+                        pass  # device caches are allocated at max_seq_len up front
+
+            def read_one(l, p, values):
+                try:
+                    k, v = kv.read(l, p, p + 1)
+                except A.AttentionStatusError as e:
+                    assert e.status == A.UNAVAILABLE, e
+                    return None
+                return (v if values else k)
+
+            def check(exps):
+                for e in exps:
+                    kind = e[0]
+                    if kind in ("key", "value"):
+                        got = read_one(e[1], e[2], kind == "value")
+                        if e[3] is None:
+                            assert got is None, (case["name"], e)
+                        else:
+                            np.testing.assert_array_equal(got[:len(e[3])], np.float32(e[3]))
+                            assert not np.any(got[len(e[3]):]), (case["name"], e)
+                    elif kind in ("keyNotNull", "valueNotNull"):
+                        assert read_one(e[1], e[2], kind == "valueNotNull") is not None
+                    elif kind in ("keySlice", "valueSlice"):
+                        if isinstance(e[4], str):
+                            with pytest.raises(A.AttentionStatusError) as info:
+                                kv.read(e[1], e[2], e[3])
+                            assert info.value.status == A.UNAVAILABLE
+                        else:
+                            k, v = kv.read(e[1], e[2], e[3])
+                            got = (k if kind == "keySlice" else v).reshape(e[3] - e[2], 16)
+                            width = len(e[4]) // (e[3] - e[2])
+                            np.testing.assert_array_equal(got[:, :width].reshape(-1), np.float32(e[4]))
+                    elif kind == "storeError":
+                        with pytest.raises(A.AttentionStatusError) as info:
+                            kv.store(e[1], e[2], np.zeros(16), np.zeros(16))
+                        assert info.value.status == A.OUT_OF_RANGE, e
+            run(case["ops"])
+            check(case["expect"])
+            if "then_ops" in case:
+                run(case["then_ops"])
+                check(case["then_expect"])
+        finally:
+            kv.close()
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("neox", [False, True])
+def test_append_rope_is_bit_exact(hip, half, neox):
+    hq, hkv, d, n, theta, scale = 8, 2, 64, 40, 500000.0, 0.5
+    rope = hip.rotary_table(d, theta, scale, max_positions=4096)
+    kv = hip.kv_cache(2, 4096, hkv, d, d, half_precision=half)
+    try:
+        positions = np.array([0, 1, 2, 31, 32, 33, 1000, 4095] + list(range(100, 132)))[:n]
+        q = normal(11, "q", (n, hq * d))
+        k = normal(11, "k", (n, hkv * d))
+        v = normal(11, "v", (n, hkv * d))
+        layer = A.AttentionLayer(1, hq, neox=neox, rope=rope)
+        qr = kv.append(layer, positions, q, k, v).reshape(n, hq * d)
+        q_ref = rope_rows(q, positions, hq, d, d, theta, neox, scale)
+        k_ref = rope_rows(k, positions, hkv, d, d, theta, neox, scale)
+        np.testing.assert_array_equal(qr, q_ref)
+        if half:
+            k_ref = oracle.f16_round(k_ref)
+            v = oracle.f16_round(v)
+        for i, p in enumerate(positions):
+            kk, vv = kv.read(1, int(p), int(p) + 1)
+            np.testing.assert_array_equal(kk, k_ref[i])
+            np.testing.assert_array_equal(vv, v[i])
+        assert not kv.contains(0, int(positions[0]))
+    finally:
+        kv.close()
+        rope.close()
+
+
+def test_rope_gemma4_proportional_golden_on_device(hip, known_answers):
+    case = known_answers["rope"][0]  # RotaryTableTest :80-91
+    rope = hip.rotary_table(case["rotary_dim"], case["theta"], case["frequency_scale"],
+                            max_positions=8, frequency_factors=case["factors"])
+    kv = hip.kv_cache(1, 8, 1, 16, 16, half_precision=False)
+    try:
+        head = _pad(case["input"], 16)
+        layer = A.AttentionLayer(0, 1, neox=True, rope=rope)
+        qr = kv.append(layer, [case["position"]], head, head, np.zeros(16))
+        for idx, value, tol in case["expect_close"]:
+            assert abs(float(qr[idx]) - value) <= tol
+        for idx, value in case["expect_exact"]:
+            assert qr[idx] == np.float32(value)
+        assert not np.any(qr[8:])
+    finally:
+        kv.close()
+        rope.close()
+
+
+# ------------------------------------------------------------------ C1: Qwen3-0.6B f32 decode
+
+def test_c1_qwen3_decode_f32(hip):
+    """16 Q heads, 8 KV heads, d 128, NeoX theta 1e6, f32 KV: 512 prior positions (causal prefill
+    through the split-K kernel) then the decode step at position 512. Full size."""
+    hq, hkv, d, prior, theta = 16, 8, 128, 512, 1e6
+    scale = A.default_scale(d)
+    q = normal(1, "c1/q", (prior + 1, hq * d))
+    k = normal(1, "c1/k", (prior + 1, hkv * d))
+    v = normal(1, "c1/v", (prior + 1, hkv * d))
+    ref = OracleKv(1, 1024, hkv * d, hkv * d)
+    ref_prefill, _, _ = ref.prefill_layer(0, 0, q[:prior], k[:prior], v[:prior], hq, hkv, d, d,
+                                          theta, 1.0, True, scale)
+    ref_out, _, _ = ref.decode_layer(0, prior, q[prior], k[prior], v[prior], hq, hkv, d, d, theta,
+                                     1.0, True, scale)
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=1024)
+    kv = hip.kv_cache(1, 1024, hkv, d, d, half_precision=False)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior])
+        got = kv.decode(layer, [prior], q[prior], k[prior], v[prior])
+        e1 = assert_f32_close(got_prefill, ref_prefill, "C1 prefill rows")
+        e2 = assert_f32_close(got, ref_out, "C1 decode")
+        _say(f"C1 max abs err prefill {e1:.2e} decode {e2:.2e}")
+        np.testing.assert_array_equal(kv.key_slice(0, 0, prior + 1), ref.key_slice(0, 0, prior + 1))
+        np.testing.assert_array_equal(kv.value_slice(0, 0, prior + 1),
+                                      ref.value_slice(0, 0, prior + 1))
+    finally:
+        kv.close()
+        rope.close()
+
+
+# ------------------------------------------------------------------ C2: Llama-3.2-1B f16 decode
+
+def test_c2_llama_decode_f16_reduced(hip):
+    """32 Q heads, 8 KV heads, d 64, interleaved theta 5e5, f16 KV; 2 layers, 1000 prior
+    positions (MFMA prefill), then 4 consecutive decode steps per layer."""
+    hq, hkv, d, prior, steps, theta, layers = 32, 8, 64, 1000, 4, 5e5, 2
+    scale = A.default_scale(d)
+    n = prior + steps
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=n)
+    kv = hip.kv_cache(layers, n, hkv, d, d, half_precision=True)
+    try:
+        for l in range(layers):
+            q = normal(2, f"c2/q{l}", (n, hq * d))
+            k = normal(2, f"c2/k{l}", (n, hkv * d))
+            v = normal(2, f"c2/v{l}", (n, hkv * d))
+            ref = OracleKv(1, n, hkv * d, hkv * d, half_precision=True)
+            k_rot = rope_rows(k, range(n), hkv, d, d, theta, False)
+            for p in range(prior):
+                ref.store(0, p, k_rot[p], v[p])
+            layer = A.AttentionLayer(l, hq, neox=False, rope=rope)
+            got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior]).reshape(prior, -1)
+            q_rot = rope_rows(q, range(n), hq, d, d, theta, False)
+            for row in (0, 1, 31, 32, 500, prior - 1):
+                want = ref.gqa(0, row, q_rot[row], hq, hkv, d, d, scale)
+                assert_f16_close(got_prefill[row], want, f"C2 prefill row {row}")
+            for s in range(steps):
+                p = prior + s
+                got = kv.decode(layer, [p], q[p], k[p], v[p])
+                want, _, _ = ref.decode_layer(0, p, q[p], k[p], v[p], hq, hkv, d, d, theta, 1.0,
+                                              False, scale)
+                rel = assert_f16_close(got, want, f"C2 layer {l} step {s}")
+            _say(f"C2 layer {l} last-step normwise rel err {rel:.2e}")
+            np.testing.assert_array_equal(kv.key_slice(l, 0, n), ref.key_slice(0, 0, n))
+            np.testing.assert_array_equal(kv.value_slice(l, 0, n), ref.value_slice(0, 0, n))
+    finally:
+        kv.close()
+        rope.close()
+
+
+# ------------------------------------------------------------------ C3: Llama-3.2-3B prefill
+
+def test_c3_llama_prefill_f16_full(hip):
+    """S 2048, 24 Q heads, 8 KV heads, d 128, interleaved theta 5e5, f16 Q/K/V, causal. Full
+    size: the oracle runs per-row GQA over each causal prefix on 16 threads."""
+    hq, hkv, d, S, theta = 24, 8, 128, 2048, 5e5
+    scale = A.default_scale(d)
+    q = oracle.f16_round(normal(3, "c3/q", (S, hq * d)))
+    k = oracle.f16_round(normal(3, "c3/k", (S, hkv * d)))
+    v = oracle.f16_round(normal(3, "c3/v", (S, hkv * d)))
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=S)
+    kv = hip.kv_cache(1, S, hkv, d, d, half_precision=True)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=False, rope=rope)
+        got = kv.prefill(layer, 0, q, k, v).reshape(S, hq * d)
+        k_ref = oracle.f16_round(rope_rows(k, range(S), hkv, d, d, theta, False))
+        keys, values = kv.read(0, 0, S)
+        np.testing.assert_array_equal(keys, k_ref.reshape(-1))
+        np.testing.assert_array_equal(values, v.reshape(-1))
+        q_rot = rope_rows(q, range(S), hq, d, d, theta, False)
+        keys = keys.reshape(S, -1)
+        values = values.reshape(S, -1)
+        rows = list(range(S))
+        outs = oracle.gqa_rows_batch([q_rot[r] for r in rows], [keys[:r + 1] for r in rows],
+                                     [values[:r + 1] for r in rows], hq, hkv, d, d, scale,
+                                     threads=16)
+        rel = assert_f16_close(got, np.stack(outs), "C3 prefill")
+        _say(f"C3 normwise rel err {rel:.2e}")
+    finally:
+        kv.close()
+        rope.close()
+
+
+def test_prefill_chunked_and_windowed_matches_oracle(hip):
+    """Chunked prefill (start > 0 attends to cached rows) and a sliding window through the MFMA
+    kernel, against the oracle's prefill (computeBatchedAttention) on the same cache."""
+    hq, hkv, d, theta, w = 6, 2, 64, 1e4, 48
+    scale = A.default_scale(d)
+    n1, n2 = 70, 93
+    n = n1 + n2
+    q = normal(4, "pc/q", (n, hq * d))
+    k = normal(4, "pc/k", (n, hkv * d))
+    v = normal(4, "pc/v", (n, hkv * d))
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=256)
+    for window in (0, w):
+        ref = OracleKv(1, 256, hkv * d, hkv * d, half_precision=True)
+        r1, _, _ = ref.prefill_layer(0, 0, q[:n1], k[:n1], v[:n1], hq, hkv, d, d, theta, 1.0,
+                                     True, scale, window=window)
+        r2, _, _ = ref.prefill_layer(0, n1, q[n1:], k[n1:], v[n1:], hq, hkv, d, d, theta, 1.0,
+                                     True, scale, window=window)
+        kv = hip.kv_cache(1, 256, hkv, d, d, half_precision=True)
+        try:
+            layer = A.AttentionLayer(0, hq, sliding_window=window, neox=True, rope=rope)
+            g1 = kv.prefill(layer, 0, q[:n1], k[:n1], v[:n1])
+            g2 = kv.prefill(layer, n1, q[n1:], k[n1:], v[n1:])
+            assert_f16_close(g1, r1, f"chunk 1 window {window}")
+            assert_f16_close(g2, r2, f"chunk 2 window {window}")
+        finally:
+            kv.close()
+    rope.close()
+
+
+# ------------------------------------------------------------------ C4: ragged batched decode
+
+def test_c4_ragged_decode_reduced(hip):
+    """64 sessions with KV lengths uniform on [256, 2048] (the full config draws up to 16384),
+    12 Q heads, 2 KV heads, d 128, NeoX theta 1e6, f16 KV; one new token per session."""
+    hq, hkv, d, theta, B = 12, 2, 128, 1e6, 64
+    scale = A.default_scale(d)
+    lens = [int(x) for x in synth.uniform_int(4, "c4/len", B, 256, 2048)]
+    maxlen = max(lens) + 1
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=maxlen)
+    kv = hip.kv_cache(1, maxlen, hkv, d, d, half_precision=True, sequences=B)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        for s, L in enumerate(lens):
+            k = normal(4, f"c4/k{s}", (L, hkv * d))
+            v = normal(4, f"c4/v{s}", (L, hkv * d))
+            kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32), k, v,
+                      sequences=np.full(L, s))
+        qn = normal(4, "c4/qn", (B, hq * d))
+        kn = normal(4, "c4/kn", (B, hkv * d))
+        vn = normal(4, "c4/vn", (B, hkv * d))
+        got = kv.decode(layer, lens, qn, kn, vn, sequences=np.arange(B)).reshape(B, -1)
+        worst = 0.0
+        for s, L in enumerate(lens):
+            keys, values = kv.read(0, 0, L + 1, sequence=s)
+            q_rot = rope_rows(qn[s:s + 1], [L], hq, d, d, theta, True, check_against_oracle=(s == 0))
+            k_new = oracle.f16_round(rope_rows(kn[s:s + 1], [L], hkv, d, d, theta, True,
+                                               check_against_oracle=False))
+            np.testing.assert_array_equal(keys.reshape(L + 1, -1)[L], k_new[0])
+            want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
+            worst = max(worst, assert_f16_close(got[s], want, f"C4 session {s} (L={L})"))
+        _say(f"C4 worst normwise rel err {worst:.2e}")
+    finally:
+        kv.close()
+        rope.close()
+
+
+# ------------------------------------------------------------------ C5: Gemma-3 SWA / global
+
+@pytest.mark.parametrize("ring", [False, True])
+def test_c5_gemma3_sliding_window_reduced(hip, ring):
+    """4 Q heads, 1 KV head (MQA), d 256, 6 layers in the 5 sliding (window 512, theta 1e4) : 1
+    global (theta 1e6) pattern, f16 KV, 1500 prior positions and 3 decode steps (the full config
+    runs 26 layers at 32768). With ring=True the sliding layers keep a 544-slot ring
+    (window + one 32-row chunk, LayeredKvCache RING retention)."""
+    hq, hkv, d, prior, steps, layers, w = 4, 1, 256, 1500, 3, 6, 512
+    scale = A.default_scale(d)
+    n = prior + steps
+    rope_swa = hip.rotary_table(d, 1e4, 1.0, max_positions=n)
+    rope_glb = hip.rotary_table(d, 1e6, 1.0, max_positions=n)
+    sliding = [A.uses_sliding_window(l, 6, w) for l in range(layers)]
+    ring_caps = [544 if s else 0 for s in sliding] if ring else None
+    kv = hip.kv_cache(layers, n, hkv, d, d, half_precision=True, ring_capacity=ring_caps)
+    try:
+        for l in range(layers):
+            theta = 1e4 if sliding[l] else 1e6
+            window = w if sliding[l] else 0
+            layer = A.AttentionLayer(l, hq, sliding_window=window, neox=True,
+                                     rope=rope_swa if sliding[l] else rope_glb)
+            q = normal(5, f"c5/q{l}", (n, hq * d))
+            k = normal(5, f"c5/k{l}", (n, hkv * d))
+            v = normal(5, f"c5/v{l}", (n, hkv * d))
+            ref = OracleKv(1, n, hkv * d, hkv * d, half_precision=True)
+            k_rot = rope_rows(k, range(n), hkv, d, d, theta, True)
+            for p in range(prior):
+                ref.store(0, p, k_rot[p], v[p])
+            # Fill the prior positions in chunks no longer than the ring can hold with the window.
+            chunk = 32 if (ring and sliding[l]) else prior
+            for start in range(0, prior, chunk):
+                stop = min(prior, start + chunk)
+                kv.prefill(layer, start, q[start:stop], k[start:stop], v[start:stop])
+            for s in range(steps):
+                p = prior + s
+                got = kv.decode(layer, [p], q[p], k[p], v[p])
+                want, _, _ = ref.decode_layer(0, p, q[p], k[p], v[p], hq, hkv, d, d, theta, 1.0,
+                                              True, scale, window=window)
+                rel = assert_f16_close(got, want, f"C5 layer {l} step {s}")
+            _say(f"C5 ring={ring} layer {l} ({'swa' if sliding[l] else 'global'}) rel {rel:.2e}")
+            if ring and sliding[l]:
+                assert not kv.contains(l, 0) and kv.contains(l, n - 1)
+                assert kv.contains(l, n - 544) and not kv.contains(l, n - 545)
+    finally:
+        kv.close()
+        rope_swa.close()
+        rope_glb.close()
+
+
+# ------------------------------------------------------------------ error paths
+
+def test_error_paths_match_reference_exceptions(hip):
+    hq, hkv, d = 4, 2, 32
+    rope = hip.rotary_table(d, 1e4, 1.0, max_positions=64)
+    kv = hip.kv_cache(2, 64, hkv, d, d, half_precision=True, ring_capacity=[0, 32])
+    try:
+        layer = A.AttentionLayer(0, hq, rope=rope)
+        z = lambda *shape: np.zeros(shape, np.float32)  # noqa: E731
+        kv.append(layer, [0, 1, 2, 3], normal(6, "q", (4, hq * d)), normal(6, "k", (4, hkv * d)),
+                  normal(6, "v", (4, hkv * d)))
+        # reading past the populated prefix: IllegalStateException -> UNAVAILABLE
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.attend(layer, [5], z(hq * d))
+        assert e.value.status == A.UNAVAILABLE
+        # decode at 5 needs 4 populated
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.decode(layer, [5], z(hq * d), z(hkv * d), z(hkv * d))
+        assert e.value.status == A.UNAVAILABLE
+        # position beyond maxSeqLen: IllegalArgumentException -> OUT_OF_RANGE
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.decode(layer, [64], z(hq * d), z(hkv * d), z(hkv * d))
+        assert e.value.status == A.OUT_OF_RANGE
+        # layer out of range
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.attend(A.AttentionLayer(2, hq, rope=rope), [0], z(hq * d))
+        assert e.value.status == A.OUT_OF_RANGE
+        # undersized buffer
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.attend(layer, [3], z(hq * d - 1))
+        assert e.value.status == A.BUFFER_TOO_SMALL
+        # NaN query -> softmax rejects NaN scores -> NON_FINITE, and the context recovers
+        bad = normal(6, "bad", (hq * d,))
+        bad[5] = np.nan
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.attend(layer, [3], bad)
+        assert e.value.status == A.NON_FINITE
+        ok = kv.attend(layer, [3], normal(6, "good", (hq * d,)))
+        assert np.all(np.isfinite(ok))
+        # discardFrom then read: the tail is gone
+        kv.discard_from(2)
+        assert kv.contains(0, 1) and not kv.contains(0, 2)
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.attend(layer, [3], z(hq * d))
+        assert e.value.status == A.UNAVAILABLE
+        # ring layer: a window wider than the ring -> OUT_OF_RANGE (attentionView :185-191)
+        ring_layer = A.AttentionLayer(1, hq, rope=rope)
+        kv.append(ring_layer, list(range(40)), z(40, hq * d), normal(7, "k", (40, hkv * d)),
+                  normal(7, "v", (40, hkv * d)))
+        assert not kv.contains(1, 7) and kv.contains(1, 8)
+        with pytest.raises(A.AttentionStatusError) as e:
+            kv.attend(ring_layer, [39], z(hq * d))
+        assert e.value.status == A.OUT_OF_RANGE
+        windowed = A.AttentionLayer(1, hq, sliding_window=32, rope=rope)
+        assert np.all(np.isfinite(kv.attend(windowed, [39], normal(7, "q", (hq * d,)))))
+        # sessions of one batch must be distinct
+        kv2 = hip.kv_cache(1, 64, hkv, d, d, sequences=2)
+        try:
+            with pytest.raises(A.AttentionStatusError) as e:
+                kv2.decode(layer, [0, 1], z(2, hq * d), z(2, hkv * d), z(2, hkv * d),
+                           sequences=[0, 0])
+            assert e.value.status == A.INVALID_SHAPE
+        finally:
+            kv2.close()
+    finally:
+        kv.close()
+        rope.close()
+
+
+# ------------------------------------------------------------------ properties at full size
+
+def test_c2_full_size_spot_checks_and_properties(hip):
+    """C2 at its full size (16 layers, 4096 prior positions, 128 steps) through the device-pointer
+    entry points, as the benchmark runs it. Checks: oracle spot checks at the first and last step
+    of the first and last layer; a second replay after discard_from(4096) reproduces the outputs
+    exactly (idempotence of the resident cache); the rows the run appended equal the oracle's
+    rotated, f16-rounded K."""
+    from models_amd.hip_runtime import DeviceArray
+    hq, hkv, d, prior, steps, layers, theta = 32, 8, 64, 4096, 128, 16, 5e5
+    scale = A.default_scale(d)
+    n = prior + steps
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=n)
+    kv = hip.kv_cache(layers, n, hkv, d, d, half_precision=True)
+    qd, kd = hq * d, hkv * d
+    zeros_q = DeviceArray(prior * qd)
+    zeros_q.zero()
+    dq = DeviceArray(layers * steps * qd)
+    dk = DeviceArray(layers * n * kd)
+    dv = DeviceArray(layers * n * kd)
+    dout = DeviceArray(layers * steps * qd)
+    try:
+        q_host = normal(2, "c2full/q", (layers, steps, qd))
+        dq.upload(q_host)
+        k_host, v_host = [], []
+        for l in range(layers):
+            k_host.append(normal(2, f"c2full/k{l}", (n, kd)))
+            v_host.append(normal(2, f"c2full/v{l}", (n, kd)))
+            dk.upload(k_host[l], l * n * kd)
+            dv.upload(v_host[l], l * n * kd)
+        _say("C2 full: inputs uploaded")
+        seqs = np.zeros(prior, np.uint32)
+        for l in range(layers):
+            layer = A.AttentionLayer(l, hq, neox=False, rope=rope)
+            kv.append_device(layer, seqs, np.arange(prior), zeros_q.ptr, prior * qd,
+                             dk.at(l * n * kd), prior * kd, dv.at(l * n * kd), prior * kd)
+        hip.synchronize()
+        layers_p = [A.AttentionLayer(l, hq, neox=False, rope=rope) for l in range(layers)]
+
+        def run_steps():
+            for s in range(steps):
+                p = prior + s
+                for l in range(layers):
+                    kv.decode_device(layers_p[l], [0], [p], dq.at((l * steps + s) * qd), qd,
+                                     dk.at((l * n + p) * kd), kd, dv.at((l * n + p) * kd), kd,
+                                     dout.at((l * steps + s) * qd), qd)
+            hip.synchronize()
+            return dout.download().reshape(layers, steps, qd)
+
+        first = run_steps()
+        kv.discard_from(prior)
+        second = run_steps()
+        np.testing.assert_array_equal(first, second)
+        _say("C2 full: replay identical")
+        for l in (0, layers - 1):
+            keys, values = kv.read(l, 0, n)
+            keys = keys.reshape(n, -1)
+            values = values.reshape(n, -1)
+            k_rot = oracle.f16_round(rope_rows(k_host[l][prior:], range(prior, n), hkv, d, d,
+                                               theta, False))
+            np.testing.assert_array_equal(keys[prior:], k_rot)
+            np.testing.assert_array_equal(values, oracle.f16_round(v_host[l]))
+            for s in (0, steps - 1):
+                p = prior + s
+                q_rot = rope_rows(q_host[l, s:s + 1], [p], hq, d, d, theta, False)
+                want = oracle.gqa_rows(q_rot[0], keys[:p + 1], values[:p + 1], hq, hkv, d, d,
+                                       scale)
+                rel = assert_f16_close(first[l, s], want, f"C2 full layer {l} step {s}")
+                _say(f"C2 full layer {l} step {s} rel {rel:.2e}")
+    finally:
+        for buf in (zeros_q, dq, dk, dv, dout):
+            buf.free()
+        kv.close()
+        rope.close()
+
+
+# ------------------------------------------------------------------ entry-point equivalences
+
+def test_attend_causal_equals_prefill(hip):
+    """prefill == append + attend_causal (prepareBatchedAttention then computeBatchedAttention)."""
+    hq, hkv, d, n, theta = 12, 4, 128, 300, 1e6
+    q = normal(12, "ac/q", (n, hq * d))
+    k = normal(12, "ac/k", (n, hkv * d))
+    v = normal(12, "ac/v", (n, hkv * d))
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=n)
+    a = hip.kv_cache(1, n, hkv, d, d, half_precision=True)
+    b = hip.kv_cache(1, n, hkv, d, d, half_precision=True)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        want = a.prefill(layer, 0, q, k, v)
+        q_rot = b.append(layer, np.arange(n), q, k, v)
+        got = b.attend_causal(layer, 0, q_rot)
+        np.testing.assert_array_equal(got, want)
+    finally:
+        a.close()
+        b.close()
+        rope.close()
+
+
+@pytest.mark.parametrize("neox", [False, True])
+def test_split_plans_and_fusion_agree(hip, monkeypatch, neox):
+    """Split-K invariance and fusion equivalence on a ragged multi-session decode batch: many
+    splits (one tile per wave, up to 32 splits) or one split per row, with RoPE + append + split
+    reduction fused into the decode kernel or run as separate kernels (JMA_UNFUSED=1), change only
+    the summation order; the appended cache rows are bit-identical."""
+    hq, hkv, d, theta, B = 8, 2, 64, 1e4, 5
+    lens = [40, 700, 1333, 2048, 97]
+    outs, rows = [], []
+    for env in ({"JMA_DECODE_TILES_PER_WAVE": "1", "JMA_DECODE_TARGET_BLOCKS": "4096"},
+                {"JMA_DECODE_TILES_PER_WAVE": "64", "JMA_DECODE_TARGET_BLOCKS": "1"},
+                {"JMA_DECODE_TILES_PER_WAVE": "1", "JMA_DECODE_TARGET_BLOCKS": "4096",
+                 "JMA_UNFUSED": "1"}):
+        for key in ("JMA_DECODE_TILES_PER_WAVE", "JMA_DECODE_TARGET_BLOCKS", "JMA_UNFUSED"):
+            monkeypatch.delenv(key, raising=False)
+        for key, value in env.items():
+            monkeypatch.setenv(key, value)
+        lib = A.HipAttentionLibrary(0)
+        try:
+            rope = lib.rotary_table(d, theta, 1.0, max_positions=2051)
+            kv = lib.kv_cache(1, 2051, hkv, d, d, half_precision=True, sequences=B)
+            layer = A.AttentionLayer(0, hq, neox=neox, rope=rope)
+            for s, L in enumerate(lens):
+                kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32),
+                          normal(13, f"fs/k{s}", (L, hkv * d)), normal(13, f"fs/v{s}", (L, hkv * d)),
+                          sequences=np.full(L, s))
+            for step in range(3):
+                p = [L + step for L in lens]
+                outs.append(kv.decode(layer, p, normal(13, f"fs/q{step}", (B, hq * d)),
+                                      normal(13, f"fs/kn{step}", (B, hkv * d)),
+                                      normal(13, f"fs/vn{step}", (B, hkv * d)),
+                                      sequences=np.arange(B)))
+            rows.append([kv.read(0, L, L + 3, sequence=s) for s, L in enumerate(lens)])
+            kv.close()
+            rope.close()
+        finally:
+            lib.close()
+    for variant in (1, 2):
+        for step in range(3):
+            np.testing.assert_allclose(outs[3 * variant + step], outs[step], rtol=2e-6, atol=2e-7)
+        for s in range(B):
+            np.testing.assert_array_equal(rows[variant][s][0], rows[0][s][0])
+            np.testing.assert_array_equal(rows[variant][s][1], rows[0][s][1])
+
+
+def test_graph_replays_match_eager_decode(hip):
+    """Per-token HIP graphs of decode_device (as the benchmark replays them): every replay, with
+    eager work and synchronizations in between, reproduces the eager outputs exactly."""
+    from models_amd import hip_runtime as rt
+    hq, hkv, d, prior, steps, layers = 16, 4, 64, 300, 4, 2
+    n = prior + steps
+    rope = hip.rotary_table(d, 5e5, 1.0, max_positions=n)
+    kv = hip.kv_cache(layers, n, hkv, d, d, half_precision=True)
+    qd, kd = hq * d, hkv * d
+    dq = rt.DeviceArray.from_host(normal(14, "g/q", (layers, n, qd)))
+    dk = rt.DeviceArray.from_host(normal(14, "g/k", (layers, n, kd)))
+    dv = rt.DeviceArray.from_host(normal(14, "g/v", (layers, n, kd)))
+    dout = rt.DeviceArray(layers * n * qd)
+    stream = hip.stream()
+    try:
+        lp = [A.AttentionLayer(l, hq, rope=rope) for l in range(layers)]
+        for l in range(layers):
+            kv.append_device(lp[l], np.zeros(prior, np.uint32), np.arange(prior),
+                             dq.at(l * n * qd), prior * qd, dk.at(l * n * kd), prior * kd,
+                             dv.at(l * n * kd), prior * kd)
+
+        def token(s):
+            p = prior + s
+            for l in range(layers):
+                kv.decode_device(lp[l], [0], [p], dq.at((l * n + p) * qd), qd,
+                                 dk.at((l * n + p) * kd), kd, dv.at((l * n + p) * kd), kd,
+                                 dout.at((l * n + p) * qd), qd)
+
+        dout.zero()
+        for s in range(steps):
+            token(s)
+        hip.synchronize()
+        eager = dout.download().reshape(layers, n, qd)[:, prior:]
+        assert np.all(np.isfinite(eager)) and np.any(eager)
+        kv.discard_from(prior)
+        graphs = [rt.Graph(stream, lambda s=s: token(s)) for s in range(steps)]
+        kv.discard_from(prior)
+        try:
+            for replay in range(3):
+                dout.zero()
+                for s in range(steps):
+                    graphs[s].launch()
+                hip.synchronize()
+                got = dout.download().reshape(layers, n, qd)[:, prior:]
+                np.testing.assert_array_equal(got, eager, err_msg=f"replay {replay}")
+                kv.discard_from(prior)
+                # eager work between replays
+                kv.attend(lp[0], [prior - 1], normal(14, "g/x", (qd,)))
+        finally:
+            for g in graphs:
+                g.destroy()
+    finally:
+        for b in (dq, dk, dv, dout):
+            b.free()
+        kv.close()
+        rope.close()
