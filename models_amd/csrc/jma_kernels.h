@@ -80,14 +80,15 @@ struct DecodeArgs {
 struct PrefillArgs {
   KvView kv;
   const float* q;       // [n][num_heads][dk], rotated
-  float qscale;         // score scale * log2(e)
   float* out;           // [n][num_heads][dv]
   int* err;
+  float qscale;         // score scale * log2(e)
   uint32_t n, start, seq, window;
-  uint32_t num_heads, group;
-  uint32_t heads_per_block;  // query heads of one kv head handled by a workgroup
-  uint32_t rows_per_block;   // query rows per workgroup (multiple of 16)
-  uint32_t q_tiles;
+  uint32_t num_heads, num_kv_heads, group;
+  uint32_t heads_per_stripe;  // query heads of one kv head sharing a stripe's 32 MFMA columns
+  uint32_t rows_per_stripe;   // query rows of a stripe; rows * heads <= 32
+  uint32_t head_groups;       // ceil(group / heads_per_stripe)
+  uint32_t row_blocks;        // set by launch_prefill
 };
 
 // Storage block (slots) of the transposed V layout.

@@ -692,159 +692,465 @@ hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStrea
 
 // ================================================================ kernel 3: prefill (f16 MFMA)
 
-// Workgroup = (block of rows_per_block query rows, kv head, group of heads_per_block query
-// heads); wave w owns 16 query rows of one head. Every wave iterates the same 32-row K/V tiles,
-// staged once in LDS per workgroup, so the GQA heads and query rows of the workgroup share each
-// HBM read. S^T = K * Q^T per 16-row block puts query columns in lanes, as in decode_kernel.
-template <int DK, int DV>
-__global__ __launch_bounds__(1024) void prefill_kernel(const PrefillArgs a) {
-  constexpr int kC = DK / 32;
-  constexpr int kNv = DV / 16;
-  constexpr int kKPad = DK + 8;   // halves per LDS K row (16-byte pad against bank conflicts)
-  constexpr int kVPad = 32 + 8;   // halves per LDS V^T row
-  __shared__ __attribute__((aligned(16))) _Float16 sk[32 * kKPad];
-  __shared__ __attribute__((aligned(16))) _Float16 sv[DV * kVPad];
+// v_mfma_f32_32x32x16_f16 operand layouts, lane l, j = l % 32, h = l / 32:
+//   A[i][k]: i = j, k = 8h + e (e < 8)      B[k][c]: c = j, k = 8h + e
+//   D[i][c]: c = j, i = 8(e/4) + 4h + e%4 (e < 16)
+// Prefill computes S^T = K Q^T. The 32 MFMA columns are (query row, query head) pairs of one kv
+// head, so every query head of a GQA group shares each K/V operand; the 32 MFMA rows are the
+// slots of a 32-slot kv tile. A-row i reads tile slot swap34(i) (bits 3 and 4 exchanged): then
+// the eight scores a lane holds for kv half b are exactly the slots a V^T operand finds at
+// positions 16b+8h .. 16b+8h+7 of a perm32-ordered V block, so exponentiated scores feed the PV
+// MFMA from registers and each V^T operand is one 16-byte LDS read.
+namespace pf {
 
-  const uint32_t qt = a.q_tiles - 1 - blockIdx.x;  // longest causal rows first
-  const uint32_t kvh = blockIdx.y;
-  const uint32_t hz0 = blockIdx.z * a.heads_per_block;
-  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+__device__ __forceinline__ uint32_t swap34(uint32_t i) {
+  return (i & ~24u) | ((i & 8u) << 1) | ((i & 16u) >> 1);
+}
+
+// Tile slot of score register e in lane half h.
+__device__ __forceinline__ uint32_t score_slot(int e, int h) {
+  return 16u * ((e >> 2) & 1) + 8u * (e >> 3) + 4u * h + (e & 3);
+}
+
+// XOR swizzles of 16-byte chunks inside the LDS tiles, so that the lanes of one LDS read cycle,
+// which read the same chunk column of different rows, hit different banks.
+template <int D>
+__device__ __forceinline__ uint32_t swz_k(uint32_t r) {
+  if constexpr (D >= 128) return (r & 7u) | ((r >> 1) & 8u);
+  else if constexpr (D == 64) return r & 7u;
+  else return (r >> 1) & 3u;
+}
+__device__ __forceinline__ uint32_t swz_v(uint32_t r) { return ((r >> 1) ^ (r >> 2)) & 3u; }
+
+// Combine a value across the two lane halves (lanes l and l ^ 32 hold the same column).
+__device__ __forceinline__ float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_min(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// Calls f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices keep register
+// arrays in registers).
+template <int N, typename F, int I = 0>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, F, I + 1>(static_cast<F&&>(f));
+  }
+}
+
+// Stripes (32-column query groups) and kv groups of one workgroup per head dimension.
+template <int D> struct Shape { static constexpr int S = D >= 256 ? 2 : 4, Q = 2; };
+
+}  // namespace pf
+
+// Workgroup = (kv head, head group, block of S stripes). A stripe is R query rows x Gz query heads
+// = 32 MFMA columns (R * Gz <= 32). Wave (s, q) owns stripe s and the kv tiles t0+q, t0+q+Q, ...
+// of the block's causal range: the Q waves of a stripe split its kv range, and the S waves of a kv
+// group share every K/V tile, which direct-to-LDS loads stage ahead of use.
+//
+// Each wave runs a two-tile software pipeline: step k computes the scores of tile k+1 on the
+// matrix cores while the vector units exponentiate tile k, then accumulates tile k's PV while the
+// maximum of tile k+1 is taken. K and V stream one tile apart (K(k+1) and V(k) are read in step k,
+// K(k+2) and V(k+1) are loaded), so two LDS stages hold everything and one barrier per step
+// separates reuse from loads.
+//
+// Softmax keeps a per-column reference maximum m and rescales the accumulators only when a tile
+// maximum exceeds it by more than 8 (log2 units), so exponentials stay <= 256 and most steps skip
+// the rescale; the final normalisation divides by the sum of the same exponentials, so the result
+// is the softmax of the reference up to f16 rounding of q, k, v and p.
+template <int D>
+__global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefill_kernel(
+    const PrefillArgs a) {
+  using namespace pf;
+  constexpr int S = Shape<D>::S, Q = Shape<D>::Q;
+  constexpr int kWaves = S * Q;
+  constexpr int kKS = D / 16;                    // k-steps of QK^T
+  constexpr int kNb = D / 32;                    // 32-row dv blocks of O^T
+  constexpr int kT = 32 * D;                     // halves of one K tile (or one V^T tile)
+  constexpr int kChunks = D / 16;                // 1 KB chunks per K (or V) tile
+  constexpr int kCPW = (kChunks + S - 1) / S;    // chunks of a tile one wave of its group loads
+  constexpr int kNC = D / 8;                     // 16-byte chunks per K row
+  constexpr int kC = 4 * kNb;                    // float4 chunks of O^T held per lane
+  constexpr int kArr = 2 * Q * kT;               // halves per LDS array: one K and one V stage
+  static_assert(Q == 1 || Q == 2, "the partial merge pairs at most two kv groups");
+  // Array X holds K stage 0 and V stage 1, array Y holds K stage 1 and V stage 0: a step loads
+  // into one array and reads the other, and the compiler, seeing distinct variables, does not
+  // wait for the direct-to-LDS loads before every LDS read.
+  __shared__ __attribute__((aligned(16))) _Float16 lx[kArr];
+  __shared__ __attribute__((aligned(16))) _Float16 ly[kArr];
+  __shared__ float2 s_ml[kWaves][32];
+
+  // Kv heads vary fastest: consecutive workgroups land on different XCDs, so each XCD's L2 keeps
+  // the K/V of few kv heads. Row blocks run last-first (longest causal ranges first).
+  const uint32_t kvh = blockIdx.x % a.num_kv_heads;
+  const uint32_t rest = blockIdx.x / a.num_kv_heads;
+  const uint32_t hz = rest % a.head_groups;
+  const uint32_t rb = a.row_blocks - 1 - rest / a.head_groups;
+  const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t blocks_per_head = a.rows_per_block / 16;
-  const uint32_t hz = hz0 + wave / blocks_per_head;
-  const uint32_t rb = wave % blocks_per_head;
-  const bool wave_head_ok = hz < a.group;
-  const uint32_t head = kvh * a.group + (wave_head_ok ? hz : 0);
-  const uint32_t t_row = qt * a.rows_per_block + rb * 16 + c16;  // this lane's query row
-  const bool row_ok = t_row < a.n;
-  const uint32_t qpos = a.start + t_row;
-  const uint32_t qfirst = first_visible(qpos, a.window);
+  const int s = wave % S, q = wave / S;
+  const uint32_t R = a.rows_per_stripe, Gz = a.heads_per_stripe;
 
-  // Query rows of the whole workgroup bound the K/V tiles it visits.
-  const uint32_t wg_row0 = qt * a.rows_per_block;
-  const uint32_t wg_row1 = min(wg_row0 + a.rows_per_block, a.n) - 1;
-  const uint32_t t0 = first_visible(a.start + wg_row0, a.window) / 32;
-  const uint32_t t1 = (a.start + wg_row1) / 32 + 1;
-  // This wave's rows bound the tiles it computes on.
-  const uint32_t w_row0 = qt * a.rows_per_block + rb * 16;
-  const uint32_t w_row1 = min(w_row0 + 15, a.n - 1);
-  const uint32_t w_first = first_visible(a.start + w_row0, a.window);
-  const uint32_t w_last = a.start + w_row1;
-  const bool wave_rows_ok = w_row0 < a.n && wave_head_ok;
+  const uint32_t b_row0 = rb * S * R;
+  const uint32_t b_row1 = min(b_row0 + S * R, a.n) - 1;
+  const uint32_t row0 = b_row0 + s * R;
+  const bool stripe_ok = row0 < a.n;
+  const uint32_t row_last = min(row0 + R - 1, a.n - 1);
 
-  // Q operand: this lane's query row, scaled by scale*log2(e) and rounded to f16 in registers.
-  half8_t qf[kC];
-  const float* qrow = a.q + ((uint64_t)(row_ok ? t_row : 0) * a.num_heads + head) * DK;
-  float4_t qv[kC][2];
+  // This lane's column; padding columns alias a valid row and head and are never stored.
+  const uint32_t cr = min((uint32_t)j / Gz, R - 1);
+  const uint32_t hz_head = hz * Gz + (uint32_t)j % Gz;
+  const bool col_ok = stripe_ok && (uint32_t)j < R * Gz && row0 + cr < a.n && hz_head < a.group;
+  const uint32_t crow = min(row0 + cr, a.n - 1);
+  const uint32_t head = kvh * a.group + min(hz_head, a.group - 1);
+  const uint32_t cpos = a.start + crow;
+  const uint32_t cfirst = first_visible(cpos, a.window);
+
+  // Kv tiles of the block, and the part of them this wave's stripe sees.
+  const uint32_t t0 = first_visible(a.start + b_row0, a.window) / 32;
+  const uint32_t t1 = (a.start + b_row1) / 32 + 1;
+  const uint32_t steps = (t1 - t0 + Q - 1) / Q;
+  const uint32_t w_first = first_visible(a.start + row0, a.window);
+  const uint32_t w_last = a.start + row_last;
+  const uint32_t w_first_late = first_visible(w_last, a.window);
+
+  const _Float16* kbase = (const _Float16*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
+                          (uint64_t)kvh * a.kv.cap * D;
+  const _Float16* vbase = (const _Float16*)a.kv.v + a.seq * a.kv.seq_stride_v + a.kv.layer_off_v +
+                          (uint64_t)kvh * a.kv.cap * D;
+  // Element offsets inside a tile of the 16 bytes this lane stages per chunk. A direct-to-LDS load
+  // writes lane i's 16 bytes at chunk base + 16 i, so the LDS swizzle is applied on the global side.
+  uint32_t koff[kCPW], voff[kCPW];
 #pragma unroll
-  for (int c = 0; c < kC; ++c) {  // qrow is clamped to a valid row: load unconditionally
-    qv[c][0] = *(const float4_t*)(qrow + 32 * c + 8 * g);
-    qv[c][1] = *(const float4_t*)(qrow + 32 * c + 8 * g + 4);
+  for (int i = 0; i < kCPW; ++i) {
+    const uint32_t c = s + S * i;
+    const uint32_t rk = c * (512 / D) + lane / kNC;
+    koff[i] = rk * D + 8 * ((lane % kNC) ^ swz_k<D>(rk));
+    const uint32_t rv = c * 16 + lane / 4;
+    voff[i] = rv * 32 + 8 * ((lane % 4) ^ swz_v(rv));
   }
-  const float qs = (row_ok && wave_head_ok) ? a.qscale : 0.0f;
-#pragma unroll
-  for (int c = 0; c < kC; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qf[c][e] = (_Float16)(qv[c][e >> 2][e & 3] * qs);
+  auto has_tile = [&](uint32_t k) { return k < steps && t0 + k * Q + q < t1; };
+  // Whether this wave computes on step k's tile: it exists and meets the stripe's visible range.
+  auto visible = [&](uint32_t k) {
+    const uint32_t p0 = 32 * (t0 + k * Q + q);
+    return stripe_ok && has_tile(k) && p0 <= w_last && p0 + 31 >= w_first;
+  };
+  // Whether every column of the stripe sees all of step k's tile (no mask needed).
+  auto full = [&](uint32_t k) {
+    const uint32_t p0 = 32 * (t0 + k * Q + q);
+    return p0 + 31 <= a.start + row0 && p0 >= w_first_late;
+  };
+  auto slot0_of = [&](uint32_t k) {
+    const uint32_t p0 = 32 * (t0 + k * Q + q);
+    return a.kv.ring ? p0 % a.kv.cap : p0;
+  };
+  // This wave's chunk i of step k's K tile or V tile, into the stage at `stage` (the group's
+  // tiles sit q tiles into it).
+  auto dma_k = [&](uint32_t k, _Float16* stage, int i) {
+    const uint32_t c = s + S * i;
+    if (c >= (uint32_t)kChunks) return;
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(kbase + (uint64_t)slot0_of(k) * D + koff[i]),
+        (__attribute__((address_space(3))) void*)(stage + q * kT + 512 * c), 16, 0, 0);
+  };
+  auto dma_v = [&](uint32_t k, _Float16* stage, int i) {
+    const uint32_t c = s + S * i;
+    if (c >= (uint32_t)kChunks) return;
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(vbase + (uint64_t)slot0_of(k) * D + voff[i]),
+        (__attribute__((address_space(3))) void*)(stage + q * kT + 512 * c), 16, 0, 0);
+  };
+  _Float16* const k_st[2] = {lx, ly};
+  _Float16* const v_st[2] = {ly + Q * kT, lx + Q * kT};
 
-  const _Float16* kb = (const _Float16*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
-                       (uint64_t)kvh * a.kv.cap * DK;
-  const _Float16* vb = (const _Float16*)a.kv.v + a.seq * a.kv.seq_stride_v + a.kv.layer_off_v +
-                       (uint64_t)kvh * a.kv.cap * DV;
-
-  float m = -INFINITY, l = 0.0f;
-  float4_t acc[kNv];
+  // The first K tile goes out before the Q loads, so the two latencies overlap.
+  if (has_tile(0)) {
 #pragma unroll
-  for (int n = 0; n < kNv; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
-  bool bad = false;
+    for (int i = 0; i < kCPW; ++i) dma_k(0, lx, i);
+  }
 
-  for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t p0 = t * 32;
-    const uint32_t slot0 = a.kv.ring ? p0 % a.kv.cap : p0;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < 32 * DK / 8; i += blockDim.x) {
-      const uint32_t r = i / (DK / 8), cc = i % (DK / 8);
-      *(half8_t*)&sk[r * kKPad + 8 * cc] = *(const half8_t*)(kb + (uint64_t)(slot0 + r) * DK + 8 * cc);
-    }
-    const _Float16* vblk = vb + (uint64_t)(slot0 / 32) * DV * 32;
-    for (uint32_t i = threadIdx.x; i < DV * 4; i += blockDim.x) {
-      const uint32_t d = i / 4, cc = i % 4;
-      *(half8_t*)&sv[d * kVPad + 8 * cc] = *(const half8_t*)(vblk + d * 32 + 8 * cc);
-    }
-    __syncthreads();
-    if (!wave_rows_ok || p0 > w_last || p0 + 31 < w_first) continue;
-
-    float s[8];
+  // Q^T operands: 8 consecutive dims of this lane's column per k-step, scaled by
+  // scale * log2(e) and rounded to f16.
+  half8_t qf[kKS];
+  {
+    const float* qrow = a.q + ((uint64_t)crow * a.num_heads + head) * D + 8 * h;
+    const float qs = col_ok ? a.qscale : 0.0f;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      float4_t sc = {0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < kKS; ++ks) {
+      const float4_t x0 = *(const float4_t*)(qrow + 16 * ks);
+      const float4_t x1 = *(const float4_t*)(qrow + 16 * ks + 4);
 #pragma unroll
-      for (int c = 0; c < kC; ++c) {
-        const half8_t kf = *(const half8_t*)&sk[(16 * b + c16) * kKPad + 32 * c + 8 * g];
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[c], sc, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) {
+        qf[ks][e] = (_Float16)(x0[e] * qs);
+        qf[ks][4 + e] = (_Float16)(x1[e] * qs);
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s[4 * b + e] = sc[e];
-    }
-    float mt = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t p = p0 + 16 * (i >> 2) + 4 * g + (i & 3);
-      const bool valid = row_ok && p >= qfirst && p <= qpos;
-      bad |= valid && (s[i] != s[i] || s[i] == INFINITY);
-      s[i] = valid ? s[i] : -INFINITY;
-      mt = fmaxf(mt, s[i]);
-    }
-    mt = wave_max_groups(mt);
-    const float mn = fmaxf(m, mt);
-    const float mu = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = exp2f(m - mu);
-    m = mn;
-    float psum = 0.0f;
-    half8_t pf;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float p = exp2f(s[i] - mu);
-      psum += p;
-      pf[i] = (_Float16)p;
-    }
-    l = l * alpha + psum;
-#pragma unroll
-    for (int n = 0; n < kNv; ++n) {
-      const half8_t vf = *(const half8_t*)&sv[(16 * n + c16) * kVPad + 8 * g];
-      acc[n] *= alpha;
-      acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, acc[n], 0, 0, 0);
     }
   }
 
-  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
-  l = wave_sum_groups(l);
-  if (!(row_ok && wave_head_ok)) return;
-  if (l == 0.0f && g == 0) atomicOr(a.err, 1);
-  const float inv = 1.0f / l;
-  float* o = a.out + ((uint64_t)t_row * a.num_heads + head) * DV;
+  float16_t o[kNb];
 #pragma unroll
-  for (int n = 0; n < kNv; ++n) *(float4_t*)(o + 16 * n + 4 * g) = acc[n] * inv;
+  for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[nb][e] = 0.0f;
+  float m = -INFINITY, l = 0.0f, mn = INFINITY;
+  const uint32_t kr = swap34(j);
+
+  // S^T of one tile; `issue(i)` runs after the i-th matrix op, to spread loads between them.
+  auto qk = [&](const _Float16* sk, auto issue) {
+    float16_t sc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) {
+      const half8_t kf = *(const half8_t*)(sk + kr * D + 8 * ((2 * ks + h) ^ swz_k<D>(kr)));
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], sc, 0, 0, 0);
+      issue(ks);
+    }
+    return sc;
+  };
+  // Masks step k's scores (positions outside [first, position] of each column become -inf),
+  // returns the per-column tile maximum and tracks the minimum valid score.
+  auto mask_max = [&](float16_t& sc, uint32_t k, bool whole) {
+    float tmax = -INFINITY;
+    if (whole) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        tmax = fmaxf(tmax, sc[e]);
+        mn = fminf(mn, sc[e]);
+      }
+    } else {
+      const uint32_t p0 = 32 * (t0 + k * Q + q);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t p = p0 + score_slot(e, h);
+        const bool ok = p >= cfirst && p <= cpos;
+        mn = fminf(mn, ok ? sc[e] : INFINITY);
+        sc[e] = ok ? sc[e] : -INFINITY;
+        tmax = fmaxf(tmax, sc[e]);
+      }
+    }
+    return half_max(tmax);
+  };
+  // Raises the reference maximum when a tile maximum exceeds it by more than 8.
+  auto rescale = [&](float tmax) {
+    if (__ballot(tmax > m + 8.0f) != 0) {
+      const bool up = tmax > m + 8.0f;
+      const float alpha = up ? __builtin_amdgcn_exp2f(m - tmax) : 1.0f;
+      m = up ? tmax : m;
+      l *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb) o[nb] *= alpha;
+    }
+  };
+  auto exp_tile = [&](const float16_t& sc, half8_t* pf) {
+    const float mu = m == -INFINITY ? 0.0f : m;
+    float ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sc[e] - mu);
+      ps += p;
+      pf[e >> 3][e & 7] = (_Float16)p;
+    }
+    l += ps;
+  };
+  auto pv = [&](const _Float16* sv, const half8_t* pf) {
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const uint32_t vr = 32 * nb + j;
+        const half8_t vf = *(const half8_t*)(sv + vr * 32 + 8 * ((2 * b + h) ^ swz_v(vr)));
+        o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[b], o[nb], 0, 0, 0);
+      }
+  };
+  auto no_issue = [](int) {};
+
+  // Prologue: scores of step 0 (masked, maximum taken, accumulators scaled for it).
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (has_tile(1)) {
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) dma_k(1, ly, i);
+  }
+  if (has_tile(0)) {
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) dma_v(0, ly + Q * kT, i);
+  }
+  float16_t scur;
+  bool vcur = visible(0);
+  if (vcur) {
+    scur = qk(lx + q * kT, no_issue);
+    rescale(mask_max(scur, 0, full(0)));
+  }
+
+  // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
+  // before tile k+1's scores are computed.
+  constexpr bool kOverlap = D <= 128;
+  // Step k: K(k+1) and V(k) are ready after the barrier; K(k+2) and V(k+1) are loaded into the
+  // stages that K(k) and V(k-1) held. `kp` is k's parity, fixed per unrolled copy.
+  auto step = [&](uint32_t k, auto kp) {
+    constexpr int P = decltype(kp)::value;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const bool pre_k = has_tile(k + 2), pre_v = has_tile(k + 1);
+    const bool vnxt = visible(k + 1);
+    _Float16* const kdst = k_st[P];
+    _Float16* const vdst = v_st[P ^ 1];
+    const _Float16* const ksrc = k_st[P ^ 1] + q * kT;
+    const _Float16* const vsrc = v_st[P] + q * kT;
+    if (kOverlap && vcur && vnxt && full(k + 1)) {
+      // Fast path: QK^T of tile k+1 overlaps the exponentials of tile k; PV of tile k overlaps
+      // the maximum of tile k+1.
+      half8_t pf[2];
+      auto spread = [&](int ks) {
+        constexpr int kEvery = kKS / kCPW;
+        if (ks % kEvery == 0) {
+          if (pre_k) dma_k(k + 2, kdst, ks / kEvery);
+          if (pre_v) dma_v(k + 1, vdst, ks / kEvery);
+        }
+      };
+      float16_t snxt;
+      if constexpr (kOverlap) {
+        snxt = qk(ksrc, spread);
+        exp_tile(scur, pf);
+        pv(vsrc, pf);
+      } else {
+        exp_tile(scur, pf);
+        pv(vsrc, pf);
+        snxt = qk(ksrc, spread);
+      }
+      const float tmax = mask_max(snxt, k + 1, true);
+      rescale(tmax);
+      scur = snxt;
+    } else {
+      if (pre_k) {
+#pragma unroll
+        for (int i = 0; i < kCPW; ++i) dma_k(k + 2, kdst, i);
+      }
+      if (pre_v) {
+#pragma unroll
+        for (int i = 0; i < kCPW; ++i) dma_v(k + 1, vdst, i);
+      }
+      if (vcur) {
+        half8_t pf[2];
+        exp_tile(scur, pf);
+        pv(vsrc, pf);
+      }
+      float16_t snxt;
+      if (vnxt) snxt = qk(ksrc, no_issue);
+      if (vnxt) {
+        rescale(mask_max(snxt, k + 1, full(k + 1)));
+        scur = snxt;
+      }
+    }
+    vcur = vnxt;
+  };
+  uint32_t k = 0;
+  for (; k + 2 <= steps; k += 2) {
+    step(k, std::integral_constant<int, 0>{});
+    step(k + 1, std::integral_constant<int, 1>{});
+  }
+  if (k < steps) step(k, std::integral_constant<int, 0>{});
+
+  // Merge the kv-group partials of each stripe in one LDS exchange: every wave posts (m, l) and
+  // the O^T chunks its partner finishes, then finishes its own half from registers.
+  l = half_sum(l);
+  mn = half_min(mn);
+  __syncthreads();  // every wave is done with the tile stages the exchange overwrites
+  float* const part = (float*)(wave < kWaves / 2 ? lx : ly) + (wave % (kWaves / 2)) * (kC / Q) * 256;
+  // O^T chunk c (c < kC) of this lane: dims 32(c/4) + 8(c%4) + 4h .. +3 of its column. The
+  // half a wave finishes is chosen by a wave-uniform branch so that o[] is indexed statically.
+  auto chunk = [&](auto cc) {
+    constexpr int c = decltype(cc)::value;
+    const float16_t& acc = o[c >> 2];
+    return float4_t{acc[4 * (c & 3)], acc[4 * (c & 3) + 1], acc[4 * (c & 3) + 2],
+                    acc[4 * (c & 3) + 3]};
+  };
+  if constexpr (Q == 2) {
+    if (h == 0) s_ml[wave][j] = float2{m, l};
+    auto post = [&](auto other) {
+      constexpr int base = decltype(other)::value * (kC / 2);
+      static_for<kC / 2>([&](auto idx) {
+        *(float4_t*)(part + idx.value * 256 + 4 * lane) =
+            chunk(std::integral_constant<int, base + decltype(idx)::value>{});
+      });
+    };
+    if (q == 0) post(std::integral_constant<int, 1>{});
+    else post(std::integral_constant<int, 0>{});
+  }
+  __syncthreads();
+  float ws = 0.0f, wp = 0.0f, L = l;
+  const int partner = (1 - q) * S + s;
+  if constexpr (Q == 2) {
+    const float2 pm = s_ml[partner][j];
+    const float M = fmaxf(m, pm.x);
+    const float es = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+    const float ep = pm.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pm.x - M);
+    L = l * es + pm.y * ep;
+    if (L > 0.0f) {
+      ws = es / L;
+      wp = ep / L;
+    }
+  } else {
+    if (L > 0.0f) ws = 1.0f / L;
+  }
+  const bool bad = col_ok && (mn == -INFINITY || !(L > 0.0f && L < INFINITY));
+  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
+  const float* const ppart = (const float*)(partner < kWaves / 2 ? lx : ly) +
+                             (partner % (kWaves / 2)) * (kC / Q) * 256;
+  float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
+  auto finish = [&](auto own) {
+    constexpr int base = decltype(own)::value * (kC / Q);
+    static_for<kC / Q>([&](auto idx) {
+      constexpr int c = base + decltype(idx)::value;
+      float4_t v = chunk(std::integral_constant<int, c>{}) * ws;
+      if constexpr (Q == 2) v += *(const float4_t*)(ppart + idx.value * 256 + 4 * lane) * wp;
+      if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = v;
+    });
+  };
+  if (q == 0) finish(std::integral_constant<int, 0>{});
+  else if constexpr (Q == 2) finish(std::integral_constant<int, 1>{});
 }
 
 bool prefill_supported(int dk, int dv) {
   return dk == dv && (dk == 32 || dk == 64 || dk == 128 || dk == 256);
 }
 
+template <int D>
+hipError_t launch_prefill_t(PrefillArgs a, hipStream_t stream) {
+  constexpr int S = pf::Shape<D>::S, Q = pf::Shape<D>::Q;
+  const uint32_t rows_per_block = S * a.rows_per_stripe;
+  a.row_blocks = (a.n + rows_per_block - 1) / rows_per_block;
+  const uint64_t blocks = (uint64_t)a.row_blocks * a.head_groups * a.num_kv_heads;
+  if (blocks == 0) return hipSuccess;
+  if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prefill_kernel<D>), dim3((uint32_t)blocks), dim3(64 * S * Q), 0, stream, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stream) {
   if (!prefill_supported(dk, dv)) return hipErrorInvalidValue;
-  const uint32_t head_blocks = (a.group + a.heads_per_block - 1) / a.heads_per_block;
-  const uint32_t num_kv_heads = a.num_heads / a.group;
-  const dim3 grid(a.q_tiles, num_kv_heads, head_blocks);
-  const dim3 block(64 * a.heads_per_block * (a.rows_per_block / 16));
+  if (a.heads_per_stripe == 0 || a.heads_per_stripe > 32 ||
+      a.rows_per_stripe * a.heads_per_stripe > 32 || a.rows_per_stripe == 0 ||
+      a.num_kv_heads == 0 || a.num_heads != a.num_kv_heads * a.group)
+    return hipErrorInvalidValue;
   switch (dk) {
-    case 32: hipLaunchKernelGGL((prefill_kernel<32, 32>), grid, block, 0, stream, a); break;
-    case 64: hipLaunchKernelGGL((prefill_kernel<64, 64>), grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((prefill_kernel<128, 128>), grid, block, 0, stream, a); break;
-    case 256: hipLaunchKernelGGL((prefill_kernel<256, 256>), grid, block, 0, stream, a); break;
+    case 32: return launch_prefill_t<32>(a, stream);
+    case 64: return launch_prefill_t<64>(a, stream);
+    case 128: return launch_prefill_t<128>(a, stream);
+    case 256: return launch_prefill_t<256>(a, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace jma

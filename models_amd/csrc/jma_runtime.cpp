@@ -470,10 +470,11 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.seq = sequence;
     a.window = lc.window;
     a.num_heads = lc.num_heads;
+    a.num_kv_heads = kv->hkv;
     a.group = lc.group;
-    a.heads_per_block = std::min<uint32_t>(lc.group, 16);
-    a.rows_per_block = a.heads_per_block <= 4 ? 64 : (a.heads_per_block <= 8 ? 32 : 16);
-    a.q_tiles = (n + a.rows_per_block - 1) / a.rows_per_block;
+    a.heads_per_stripe = std::min<uint32_t>(lc.group, 32);
+    a.rows_per_stripe = 32 / a.heads_per_stripe;
+    a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
     hip_check(jma::launch_prefill(a, (int)kv->dk, (int)kv->dv, ctx->stream), "prefill launch");
     return;
   }
