@@ -701,6 +701,10 @@ hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStrea
 // the eight scores a lane holds for kv half b are exactly the slots a V^T operand finds at
 // positions 16b+8h .. 16b+8h+7 of a perm32-ordered V block, so exponentiated scores feed the PV
 // MFMA from registers and each V^T operand is one 16-byte LDS read.
+// The prefill kernel is written with lambdas over shared state; every one must inline, or the
+// captured state (accumulators included) would be spilled to scratch memory.
+#define JMA_INL __attribute__((always_inline))
+
 namespace pf {
 
 __device__ __forceinline__ uint32_t swap34(uint32_t i) {
@@ -783,11 +787,17 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   constexpr int kC = 4 * kNb;                    // float4 chunks of O^T held per lane
   constexpr int kArr = 2 * Q * kT;               // halves per LDS array: one K and one V stage
   static_assert(Q == 1 || Q == 2, "the partial merge pairs at most two kv groups");
-  // Array X holds K stage 0 and V stage 1, array Y holds K stage 1 and V stage 0: a step loads
-  // into one array and reads the other, and the compiler, seeing distinct variables, does not
-  // wait for the direct-to-LDS loads before every LDS read.
+  // N stages: loads run N-1 steps ahead of use (every wave issues the same number of loads per
+  // step, so the wait can count them). Three stages measured slower than two on C3-sized work
+  // (more live registers for one more step of lookahead), so two are used.
+  constexpr int N = 2;
+  constexpr int kDmaPerStep = 2 * kCPW;          // K and V loads one wave issues per step
+  // Array i holds K stage i and V stage (i - 1) mod N. Step k loads K(k+N) and V(k+N-1) into
+  // array k mod N and reads K(k+1) and V(k) from array (k+1) mod N; as distinct variables, the
+  // compiler sees that the loads in flight do not alias the reads and adds no waits for them.
   __shared__ __attribute__((aligned(16))) _Float16 lx[kArr];
   __shared__ __attribute__((aligned(16))) _Float16 ly[kArr];
+  __shared__ __attribute__((aligned(16))) _Float16 lz[N == 3 ? kArr : 8];  // (third stage)
   __shared__ float2 s_ml[kWaves][32];
 
   // Kv heads vary fastest: consecutive workgroups land on different XCDs, so each XCD's L2 keeps
@@ -839,39 +849,53 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     const uint32_t rv = c * 16 + lane / 4;
     voff[i] = rv * 32 + 8 * ((lane % 4) ^ swz_v(rv));
   }
-  auto has_tile = [&](uint32_t k) { return k < steps && t0 + k * Q + q < t1; };
+  auto has_tile = [&](uint32_t k) JMA_INL { return k < steps && t0 + k * Q + q < t1; };
   // Whether this wave computes on step k's tile: it exists and meets the stripe's visible range.
-  auto visible = [&](uint32_t k) {
+  auto visible = [&](uint32_t k) JMA_INL {
     const uint32_t p0 = 32 * (t0 + k * Q + q);
     return stripe_ok && has_tile(k) && p0 <= w_last && p0 + 31 >= w_first;
   };
   // Whether every column of the stripe sees all of step k's tile (no mask needed).
-  auto full = [&](uint32_t k) {
+  auto full = [&](uint32_t k) JMA_INL {
     const uint32_t p0 = 32 * (t0 + k * Q + q);
     return p0 + 31 <= a.start + row0 && p0 >= w_first_late;
   };
-  auto slot0_of = [&](uint32_t k) {
-    const uint32_t p0 = 32 * (t0 + k * Q + q);
-    return a.kv.ring ? p0 % a.kv.cap : p0;
+  // First slot of step k's tile. Positions of a non-ring cache are below its capacity, and a ring
+  // holds the whole visible range, so one conditional subtraction wraps (no division, no branch).
+  const uint32_t slot_base = (32 * (t0 + q)) % a.kv.cap;
+  auto slot0_of = [&](uint32_t k) JMA_INL {
+    const uint32_t x = slot_base + 32 * Q * k;
+    return x >= a.kv.cap ? x - a.kv.cap : x;
   };
-  // This wave's chunk i of step k's K tile or V tile, into the stage at `stage` (the group's
-  // tiles sit q tiles into it).
-  auto dma_k = [&](uint32_t k, _Float16* stage, int i) {
+  // This wave's chunk i of step k's K tile or V tile into LDS array `arr` (the group's tiles sit
+  // q tiles into the stage). A step that has no tile for this group loads slot 0 instead, into a
+  // stage nothing reads, so every wave issues the same number of loads each step.
+  auto tile_slot = [&](uint32_t k) JMA_INL { return has_tile(k) ? slot0_of(k) : 0u; };
+  auto dma_k = [&](uint32_t k, _Float16* arr, int i) JMA_INL {
     const uint32_t c = s + S * i;
     if (c >= (uint32_t)kChunks) return;
     __builtin_amdgcn_global_load_lds(
-        (const void*)(kbase + (uint64_t)slot0_of(k) * D + koff[i]),
-        (__attribute__((address_space(3))) void*)(stage + q * kT + 512 * c), 16, 0, 0);
+        (const void*)(kbase + (uint64_t)tile_slot(k) * D + koff[i]),
+        (__attribute__((address_space(3))) void*)(arr + q * kT + 512 * c), 16, 0, 0);
   };
-  auto dma_v = [&](uint32_t k, _Float16* stage, int i) {
+  auto dma_v = [&](uint32_t k, _Float16* arr, int i) JMA_INL {
     const uint32_t c = s + S * i;
     if (c >= (uint32_t)kChunks) return;
     __builtin_amdgcn_global_load_lds(
-        (const void*)(vbase + (uint64_t)slot0_of(k) * D + voff[i]),
-        (__attribute__((address_space(3))) void*)(stage + q * kT + 512 * c), 16, 0, 0);
+        (const void*)(vbase + (uint64_t)tile_slot(k) * D + voff[i]),
+        (__attribute__((address_space(3))) void*)(arr + Q * kT + q * kT + 512 * c), 16, 0, 0);
   };
-  _Float16* const k_st[2] = {lx, ly};
-  _Float16* const v_st[2] = {ly + Q * kT, lx + Q * kT};
+  auto arr_of = [&](auto idx) JMA_INL -> _Float16* {
+    constexpr int i = decltype(idx)::value % N;
+    return i == 0 ? lx : (i == 1 ? ly : lz);
+  };
+  // Waits until at most `outstanding` of this wave's loads are in flight, then barrier. (The
+  // barrier is bare: __syncthreads() would also wait for the loads still meant to be in flight.)
+  auto wait_barrier = [](auto outstanding) JMA_INL {
+    constexpr int n = decltype(outstanding)::value;
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
 
   // The first K tile goes out before the Q loads, so the two latencies overlap.
   if (has_tile(0)) {
@@ -905,22 +929,34 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   float m = -INFINITY, l = 0.0f, mn = INFINITY;
   const uint32_t kr = swap34(j);
 
+  // LDS reads are issued in batches of up to 8 ahead of the matrix ops that consume them: with
+  // eight waves and the direct-to-LDS traffic sharing the LDS, one read's latency is several
+  // hundred cycles, and a read-use-read chain would serialise on it.
+  constexpr int kBatch = kKS < 8 ? kKS : 8;
   // S^T of one tile; `issue(i)` runs after the i-th matrix op, to spread loads between them.
-  auto qk = [&](const _Float16* sk, auto issue) {
+  auto qk = [&](const _Float16* sk, auto issue) JMA_INL {
     float16_t sc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < kKS; ++ks) {
-      const half8_t kf = *(const half8_t*)(sk + kr * D + 8 * ((2 * ks + h) ^ swz_k<D>(kr)));
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], sc, 0, 0, 0);
-      issue(ks);
+    for (int ks0 = 0; ks0 < kKS; ks0 += kBatch) {
+      half8_t kf[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int ks = ks0 + i;
+        kf[i] = *(const half8_t*)(sk + kr * D + 8 * ((2 * ks + h) ^ swz_k<D>(kr)));
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[ks0 + i], sc, 0, 0, 0);
+        issue(ks0 + i);
+      }
     }
     return sc;
   };
   // Masks step k's scores (positions outside [first, position] of each column become -inf),
   // returns the per-column tile maximum and tracks the minimum valid score.
-  auto mask_max = [&](float16_t& sc, uint32_t k, bool whole) {
+  auto mask_max = [&](float16_t& sc, uint32_t k, bool whole) JMA_INL {
     float tmax = -INFINITY;
     if (whole) {
 #pragma unroll
@@ -942,7 +978,7 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     return half_max(tmax);
   };
   // Raises the reference maximum when a tile maximum exceeds it by more than 8.
-  auto rescale = [&](float tmax) {
+  auto rescale = [&](float tmax) JMA_INL {
     if (__ballot(tmax > m + 8.0f) != 0) {
       const bool up = tmax > m + 8.0f;
       const float alpha = up ? __builtin_amdgcn_exp2f(m - tmax) : 1.0f;
@@ -952,7 +988,7 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
       for (int nb = 0; nb < kNb; ++nb) o[nb] *= alpha;
     }
   };
-  auto exp_tile = [&](const float16_t& sc, half8_t* pf) {
+  auto exp_tile = [&](const float16_t& sc, half8_t* pf) JMA_INL {
     const float mu = m == -INFINITY ? 0.0f : m;
     float ps = 0.0f;
 #pragma unroll
@@ -963,29 +999,38 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     }
     l += ps;
   };
-  auto pv = [&](const _Float16* sv, const half8_t* pf) {
+  auto pv = [&](const _Float16* sv, const half8_t* pf) JMA_INL {
+    constexpr int kNbB = kBatch / 2;  // dv blocks per batch of reads
 #pragma unroll
-    for (int nb = 0; nb < kNb; ++nb)
+    for (int nb0 = 0; nb0 < kNb; nb0 += kNbB) {
+      half8_t vf[kNbB][2];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const uint32_t vr = 32 * nb + j;
-        const half8_t vf = *(const half8_t*)(sv + vr * 32 + 8 * ((2 * b + h) ^ swz_v(vr)));
-        o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[b], o[nb], 0, 0, 0);
-      }
+      for (int i = 0; i < kNbB; ++i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const uint32_t vr = 32 * (nb0 + i) + j;
+          vf[i][b] = *(const half8_t*)(sv + vr * 32 + 8 * ((2 * b + h) ^ swz_v(vr)));
+        }
+#pragma unroll
+      for (int i = 0; i < kNbB; ++i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          o[nb0 + i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i][b], pf[b], o[nb0 + i], 0, 0, 0);
+    }
   };
-  auto no_issue = [](int) {};
+  auto no_issue = [](int) JMA_INL {};
 
-  // Prologue: scores of step 0 (masked, maximum taken, accumulators scaled for it).
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (has_tile(1)) {
+  // Prologue: K(0) ready; the loads of "steps" 1-N .. -1 go out (K(j+1) and V(j) into array
+  // j+1); scores of step 0 (masked, maximum taken, accumulators scaled for it).
+  wait_barrier(std::integral_constant<int, 0>{});
+  static_for<N - 1>([&](auto jj) JMA_INL {
+    constexpr int jv = decltype(jj)::value;
 #pragma unroll
-    for (int i = 0; i < kCPW; ++i) dma_k(1, ly, i);
-  }
-  if (has_tile(0)) {
-#pragma unroll
-    for (int i = 0; i < kCPW; ++i) dma_v(0, ly + Q * kT, i);
-  }
+    for (int i = 0; i < kCPW; ++i) {
+      dma_k(jv + 1, arr_of(std::integral_constant<int, jv + 1>{}), i);
+      dma_v(jv, arr_of(std::integral_constant<int, jv + 1>{}), i);
+    }
+  });
   float16_t scur;
   bool vcur = visible(0);
   if (vcur) {
@@ -996,50 +1041,49 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
   // before tile k+1's scores are computed.
   constexpr bool kOverlap = D <= 128;
-  // Step k: K(k+1) and V(k) are ready after the barrier; K(k+2) and V(k+1) are loaded into the
-  // stages that K(k) and V(k-1) held. `kp` is k's parity, fixed per unrolled copy.
-  auto step = [&](uint32_t k, auto kp) {
+  // Step k (P = k mod N, fixed per unrolled copy): K(k+1) and V(k) are ready after the barrier;
+  // K(k+N) and V(k+N-1) are loaded into the array that K(k) and V(k-1) held.
+  auto step = [&](uint32_t k, auto kp) JMA_INL {
     constexpr int P = decltype(kp)::value;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    const bool pre_k = has_tile(k + 2), pre_v = has_tile(k + 1);
+    wait_barrier(std::integral_constant<int, (N - 2) * kDmaPerStep>{});
     const bool vnxt = visible(k + 1);
-    _Float16* const kdst = k_st[P];
-    _Float16* const vdst = v_st[P ^ 1];
-    const _Float16* const ksrc = k_st[P ^ 1] + q * kT;
-    const _Float16* const vsrc = v_st[P] + q * kT;
+    _Float16* const dst = arr_of(std::integral_constant<int, P>{});
+    const _Float16* const ksrc = arr_of(std::integral_constant<int, P + 1>{}) + q * kT;
+    const _Float16* const vsrc = arr_of(std::integral_constant<int, P + 1>{}) + Q * kT + q * kT;
     if (kOverlap && vcur && vnxt && full(k + 1)) {
-      // Fast path: QK^T of tile k+1 overlaps the exponentials of tile k; PV of tile k overlaps
-      // the maximum of tile k+1.
+      // Fast path, kept free of branches so that the scheduler can interleave it: QK^T of tile
+      // k+1 overlaps the exponentials of tile k; PV of tile k overlaps the maximum of tile k+1.
       half8_t pf[2];
-      auto spread = [&](int ks) {
+      auto spread = [&](int ks) JMA_INL {
         constexpr int kEvery = kKS / kCPW;
         if (ks % kEvery == 0) {
-          if (pre_k) dma_k(k + 2, kdst, ks / kEvery);
-          if (pre_v) dma_v(k + 1, vdst, ks / kEvery);
+          dma_k(k + N, dst, ks / kEvery);
+          dma_v(k + N - 1, dst, ks / kEvery);
         }
       };
-      float16_t snxt;
-      if constexpr (kOverlap) {
-        snxt = qk(ksrc, spread);
-        exp_tile(scur, pf);
-        pv(vsrc, pf);
-      } else {
-        exp_tile(scur, pf);
-        pv(vsrc, pf);
-        snxt = qk(ksrc, spread);
-      }
+      float16_t snxt = qk(ksrc, spread);
+      exp_tile(scur, pf);
+      pv(vsrc, pf);
       const float tmax = mask_max(snxt, k + 1, true);
+      // Order: the K reads, then each QK^T matrix op followed by a share of the exponentials,
+      // the V reads, then each PV matrix op followed by a share of the maximum.
+      __builtin_amdgcn_sched_group_barrier(0x100, kKS, 0);
+      static_for<kKS>([&](auto) JMA_INL {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+      });
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kNb, 0);
+      static_for<2 * kNb>([&](auto) JMA_INL {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      });
       rescale(tmax);
       scur = snxt;
     } else {
-      if (pre_k) {
 #pragma unroll
-        for (int i = 0; i < kCPW; ++i) dma_k(k + 2, kdst, i);
-      }
-      if (pre_v) {
-#pragma unroll
-        for (int i = 0; i < kCPW; ++i) dma_v(k + 1, vdst, i);
+      for (int i = 0; i < kCPW; ++i) {
+        dma_k(k + N, dst, i);
+        dma_v(k + N - 1, dst, i);
       }
       if (vcur) {
         half8_t pf[2];
@@ -1055,22 +1099,24 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     }
     vcur = vnxt;
   };
-  uint32_t k = 0;
-  for (; k + 2 <= steps; k += 2) {
-    step(k, std::integral_constant<int, 0>{});
-    step(k + 1, std::integral_constant<int, 1>{});
-  }
-  if (k < steps) step(k, std::integral_constant<int, 0>{});
+  // (The last copies are guarded inside the loop: remainder copies after it would double the
+  // code the register allocator spans and spill.)
+  for (uint32_t k = 0; k < steps; k += N)
+    static_for<N>([&](auto pp) JMA_INL {
+      if (k + decltype(pp)::value < steps) step(k + decltype(pp)::value, pp);
+    });
 
   // Merge the kv-group partials of each stripe in one LDS exchange: every wave posts (m, l) and
   // the O^T chunks its partner finishes, then finishes its own half from registers.
   l = half_sum(l);
   mn = half_min(mn);
-  __syncthreads();  // every wave is done with the tile stages the exchange overwrites
+  // Every wave is done with the tile stages the exchange overwrites, and no load is in flight.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
   float* const part = (float*)(wave < kWaves / 2 ? lx : ly) + (wave % (kWaves / 2)) * (kC / Q) * 256;
   // O^T chunk c (c < kC) of this lane: dims 32(c/4) + 8(c%4) + 4h .. +3 of its column. The
   // half a wave finishes is chosen by a wave-uniform branch so that o[] is indexed statically.
-  auto chunk = [&](auto cc) {
+  auto chunk = [&](auto cc) JMA_INL {
     constexpr int c = decltype(cc)::value;
     const float16_t& acc = o[c >> 2];
     return float4_t{acc[4 * (c & 3)], acc[4 * (c & 3) + 1], acc[4 * (c & 3) + 2],
@@ -1078,9 +1124,9 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   };
   if constexpr (Q == 2) {
     if (h == 0) s_ml[wave][j] = float2{m, l};
-    auto post = [&](auto other) {
+    auto post = [&](auto other) JMA_INL {
       constexpr int base = decltype(other)::value * (kC / 2);
-      static_for<kC / 2>([&](auto idx) {
+      static_for<kC / 2>([&](auto idx) JMA_INL {
         *(float4_t*)(part + idx.value * 256 + 4 * lane) =
             chunk(std::integral_constant<int, base + decltype(idx)::value>{});
       });
@@ -1109,9 +1155,9 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   const float* const ppart = (const float*)(partner < kWaves / 2 ? lx : ly) +
                              (partner % (kWaves / 2)) * (kC / Q) * 256;
   float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
-  auto finish = [&](auto own) {
+  auto finish = [&](auto own) JMA_INL {
     constexpr int base = decltype(own)::value * (kC / Q);
-    static_for<kC / Q>([&](auto idx) {
+    static_for<kC / Q>([&](auto idx) JMA_INL {
       constexpr int c = base + decltype(idx)::value;
       float4_t v = chunk(std::integral_constant<int, c>{}) * ws;
       if constexpr (Q == 2) v += *(const float4_t*)(ppart + idx.value * 256 + 4 * lane) * wp;
