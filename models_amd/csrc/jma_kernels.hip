@@ -498,24 +498,31 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
     float* pa = a.part_acc + ((uint64_t)item * 16 + c16) * DV;
     float* pm = a.part_ml + ((uint64_t)item * 16 + c16) * 2;
+    // Partials of the padding head lanes (the MFMA has 16 columns, the group may have fewer
+    // heads) are neither written nor read back.
     if (!fused) {  // reduce_kernel combines the splits after this launch
+      if (head_ok) {
 #pragma unroll
-      for (int n = 0; n < kNv; ++n) *(float4_t*)(pa + 16 * n + 4 * g) = acc[n];
-      if (g == 0) {
-        pm[0] = mx;
-        pm[1] = l;
+        for (int n = 0; n < kNv; ++n) *(float4_t*)(pa + 16 * n + 4 * g) = acc[n];
+        if (g == 0) {
+          pm[0] = mx;
+          pm[1] = l;
+        }
       }
       return;
     }
     // Kernel 4 fused. Device-coherent (write-through) stores, then wait for them before counting
     // this arrival; the last workgroup of the group to arrive reduces.
+    if (head_ok) {
 #pragma unroll
-    for (int n = 0; n < kNv; ++n)
+      for (int n = 0; n < kNv; ++n)
 #pragma unroll
-      for (int e = 0; e < 4; e += 2)
-        __hip_atomic_store((uint64_t*)(pa + 16 * n + 4 * g + e), pack2(acc[n][e], acc[n][e + 1]),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (g == 0) __hip_atomic_store((uint64_t*)pm, pack2(mx, l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int e = 0; e < 4; e += 2)
+          __hip_atomic_store((uint64_t*)(pa + 16 * n + 4 * g + e), pack2(acc[n][e], acc[n][e + 1]),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (g == 0)
+        __hip_atomic_store((uint64_t*)pm, pack2(mx, l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t arrived = 0;
     if (lane == 0)
@@ -535,7 +542,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   // past the last split).
   constexpr int kF = kNv >= kDecodeWaves ? kNv / kDecodeWaves : 1;  // fragments per wave
   constexpr int kS = kMaxSplits / kF < kMaxSplits ? kMaxSplits / kF : kMaxSplits;  // batch
-  if (wave >= kNv) return;
+  if (wave >= kNv || !head_ok) return;
   const uint64_t item0 = item - split;
   float2 ml[kMaxSplits];
 #pragma unroll
@@ -582,7 +589,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         for (int f = 0; f < kF; ++f) gacc[f] += x[u][f] * wsp[b * kS + u];
     }
   }
-  if (!head_ok) return;
   if (gl == 0.0f && g == 0 && wave == 0) atomicOr(a.err, 1);
   const float inv = 1.0f / gl;
 #pragma unroll
