@@ -216,6 +216,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill figure")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="profiling aid: run only the C3 prefill measurement, print its figures")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="profiling aid: one device-to-device copy of MIB MiB (the runtime's copy "
+                         "kernel), to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -231,6 +236,19 @@ def main() -> int:
 
     hip = A.HipAttentionLibrary(0)
     log("context created on device 0")
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src, dst = rt.DeviceArray(n), rt.DeviceArray(n)
+        src.zero()
+        rt.check(rt.hip().hipMemcpy(dst.ptr, src.ptr, src.nbytes, rt.D2D), "hipMemcpy D2D")
+        rt.device_synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.nbytes}), flush=True)
+        return 0
+    if args.prefill_only:
+        c3 = run_c3(hip, A, rt, synth)
+        print(json.dumps({"prefill_us": round(c3["ms"] * 1e3, 2), "tflops": round(c3["tflops"], 2),
+                          "flops": c3["flops"]}), flush=True)
+        return 0
     c2 = run_c2(hip, A, rt, synth, args.steps, args.warmup)
     log(f"C2: {args.steps} steps in {c2['elapsed'] * 1e3:.2f} ms; decode kernel "
         f"{c2['kernel_ms'] * 1e3:.2f} us avg")
