@@ -836,7 +836,6 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   const uint32_t t0 = first_visible(a.start + b_row0, a.window) / 32;
   const uint32_t t1 = (a.start + b_row1) / 32 + 1;
   const uint32_t steps = (t1 - t0 + Q - 1) / Q;
-  const uint32_t w_first = first_visible(a.start + row0, a.window);
   const uint32_t w_last = a.start + row_last;
   const uint32_t w_first_late = first_visible(w_last, a.window);
 
@@ -856,11 +855,6 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     voff[i] = rv * 32 + 8 * ((lane % 4) ^ swz_v(rv));
   }
   auto has_tile = [&](uint32_t k) JMA_INL { return k < steps && t0 + k * Q + q < t1; };
-  // Whether this wave computes on step k's tile: it exists and meets the stripe's visible range.
-  auto visible = [&](uint32_t k) JMA_INL {
-    const uint32_t p0 = 32 * (t0 + k * Q + q);
-    return stripe_ok && has_tile(k) && p0 <= w_last && p0 + 31 >= w_first;
-  };
   // Whether every column of the stripe sees all of step k's tile (no mask needed).
   auto full = [&](uint32_t k) JMA_INL {
     const uint32_t p0 = 32 * (t0 + k * Q + q);
@@ -1026,6 +1020,13 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   };
   auto no_issue = [](int) JMA_INL {};
 
+  // V stages start zeroed: a step whose tile this wave does not see still runs its PV product,
+  // with p = 0, and 0 * (anything the stage held) must be 0. Only cache data (finite) or zeros
+  // ever reach a V stage.
+  for (int i = threadIdx.x; i < Q * kT / 8; i += 64 * kWaves) {
+    *(half8_t*)(lx + Q * kT + 8 * i) = half8_t{};
+    *(half8_t*)(ly + Q * kT + 8 * i) = half8_t{};
+  }
   // Prologue: K(0) ready; the loads of "steps" 1-N .. -1 go out (K(j+1) and V(j) into array
   // j+1); scores of step 0 (masked, maximum taken, accumulators scaled for it).
   wait_barrier(std::integral_constant<int, 0>{});
@@ -1037,73 +1038,54 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
       dma_v(jv, arr_of(std::integral_constant<int, jv + 1>{}), i);
     }
   });
-  float16_t scur;
-  bool vcur = visible(0);
-  if (vcur) {
-    scur = qk(lx + q * kT, no_issue);
-    rescale(mask_max(scur, 0, full(0)));
-  }
+  // Masks step k's scores when some column does not see all of the tile (a tile this wave does
+  // not see at all, or one that does not exist, is masked completely: its stale scores become
+  // -inf, so its exponentials are 0). Returns the column maximum.
+  auto mask_step = [&](float16_t& sc, uint32_t k) JMA_INL {
+    return full(k) ? mask_max(sc, k, true) : mask_max(sc, k, false);
+  };
+  float16_t scur = qk(lx + q * kT, no_issue);
+  rescale(mask_step(scur, 0));
 
   // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
   // before tile k+1's scores are computed.
   constexpr bool kOverlap = D <= 128;
   // Step k (P = k mod N, fixed per unrolled copy): K(k+1) and V(k) are ready after the barrier;
-  // K(k+N) and V(k+N-1) are loaded into the array that K(k) and V(k-1) held.
+  // K(k+N) and V(k+N-1) are loaded into the array that K(k) and V(k-1) held. Every step runs
+  // the same code (one path, no register shuffling between paths); only the masking of partly
+  // visible tiles and the occasional rescale branch.
   auto step = [&](uint32_t k, auto kp) JMA_INL {
     constexpr int P = decltype(kp)::value;
     wait_barrier(std::integral_constant<int, (N - 2) * kDmaPerStep>{});
-    const bool vnxt = visible(k + 1);
     _Float16* const dst = arr_of(std::integral_constant<int, P>{});
     const _Float16* const ksrc = arr_of(std::integral_constant<int, P + 1>{}) + q * kT;
     const _Float16* const vsrc = arr_of(std::integral_constant<int, P + 1>{}) + Q * kT + q * kT;
-    if (kOverlap && vcur && vnxt && full(k + 1)) {
-      // Fast path, kept free of branches so that the scheduler can interleave it: QK^T of tile
-      // k+1 overlaps the exponentials of tile k; PV of tile k overlaps the maximum of tile k+1.
-      half8_t pf[2];
-      auto spread = [&](int ks) JMA_INL {
-        constexpr int kEvery = kKS / kCPW;
-        if (ks % kEvery == 0) {
-          dma_k(k + N, dst, ks / kEvery);
-          dma_v(k + N - 1, dst, ks / kEvery);
-        }
-      };
-      float16_t snxt = qk(ksrc, spread);
+    half8_t pf[2];
+    auto spread = [&](int ks) JMA_INL {
+      constexpr int kEvery = kKS / kCPW;
+      if (ks % kEvery == 0) {
+        dma_k(k + N, dst, ks / kEvery);
+        dma_v(k + N - 1, dst, ks / kEvery);
+      }
+    };
+    float16_t snxt;
+    if constexpr (kOverlap) {
+      // QK^T of tile k+1 overlaps the exponentials of tile k.
+      snxt = qk(ksrc, spread);
       exp_tile(scur, pf);
       pv(vsrc, pf);
-      const float tmax = mask_max(snxt, k + 1, true);
-      // Order: the K reads, then each QK^T matrix op followed by a share of the exponentials,
-      // the V reads, then each PV matrix op followed by a share of the maximum.
       __builtin_amdgcn_sched_group_barrier(0x100, kKS, 0);
       static_for<kKS>([&](auto) JMA_INL {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
       });
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kNb, 0);
-      static_for<2 * kNb>([&](auto) JMA_INL {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-      });
-      rescale(tmax);
-      scur = snxt;
     } else {
-#pragma unroll
-      for (int i = 0; i < kCPW; ++i) {
-        dma_k(k + N, dst, i);
-        dma_v(k + N - 1, dst, i);
-      }
-      if (vcur) {
-        half8_t pf[2];
-        exp_tile(scur, pf);
-        pv(vsrc, pf);
-      }
-      float16_t snxt;
-      if (vnxt) snxt = qk(ksrc, no_issue);
-      if (vnxt) {
-        rescale(mask_max(snxt, k + 1, full(k + 1)));
-        scur = snxt;
-      }
+      exp_tile(scur, pf);
+      pv(vsrc, pf);
+      snxt = qk(ksrc, spread);
     }
-    vcur = vnxt;
+    rescale(mask_step(snxt, k + 1));
+    scur = snxt;
   };
   // (The last copies are guarded inside the loop: remainder copies after it would double the
   // code the register allocator spans and spill.)
