@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define JMODELS_ATTN_ABI_VERSION 1u
+#define JMODELS_ATTN_ABI_VERSION 2u
 
 #if defined(__GNUC__)
 #define JMODELS_ATTN_API __attribute__((visibility("default")))
@@ -61,6 +61,7 @@ extern "C" {
 #define JMODELS_ATTN_CAP_SLIDING_WINDOW (1ull << 4)  /* causal window max(0, p - w + 1) */
 #define JMODELS_ATTN_CAP_RING_LAYERS (1ull << 5)     /* LayeredKvCache RING retention */
 #define JMODELS_ATTN_CAP_DEVICE_POINTERS (1ull << 6) /* *_device entry points */
+#define JMODELS_ATTN_CAP_QK_NORM (1ull << 7)         /* per-head RMS norm of q and k before RoPE */
 
 /* KV storage element types. F16 stores IEEE binary16 (round to nearest even), which widens to
  * exactly Float.float16ToFloat(Float.floatToFloat16(x)) — the reference's half-precision KV
@@ -71,6 +72,7 @@ extern "C" {
 typedef struct jmodels_attn_context jmodels_attn_context;
 typedef struct jmodels_attn_kv jmodels_attn_kv;
 typedef struct jmodels_attn_rope jmodels_attn_rope;
+typedef struct jmodels_attn_norm jmodels_attn_norm;
 
 /* One attention layer's parameters for a call.
  *   layer           zero-based layer of the KV cache
@@ -82,7 +84,10 @@ typedef struct jmodels_attn_rope jmodels_attn_rope;
  *                   (TensorOps.ropeNeox / rope, BJ/ops/TensorOps.java:1336-1390)
  *   scale           score multiplier; 0 selects (float)(1 / sqrt(key_length))
  *                   (BJ/llama/LlamaForwardPass.java:1559); Gemma 4 passes 1.0
- *   rope            NULL = this layer applies no RoPE (LlamaConfig.usesRope false) */
+ *   rope            NULL = this layer applies no RoPE (LlamaConfig.usesRope false)
+ *   qk_norm         NULL = no QK-norm; else each q and k head is RMS-normalised with the
+ *                   object's weights before RoPE (normalizeHead, BJ/llama/LlamaForwardPass.java:
+ *                   1070-1083, 1672-1676) */
 typedef struct jmodels_attn_layer {
   uint32_t layer;
   uint32_t num_heads;
@@ -91,6 +96,7 @@ typedef struct jmodels_attn_layer {
   float scale;
   uint32_t reserved;
   const jmodels_attn_rope* rope;
+  const jmodels_attn_norm* qk_norm;
 } jmodels_attn_layer;
 
 /* ---------------------------------------------------------------- library and context */
@@ -127,6 +133,18 @@ JMODELS_ATTN_API int32_t jmodels_attn_rope_create(jmodels_attn_context* ctx, uin
                                  uint32_t factor_count, uint32_t max_positions,
                                  jmodels_attn_rope** rope_out);
 JMODELS_ATTN_API int32_t jmodels_attn_rope_destroy(jmodels_attn_rope* rope);
+
+/* ---------------------------------------------------------------- QK-norm weights */
+
+/* A layer's attn_q_norm / attn_k_norm weights (BJ/llama/LlamaWeights.java:99-101), kept in HBM.
+ * Each head x (head_dim elements) becomes x * (1 / rms) * w with rms = (float)sqrt(sum(x^2) /
+ * head_dim + eps) (TensorOps.rmsNorm, BJ/ops/TensorOps.java:50-58), applied before RoPE when the
+ * weights are present. q_weight or k_weight may be NULL: that side is left as is, as
+ * normalizeHead does for an empty weight array. head_dim must equal the cache's key_length. */
+JMODELS_ATTN_API int32_t jmodels_attn_norm_create(jmodels_attn_context* ctx, uint32_t head_dim,
+                                 const float* q_weight, const float* k_weight, float eps,
+                                 jmodels_attn_norm** norm_out);
+JMODELS_ATTN_API int32_t jmodels_attn_norm_destroy(jmodels_attn_norm* norm);
 
 /* ---------------------------------------------------------------- KV cache */
 

@@ -9,8 +9,9 @@ This is the host side above the C ABI (``include/jmodels_attn.h``). Names follow
 * :class:`HipRotaryTable` — ``ops/RotaryTable.java`` (factors resident in HBM).
 * :class:`HipKvCache` — ``cache/KvCache.java`` / ``cache/LayeredKvCache.java`` resident in HBM:
   ``store``, ``key_slice``/``value_slice``, ``contains``, ``discard_from``, ``clear``.
+* :class:`HipQkNorm` — a layer's QK-norm weights (``LlamaForwardPass.normalizeHead``).
 * :class:`AttentionLayer` — the per-layer flags ``LlamaConfig`` supplies (heads, window, NeoX,
-  scale, RoPE table).
+  scale, RoPE table, QK-norm).
 * ``decode`` / ``attend`` / ``append`` / ``prefill`` — the attention block of
   ``llama/LlamaForwardPass.java`` (:1069-1128, :1479-1541, :793-839).
 
@@ -30,7 +31,7 @@ from typing import Optional, Sequence
 
 import numpy as np
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 NULL_POINTER = 1
@@ -49,6 +50,7 @@ CAP_RAGGED_DECODE = 1 << 3
 CAP_SLIDING_WINDOW = 1 << 4
 CAP_RING_LAYERS = 1 << 5
 CAP_DEVICE_POINTERS = 1 << 6
+CAP_QK_NORM = 1 << 7
 
 KV_F32 = 0
 KV_F16 = 1
@@ -63,7 +65,7 @@ EXPORTS = (
     "jmodels_attn_append", "jmodels_attn_attend", "jmodels_attn_decode", "jmodels_attn_prefill",
     "jmodels_attn_append_device", "jmodels_attn_attend_device", "jmodels_attn_decode_device",
     "jmodels_attn_prefill_device", "jmodels_attn_attend_causal",
-    "jmodels_attn_attend_causal_device",
+    "jmodels_attn_attend_causal_device", "jmodels_attn_norm_create", "jmodels_attn_norm_destroy",
 )
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -90,6 +92,7 @@ class _Layer(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("reserved", ctypes.c_uint32),
         ("rope", ctypes.c_void_p),
+        ("qk_norm", ctypes.c_void_p),
     ]
 
 
@@ -112,6 +115,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "jmodels_attn_rope_create": (_i32, [_vp, _u32, _cf, _cf, _vp, _u32, _u32,
                                             ctypes.POINTER(_vp)]),
         "jmodels_attn_rope_destroy": (_i32, [_vp]),
+        "jmodels_attn_norm_create": (_i32, [_vp, _u32, _vp, _vp, _cf, ctypes.POINTER(_vp)]),
+        "jmodels_attn_norm_destroy": (_i32, [_vp]),
         "jmodels_attn_kv_create": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp,
                                           ctypes.POINTER(_vp)]),
         "jmodels_attn_kv_destroy": (_i32, [_vp]),
@@ -239,6 +244,10 @@ class HipAttentionLibrary:
         return HipRotaryTable(self, rotary_dim, theta, frequency_scale, max_positions,
                               frequency_factors)
 
+    def qk_norm(self, head_dim: int, q_weight=None, k_weight=None,
+                eps: float = 1e-6) -> "HipQkNorm":
+        return HipQkNorm(self, head_dim, q_weight, k_weight, eps)
+
     def kv_cache(self, num_layers: int, max_seq_len: int, num_kv_heads: int, key_length: int,
                  value_length: int, half_precision: bool = True, sequences: int = 1,
                  ring_capacity: Optional[Sequence[int]] = None) -> "HipKvCache":
@@ -273,6 +282,31 @@ class HipRotaryTable:
             self.handle = None
 
 
+class HipQkNorm:
+    """A layer's attn_q_norm / attn_k_norm weights (llama/LlamaWeights.java:99-101) in HBM; each q
+    and k head is RMS-normalised with them before RoPE (LlamaForwardPass.normalizeHead, :1672-1676).
+    A missing weight (None) leaves that side unnormalised, as an empty weight array does."""
+
+    def __init__(self, owner: HipAttentionLibrary, head_dim: int, q_weight, k_weight, eps: float):
+        self.owner = owner
+        qw = None if q_weight is None else _f32(q_weight)
+        kw = None if k_weight is None else _f32(k_weight)
+        for w in (qw, kw):
+            if w is not None and w.size != head_dim:
+                raise ValueError(f"norm weight has {w.size} elements, head_dim is {head_dim}")
+        out = _vp()
+        owner.check(owner.lib.jmodels_attn_norm_create(
+            owner.ctx, head_dim, None if qw is None else _ptr(qw), None if kw is None else _ptr(kw),
+            eps, ctypes.byref(out)), "norm_create")
+        self.handle = out.value
+        self.head_dim, self.eps = head_dim, eps
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.owner.check(self.owner.lib.jmodels_attn_norm_destroy(self.handle), "norm_destroy")
+            self.handle = None
+
+
 @dataclass
 class AttentionLayer:
     """Per-layer attention parameters (LlamaConfig flags for one layer)."""
@@ -283,10 +317,12 @@ class AttentionLayer:
     neox: bool = False
     scale: float = 0.0  # 0 -> (float)(1/sqrt(key_length))
     rope: Optional[HipRotaryTable] = None
+    qk_norm: Optional[HipQkNorm] = None
 
     def struct(self) -> _Layer:
         return _Layer(self.layer, self.num_heads, self.sliding_window, int(bool(self.neox)),
-                      self.scale, 0, self.rope.handle if self.rope is not None else None)
+                      self.scale, 0, self.rope.handle if self.rope is not None else None,
+                      self.qk_norm.handle if self.qk_norm is not None else None)
 
 
 class HipKvCache:

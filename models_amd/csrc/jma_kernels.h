@@ -50,6 +50,9 @@ struct AppendArgs {
   KvView kv;
   uint32_t pairs, neox, num_heads, num_kv_heads, dk, dv;
   uint32_t blocks_per_row;  // 256-thread blocks per row; one thread per element pair
+  const float* q_norm_w;    // [dk] QK-norm weights applied before RoPE; null = none
+  const float* k_norm_w;
+  float norm_eps;
   RowList rows;
 };
 

@@ -62,6 +62,22 @@ __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float
   x1 = b;
 }
 
+// QK-norm of one head before RoPE (normalizeHead -> TensorOps.rmsNorm, llama/LlamaForwardPass.java:
+// 1672-1676, ops/TensorOps.java:50-58): sumSq of the head in order, rms = (float)sqrt(sumSq / d +
+// eps) in double, scale = 1 / rms, element = x * scale * w, each operation rounded on its own.
+// Every thread of the head computes the same sum (the head row is in L1), so the result is the
+// oracle's bit for bit; it replaces the pair's values y0 = x[e0], y1 = x[e1].
+__device__ __forceinline__ void head_rms_norm(const float* x, uint32_t d, const float* w, float eps,
+                                              uint32_t e0, uint32_t e1, float& y0, float& y1) {
+#pragma clang fp contract(off)
+  float ss = 0.0f;
+  for (uint32_t i = 0; i < d; ++i) ss = ss + x[i] * x[i];
+  const float rms = (float)sqrt((double)(ss / (float)d + eps));
+  const float scale = 1.0f / rms;
+  y0 = y0 * scale * w[e0];
+  y1 = y1 * scale * w[e1];
+}
+
 // One thread per element pair of a row: a RoPE pair of q or k (or a pass-through pair beyond the
 // rotary dims), or two V elements. Every load a thread needs is independent of the others, so a
 // row costs one memory round trip.
@@ -90,6 +106,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const AppendArgs a) {
     const uint32_t e0 = rotate && a.neox ? j : 2 * j;
     const uint32_t e1 = rotate && a.neox ? j + a.pairs : 2 * j + 1;
     float y0 = x[e0], y1 = x[e1];
+    const float* nw = is_q ? a.q_norm_w : a.k_norm_w;
+    if (nw != nullptr) head_rms_norm(x, a.dk, nw, a.norm_eps, e0, e1, y0, y1);
     if (rotate) {
       const float c = a.cos_t[(uint64_t)pos * a.pairs + j];
       const float s = a.sin_t[(uint64_t)pos * a.pairs + j];

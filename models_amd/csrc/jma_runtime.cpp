@@ -111,6 +111,14 @@ struct jmodels_attn_rope {
   float* d_sin = nullptr;
 };
 
+struct jmodels_attn_norm {
+  jmodels_attn_context* ctx = nullptr;
+  uint32_t head_dim = 0;
+  float eps = 0.0f;
+  float* d_q = nullptr;  // null: q heads are not normalised
+  float* d_k = nullptr;
+};
+
 struct jmodels_attn_kv {
   jmodels_attn_context* ctx = nullptr;
   uint32_t sequences = 0, layers = 0, max_seq_len = 0, hkv = 0, dk = 0, dv = 0, dtype = 0;
@@ -196,6 +204,7 @@ struct LayerCall {
   uint32_t layer, num_heads, group, window, neox;
   float scale;
   const jmodels_attn_rope* rope;
+  const jmodels_attn_norm* norm;  // null or weights on neither side = no QK-norm
 };
 
 LayerCall resolve_layer(const jmodels_attn_kv* kv, const jmodels_attn_layer* p) {
@@ -217,6 +226,13 @@ LayerCall resolve_layer(const jmodels_attn_kv* kv, const jmodels_attn_layer* p) 
   if (c.rope) {
     require(c.rope->ctx == kv->ctx, JMODELS_ATTN_INVALID_SHAPE, "rope table belongs to another context");
     require(c.rope->rotary_dim <= kv->dk, JMODELS_ATTN_INVALID_SHAPE, "rotary_dim exceeds key_length");
+  }
+  c.norm = p->qk_norm;
+  if (c.norm) {
+    require(c.norm->ctx == kv->ctx, JMODELS_ATTN_INVALID_SHAPE, "qk-norm belongs to another context");
+    require(c.norm->head_dim == kv->dk, JMODELS_ATTN_INVALID_SHAPE,
+            "qk-norm head_dim differs from key_length");
+    if (!c.norm->d_q && !c.norm->d_k) c.norm = nullptr;
   }
   return c;
 }
@@ -297,6 +313,11 @@ void run_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall&
   a.dk = kv->dk;
   a.dv = kv->dv;
   a.blocks_per_row = append_blocks_per_row(lc.num_heads, kv);
+  if (lc.norm) {
+    a.q_norm_w = lc.norm->d_q;
+    a.k_norm_w = lc.norm->d_k;
+    a.norm_eps = lc.norm->eps;
+  }
   a.rows = rows;
   hip_check(jma::launch_append(a, kv->f16(), ctx->stream), "rope_append launch");
 }
@@ -387,8 +408,9 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
 
 // The decode kernel rotates q and appends the new rows itself when its RoPE chunks line up with
 // the rotary pairs (a multiple of 8 pairs) and the context does not ask for separate kernels.
+// QK-norm layers take the append kernel (it normalises each head before RoPE), then attention.
 bool can_fuse_decode(const jmodels_attn_context* ctx, const LayerCall& lc) {
-  if (ctx->unfused) return false;
+  if (ctx->unfused || lc.norm != nullptr) return false;
   return lc.rope == nullptr || lc.rope->pairs % 8 == 0;
 }
 
@@ -558,7 +580,7 @@ uint32_t jmodels_attn_abi_version(void) { return JMODELS_ATTN_ABI_VERSION; }
 uint64_t jmodels_attn_capabilities(void) {
   return JMODELS_ATTN_CAP_DECODE_F32 | JMODELS_ATTN_CAP_DECODE_F16 | JMODELS_ATTN_CAP_PREFILL_MFMA |
          JMODELS_ATTN_CAP_RAGGED_DECODE | JMODELS_ATTN_CAP_SLIDING_WINDOW |
-         JMODELS_ATTN_CAP_RING_LAYERS | JMODELS_ATTN_CAP_DEVICE_POINTERS;
+         JMODELS_ATTN_CAP_RING_LAYERS | JMODELS_ATTN_CAP_DEVICE_POINTERS | JMODELS_ATTN_CAP_QK_NORM;
 }
 
 const char* jmodels_attn_status_name(int32_t status) {
@@ -707,6 +729,50 @@ int32_t jmodels_attn_rope_destroy(jmodels_attn_rope* rope) {
     (void)hipFree(rope->d_cos);
     (void)hipFree(rope->d_sin);
     delete rope;
+  });
+}
+
+int32_t jmodels_attn_norm_create(jmodels_attn_context* ctx, uint32_t head_dim, const float* q_weight,
+                                 const float* k_weight, float eps, jmodels_attn_norm** norm_out) {
+  return guard([&] {
+    check_ctx(ctx);
+    require(norm_out != nullptr, JMODELS_ATTN_NULL_POINTER, "norm_out is null");
+    *norm_out = nullptr;
+    require(head_dim > 0 && head_dim <= 4096, JMODELS_ATTN_INVALID_SHAPE, "head_dim must be in [1, 4096]");
+    require(isfinite(eps) && eps >= 0.0f, JMODELS_ATTN_INVALID_SHAPE, "eps must be finite and >= 0");
+    hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+    auto* norm = new jmodels_attn_norm();
+    norm->ctx = ctx;
+    norm->head_dim = head_dim;
+    norm->eps = eps;
+    const size_t bytes = (size_t)head_dim * sizeof(float);
+    try {
+      if (q_weight) {
+        hip_check(hipMalloc(&norm->d_q, bytes), "hipMalloc qk-norm");
+        hip_check(hipMemcpy(norm->d_q, q_weight, bytes, hipMemcpyHostToDevice), "upload q-norm");
+      }
+      if (k_weight) {
+        hip_check(hipMalloc(&norm->d_k, bytes), "hipMalloc qk-norm");
+        hip_check(hipMemcpy(norm->d_k, k_weight, bytes, hipMemcpyHostToDevice), "upload k-norm");
+      }
+    } catch (...) {
+      (void)hipFree(norm->d_q);
+      (void)hipFree(norm->d_k);
+      delete norm;
+      throw;
+    }
+    *norm_out = norm;
+  });
+}
+
+int32_t jmodels_attn_norm_destroy(jmodels_attn_norm* norm) {
+  if (!norm) return JMODELS_ATTN_NULL_POINTER;
+  return guard([&] {
+    (void)hipSetDevice(norm->ctx->device);
+    (void)hipStreamSynchronize(norm->ctx->stream);
+    (void)hipFree(norm->d_q);
+    (void)hipFree(norm->d_k);
+    delete norm;
   });
 }
 

@@ -185,6 +185,14 @@ void jmo_rms_norm(float* out, const float* x, const float* weight, int size, flo
   for (int i = 0; i < size; i++) out[i] = x[i] * scale * weight[i];
 }
 
+void jmo_qk_norm_heads(float* x, int heads, int head_dim, const float* weight, float eps) {
+  /* normalizeHead per head, in place (llama/LlamaForwardPass.java:1070-1083, 1672-1676): the
+   * reference calls rmsNorm(vector, offset, vector, offset, ...), which reads each element before
+   * writing it. */
+  for (int h = 0; h < heads; h++) jmo_rms_norm(x + (int64_t)h * head_dim, x + (int64_t)h * head_dim,
+                                                weight, head_dim, eps);
+}
+
 /* ================================================================ KvCache */
 
 struct jmo_kv {

@@ -66,6 +66,8 @@ int jmo_softmax(float* x, int size);
 
 /* TensorOps.rmsNorm (ops/TensorOps.java:50-58); out may alias x. */
 void jmo_rms_norm(float* out, const float* x, const float* weight, int size, float eps);
+/* normalizeHead over `heads` consecutive heads of x, in place. */
+void jmo_qk_norm_heads(float* x, int heads, int head_dim, const float* weight, float eps);
 
 /* VectorUtil.dotProduct restated as a sequential float sum (vectors-core is not vendored, so its
  * lane order is unpinned; see oracle.py). */

@@ -20,6 +20,8 @@ softmax                     TensorOpsTest :1368-1454 (uniform, sum-to-1, large, 
                             rejections); float64 softmax on random rows
 KvCache                     KvCacheTest offsets/buffers/growth/discard/clear/bounds (:42-300)
 LayeredKvCache              LayeredKvCacheTest spans (2,2,4,2),(4,2,0,0), buffers, bytes (:28-160)
+rms_norm / qk_norm_heads    TensorOpsTest.RmsNorm known answers (:42-67); float64 rms on random
+                            heads; in place == out of place; zero head -> 0 (rms = sqrt(eps))
 attention start (window)    EncoderAttentionWindowTest causal bounds (:76-145); brute force
 gqa / decode / prefill      float64 dense softmax(QK^T s)V on small shapes (brute force); L=1 -> V;
                             uniform scores -> mean of V rows; one-hot key; equal Q within a GQA
@@ -83,6 +85,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "jmo_rope_direct": (None, [_f32p, c_int, c_int, c_float, c_float, c_int]),
         "jmo_softmax": (c_int, [_f32p, c_int]),
         "jmo_rms_norm": (None, [_f32p, _f32p, _f32p, c_int, c_float]),
+        "jmo_qk_norm_heads": (None, [_f32p, c_int, c_int, _f32p, c_float]),
         "jmo_dot": (c_float, [_f32p, _f32p, c_int]),
         "jmo_kv_create": (c_void, [c_int, c_int, c_int, c_int, c_int]),
         "jmo_kv_destroy": (None, [c_void]),
@@ -221,6 +224,15 @@ def rms_norm(x, weight, eps: float) -> np.ndarray:
     out = np.empty_like(x)
     lib().jmo_rms_norm(_ptr(out), _ptr(x), _ptr(w), x.size, eps)
     return out
+
+
+def qk_norm_heads(x, heads: int, head_dim: int, weight, eps: float) -> np.ndarray:
+    """normalizeHead applied to each of ``heads`` consecutive heads (a copy of x)."""
+    v = _f32(x).copy()
+    w = _f32(weight)
+    assert v.size == heads * head_dim and w.size == head_dim
+    lib().jmo_qk_norm_heads(_ptr(v), heads, head_dim, _ptr(w), eps)
+    return v
 
 
 def attention_start(position: int, window: int) -> int:

@@ -295,6 +295,18 @@ def softmax_cases():
     ]
 
 
+def rms_norm_cases():
+    # TensorOpsTest.RmsNorm (:42-67): out = x * (1 / rms) * w, rms = sqrt(mean(x^2) + eps).
+    return [
+        {"name": "identityWeightNormalizesCorrectly", "src": "ops/TensorOpsTest.java:42-54",
+         "x": [3.0, 4.0], "weight": [1.0, 1.0], "eps": 1e-5,
+         "expect_close": [[0, 3.0 / math.sqrt(12.5), 1e-4], [1, 4.0 / math.sqrt(12.5), 1e-4]]},
+        {"name": "weightScalesOutput", "src": "ops/TensorOpsTest.java:56-67",
+         "x": [1.0, 1.0], "weight": [2.0, 3.0], "eps": 1e-5,
+         "expect_close": [[0, 2.0, 1e-4], [1, 3.0, 1e-4]]},
+    ]
+
+
 def window_cases():
     # EncoderAttentionWindowTest CausalWindow (GEMMA3, window 512, pattern 6): layer 0 slides,
     # layer 5 is global (:37-40, 128-145); LlamaConfig.usesSlidingWindow (:157-162).
@@ -326,6 +338,7 @@ def main():
         "layered_kv_cache": layered_cases(),
         "rope": rope_cases(),
         "softmax": softmax_cases(),
+        "rms_norm": rms_norm_cases(),
         "attention_start": window_cases(),
         "sliding_layers": sliding_layers(),
     }

@@ -33,7 +33,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     declared = _declared_functions()
-    assert len(declared) >= 28
+    assert len(declared) >= 30
     assert declared == set(A.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
@@ -46,10 +46,10 @@ def test_library_only_exports_the_abi():
 
 
 def test_abi_version_and_capabilities(lib):
-    assert lib.jmodels_attn_abi_version() == A.ABI_VERSION == 1
+    assert lib.jmodels_attn_abi_version() == A.ABI_VERSION == 2
     caps = lib.jmodels_attn_capabilities()
     for bit in (A.CAP_DECODE_F32, A.CAP_DECODE_F16, A.CAP_PREFILL_MFMA, A.CAP_RAGGED_DECODE,
-                A.CAP_SLIDING_WINDOW, A.CAP_RING_LAYERS, A.CAP_DEVICE_POINTERS):
+                A.CAP_SLIDING_WINDOW, A.CAP_RING_LAYERS, A.CAP_DEVICE_POINTERS, A.CAP_QK_NORM):
         assert caps & bit
 
 
@@ -66,13 +66,17 @@ def test_null_handles_are_rejected_without_a_gpu(lib):
     assert lib.jmodels_attn_context_destroy(None) == A.NULL_POINTER
     assert lib.jmodels_attn_rope_destroy(None) == A.NULL_POINTER
     assert lib.jmodels_attn_kv_destroy(None) == A.NULL_POINTER
+    assert lib.jmodels_attn_norm_destroy(None) == A.NULL_POINTER
+    out_h = ctypes.c_void_p()
+    assert lib.jmodels_attn_norm_create(None, 128, None, None, 1e-6, ctypes.byref(out_h)) == \
+        A.NULL_POINTER
     assert lib.jmodels_attn_kv_clear(None, -1) == A.NULL_POINTER
     assert lib.jmodels_attn_kv_discard_from(None, 0, 0) == A.NULL_POINTER
     out = ctypes.c_int32()
     assert lib.jmodels_attn_kv_contains(None, 0, 0, 0, ctypes.byref(out)) == A.NULL_POINTER
     assert lib.jmodels_attn_context_synchronize(None) == A.NULL_POINTER
     assert "null" in lib.jmodels_attn_last_error().decode()
-    layer = A._Layer(0, 8, 0, 0, 0.0, 0, None)
+    layer = A._Layer(0, 8, 0, 0, 0.0, 0, None, None)
     rows = (ctypes.c_uint32 * 1)(0)
     assert lib.jmodels_attn_decode(None, None, ctypes.byref(layer), 1, rows, rows, None, 0, None,
                                    0, None, 0, None, 0) == A.NULL_POINTER
@@ -81,9 +85,10 @@ def test_null_handles_are_rejected_without_a_gpu(lib):
 
 
 def test_layer_struct_matches_header_layout():
-    # jmodels_attn_layer: 6 x 4-byte fields then a pointer (8-byte aligned) = 32 bytes.
-    assert ctypes.sizeof(A._Layer) == 32
+    # jmodels_attn_layer: 6 x 4-byte fields, then the rope and qk_norm pointers = 40 bytes.
+    assert ctypes.sizeof(A._Layer) == 40
     assert A._Layer.rope.offset == 24
+    assert A._Layer.qk_norm.offset == 32
 
 
 def test_window_helpers_follow_llama_config():

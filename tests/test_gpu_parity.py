@@ -132,6 +132,105 @@ def test_append_rope_is_bit_exact(hip, half, neox):
         rope.close()
 
 
+def _qk_norm_rows(x, heads, d, weight, eps):
+    """normalizeHead over every head of every row (LlamaForwardPass.java:1070-1083)."""
+    if weight is None:
+        return np.asarray(x, np.float32).copy()
+    return np.stack([oracle.qk_norm_heads(row, heads, d, weight, eps) for row in x])
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("neox", [True, False])
+@pytest.mark.parametrize("sides", ["both", "k_only"])
+def test_append_qk_norm_is_bit_exact(hip, half, neox, sides):
+    """QK-norm then RoPE in the append kernel: q_out and the K cache equal the oracle's sequential
+    float sum of squares, double sqrt, reciprocal and two products, bit for bit. With only a k
+    weight, q passes through unnormalised (an empty attn_q_norm array)."""
+    hq, hkv, d, n, theta, eps = 8, 2, 128, 24, 1e6, 1e-6
+    positions = np.array([0, 1, 7, 63, 64, 500, 1023] + list(range(200, 217)))[:n]
+    q = normal(12, "qn/q", (n, hq * d)) * 3.0
+    k = normal(12, "qn/k", (n, hkv * d)) * 0.25
+    v = normal(12, "qn/v", (n, hkv * d))
+    wq = None if sides == "k_only" else normal(12, "qn/wq", (d,)) + 1.0
+    wk = normal(12, "qn/wk", (d,)) + 1.0
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=1024)
+    kv = hip.kv_cache(1, 1024, hkv, d, d, half_precision=half)
+    norm = hip.qk_norm(d, wq, wk, eps)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=neox, rope=rope, qk_norm=norm)
+        qr = kv.append(layer, positions, q, k, v).reshape(n, hq * d)
+        q_ref = rope_rows(_qk_norm_rows(q, hq, d, wq, eps), positions, hq, d, d, theta, neox)
+        k_ref = rope_rows(_qk_norm_rows(k, hkv, d, wk, eps), positions, hkv, d, d, theta, neox)
+        np.testing.assert_array_equal(qr, q_ref)
+        if half:
+            k_ref = oracle.f16_round(k_ref)
+            v = oracle.f16_round(v)
+        for i, p in enumerate(positions):
+            kk, vv = kv.read(0, int(p), int(p) + 1)
+            np.testing.assert_array_equal(kk, k_ref[i])
+            np.testing.assert_array_equal(vv, v[i])
+    finally:
+        norm.close()
+        kv.close()
+        rope.close()
+
+
+@pytest.mark.parametrize("half", [False, True])
+def test_qk_norm_prefill_then_decode(hip, half):
+    """Qwen3-shaped layer with attn_q_norm / attn_k_norm (16 Q / 8 KV heads, d 128, NeoX theta 1e6):
+    300 prior rows through the MFMA prefill, then 3 decode steps (QK-norm layers take the unfused
+    append + split-K decode path). The oracle normalises q and k the same way before its own RoPE."""
+    hq, hkv, d, prior, steps, theta, eps = 16, 8, 128, 300, 3, 1e6, 1e-6
+    n = prior + steps
+    scale = A.default_scale(d)
+    q = normal(13, "qnd/q", (n, hq * d))
+    k = normal(13, "qnd/k", (n, hkv * d))
+    v = normal(13, "qnd/v", (n, hkv * d))
+    wq = normal(13, "qnd/wq", (d,)) * 0.2 + 1.0
+    wk = normal(13, "qnd/wk", (d,)) * 0.2 + 1.0
+    qn = _qk_norm_rows(q, hq, d, wq, eps)
+    kn = _qk_norm_rows(k, hkv, d, wk, eps)
+    ref = OracleKv(1, 512, hkv * d, hkv * d, half_precision=half)
+    ref_prefill, _, _ = ref.prefill_layer(0, 0, qn[:prior], kn[:prior], v[:prior], hq, hkv, d, d,
+                                          theta, 1.0, True, scale)
+    ref_dec = [ref.decode_layer(0, prior + s, qn[prior + s], kn[prior + s], v[prior + s], hq, hkv,
+                                d, d, theta, 1.0, True, scale)[0] for s in range(steps)]
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=512)
+    kv = hip.kv_cache(1, 512, hkv, d, d, half_precision=half)
+    norm = hip.qk_norm(d, wq, wk, eps)
+    close = assert_f16_close if half else assert_f32_close
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope, qk_norm=norm)
+        got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior])
+        e = [close(got_prefill, ref_prefill, "QK-norm prefill")]
+        for s in range(steps):
+            got = kv.decode(layer, [prior + s], q[prior + s], k[prior + s], v[prior + s])
+            e.append(close(got, ref_dec[s], f"QK-norm decode step {s}"))
+        _say(f"QK-norm half={half} errors " + " ".join(f"{x:.2e}" for x in e))
+        np.testing.assert_array_equal(kv.key_slice(0, 0, n), ref.key_slice(0, 0, n))
+    finally:
+        norm.close()
+        kv.close()
+        rope.close()
+
+
+def test_qk_norm_rejects_bad_weights(hip):
+    with pytest.raises(ValueError):
+        hip.qk_norm(64, np.ones(32), None)
+    norm = hip.qk_norm(64, None, None)
+    rope = hip.rotary_table(128, 1e4, 1.0, max_positions=8)
+    kv = hip.kv_cache(1, 8, 1, 128, 128, half_precision=False)
+    try:
+        layer = A.AttentionLayer(0, 1, neox=True, rope=rope, qk_norm=norm)
+        with pytest.raises(A.AttentionStatusError) as info:
+            kv.append(layer, [0], np.ones(128), np.ones(128), np.ones(128))
+        assert info.value.status == A.INVALID_SHAPE
+    finally:
+        kv.close()
+        rope.close()
+        norm.close()
+
+
 def test_rope_gemma4_proportional_golden_on_device(hip, known_answers):
     case = known_answers["rope"][0]  # RotaryTableTest :80-91
     rope = hip.rotary_table(case["rotary_dim"], case["theta"], case["frequency_scale"],

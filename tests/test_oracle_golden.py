@@ -218,3 +218,11 @@ def test_sliding_layer_pattern(known_answers):
     case = known_answers["sliding_layers"]
     got = [uses_sliding_window(l, case["pattern"], 512) for l in range(case["layers"])]
     assert got == case["sliding"]
+
+
+def test_rms_norm_known_answers(oracle, known_answers):
+    # TensorOpsTest.RmsNorm (ops/TensorOpsTest.java:42-67).
+    for case in known_answers["rms_norm"]:
+        out = oracle.rms_norm(case["x"], case["weight"], case["eps"])
+        for i, want, tol in case["expect_close"]:
+            assert abs(float(out[i]) - want) <= tol, (case["name"], i, out[i], want)

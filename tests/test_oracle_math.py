@@ -227,3 +227,21 @@ def test_batch_threads_match_single(oracle):
         np.testing.assert_array_equal(one[i], many[i])
         np.testing.assert_array_equal(one[i], oracle.gqa_rows(qs[i], ks[i], vs[i], hq, hkv, d, d,
                                                               0.25))
+
+
+def test_rms_norm_against_float64_and_in_place(oracle):
+    # rms = sqrt(mean(x^2) + eps) computed in float64; the oracle's float sum and rounding stay
+    # within a few ulp. A wrong divisor (d vs d-1), a missing eps or a missing weight fails this.
+    rng = np.random.default_rng(5)
+    for d in (2, 16, 64, 128, 256):
+        x = rng.standard_normal(d).astype(np.float32) * 3
+        w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+        eps = 1e-6
+        ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps) * w
+        got = oracle.rms_norm(x, w, eps)
+        np.testing.assert_allclose(got, ref, rtol=4e-6, atol=0)
+        heads = np.concatenate([x, 2 * x, np.zeros(d, np.float32)])
+        out = oracle.qk_norm_heads(heads, 3, d, w, eps)
+        np.testing.assert_array_equal(out[:d], got)  # in place (per head) == out of place
+        np.testing.assert_allclose(out[d:2 * d], got, rtol=4e-6)  # scale invariance
+        np.testing.assert_array_equal(out[2 * d:], np.zeros(d, np.float32))
