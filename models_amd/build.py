@@ -26,6 +26,10 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     # no packed-FP32 instructions in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep single-lane atomics as written: the wave-level aggregation rewrite waits for an
+    # atomic's result right after issuing it, which puts a memory round trip in front of the
+    # decode kernel's tile loads
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
     "-Wno-unused-result",
 ]

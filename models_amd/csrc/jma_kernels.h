@@ -61,7 +61,9 @@ struct DecodeArgs {
   float* out;           // [count][num_heads * dv]
   float* part_acc;      // [items][16][dv]
   float* part_ml;       // [items][16][2]  (running max in log2 units, sum)
-  uint32_t* counters;   // [rows][kv heads][head groups] arrival counts, zero between launches;
+  uint64_t* part_tag;   // [items][16][dv + 2] tagged words {f32 value, u32 tag} (acc, m, l) of the
+                        // fused reduction; every tag is clear between launches
+  uint32_t* counters;   // [rows][kv heads][head groups] arrival tickets, zero between launches;
                         // null = reduce_kernel combines the splits
   const float* k_new;   // [count][num_kv_heads * dk] raw keys to rotate and append; null = none
   const float* v_new;   // [count][num_kv_heads * dv]
@@ -71,10 +73,13 @@ struct DecodeArgs {
   KvView kv;
   float qscale;         // score scale * log2(e), folded into q
   uint32_t num_heads, group, hgroups, window;
+  uint32_t num_kv_heads;
   uint32_t pairs, neox, rope_q;  // rope_q: q is raw and the kernel rotates it
   uint32_t tiles_per_split;
   uint32_t total_items;
-  uint32_t ns_uniform;  // > 0: every row has this many splits, rows located arithmetically
+  uint32_t max_splits;  // splits of the row with the most; the grid is (max_splits, kv heads *
+                        // head groups, rows)
+  uint32_t ns_uniform;  // > 0: every row has this many splits
   RowList rows;
   uint32_t item_start[kMaxRows + 1];
   uint32_t nsplit[kMaxRows];

@@ -25,6 +25,11 @@ namespace jma {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+// Lambdas over shared state must inline, or the captured state (accumulators included) would be
+// spilled to scratch memory.
+#define JMA_INL __attribute__((always_inline))
+#define JMA_GLOBAL __attribute__((address_space(1)))
+
 // Index of slot r (0..31) inside a 32-slot f16 V block. A 16x16x32 MFMA lane (g = lane/16)
 // supplies k-slots 8g..8g+7; the score tile gives that lane rows {4g..4g+3, 16+4g..16+4g+3},
 // so storing those rows at 8g..8g+7 makes one 16-byte load a ready PV operand.
@@ -207,53 +212,211 @@ __device__ __forceinline__ uint64_t pack2(float lo, float hi) {
   return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
 }
 
+// M consecutive floats from p (M = 2 or a multiple of 4; p aligned to 8 or 16 bytes to match).
+template <int M>
+__device__ __forceinline__ void load_floats(const float* __restrict__ p, float (&out)[M]) {
+  if constexpr (M == 2) {
+    const float2 t = *(const float2*)p;
+    out[0] = t.x, out[1] = t.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < M; i += 4) {
+      const float4_t t = *(const float4_t*)(p + i);
+      out[i] = t[0], out[i + 1] = t[1], out[i + 2] = t[2], out[i + 3] = t[3];
+    }
+  }
+}
+
 // N consecutive elements e0 .. e0+N-1 of one head, rotated as TensorOps.rope / ropeNeox do. x is
 // the head's first element; e0 is a multiple of N and N divides the rotary pair count, so a chunk
-// lies wholly in the first half, the second half or the pass-through tail of the head.
+// lies wholly in the first half, the second half or the pass-through tail of the head. Every
+// load (the chunk, its NeoX partner chunk, the factors) is issued before any is used: the chunk
+// costs one memory round trip. Lanes in the pass-through tail read factor row entry 0 and keep
+// their elements.
 template <int N>
 __device__ __forceinline__ void rope_chunk(const float* __restrict__ x, uint32_t e0,
                                            const float* __restrict__ cs,
                                            const float* __restrict__ sn, uint32_t pairs,
                                            uint32_t neox, float (&out)[N]) {
   float v[N];
-#pragma unroll
-  for (int i = 0; i < N; i += 4) {
-    const float4_t t = *(const float4_t*)(x + e0 + i);
-    v[i] = t[0], v[i + 1] = t[1], v[i + 2] = t[2], v[i + 3] = t[3];
-  }
-  if (cs == nullptr || e0 >= 2 * pairs) {
+  load_floats<N>(x + e0, v);
+  if (cs == nullptr) {
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = v[i];
     return;
   }
+  const bool rot = e0 < 2 * pairs;
   if (!neox) {  // interleaved pairs (2j, 2j+1) sit inside the chunk
+    const uint32_t j = rot ? e0 / 2 : 0u;
+    float c[N / 2], sf[N / 2];
+    load_floats<N / 2>(cs + j, c);
+    load_floats<N / 2>(sn + j, sf);
 #pragma unroll
     for (int i = 0; i < N; i += 2) {
       float a0 = v[i], a1 = v[i + 1];
-      rotate_pair(a0, a1, cs[(e0 + i) / 2], sn[(e0 + i) / 2]);
-      out[i] = a0, out[i + 1] = a1;
+      rotate_pair(a0, a1, c[i / 2], sf[i / 2]);
+      out[i] = rot ? a0 : v[i];
+      out[i + 1] = rot ? a1 : v[i + 1];
     }
     return;
   }
   const bool lower = e0 < pairs;  // split-half pairs (j, j + pairs)
-  const uint32_t j0 = lower ? e0 : e0 - pairs;
-  float w[N];
-#pragma unroll
-  for (int i = 0; i < N; i += 4) {
-    const float4_t t = *(const float4_t*)(x + (lower ? e0 + pairs : j0) + i);
-    w[i] = t[0], w[i + 1] = t[1], w[i + 2] = t[2], w[i + 3] = t[3];
-  }
+  const uint32_t j = rot ? (lower ? e0 : e0 - pairs) : 0u;
+  float w[N], c[N], sf[N];
+  load_floats<N>(x + (lower ? e0 + pairs : e0 - pairs), w);  // the partner chunk, inside the head
+  load_floats<N>(cs + j, c);
+  load_floats<N>(sn + j, sf);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     float a0 = lower ? v[i] : w[i], a1 = lower ? w[i] : v[i];
-    rotate_pair(a0, a1, cs[j0 + i], sn[j0 + i]);
-    out[i] = lower ? a0 : a1;
+    rotate_pair(a0, a1, c[i], sf[i]);
+    out[i] = rot ? (lower ? a0 : a1) : v[i];
   }
 }
 
+__device__ __forceinline__ uint64_t tagged(float x) {
+  return (uint64_t)__float_as_uint(x) | ((uint64_t)1u << 32);
+}
+
+__device__ __forceinline__ bool tag_set(uint64_t w) { return (w >> 32) != 0; }
+
+// Polls of one reducer before it gives up and reports a reduction timeout (error bit 1). Each
+// poll waits one memory round trip, so this bounds the wait at seconds; it is reached only if a
+// producer of the group never stores, which the ticket order rules out.
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ uint64_t poll_word(uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void clear_word(uint64_t* p) {
+  __hip_atomic_store(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One workgroup's partial for output element (head slot hs, element e): its waves' states
+// (s_ml, s_acc) rescaled to their common maximum and summed in wave order. Every multiply-add is
+// an explicit fmaf, so the reducer (which keeps its own partial) and a producer (which stores it)
+// compute the same bits and the result does not depend on which workgroup reduces.
+template <int DV>
+__device__ __forceinline__ void wave_partial(const float (*s_acc)[16][DV], const float (*s_ml)[16][2],
+                                             uint32_t hs, uint32_t e, float& mx, float& lw,
+                                             float& aw) {
+  mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_ml[w][hs][0]);
+  const float mu = mx == -INFINITY ? 0.0f : mx;
+  lw = 0.0f;
+  aw = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kDecodeWaves; ++w) {
+    const float f = exp2f(s_ml[w][hs][0] - mu);
+    lw = fmaf(s_ml[w][hs][1], f, lw);
+    aw = fmaf(s_acc[w][hs][e], f, aw);
+  }
+}
+
+// The reducer's side of the fused cross-split reduction of one group (row, kv head, head group)
+// whose ns partials start at item0; this workgroup is split `split`, and its own per-wave state
+// is in s_acc / s_ml. Partial words per (item, head slot): dv acc elements, then m, then l.
+// Output elements go in passes of kE per thread (element j = head slot * dv + e): a pass loads,
+// for each of the other B >= ns - 1 splits (indices past the last clamped to it), the element
+// word and the head's (m, l) words, reloads whatever tag is still clear until every tag is set,
+// combines all splits in split order (its own at index `split`), stores the output and clears the
+// element words. The (m, l) words, read by every thread of a head, are cleared after a barrier.
+template <int B, int kE, int DV>
+__device__ __forceinline__ void reduce_group(uint64_t* part, uint64_t item0, uint32_t ns,
+                                             uint32_t split, uint32_t nreal,
+                                             const float (*s_acc)[16][DV],
+                                             const float (*s_ml)[16][2], float* out, int* err) {
+  constexpr uint32_t kT = 64 * kDecodeWaves;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t E = nreal * DV;
+  auto words = [&](uint32_t o, uint32_t hs) JMA_INL {
+    return part + ((item0 + o + (o >= split ? 1u : 0u)) * 16 + hs) * (DV + 2);
+  };
+  bool timed_out = false;
+  for (uint32_t j0 = 0; j0 < E; j0 += kT * kE) {
+    uint64_t xv[kE][B], mv[kE][B], lv[kE][B];
+    auto load = [&](int u, int s) JMA_INL {
+      const uint32_t j = min(j0 + tid + kT * u, E - 1);
+      uint64_t* w = words(min((uint32_t)s, ns - 2), j / DV);
+      xv[u][s] = poll_word(w + j % DV);
+      mv[u][s] = poll_word(w + DV);
+      lv[u][s] = poll_word(w + DV + 1);
+    };
+    auto set = [&](int u, int s) JMA_INL {
+      return tag_set(xv[u][s]) && tag_set(mv[u][s]) && tag_set(lv[u][s]);
+    };
+#pragma unroll
+    for (int u = 0; u < kE; ++u)
+#pragma unroll
+      for (int s = 0; s < B; ++s) load(u, s);
+    for (uint32_t spin = 0;; ++spin) {
+      bool ready = true;
+#pragma unroll
+      for (int u = 0; u < kE; ++u)
+#pragma unroll
+        for (int s = 0; s < B; ++s) ready &= set(u, s);
+      if (ready) break;
+      if (spin == kSpinLimit) {
+        timed_out = true;
+        break;
+      }
+#pragma unroll
+      for (int u = 0; u < kE; ++u)
+#pragma unroll
+        for (int s = 0; s < B; ++s)
+          if (!set(u, s)) load(u, s);
+    }
+#pragma unroll
+    for (int u = 0; u < kE; ++u) {
+      const uint32_t j = j0 + tid + kT * u;
+      if (j >= E) continue;
+      const uint32_t hs = j / DV, e = j % DV;
+      float mx, lo, ao;  // this workgroup's own partial
+      wave_partial<DV>(s_acc, s_ml, hs, e, mx, lo, ao);
+      float gm = mx;
+#pragma unroll
+      for (int s = 0; s < B; ++s)
+        gm = (uint32_t)s < ns - 1 ? fmaxf(gm, __uint_as_float((uint32_t)mv[u][s])) : gm;
+      const float gmu = gm == -INFINITY ? 0.0f : gm;
+      float gl = 0.0f, ga = 0.0f;
+      bool own = false;
+#pragma unroll
+      for (int s = 0; s < B; ++s) {
+        if (!own && (uint32_t)s == split) {
+          own = true;
+          const float f = exp2f(mx - gmu);
+          gl = fmaf(lo, f, gl);
+          ga = fmaf(ao, f, ga);
+        }
+        if ((uint32_t)s < ns - 1) {
+          const float f = exp2f(__uint_as_float((uint32_t)mv[u][s]) - gmu);
+          gl = fmaf(__uint_as_float((uint32_t)lv[u][s]), f, gl);
+          ga = fmaf(__uint_as_float((uint32_t)xv[u][s]), f, ga);
+          clear_word(words(s, hs) + e);
+        }
+      }
+      if (!own) {
+        const float f = exp2f(mx - gmu);
+        gl = fmaf(lo, f, gl);
+        ga = fmaf(ao, f, ga);
+      }
+      if (!(gl > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
+      out[j] = ga * (1.0f / gl);
+    }
+  }
+  __syncthreads();
+  for (uint32_t k = tid; k < (ns - 1) * nreal; k += kT) {
+    uint64_t* w = words(k / nreal, k % nreal) + DV;
+    clear_word(w);
+    clear_word(w + 1);
+  }
+  if (timed_out) atomicOr(err, 2);
+}
+
 // One workgroup = one work item (row, kv head, head group of <= 16 query heads, split); its
-// kDecodeWaves waves stride over the split's tiles, keeping the next tile's loads in flight while
-// the current one is computed, and combine in LDS. Scores are computed as S = K * Q^T on 16-row
+// kDecodeWaves waves stride over the split's tiles. Scores are computed as S = K * Q^T on 16-row
 // blocks so lane (g, c) holds rows 4g+e of query head c: every lane works on a single head, the
 // online-softmax rescale is one factor per lane, and the score registers are already the B
 // operand of the PV product O^T = V^T * P.
@@ -262,14 +425,21 @@ __device__ __forceinline__ void rope_chunk(const float* __restrict__ x, uint32_t
 // to ~2^-22), so both products run at near-f32 accuracy against the f32 reference.
 // f32 KV: v_mfma_f32_16x16x4_f32 with f32 operands throughout.
 //
-// Decode fuses the other per-token work into this one launch:
+// The kernel is bound by memory latency, not bandwidth (a layer-step at 4k context moves a few
+// MB), so it is laid out to put as few dependent memory round trips on the critical path as it
+// can:
+//  - each wave issues the loads of its first two tiles before it loads q, and one tile ahead
+//    after that;
 //  - RoPE on q (rope_q): each lane rotates the q elements it loads;
-//  - the append (k_new/v_new): the workgroup of a row's last split rotates and stores that kv
-//    head's new K/V row before any wave loads a tile, so the row's own tile reads it back;
-//  - the cross-split reduction (counters): partials are written with device-coherent stores, the
-//    last workgroup of a (row, kv head, head group) to arrive reduces them with device-coherent
-//    loads and resets the counter. No cache-wide fence is needed: the partials bypass the
-//    per-XCD L2s.
+//  - the append (k_new/v_new): the workgroups whose last tile holds the new position rotate the
+//    new K row and patch it, with the new V row, into the registers of that tile; the head
+//    group 0 workgroup also stores the row to the cache, and nobody waits for that store;
+//  - the cross-split reduction (counters): every workgroup of a (row, kv head, head group) takes
+//    an arrival ticket with one atomic at its start. The last to arrive becomes the reducer:
+//    every other workgroup of its group has started by then and so will finish. The others store
+//    their partial (m, l, acc) as tagged 64-bit words {value, 1} and exit without waiting; the
+//    reducer reads them back with device-coherent loads, reloading until every tag is set, then
+//    clears what it read (tag 0), so every partial word is clear again when the launch ends.
 template <typename KV, int DK, int DV>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
@@ -279,46 +449,82 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   constexpr int kNv = DV / 16;        // output fragments per lane
   constexpr int kC = kF16 ? DK / 32 : DK / 16;
   constexpr int kQ = kF16 ? 8 : 4;    // q elements per lane per k-chunk
-  __shared__ __attribute__((aligned(16))) float s_acc[kDecodeWaves - 1][16][DV];
-  __shared__ __attribute__((aligned(16))) float s_ml[kDecodeWaves - 1][16][2];
-  __shared__ uint32_t s_last;
+  constexpr uint32_t kW = kDecodeWaves;
+  __shared__ __attribute__((aligned(16))) float s_acc[kW][16][DV];
+  __shared__ float s_ml[kW][16][2];
+  __shared__ uint32_t s_ticket;
+  __shared__ __attribute__((aligned(16))) KV s_new_k[DK];  // the appended row, rotated
+  __shared__ KV s_new_v[DV];
+  __shared__ __attribute__((aligned(16))) float s_q[16][DK + 4];  // q rows, padded against bank conflicts
 
-  // Fetch the scalar arguments the prologue needs in one batch: left to itself the compiler
-  // loads each right before its use, behind its own wait.
-  uint32_t num_heads = a.num_heads, group = a.group, hgroups = a.hgroups, ns_uniform = a.ns_uniform;
-  uint32_t rows_contig = a.rows.contiguous, rows_seq0 = a.rows.seq0, rows_start = a.rows.start;
+  // The grid is (split, kv head * head groups + head group, row). Every scalar argument the
+  // kernel uses, the row's own table entries included, is fetched in one batch: left to itself
+  // the compiler loads each right before its use, behind its own wait, and a scalar load costs
+  // about half a vector memory round trip here.
+  const uint32_t split = blockIdx.x, rest = blockIdx.y, row = blockIdx.z;
+  uint32_t num_heads = a.num_heads, group = a.group, hgroups = a.hgroups, hkv = a.num_kv_heads;
+  uint32_t ns_uniform = a.ns_uniform, rows_contig = a.rows.contiguous;
+  uint32_t r_seq = a.rows.seq[row], r_pos = a.rows.pos[row], r_ns = a.nsplit[row],
+           r_item0 = a.item_start[row];
+  uint32_t rows_seq0 = a.rows.seq0, rows_start = a.rows.start;
   uint32_t window = a.window, tps = a.tiles_per_split, cap = a.kv.cap, ring = a.kv.ring;
+  uint32_t pairs = a.pairs, neox = a.neox, rope_q = a.rope_q;
+  float qscale = a.qscale;
   uint64_t seq_stride_k = a.kv.seq_stride_k, seq_stride_v = a.kv.seq_stride_v;
   uint64_t layer_off_k = a.kv.layer_off_k, layer_off_v = a.kv.layer_off_v;
-  asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hgroups), "+s"(ns_uniform), "+s"(rows_contig),
+  // Pointers go through the asm typed as global memory so the loads through them stay global
+  // (a generic pointer would turn them into flat loads, which also count against lgkmcnt).
+  JMA_GLOBAL const KV *g_k = (JMA_GLOBAL const KV*)a.kv.k, *g_v = (JMA_GLOBAL const KV*)a.kv.v;
+  JMA_GLOBAL const float *g_q = (JMA_GLOBAL const float*)a.q;
+  JMA_GLOBAL const float *g_cos = (JMA_GLOBAL const float*)a.cos_t;
+  JMA_GLOBAL const float *g_sin = (JMA_GLOBAL const float*)a.sin_t;
+  JMA_GLOBAL const float *g_kn = (JMA_GLOBAL const float*)a.k_new;
+  JMA_GLOBAL const float *g_vn = (JMA_GLOBAL const float*)a.v_new;
+  JMA_GLOBAL uint32_t* g_ctr = (JMA_GLOBAL uint32_t*)a.counters;
+  JMA_GLOBAL float* g_out = (JMA_GLOBAL float*)a.out;
+  JMA_GLOBAL uint64_t* g_tag = (JMA_GLOBAL uint64_t*)a.part_tag;
+  JMA_GLOBAL float* g_pacc = (JMA_GLOBAL float*)a.part_acc;
+  JMA_GLOBAL float* g_pml = (JMA_GLOBAL float*)a.part_ml;
+  JMA_GLOBAL int* g_err = (JMA_GLOBAL int*)a.err;
+  asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hgroups), "+s"(hkv), "+s"(ns_uniform),
+               "+s"(rows_contig), "+s"(r_seq), "+s"(r_pos), "+s"(r_ns), "+s"(r_item0),
                "+s"(rows_seq0), "+s"(rows_start), "+s"(window), "+s"(tps), "+s"(cap), "+s"(ring),
+               "+s"(pairs), "+s"(neox), "+s"(rope_q), "+s"(qscale),
                "+s"(seq_stride_k), "+s"(seq_stride_v), "+s"(layer_off_k), "+s"(layer_off_v));
+  asm volatile("" : "+s"(g_k), "+s"(g_v), "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn),
+               "+s"(g_ctr), "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
+  const KV *kv_k = (const KV*)g_k, *kv_v = (const KV*)g_v;
+  const float *q_in = (const float*)g_q, *cos_t = (const float*)g_cos, *sin_t = (const float*)g_sin;
+  const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
+  uint32_t* counters = (uint32_t*)g_ctr;
+  float* out = (float*)g_out;
+  uint64_t* part_tag = (uint64_t*)g_tag;
+  float* part_acc = (float*)g_pacc;
+  float* part_ml = (float*)g_pml;
+  int* err = (int*)g_err;
 
-  const uint32_t item = blockIdx.x;
-  const uint32_t hkv = num_heads / group;
-  uint32_t row, ns, local;
-  if (ns_uniform) {
-    ns = ns_uniform;
-    row = item / (hkv * hgroups * ns);
-    local = item - row * hkv * hgroups * ns;
-  } else {
-    // Count the rows that start at or before this item: independent table loads, one round trip.
-    row = 0;
-#pragma unroll
-    for (uint32_t r = 1; r < kMaxRows; ++r) row += (r < a.rows.count && a.item_start[r] <= item) ? 1u : 0u;
-    ns = a.nsplit[row];
-    local = item - a.item_start[row];
-  }
-  const uint32_t split = local % ns;
-  const uint32_t rest = local / ns;
-  const uint32_t hg = rest % hgroups;
-  const uint32_t kvh = rest / hgroups;
-  const uint32_t seq = rows_contig ? rows_seq0 : a.rows.seq[row];
-  const uint32_t pos = rows_contig ? rows_start + row : a.rows.pos[row];
+  const uint32_t ns = ns_uniform ? ns_uniform : r_ns;
+  if (split >= ns) return;  // a listed row with fewer splits than the grid's widest row
+  const uint32_t item = ns_uniform ? (row * hkv * hgroups + rest) * ns + split : r_item0 + rest * ns + split;
+  const uint32_t hg = hgroups == 1 ? 0u : rest % hgroups;
+  const uint32_t kvh = hgroups == 1 ? rest : rest / hgroups;
+  const bool fused = ns > 1 && counters != nullptr;
+  const uint64_t gid = ((uint64_t)row * hkv + kvh) * hgroups + hg;
+  // Arrival ticket first: its round trip overlaps the tile loads.
+  uint32_t ticket = 0;
+  if (fused && threadIdx.x == 0)
+    ticket = __hip_atomic_fetch_add(&counters[gid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  const uint32_t seq = rows_contig ? rows_seq0 : r_seq;
+  const uint32_t pos = rows_contig ? rows_start + row : r_pos;
   const uint32_t first = first_visible(pos, window);
   const uint32_t t_begin = first / kBlk, t_end = pos / kBlk + 1;
   const uint32_t s_t0 = t_begin + split * tps;
   const uint32_t s_t1 = min(s_t0 + tps, t_end);
+  // Ring layers: the split's first tile slot, then consecutive tiles wrap at most once (a
+  // split spans fewer positions than the ring holds).
+  uint32_t slot_base = s_t0 * kBlk;
+  if (ring) slot_base %= cap;
 
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -326,63 +532,132 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t hl = hg * 16 + c16;
   const bool head_ok = hl < group;
-  const uint32_t head = kvh * group + hl;
-  const float* qrow = a.q + ((uint64_t)row * num_heads + (head_ok ? head : 0)) * DK;
-  const float* cs = a.cos_t ? a.cos_t + (uint64_t)pos * a.pairs : nullptr;
-  const float* sn = a.cos_t ? a.sin_t + (uint64_t)pos * a.pairs : nullptr;
+  const float* cs = cos_t ? cos_t + (uint64_t)pos * pairs : nullptr;
+  const float* sn = cos_t ? sin_t + (uint64_t)pos * pairs : nullptr;
 
-  KV* kb = (KV*)a.kv.k + seq * seq_stride_k + layer_off_k + (uint64_t)kvh * cap * DK;
-  KV* vb = (KV*)a.kv.v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV;
+  KV* kb = (KV*)kv_k + seq * seq_stride_k + layer_off_k + (uint64_t)kvh * cap * DK;
+  KV* vb = (KV*)kv_v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV;
+  auto slot0_of = [&](uint32_t t) JMA_INL {
+    const uint32_t x = slot_base + (t - s_t0) * kBlk;
+    return ring && x >= cap ? x - cap : x;
+  };
 
-  // Fused append: the last split of the row holds the new position's tile.
-  if (a.k_new != nullptr && split == ns - 1) {
-    if (hg == 0) {
-      const uint32_t slot = slot_of(a.kv, pos);
-      const float* kx = a.k_new + ((uint64_t)row * hkv + kvh) * DK;
-      const float* vx = a.v_new + ((uint64_t)row * hkv + kvh) * DV;
-      const uint32_t tid = threadIdx.x;
-      if (tid < DK / 4) {
-        float r[4];
-        rope_chunk<4>(kx, 4 * tid, cs, sn, a.pairs, a.neox, r);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kb[(uint64_t)slot * DK + 4 * tid + i] = (KV)r[i];
-      } else if (tid < DK / 4 + DV / 4) {
-        const uint32_t d = 4 * (tid - DK / 4);
-        const float4_t x = *(const float4_t*)(vx + d);
-        const uint32_t s = kF16 ? perm32(slot % kBlk) : slot % kBlk;
-        KV* vp = vb + (uint64_t)(slot / kBlk) * DV * kBlk + (uint64_t)d * kBlk + s;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) vp[i * kBlk] = (KV)x[i];
-      }
-      // The stores must land before any wave of this workgroup loads the tile holding them.
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __syncthreads();
-  }
-
-  // Start the first tile's loads before preparing Q.
+  // The first two tiles of this wave are in flight before anything else is loaded (at head
+  // dimension 256 the second waits until q is prepared: two tiles are half the register file).
+  constexpr bool kEarly2 = DK <= 128;
   uint32_t t = s_t0 + wave;
-  TileT cur;
-  if (t < s_t1) cur.load(kb, vb, ring ? (t * kBlk) % cap : t * kBlk, c16, g);
+  TileT ta, tb;
+  if (t < s_t1) ta.load(kb, vb, slot0_of(t), c16, g);
+  if (kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
 
-  // Q operand (B of S = K Q^T), rotated here when the caller passed raw q.
-  const float qs = head_ok ? a.qscale : 0.0f;
+  // Fused append. The new row's tile is the last of the row's last split: the row is rotated
+  // into LDS, from where the wave owning that tile patches it into its registers, and the head
+  // group 0 workgroup stores it to the cache (the next launches read it there).
+  const bool append = k_new != nullptr && split == ns - 1;
+  if (append) {
+    // One thread per K pair (rotated as rope_append_kernel rotates it) or V element pair; every
+    // load is issued before any is used.
+    const uint32_t slot = ring ? pos % cap : pos;
+    const float* kx = k_new + ((uint64_t)row * hkv + kvh) * DK;
+    const float* vx = v_new + ((uint64_t)row * hkv + kvh) * DV;
+    const uint32_t tid = threadIdx.x;
+    if (tid < DK / 2) {
+      const uint32_t j = tid;
+      const bool rot = cs != nullptr && j < pairs;
+      const uint32_t e0 = rot && neox ? j : 2 * j, e1 = rot && neox ? j + pairs : 2 * j + 1;
+      float y0 = kx[e0], y1 = kx[e1], fc = 1.0f, fs = 0.0f;
+      if (cs != nullptr) {
+        fc = cs[rot ? j : 0u];
+        fs = sn[rot ? j : 0u];
+      }
+      if (rot) rotate_pair(y0, y1, fc, fs);
+      s_new_k[e0] = (KV)y0;
+      s_new_k[e1] = (KV)y1;
+      if (hg == 0) {
+        kb[(uint64_t)slot * DK + e0] = (KV)y0;
+        kb[(uint64_t)slot * DK + e1] = (KV)y1;
+      }
+    } else if (tid < DK / 2 + DV / 2) {
+      const uint32_t d = 2 * (tid - DK / 2);
+      const float v0 = vx[d], v1 = vx[d + 1];
+      s_new_v[d] = (KV)v0;
+      s_new_v[d + 1] = (KV)v1;
+      if (hg == 0) {
+        const uint32_t r = kF16 ? perm32(slot % kBlk) : slot % kBlk;
+        KV* vp = vb + (uint64_t)(slot / kBlk) * DV * kBlk + (uint64_t)d * kBlk + r;
+        vp[0] = (KV)v0;
+        vp[kBlk] = (KV)v1;
+      }
+    }
+  }
+  // Lanes of the wave owning the new row's tile that hold that row: K lanes hold tile rows
+  // 16b + c16 (f16) or c16 (f32); V lanes hold tile rows by MFMA k-group g.
+  const uint32_t t_new = pos / kBlk, r_new = pos % kBlk;
+  const bool patch_wave = append && (t_new - s_t0) % kW == (uint32_t)wave;
+  const uint32_t v_at = kF16 ? perm32(r_new) : r_new;  // V block index of the new row
+  const bool k_lane = patch_wave && (uint32_t)c16 == (r_new & 15u);
+  const bool v_lane = patch_wave && (uint32_t)g == v_at / (kF16 ? 8u : 4u);
+
+  // q of this head group, rotated here when the caller passed raw q, times the score scale,
+  // staged in LDS by the whole workgroup: thread k takes RoPE pair k (head k / (DK/2)). Every
+  // load is issued (indices clamped) before any is used, so this costs one memory round trip.
+  const uint32_t nreal = min(16u, group - hg * 16);  // query heads of this head group
+  {
+    constexpr uint32_t kHalf = DK / 2;
+    constexpr int kIt = (16 * kHalf + 64 * kW - 1) / (64 * kW);
+    const uint32_t nq = nreal * kHalf;
+    const bool rope_on = rope_q != 0 && cs != nullptr;
+    const float* qg = q_in + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DK;
+    float y0[kIt], y1[kIt], fc[kIt], fs[kIt];
+    uint32_t e0[kIt], e1[kIt];
+    bool rot[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const uint32_t k = min(threadIdx.x + 64 * kW * it, nq - 1);
+      const uint32_t hs = k / kHalf, j = k % kHalf;
+      rot[it] = rope_on && j < pairs;
+      e0[it] = hs * DK + (rot[it] && neox ? j : 2 * j);
+      e1[it] = hs * DK + (rot[it] && neox ? j + pairs : 2 * j + 1);
+      y0[it] = qg[e0[it]];
+      y1[it] = qg[e1[it]];
+      if (rope_on) {
+        fc[it] = cs[rot[it] ? j : 0u];
+        fs[it] = sn[rot[it] ? j : 0u];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      if (threadIdx.x + 64 * kW * it >= nq) continue;
+      float u0 = y0[it], u1 = y1[it];
+      if (rot[it]) rotate_pair(u0, u1, fc[it], fs[it]);
+      const uint32_t hs = e0[it] / DK;
+      s_q[hs][e0[it] - hs * DK] = u0 * qscale;
+      s_q[hs][e1[it] - hs * DK] = u1 * qscale;
+    }
+  }
+  if (!kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
+  __syncthreads();  // q (and the appended row) are in LDS
+
+  // Q operand (B of S = K Q^T); the padding head lanes hold zeros.
   half8_t qhi[kF16 ? kC : 1], qlo[kF16 ? kC : 1];
   float4_t qf[kF16 ? 1 : kC];
 #pragma unroll
   for (int c = 0; c < kC; ++c) {
     float x[kQ];
-    rope_chunk<kQ>(qrow, (kF16 ? 32 : 16) * c + kQ * g, a.rope_q ? cs : nullptr, sn, a.pairs,
-                   a.neox, x);
+#pragma unroll
+    for (int i = 0; i < kQ; i += 4) {
+      const float4_t v4 = head_ok ? *(const float4_t*)&s_q[c16][(kF16 ? 32 : 16) * c + kQ * g + i]
+                                  : float4_t{0.f, 0.f, 0.f, 0.f};
+      x[i] = v4[0], x[i + 1] = v4[1], x[i + 2] = v4[2], x[i + 3] = v4[3];
+    }
 #pragma unroll
     for (int e = 0; e < kQ; ++e) {
-      const float y = x[e] * qs;
       if constexpr (kF16) {
-        const _Float16 h = (_Float16)y;
+        const _Float16 h = (_Float16)x[e];
         qhi[c][e] = h;
-        qlo[c][e] = (_Float16)(y - (float)h);
+        qlo[c][e] = (_Float16)(x[e] - (float)h);
       } else {
-        qf[c][e] = y;
+        qf[c][e] = x[e];
       }
     }
   }
@@ -391,14 +666,33 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   float4_t acc[kNv];
 #pragma unroll
   for (int n = 0; n < kNv; ++n) acc[n] = float4_t{0.f, 0.f, 0.f, 0.f};
-  bool bad = false;
 
-  while (t < s_t1) {
-    const uint32_t tn = t + kDecodeWaves;
-    TileT next;
-    if (tn < s_t1) next.load(kb, vb, ring ? (tn * kBlk) % cap : tn * kBlk, c16, g);
-    const uint32_t p0 = t * kBlk;
-
+  auto step = [&](TileT cur, uint32_t tt, auto patch) JMA_INL {
+    if constexpr (decltype(patch)::value) {
+      // The lanes holding the new row take it from LDS: K by whole 16-byte chunks, V by element.
+      if constexpr (kF16) {
+#pragma unroll
+        for (int c = 0; c < kC; ++c) {
+          const half8_t x = *(const half8_t*)&s_new_k[32 * c + 8 * g];
+          if (r_new < 16) cur.k[0][c] = k_lane ? x : cur.k[0][c];
+          else cur.k[1][c] = k_lane ? x : cur.k[1][c];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < kC; ++c) {
+          const float4_t x = *(const float4_t*)&s_new_k[16 * c + 4 * g];
+          cur.k[c] = k_lane ? x : cur.k[c];
+        }
+      }
+      if (v_lane) {
+#pragma unroll
+        for (int n = 0; n < kNv; ++n)
+#pragma unroll
+          for (int e = 0; e < kQ; ++e)
+            if ((uint32_t)e == v_at % (uint32_t)kQ) cur.v[n][e] = s_new_v[16 * n + c16];
+      }
+    }
+    const uint32_t p0 = tt * kBlk;
     float s[kNs];
     if constexpr (kF16) {
 #pragma unroll
@@ -422,28 +716,39 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[e] = sc[e];
     }
-    float mt = -INFINITY;
+    // Only the first and last tiles of the visible range hold masked rows.
+    if (p0 < first || p0 + kBlk - 1 > pos) {
 #pragma unroll
-    for (int i = 0; i < kNs; ++i) {
-      const uint32_t p = kF16 ? p0 + 16 * (i >> 2) + 4 * g + (i & 3) : p0 + 4 * g + i;
-      const bool valid = p >= first && p <= pos;
-      bad |= valid && (s[i] != s[i] || s[i] == INFINITY);
-      s[i] = valid ? s[i] : -INFINITY;
-      mt = fmaxf(mt, s[i]);
+      for (int i = 0; i < kNs; ++i) {
+        const uint32_t p = kF16 ? p0 + 16 * (i >> 2) + 4 * g + (i & 3) : p0 + 4 * g + i;
+        s[i] = p >= first && p <= pos ? s[i] : -INFINITY;
+      }
     }
+    float mt = s[0];
+#pragma unroll
+    for (int i = 1; i < kNs; ++i) mt = fmaxf(mt, s[i]);
     mt = wave_max_groups(mt);
-    const float mn = fmaxf(m, mt);
-    const float mu = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = exp2f(m - mu);
-    m = mn;
+    // Lazy rescaling: the reference maximum m moves only when a tile exceeds it by more than
+    // 2^8 somewhere in the wave, so the exponentials stay <= 256 and most tiles skip the O
+    // rescale. A NaN or +inf score turns l into NaN (exp2 of NaN or of inf - inf), which the
+    // final normalisation reports: no per-score check is needed.
+    if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f) != 0) {
+      const float mn = fmaxf(m, mt);
+      const float alpha = exp2f(m - (mn == -INFINITY ? 0.0f : mn));
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int n = 0; n < kNv; ++n) acc[n] *= alpha;
+    }
+    const float mu = m == -INFINITY ? 0.0f : m;
     float p[kNs];
     float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < kNs; ++i) {
-      p[i] = exp2f(s[i] - mu);
+      p[i] = __builtin_amdgcn_exp2f(s[i] - mu);
       psum += p[i];
     }
-    l = l * alpha + psum;
+    l += psum;
     if constexpr (kF16) {
       half8_t phi, plo;
 #pragma unroll
@@ -454,163 +759,88 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       }
 #pragma unroll
       for (int n = 0; n < kNv; ++n) {
-        acc[n] *= alpha;
         acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.v[n], phi, acc[n], 0, 0, 0);
         acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.v[n], plo, acc[n], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int n = 0; n < kNv; ++n) {
-        acc[n] *= alpha;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.v[n][e], p[e], acc[n], 0, 0, 0);
       }
     }
-    cur = next;
-    t = tn;
+  };
+
+  // Two tile buffers in turn: each is reloaded, kW * 2 tiles ahead, as soon as it is consumed.
+  // The new row's tile is the last tile of the wave that owns it; that wave takes it after the
+  // loop, where its other buffer is dead, and patches the new row in.
+  using no_patch = std::integral_constant<bool, false>;
+  using with_patch = std::integral_constant<bool, true>;
+  const uint32_t t_stop = patch_wave ? t_new : s_t1;
+  for (;;) {
+    if (t >= t_stop) break;
+    step(ta, t, no_patch{});
+    if (t + 2 * kW < s_t1) ta.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
+    t += kW;
+    if (t >= t_stop) break;
+    step(tb, t, no_patch{});
+    if (t + 2 * kW < s_t1) tb.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
+    t += kW;
+  }
+  if (patch_wave) {
+    if (((t_new - s_t0 - wave) / kW) % 2 == 0) step(ta, t_new, with_patch{});
+    else step(tb, t_new, with_patch{});
   }
 
-  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
   l = wave_sum_groups(l);
 
-  // Combine the waves of this workgroup in LDS (wave 0 keeps its state in registers).
-  if (wave != 0) {
+  // Every wave publishes its state; then one thread per (head, element) combines the waves.
+  if (head_ok) {
     if (g == 0) {
-      s_ml[wave - 1][c16][0] = m;
-      s_ml[wave - 1][c16][1] = l;
+      s_ml[wave][c16][0] = m;
+      s_ml[wave][c16][1] = l;
     }
 #pragma unroll
-    for (int n = 0; n < kNv; ++n)
-      *(float4_t*)&s_acc[wave - 1][c16][16 * n + 4 * g] = acc[n];
+    for (int n = 0; n < kNv; ++n) *(float4_t*)&s_acc[wave][c16][16 * n + 4 * g] = acc[n];
   }
+  if (fused && threadIdx.x == 0) s_ticket = ticket;
   __syncthreads();
 
-  const bool fused = ns > 1 && a.counters != nullptr;
-  float* o = a.out + ((uint64_t)row * a.num_heads + head) * DV;
-  const uint64_t gid = ((uint64_t)row * hkv + kvh) * a.hgroups + hg;
-  if (wave == 0) {
-    float mx = m;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves - 1; ++w) mx = fmaxf(mx, s_ml[w][c16][0]);
-    const float mu = mx == -INFINITY ? 0.0f : mx;
-    const float f0 = exp2f(m - mu);
-    l *= f0;
-#pragma unroll
-    for (int n = 0; n < kNv; ++n) acc[n] *= f0;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves - 1; ++w) {
-      const float fw = exp2f(s_ml[w][c16][0] - mu);
-      l += s_ml[w][c16][1] * fw;
-#pragma unroll
-      for (int n = 0; n < kNv; ++n) acc[n] += *(const float4_t*)&s_acc[w][c16][16 * n + 4 * g] * fw;
-    }
-    if (ns == 1) {
-      if (head_ok) {
-        if (l == 0.0f && g == 0) atomicOr(a.err, 1);
-        const float inv = 1.0f / l;
-#pragma unroll
-        for (int n = 0; n < kNv; ++n) *(float4_t*)(o + 16 * n + 4 * g) = acc[n] * inv;
-      }
-      return;
-    }
-    float* pa = a.part_acc + ((uint64_t)item * 16 + c16) * DV;
-    float* pm = a.part_ml + ((uint64_t)item * 16 + c16) * 2;
-    // Partials of the padding head lanes (the MFMA has 16 columns, the group may have fewer
-    // heads) are neither written nor read back.
-    if (!fused) {  // reduce_kernel combines the splits after this launch
-      if (head_ok) {
-#pragma unroll
-        for (int n = 0; n < kNv; ++n) *(float4_t*)(pa + 16 * n + 4 * g) = acc[n];
-        if (g == 0) {
-          pm[0] = mx;
-          pm[1] = l;
-        }
-      }
-      return;
-    }
-    // Kernel 4 fused. Device-coherent (write-through) stores, then wait for them before counting
-    // this arrival; the last workgroup of the group to arrive reduces.
-    if (head_ok) {
-#pragma unroll
-      for (int n = 0; n < kNv; ++n)
-#pragma unroll
-        for (int e = 0; e < 4; e += 2)
-          __hip_atomic_store((uint64_t*)(pa + 16 * n + 4 * g + e), pack2(acc[n][e], acc[n][e + 1]),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (g == 0)
-        __hip_atomic_store((uint64_t*)pm, pack2(mx, l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint32_t arrived = 0;
-    if (lane == 0)
-      arrived = __hip_atomic_fetch_add(&a.counters[gid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (lane == 0) s_last = arrived == ns - 1 ? 1u : 0u;
-  }
-  if (!fused) return;
-  __syncthreads();
-  if (s_last == 0) return;
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&a.counters[gid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-  // Last arrival. Wave w reduces output fragments w, w + 4, ... over every split. Plain loads are
-  // coherent here: the kernel-start acquire invalidated every L2, the writers stored through to
-  // memory before counting, and each partial line is read by this workgroup only, so no L2 holds
-  // a stale copy. Each batch of splits is loaded in one round trip (indices clamped, weight 0
-  // past the last split).
-  constexpr int kF = kNv >= kDecodeWaves ? kNv / kDecodeWaves : 1;  // fragments per wave
-  constexpr int kS = kMaxSplits / kF < kMaxSplits ? kMaxSplits / kF : kMaxSplits;  // batch
-  if (wave >= kNv || !head_ok) return;
+  const bool reducer = fused && s_ticket == ns - 1;
+  if (reducer && threadIdx.x == 0)  // every ticket of this launch is taken: reset for the next
+    __hip_atomic_store(&counters[gid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint64_t item0 = item - split;
-  float2 ml[kMaxSplits];
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp)
-    ml[sp] = *(const float2*)(a.part_ml + ((item0 + min((uint32_t)sp, ns - 1)) * 16 + c16) * 2);
-  float4_t x0[kS][kF];
-#pragma unroll
-  for (int sp = 0; sp < kS; ++sp) {
-    const float* ps = a.part_acc + ((item0 + min((uint32_t)sp, ns - 1)) * 16 + c16) * DV;
-#pragma unroll
-    for (int f = 0; f < kF; ++f) x0[sp][f] = *(const float4_t*)(ps + 16 * (wave + kDecodeWaves * f) + 4 * g);
+  float* o_grp = out + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DV;
+  if (reducer) {
+    if (ns <= 5) reduce_group<4, 4, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    else if (ns <= 9) reduce_group<8, 2, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    else if (ns <= 17) reduce_group<16, 1, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    else reduce_group<32, 1, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    return;
   }
-  float gm = -INFINITY;
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) gm = (uint32_t)sp < ns ? fmaxf(gm, ml[sp].x) : gm;
-  const float gmu = gm == -INFINITY ? 0.0f : gm;
-  float gl = 0.0f;
-  float wsp[kMaxSplits];
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) {
-    wsp[sp] = (uint32_t)sp < ns ? exp2f(ml[sp].x - gmu) : 0.0f;
-    gl += ml[sp].y * wsp[sp];
-  }
-  float4_t gacc[kF];
-#pragma unroll
-  for (int f = 0; f < kF; ++f) gacc[f] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int sp = 0; sp < kS; ++sp)
-#pragma unroll
-    for (int f = 0; f < kF; ++f) gacc[f] += x0[sp][f] * wsp[sp];
-#pragma unroll
-  for (int b = 1; b < kMaxSplits / kS; ++b) {
-    if ((uint32_t)(b * kS) < ns) {
-      float4_t x[kS][kF];
-#pragma unroll
-      for (int u = 0; u < kS; ++u) {
-        const float* ps = a.part_acc + ((item0 + min((uint32_t)(b * kS + u), ns - 1)) * 16 + c16) * DV;
-#pragma unroll
-        for (int f = 0; f < kF; ++f) x[u][f] = *(const float4_t*)(ps + 16 * (wave + kDecodeWaves * f) + 4 * g);
+  for (uint32_t j = threadIdx.x; j < nreal * DV; j += 64 * kW) {
+    const uint32_t hs = j / DV, e = j % DV;
+    float mx, lw, aw;
+    wave_partial<DV>(s_acc, s_ml, hs, e, mx, lw, aw);
+    if (ns == 1) {
+      if (!(lw > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
+      o_grp[j] = aw * (1.0f / lw);
+    } else if (!fused) {  // reduce_kernel combines the splits after this launch
+      part_acc[((uint64_t)item * 16 + hs) * DV + e] = aw;
+      if (e == 0) {
+        part_ml[((uint64_t)item * 16 + hs) * 2] = mx;
+        part_ml[((uint64_t)item * 16 + hs) * 2 + 1] = lw;
       }
-#pragma unroll
-      for (int u = 0; u < kS; ++u)
-#pragma unroll
-        for (int f = 0; f < kF; ++f) gacc[f] += x[u][f] * wsp[b * kS + u];
+    } else {
+      uint64_t* pt = part_tag + ((uint64_t)item * 16 + hs) * (DV + 2);
+      __hip_atomic_store(pt + e, tagged(aw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (e == 0) {
+        __hip_atomic_store(pt + DV, tagged(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pt + DV + 1, tagged(lw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
-  if (gl == 0.0f && g == 0 && wave == 0) atomicOr(a.err, 1);
-  const float inv = 1.0f / gl;
-#pragma unroll
-  for (int f = 0; f < kF; ++f) *(float4_t*)(o + 16 * (wave + kDecodeWaves * f) + 4 * g) = gacc[f] * inv;
 }
 
 // ================================================================ kernel 4: cross-split reduce
@@ -656,11 +886,11 @@ __global__ __launch_bounds__(64) void reduce_kernel(const DecodeArgs a) {
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
     const float w = (uint32_t)s < ns ? exp2f(m[s] - mu) : 0.0f;
-    l += lw[s] * w;
+    l = fmaf(lw[s], w, l);
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) sum[j] += x[s][j] * w;
+    for (int j = 0; j < kJ; ++j) sum[j] = fmaf(x[s][j], w, sum[j]);
   }
-  if (l == 0.0f && lane == 0) atomicOr(a.err, 1);
+  if (!(l > 0.0f) && lane == 0) atomicOr(a.err, 1);  // all -inf, or a NaN / +inf score
   const float inv = 1.0f / l;
   float* o = a.out + ((uint64_t)row * a.num_heads + head) * DV;
 #pragma unroll
@@ -691,7 +921,7 @@ bool decode_supported(bool f16, int dk, int dv) {
 
 template <typename KV>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
-  const dim3 grid(a.total_items), block(64 * kDecodeWaves);
+  const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * kDecodeWaves);
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
@@ -725,10 +955,6 @@ hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStrea
 // the eight scores a lane holds for kv half b are exactly the slots a V^T operand finds at
 // positions 16b+8h .. 16b+8h+7 of a perm32-ordered V block, so exponentiated scores feed the PV
 // MFMA from registers and each V^T operand is one 16-byte LDS read.
-// The prefill kernel is written with lambdas over shared state; every one must inline, or the
-// captured state (accumulators included) would be spilled to scratch memory.
-#define JMA_INL __attribute__((always_inline))
-
 namespace pf {
 
 __device__ __forceinline__ uint32_t swap34(uint32_t i) {

@@ -86,6 +86,13 @@ struct DeviceBuffer {
   }
 };
 
+// Grows `buf` to `need` bytes; a new allocation is zero-filled.
+void reserve_zeroed(DeviceBuffer& buf, size_t need, hipStream_t stream) {
+  if (need <= buf.bytes) return;
+  buf.reserve(need, stream);
+  hip_check(hipMemsetAsync(buf.ptr, 0, buf.bytes, stream), "zero scratch");
+}
+
 int env_int(const char* name, int fallback) {
   const char* v = std::getenv(name);
   if (!v || !*v) return fallback;
@@ -98,7 +105,7 @@ struct jmodels_attn_context {
   int device = 0;
   hipStream_t stream = nullptr;
   int* d_err = nullptr;
-  DeviceBuffer part_acc, part_ml, counters, qrot, stage_q, stage_k, stage_v, stage_out;
+  DeviceBuffer part_acc, part_ml, part_tag, counters, qrot, stage_q, stage_k, stage_v, stage_out;
   int decode_target_blocks = 256;   // workgroups a decode launch aims for (256 CUs)
   int tiles_per_wave = 2;           // minimum tiles each decode wave streams
   bool unfused = false;             // JMA_UNFUSED=1: separate append and reduce kernels
@@ -345,6 +352,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   a.num_heads = lc.num_heads;
   a.group = lc.group;
   a.hgroups = (lc.group + 15) / 16;
+  a.num_kv_heads = kv->hkv;
   a.window = lc.window;
   a.rows = rows;
   a.k_new = fa.k;
@@ -379,27 +387,26 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.nsplit[i] = (uint32_t)((ntiles[i] + tps - 1) / tps);
     any_split |= a.nsplit[i] > 1;
     uniform &= a.nsplit[i] == a.nsplit[0];
+    a.max_splits = std::max(a.max_splits, a.nsplit[i]);
     items += a.nsplit[i] * kv->hkv * a.hgroups;
   }
   a.item_start[rows.count] = items;
   a.total_items = items;
   a.ns_uniform = uniform ? a.nsplit[0] : 0u;
-  if (any_split) {
+  if (any_split && ctx->unfused) {
     ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream);
     ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream);
     a.part_acc = (float*)ctx->part_acc.ptr;
     a.part_ml = (float*)ctx->part_ml.ptr;
-    if (!ctx->unfused) {
-      // Arrival counters start at zero and the reducing workgroup resets its own, so they are
-      // zeroed only when (re)allocated, never inside a launch sequence a caller may capture.
-      const size_t need = (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t);
-      if (need > ctx->counters.bytes) {
-        ctx->counters.reserve(need, ctx->stream);
-        hip_check(hipMemsetAsync(ctx->counters.ptr, 0, ctx->counters.bytes, ctx->stream),
-                  "zero counters");
-      }
-      a.counters = (uint32_t*)ctx->counters.ptr;
-    }
+  } else if (any_split) {
+    // Arrival tickets start at zero and every tagged partial word starts clear; the reducing
+    // workgroups restore both, so they are zeroed only when (re)allocated, never inside a launch
+    // sequence a caller may capture.
+    reserve_zeroed(ctx->part_tag, (size_t)items * 16 * (kv->dv + 2) * sizeof(uint64_t), ctx->stream);
+    reserve_zeroed(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t),
+                   ctx->stream);
+    a.part_tag = (uint64_t*)ctx->part_tag.ptr;
+    a.counters = (uint32_t*)ctx->counters.ptr;
   }
   hip_check(jma::launch_decode(a, kv->f16(), kv->dk, kv->dv, ctx->stream), "decode launch");
   if (any_split && a.counters == nullptr)
@@ -553,6 +560,12 @@ int32_t collect_errors(jmodels_attn_context* ctx) {
   if (err != 0) {
     int zero = 0;
     hip_check(hipMemcpy(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "reset error word");
+    if (err & 2) {
+      // A reducer gave up waiting: tickets and tagged partials may be left set; clear them.
+      for (DeviceBuffer* b : {&ctx->part_tag, &ctx->counters})
+        if (b->ptr) hip_check(hipMemset(b->ptr, 0, b->bytes), "reset reduction scratch");
+      fail(JMODELS_ATTN_DEVICE_ERROR, "cross-split reduction timed out waiting for a partial");
+    }
     fail(JMODELS_ATTN_NON_FINITE, "softmax input contains NaN or positive infinity");
   }
   return JMODELS_ATTN_OK;
@@ -636,7 +649,7 @@ int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx) {
   return guard([&] {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->counters, &ctx->qrot, &ctx->stage_q,
+    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_tag, &ctx->counters, &ctx->qrot, &ctx->stage_q,
                             &ctx->stage_k, &ctx->stage_v, &ctx->stage_out})
       b->release();
     (void)hipFree(ctx->d_err);
