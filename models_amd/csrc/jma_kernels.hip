@@ -323,6 +323,8 @@ __device__ __forceinline__ void wave_partial(const float (*s_acc)[16][DV], const
 // word and the head's (m, l) words, reloads whatever tag is still clear until every tag is set,
 // combines all splits in split order (its own at index `split`), stores the output and clears the
 // element words. The (m, l) words, read by every thread of a head, are cleared after a barrier.
+// The split weights use the hardware exp2 (v_exp_f32) for every split, this workgroup's own
+// included, so the weights do not depend on which workgroup reduces.
 template <int B, int kE, int DV>
 __device__ __forceinline__ void reduce_group(uint64_t* part, uint64_t item0, uint32_t ns,
                                              uint32_t split, uint32_t nreal,
@@ -386,19 +388,19 @@ __device__ __forceinline__ void reduce_group(uint64_t* part, uint64_t item0, uin
       for (int s = 0; s < B; ++s) {
         if (!own && (uint32_t)s == split) {
           own = true;
-          const float f = exp2f(mx - gmu);
+          const float f = __builtin_amdgcn_exp2f(mx - gmu);
           gl = fmaf(lo, f, gl);
           ga = fmaf(ao, f, ga);
         }
         if ((uint32_t)s < ns - 1) {
-          const float f = exp2f(__uint_as_float((uint32_t)mv[u][s]) - gmu);
+          const float f = __builtin_amdgcn_exp2f(__uint_as_float((uint32_t)mv[u][s]) - gmu);
           gl = fmaf(__uint_as_float((uint32_t)lv[u][s]), f, gl);
           ga = fmaf(__uint_as_float((uint32_t)xv[u][s]), f, ga);
           clear_word(words(s, hs) + e);
         }
       }
       if (!own) {
-        const float f = exp2f(mx - gmu);
+        const float f = __builtin_amdgcn_exp2f(mx - gmu);
         gl = fmaf(lo, f, gl);
         ga = fmaf(ao, f, ga);
       }
@@ -440,7 +442,7 @@ __device__ __forceinline__ void reduce_group(uint64_t* part, uint64_t item0, uin
 //    their partial (m, l, acc) as tagged 64-bit words {value, 1} and exit without waiting; the
 //    reducer reads them back with device-coherent loads, reloading until every tag is set, then
 //    clears what it read (tag 0), so every partial word is clear again when the launch ends.
-template <typename KV, int DK, int DV>
+template <typename KV, int DK, int DV, bool kSimple>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
   using TileT = Tile<KV, DK, DV>;
@@ -460,21 +462,18 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   // The grid is (split, kv head * head groups + head group, row). Every scalar argument the
   // kernel uses, the row's own table entries included, is fetched in one batch: left to itself
   // the compiler loads each right before its use, behind its own wait, and a scalar load costs
-  // about half a vector memory round trip here.
+  // about half a vector memory round trip here. kSimple (contiguous rows of one sequence, equal
+  // split counts, one head group, a LINEAR layer) takes its cache base from the host and needs
+  // almost no address arithmetic before the first tile load.
   const uint32_t split = blockIdx.x, rest = blockIdx.y, row = blockIdx.z;
   uint32_t num_heads = a.num_heads, group = a.group, hgroups = a.hgroups, hkv = a.num_kv_heads;
   uint32_t ns_uniform = a.ns_uniform, rows_contig = a.rows.contiguous;
-  uint32_t r_seq = a.rows.seq[row], r_pos = a.rows.pos[row], r_ns = a.nsplit[row],
-           r_item0 = a.item_start[row];
   uint32_t rows_seq0 = a.rows.seq0, rows_start = a.rows.start;
   uint32_t window = a.window, tps = a.tiles_per_split, cap = a.kv.cap, ring = a.kv.ring;
   uint32_t pairs = a.pairs, neox = a.neox, rope_q = a.rope_q;
   float qscale = a.qscale;
-  uint64_t seq_stride_k = a.kv.seq_stride_k, seq_stride_v = a.kv.seq_stride_v;
-  uint64_t layer_off_k = a.kv.layer_off_k, layer_off_v = a.kv.layer_off_v;
   // Pointers go through the asm typed as global memory so the loads through them stay global
   // (a generic pointer would turn them into flat loads, which also count against lgkmcnt).
-  JMA_GLOBAL const KV *g_k = (JMA_GLOBAL const KV*)a.kv.k, *g_v = (JMA_GLOBAL const KV*)a.kv.v;
   JMA_GLOBAL const float *g_q = (JMA_GLOBAL const float*)a.q;
   JMA_GLOBAL const float *g_cos = (JMA_GLOBAL const float*)a.cos_t;
   JMA_GLOBAL const float *g_sin = (JMA_GLOBAL const float*)a.sin_t;
@@ -486,14 +485,50 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   JMA_GLOBAL float* g_pacc = (JMA_GLOBAL float*)a.part_acc;
   JMA_GLOBAL float* g_pml = (JMA_GLOBAL float*)a.part_ml;
   JMA_GLOBAL int* g_err = (JMA_GLOBAL int*)a.err;
-  asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hgroups), "+s"(hkv), "+s"(ns_uniform),
-               "+s"(rows_contig), "+s"(r_seq), "+s"(r_pos), "+s"(r_ns), "+s"(r_item0),
-               "+s"(rows_seq0), "+s"(rows_start), "+s"(window), "+s"(tps), "+s"(cap), "+s"(ring),
-               "+s"(pairs), "+s"(neox), "+s"(rope_q), "+s"(qscale),
-               "+s"(seq_stride_k), "+s"(seq_stride_v), "+s"(layer_off_k), "+s"(layer_off_v));
-  asm volatile("" : "+s"(g_k), "+s"(g_v), "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn),
-               "+s"(g_ctr), "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
-  const KV *kv_k = (const KV*)g_k, *kv_v = (const KV*)g_v;
+  uint32_t ns, item, hg, kvh, seq, pos;
+  KV *kb, *vb;
+  if constexpr (kSimple) {
+    JMA_GLOBAL KV* g_kb = (JMA_GLOBAL KV*)a.k_base;
+    JMA_GLOBAL KV* g_vb = (JMA_GLOBAL KV*)a.v_base;
+    asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hkv), "+s"(ns_uniform), "+s"(rows_start),
+                 "+s"(window), "+s"(tps), "+s"(cap), "+s"(pairs), "+s"(neox), "+s"(rope_q),
+                 "+s"(qscale), "+s"(g_kb), "+s"(g_vb));
+    asm volatile("" : "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn), "+s"(g_ctr),
+                 "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
+    ns = ns_uniform;
+    hg = 0;
+    kvh = rest;
+    item = (row * hkv + kvh) * ns + split;
+    seq = 0;
+    pos = rows_start + row;
+    ring = 0;
+    hgroups = 1;
+    kb = (KV*)g_kb + (uint64_t)kvh * cap * DK;
+    vb = (KV*)g_vb + (uint64_t)kvh * cap * DV;
+  } else {
+    uint32_t r_seq = a.rows.seq[row], r_pos = a.rows.pos[row], r_ns = a.nsplit[row],
+             r_item0 = a.item_start[row];
+    uint64_t seq_stride_k = a.kv.seq_stride_k, seq_stride_v = a.kv.seq_stride_v;
+    uint64_t layer_off_k = a.kv.layer_off_k, layer_off_v = a.kv.layer_off_v;
+    JMA_GLOBAL KV *g_k = (JMA_GLOBAL KV*)a.kv.k, *g_v = (JMA_GLOBAL KV*)a.kv.v;
+    asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hgroups), "+s"(hkv), "+s"(ns_uniform),
+                 "+s"(rows_contig), "+s"(r_seq), "+s"(r_pos), "+s"(r_ns), "+s"(r_item0),
+                 "+s"(rows_seq0), "+s"(rows_start), "+s"(window), "+s"(tps), "+s"(cap), "+s"(ring),
+                 "+s"(pairs), "+s"(neox), "+s"(rope_q), "+s"(qscale),
+                 "+s"(seq_stride_k), "+s"(seq_stride_v), "+s"(layer_off_k), "+s"(layer_off_v));
+    asm volatile("" : "+s"(g_k), "+s"(g_v), "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn),
+                 "+s"(g_vn), "+s"(g_ctr), "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml),
+                 "+s"(g_err));
+    ns = ns_uniform ? ns_uniform : r_ns;
+    if (split >= ns) return;  // a listed row with fewer splits than the grid's widest row
+    item = ns_uniform ? (row * hkv * hgroups + rest) * ns + split : r_item0 + rest * ns + split;
+    hg = hgroups == 1 ? 0u : rest % hgroups;
+    kvh = hgroups == 1 ? rest : rest / hgroups;
+    seq = rows_contig ? rows_seq0 : r_seq;
+    pos = rows_contig ? rows_start + row : r_pos;
+    kb = (KV*)g_k + seq * seq_stride_k + layer_off_k + (uint64_t)kvh * cap * DK;
+    vb = (KV*)g_v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV;
+  }
   const float *q_in = (const float*)g_q, *cos_t = (const float*)g_cos, *sin_t = (const float*)g_sin;
   const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
   uint32_t* counters = (uint32_t*)g_ctr;
@@ -503,11 +538,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   float* part_ml = (float*)g_pml;
   int* err = (int*)g_err;
 
-  const uint32_t ns = ns_uniform ? ns_uniform : r_ns;
-  if (split >= ns) return;  // a listed row with fewer splits than the grid's widest row
-  const uint32_t item = ns_uniform ? (row * hkv * hgroups + rest) * ns + split : r_item0 + rest * ns + split;
-  const uint32_t hg = hgroups == 1 ? 0u : rest % hgroups;
-  const uint32_t kvh = hgroups == 1 ? rest : rest / hgroups;
   const bool fused = ns > 1 && counters != nullptr;
   const uint64_t gid = ((uint64_t)row * hkv + kvh) * hgroups + hg;
   // Arrival ticket first: its round trip overlaps the tile loads.
@@ -515,8 +545,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   if (fused && threadIdx.x == 0)
     ticket = __hip_atomic_fetch_add(&counters[gid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  const uint32_t seq = rows_contig ? rows_seq0 : r_seq;
-  const uint32_t pos = rows_contig ? rows_start + row : r_pos;
   const uint32_t first = first_visible(pos, window);
   const uint32_t t_begin = first / kBlk, t_end = pos / kBlk + 1;
   const uint32_t s_t0 = t_begin + split * tps;
@@ -524,7 +552,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   // Ring layers: the split's first tile slot, then consecutive tiles wrap at most once (a
   // split spans fewer positions than the ring holds).
   uint32_t slot_base = s_t0 * kBlk;
-  if (ring) slot_base %= cap;
+  if (!kSimple && ring) slot_base %= cap;
 
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -535,11 +563,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const float* cs = cos_t ? cos_t + (uint64_t)pos * pairs : nullptr;
   const float* sn = cos_t ? sin_t + (uint64_t)pos * pairs : nullptr;
 
-  KV* kb = (KV*)kv_k + seq * seq_stride_k + layer_off_k + (uint64_t)kvh * cap * DK;
-  KV* vb = (KV*)kv_v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV;
   auto slot0_of = [&](uint32_t t) JMA_INL {
     const uint32_t x = slot_base + (t - s_t0) * kBlk;
-    return ring && x >= cap ? x - cap : x;
+    return !kSimple && ring && x >= cap ? x - cap : x;
   };
 
   // The first two tiles of this wave are in flight before anything else is loaded (at head
@@ -885,7 +911,7 @@ __global__ __launch_bounds__(64) void reduce_kernel(const DecodeArgs a) {
   for (int j = 0; j < kJ; ++j) sum[j] = 0.0f;
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
-    const float w = (uint32_t)s < ns ? exp2f(m[s] - mu) : 0.0f;
+    const float w = (uint32_t)s < ns ? __builtin_amdgcn_exp2f(m[s] - mu) : 0.0f;
     l = fmaf(lw[s], w, l);
 #pragma unroll
     for (int j = 0; j < kJ; ++j) sum[j] = fmaf(x[s][j], w, sum[j]);
@@ -919,20 +945,20 @@ bool decode_supported(bool f16, int dk, int dv) {
   return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256;
 }
 
-template <typename KV>
+template <typename KV, bool kSimple>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
   const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * kDecodeWaves);
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple>), grid, block, 0, stream, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32>), grid, block, 0, stream, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64>), grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128>), grid, block, 0, stream, a); break;
-    case 256: hipLaunchKernelGGL((decode_kernel<KV, 256, 256>), grid, block, 0, stream, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple>), grid, block, 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple>), grid, block, 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple>), grid, block, 0, stream, a); break;
+    case 256: hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple>), grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -941,7 +967,9 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
 hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStream_t stream) {
   if (!decode_supported(f16, dk, dv)) return hipErrorInvalidValue;
   if (a.total_items == 0) return hipSuccess;
-  return f16 ? launch_decode_t<_Float16>(a, dk, stream) : launch_decode_t<float>(a, dk, stream);
+  const bool simple = a.k_base != nullptr;
+  if (f16) return simple ? launch_decode_t<_Float16, true>(a, dk, stream) : launch_decode_t<_Float16, false>(a, dk, stream);
+  return simple ? launch_decode_t<float, true>(a, dk, stream) : launch_decode_t<float, false>(a, dk, stream);
 }
 
 // ================================================================ kernel 3: prefill (f16 MFMA)

@@ -393,6 +393,11 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   a.item_start[rows.count] = items;
   a.total_items = items;
   a.ns_uniform = uniform ? a.nsplit[0] : 0u;
+  if (uniform && rows.contiguous && a.hgroups == 1 && !a.kv.ring) {
+    const size_t es = kv->f16() ? 2 : 4;
+    a.k_base = (char*)a.kv.k + (a.kv.seq_stride_k * rows.seq0 + a.kv.layer_off_k) * es;
+    a.v_base = (char*)a.kv.v + (a.kv.seq_stride_v * rows.seq0 + a.kv.layer_off_v) * es;
+  }
   if (any_split && ctx->unfused) {
     ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream);
     ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream);
