@@ -1064,7 +1064,7 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   constexpr int kNC = D / 8;                     // 16-byte chunks per K row
   constexpr int kC = 4 * kNb;                    // float4 chunks of O^T held per lane
   constexpr int kArr = 2 * Q * kT;               // halves per LDS array: one K and one V stage
-  static_assert(Q == 1 || Q == 2, "the partial merge pairs at most two kv groups");
+  static_assert(Q == 1 || Q == 2 || Q == 4, "kv groups per stripe");
   // N stages: loads run N-1 steps ahead of use (every wave issues the same number of loads per
   // step, so the wait can count them). Three stages measured slower than two on C3-sized work
   // (more live registers for one more step of lookahead), so two are used.
@@ -1366,66 +1366,90 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
       if (k + decltype(pp)::value < steps) step(k + decltype(pp)::value, pp);
     });
 
-  // Merge the kv-group partials of each stripe in one LDS exchange: every wave posts (m, l) and
-  // the O^T chunks its partner finishes, then finishes its own half from registers.
+  // Merge the kv-group partials of each stripe in one LDS exchange: wave q of a stripe finishes
+  // the q-th of its O^T chunks. Every wave posts (m, l) and, for each other kv group r, the
+  // chunks wave r finishes; then it combines its own chunks (from registers) with the Q - 1
+  // posted ones, in kv-group order, weighted by exp2(m_r - M) / L.
   l = half_sum(l);
   mn = half_min(mn);
   // Every wave is done with the tile stages the exchange overwrites, and no load is in flight.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  float* const part = (float*)(wave < kWaves / 2 ? lx : ly) + (wave % (kWaves / 2)) * (kC / Q) * 256;
-  // O^T chunk c (c < kC) of this lane: dims 32(c/4) + 8(c%4) + 4h .. +3 of its column. The
-  // half a wave finishes is chosen by a wave-uniform branch so that o[] is indexed statically.
+  constexpr int kCQ = kC / Q;  // chunks one wave finishes
+  // Posted chunks of stripe s: [source group][destination slot][kCQ][64 lanes] float4, in lx for
+  // even stripes and ly for odd ones (each holds Q * (Q - 1) * kCQ KB <= one LDS array).
+  static_assert(Q * (Q - 1) * kCQ * 1024 <= kArr * 2 || Q == 1, "merge exchange exceeds an LDS array");
+  float* const xbase = (float*)((s & 1) ? ly : lx) + (s >> 1) * Q * (Q - 1) * kCQ * 256;
+  auto xslot = [&](int src, int dst) JMA_INL {  // where src posts the chunks dst finishes
+    return xbase + (src * (Q - 1) + (dst < src ? dst : dst - 1)) * kCQ * 256;
+  };
+  // O^T chunk c (c < kC) of this lane: dims 32(c/4) + 8(c%4) + 4h .. +3 of its column. The part a
+  // wave posts or finishes is chosen by a wave-uniform branch so that o[] is indexed statically.
   auto chunk = [&](auto cc) JMA_INL {
     constexpr int c = decltype(cc)::value;
     const float16_t& acc = o[c >> 2];
     return float4_t{acc[4 * (c & 3)], acc[4 * (c & 3) + 1], acc[4 * (c & 3) + 2],
                     acc[4 * (c & 3) + 3]};
   };
-  if constexpr (Q == 2) {
+  if constexpr (Q > 1) {
     if (h == 0) s_ml[wave][j] = float2{m, l};
-    auto post = [&](auto other) JMA_INL {
-      constexpr int base = decltype(other)::value * (kC / 2);
-      static_for<kC / 2>([&](auto idx) JMA_INL {
-        *(float4_t*)(part + idx.value * 256 + 4 * lane) =
-            chunk(std::integral_constant<int, base + decltype(idx)::value>{});
-      });
-    };
-    if (q == 0) post(std::integral_constant<int, 1>{});
-    else post(std::integral_constant<int, 0>{});
+    static_for<Q>([&](auto rr) JMA_INL {
+      constexpr int r = decltype(rr)::value;
+      if (r != q) {
+        float* const dst = xslot(q, r);
+        static_for<kCQ>([&](auto idx) JMA_INL {
+          *(float4_t*)(dst + idx.value * 256 + 4 * lane) =
+              chunk(std::integral_constant<int, r * kCQ + decltype(idx)::value>{});
+        });
+      }
+    });
   }
   __syncthreads();
-  float ws = 0.0f, wp = 0.0f, L = l;
-  const int partner = (1 - q) * S + s;
-  if constexpr (Q == 2) {
-    const float2 pm = s_ml[partner][j];
-    const float M = fmaxf(m, pm.x);
-    const float es = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-    const float ep = pm.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pm.x - M);
-    L = l * es + pm.y * ep;
-    if (L > 0.0f) {
-      ws = es / L;
-      wp = ep / L;
+  // Weights of the kv groups of this lane's column: exp2(m_r - M) / L.
+  float wr[Q];
+  float L = l;
+  if constexpr (Q > 1) {
+    float mr[Q], lr[Q];
+    float M = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < Q; ++r) {
+      const float2 v = r == q ? float2{m, l} : s_ml[r * S + s][j];
+      mr[r] = v.x;
+      lr[r] = v.y;
+      M = fmaxf(M, v.x);
     }
+    L = 0.0f;
+#pragma unroll
+    for (int r = 0; r < Q; ++r) {
+      wr[r] = mr[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr[r] - M);
+      L = fmaf(lr[r], wr[r], L);
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int r = 0; r < Q; ++r) wr[r] *= inv;
   } else {
-    if (L > 0.0f) ws = 1.0f / L;
+    wr[0] = L > 0.0f ? 1.0f / L : 0.0f;
   }
   const bool bad = col_ok && (mn == -INFINITY || !(L > 0.0f && L < INFINITY));
   if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
-  const float* const ppart = (const float*)(partner < kWaves / 2 ? lx : ly) +
-                             (partner % (kWaves / 2)) * (kC / Q) * 256;
   float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
-  auto finish = [&](auto own) JMA_INL {
-    constexpr int base = decltype(own)::value * (kC / Q);
-    static_for<kC / Q>([&](auto idx) JMA_INL {
-      constexpr int c = base + decltype(idx)::value;
-      float4_t v = chunk(std::integral_constant<int, c>{}) * ws;
-      if constexpr (Q == 2) v += *(const float4_t*)(ppart + idx.value * 256 + 4 * lane) * wp;
-      if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = v;
-    });
-  };
-  if (q == 0) finish(std::integral_constant<int, 0>{});
-  else if constexpr (Q == 2) finish(std::integral_constant<int, 1>{});
+  static_for<Q>([&](auto qq) JMA_INL {
+    constexpr int own = decltype(qq)::value;
+    if (own == q) {
+      static_for<kCQ>([&](auto idx) JMA_INL {
+        constexpr int c = own * kCQ + decltype(idx)::value;
+        float4_t v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < Q; ++r) {
+          const float4_t x = r == own ? chunk(std::integral_constant<int, c>{})
+                                      : *(const float4_t*)(xslot(r, own) + idx.value * 256 + 4 * lane);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = fmaf(x[i], wr[r], v[i]);
+        }
+        if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = v;
+      });
+    }
+  });
 }
 
 bool prefill_supported(int dk, int dv) {
