@@ -10,8 +10,9 @@ before timing; each token's 32 launches are replayed from a HIP graph captured o
 Printed: one JSON line with
   value      decode attention HBM GB/s: algorithmic KV bytes (2 * L * Hkv * d * 2 B per
              layer-step, L = visible positions) / wall time of the timed steps
-  roofline   the split-K decode kernel's own duration (HIP events around each launch on the
-             context stream) against 8 TB/s
+  roofline   the decode kernel (the only kernel of the timed region): algorithmic bytes per launch
+             over its average duration from HIP events bracketing the timed replays on the
+             context stream, against 8 TB/s
   cpu_baseline  the CPU oracle (C restatement of backend-java's loop) on a bounded sample,
              1 core, in the same unit
 and, as extra fields, us/token and the C3 prefill (S 2048, 24/8 heads, d 128) TFLOP/s.
@@ -33,6 +34,11 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix
+# HBM bytes per decode launch on C2 measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# (bench.py --no-cpu --no-prefill --steps 8 --warmup 2), each scaled by what the counter reads
+# for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4487.5 KiB x 2.0 + 620.5 KiB. Recorded with
+# its commands in profiles/decode_c2.md; counters cannot be read from inside this process.
+DECODE_TRAFFIC_BYTES = round((4487.5 * 2.0 + 620.5) * 1024)
 
 
 def log(msg: str) -> None:
@@ -102,11 +108,18 @@ def run_c2(hip, A, rt, synth, steps: int, warmup: int):
     kv.discard_from(prior)
 
     rt.device_synchronize()
+    # HIP events on the context stream bracket the timed replays: every kernel in them is the
+    # fused decode kernel (one per layer-step), so their span over the launch count is the
+    # kernel's average duration back to back (launch gaps included).
+    ev0, ev1 = rt.Event(), rt.Event()
     t = time.perf_counter()
+    ev0.record(stream)
     for s in range(steps):
         graphs[s].launch()
+    ev1.record(stream)
     rt.device_synchronize()
     elapsed = time.perf_counter() - t
+    timed_kernel_ms = ev0.elapsed_ms(ev1) / (steps * layers)
     hip.synchronize()
     replay_out = dout.download()
     eager_out = eager_out.reshape(layers, total_steps, qd)[:, :steps]
@@ -120,8 +133,8 @@ def run_c2(hip, A, rt, synth, steps: int, warmup: int):
         token(s)
     hip.synchronize()
 
-    # Roofline of the split-K decode kernel: HIP events around each attention launch on the
-    # context stream, at the last decoded position (cache resident through it).
+    # For reference: the kernel in isolation (HIP events around each attention launch at the last
+    # decoded position; each pair adds the events' own overhead).
     p_last = prior + steps - 1
     q_last = [dq.at((l * total_steps + steps - 1) * qd) for l in range(layers)]
     for l in range(layers):  # warm
@@ -154,6 +167,7 @@ def run_c2(hip, A, rt, synth, steps: int, warmup: int):
     rope.close()
     return dict(
         elapsed=elapsed, algo_bytes=algo_bytes, eager_us_per_token=eager_us_per_token,
+        timed_kernel_ms=timed_kernel_ms, launches=steps * layers,
         kernel_ms=kernel_ms, kernel_ms_min=float(np.min(durations)), kernel_bytes=kernel_bytes,
         cpu_material=(keys, values, q_host, p_last, hq, hkv, d, theta))
 
@@ -174,13 +188,14 @@ def run_c3(hip, A, rt, synth, reps: int = 10):
                      dk.count, dv.ptr, dv.count, dqr.ptr, dqr.count)
     kv.attend_causal_device(layer, 0, 0, S, dqr.ptr, dqr.count, dout.ptr, dout.count)
     hip.synchronize()
-    events = [(rt.Event(), rt.Event()) for _ in range(reps)]
-    for e0, e1 in events:
-        e0.record(stream)
+    # HIP events bracket `reps` back-to-back launches on the context stream.
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(stream)
+    for _ in range(reps):
         kv.attend_causal_device(layer, 0, 0, S, dqr.ptr, dqr.count, dout.ptr, dout.count)
-        e1.record(stream)
+    e1.record(stream)
     hip.synchronize()
-    ms = float(np.mean([e0.elapsed_ms(e1) for e0, e1 in events]))
+    ms = e0.elapsed_ms(e1) / reps
     flops = 2 * hq * d * S * (S + 1)
     for buf in (dq, dk, dv, dqr, dout):
         buf.free()
@@ -254,7 +269,8 @@ def main() -> int:
         return 0
     c2 = run_c2(hip, A, rt, synth, args.steps, args.warmup)
     log(f"C2: {args.steps} steps in {c2['elapsed'] * 1e3:.2f} ms; decode kernel "
-        f"{c2['kernel_ms'] * 1e3:.2f} us avg")
+        f"{c2['timed_kernel_ms'] * 1e3:.2f} us per launch in the timed replays, "
+        f"{c2['kernel_ms'] * 1e3:.2f} us isolated")
     c3 = None
     if not args.no_prefill:
         c3 = run_c3(hip, A, rt, synth)
@@ -262,7 +278,8 @@ def main() -> int:
     hip.close()
 
     value = c2["algo_bytes"] / c2["elapsed"] / 1e9
-    achieved = c2["kernel_bytes"] / (c2["kernel_ms"] * 1e-3) / 1e9
+    # Algorithmic bytes of an average launch of the timed region over its event-timed duration.
+    achieved = c2["algo_bytes"] / c2["launches"] / (c2["timed_kernel_ms"] * 1e-3) / 1e9
     result = {
         "metric": "decode attn HBM GB/s + us/token @4k ctx; prefill attn TFLOP/s @2k",
         "value": round(value, 2),
@@ -291,11 +308,15 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_kernel<f16,64,64> (split-K + fused cross-split reduce)",
-            "kernel_us": round(c2["kernel_ms"] * 1e3, 3),
-            "kernel_us_min": round(c2["kernel_ms_min"] * 1e3, 3),
-            "bytes_per_launch": c2["kernel_bytes"],
+            "traffic": DECODE_TRAFFIC_BYTES,
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "kernel": "decode_kernel<f16,64,64> (RoPE + append + split-K + fused cross-split reduce)",
+            "kernel_us": round(c2["timed_kernel_ms"] * 1e3, 3),
+            "kernel_us_source": "HIP events over the timed graph replays / launches",
+            "bytes_per_launch": round(c2["algo_bytes"] / c2["launches"]),
+            "kernel_us_isolated": round(c2["kernel_ms"] * 1e3, 3),
+            "kernel_us_isolated_min": round(c2["kernel_ms_min"] * 1e3, 3),
+            "bytes_per_isolated_launch": c2["kernel_bytes"],
         },
     }
     if c3 is not None:
