@@ -10,8 +10,10 @@ namespace jma {
 // Rows handled by one launch when their (sequence, position) pairs are passed as kernel
 // arguments; larger batches are split into several launches by the runtime.
 constexpr int kMaxRows = 128;
-// Waves per decode workgroup: the waves of one workgroup share a split and combine in LDS.
-constexpr int kDecodeWaves = 4;
+// Waves per decode workgroup at head dimension dk: the waves of one workgroup share a split and
+// combine in LDS. Two waves per SIMD hide each other's instruction latency; at dk = 256 two tile
+// buffers take half the register file, so one wave per SIMD.
+constexpr int decode_waves(int dk) { return dk >= 256 ? 4 : 8; }
 // Most splits one decode row may be cut into; the cross-split reduction loads them all at once.
 constexpr int kMaxSplits = 32;
 
@@ -61,8 +63,8 @@ struct DecodeArgs {
   float* out;           // [count][num_heads * dv]
   float* part_acc;      // [items][16][dv]
   float* part_ml;       // [items][16][2]  (running max in log2 units, sum)
-  uint64_t* part_tag;   // [items][16][dv + 2] tagged words {f32 value, u32 tag} (acc, m, l) of the
-                        // fused reduction; every tag is clear between launches
+  float* part_f;        // [items][16][dv + 4] partials of the fused reduction (acc, m, l, 2 pad);
+                        // every word holds 0xFFFFFFFF (not written) between launches
   uint32_t* counters;   // [rows][kv heads][head groups] arrival tickets, zero between launches;
                         // null = reduce_kernel combines the splits
   const float* k_new;   // [count][num_kv_heads * dk] raw keys to rotate and append; null = none

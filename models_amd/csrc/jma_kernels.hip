@@ -274,151 +274,194 @@ __device__ __forceinline__ void rope_chunk(const float* __restrict__ x, uint32_t
   }
 }
 
-__device__ __forceinline__ uint64_t tagged(float x) {
-  return (uint64_t)__float_as_uint(x) | ((uint64_t)1u << 32);
+// Fused cross-split exchange. Partials live in a float buffer, per (item, head slot) dv acc
+// values then m, l and two pad words, where every word not yet written this launch holds
+// kClear (0xFFFFFFFF, a NaN bit pattern no arithmetic produces once NaNs are canonicalised):
+// each 32-bit word is atomic by itself, so producers and the reducer move them with 16-byte
+// device-coherent (sc1) buffer accesses and test every word.
+constexpr uint32_t kClear = 0xFFFFFFFFu;
+constexpr int kCoherent = 16;  // buffer cache policy bit sc1: coherent across the device's L2s
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, 0x7FFFFFF0, 0x00020000);
 }
 
-__device__ __forceinline__ bool tag_set(uint64_t w) { return (w >> 32) != 0; }
+// The buffer load intrinsic reads memory without side effects, so a reload of an unchanged
+// address looks redundant to the compiler; every poll iteration starts with a compiler memory
+// barrier (no instruction) so the reloads stay in the loop.
+__device__ __forceinline__ void poll_barrier() { asm volatile("" ::: "memory"); }
+
+__device__ __forceinline__ float4_t load_part(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCoherent);
+}
+
+__device__ __forceinline__ void store_part(__amdgpu_buffer_rsrc_t rs, uint32_t off, float4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kCoherent);
+}
+
+__device__ __forceinline__ float canon(float x) {  // any NaN -> the default quiet NaN
+  return x != x ? __uint_as_float(0x7FC00000u) : x;
+}
+
+__device__ __forceinline__ bool written(float4_t v) {
+  return __float_as_uint(v[0]) != kClear && __float_as_uint(v[1]) != kClear &&
+         __float_as_uint(v[2]) != kClear && __float_as_uint(v[3]) != kClear;
+}
+
+__device__ __forceinline__ float4_t clear4() {
+  const float c = __uint_as_float(kClear);
+  return float4_t{c, c, c, c};
+}
 
 // Polls of one reducer before it gives up and reports a reduction timeout (error bit 1). Each
 // poll waits one memory round trip, so this bounds the wait at seconds; it is reached only if a
 // producer of the group never stores, which the ticket order rules out.
 constexpr uint32_t kSpinLimit = 1u << 22;
 
-__device__ __forceinline__ uint64_t poll_word(uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void clear_word(uint64_t* p) {
-  __hip_atomic_store(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// One workgroup's partial for output element (head slot hs, element e): its waves' states
+// One workgroup's partial for output elements e .. e+3 of head slot hs: its waves' states
 // (s_ml, s_acc) rescaled to their common maximum and summed in wave order. Every multiply-add is
 // an explicit fmaf, so the reducer (which keeps its own partial) and a producer (which stores it)
 // compute the same bits and the result does not depend on which workgroup reduces.
-template <int DV>
+template <int DV, int W>
 __device__ __forceinline__ void wave_partial(const float (*s_acc)[16][DV], const float (*s_ml)[16][2],
                                              uint32_t hs, uint32_t e, float& mx, float& lw,
-                                             float& aw) {
+                                             float4_t& aw) {
   mx = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kDecodeWaves; ++w) mx = fmaxf(mx, s_ml[w][hs][0]);
+  for (int w = 0; w < W; ++w) mx = fmaxf(mx, s_ml[w][hs][0]);
   const float mu = mx == -INFINITY ? 0.0f : mx;
   lw = 0.0f;
-  aw = 0.0f;
+  aw = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int w = 0; w < kDecodeWaves; ++w) {
+  for (int w = 0; w < W; ++w) {
     const float f = exp2f(s_ml[w][hs][0] - mu);
     lw = fmaf(s_ml[w][hs][1], f, lw);
-    aw = fmaf(s_acc[w][hs][e], f, aw);
+    const float4_t x = *(const float4_t*)&s_acc[w][hs][e];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aw[i] = fmaf(x[i], f, aw[i]);
   }
 }
 
-// The reducer's side of the fused cross-split reduction of one group (row, kv head, head group)
-// whose ns partials start at item0; this workgroup is split `split`, and its own per-wave state
-// is in s_acc / s_ml. Partial words per (item, head slot): dv acc elements, then m, then l.
-// Output elements go in passes of kE per thread (element j = head slot * dv + e): a pass loads,
-// for each of the other B >= ns - 1 splits (indices past the last clamped to it), the element
-// word and the head's (m, l) words, reloads whatever tag is still clear until every tag is set,
-// combines all splits in split order (its own at index `split`), stores the output and clears the
-// element words. The (m, l) words, read by every thread of a head, are cleared after a barrier.
-// The split weights use the hardware exp2 (v_exp_f32) for every split, this workgroup's own
-// included, so the weights do not depend on which workgroup reduces.
-template <int B, int kE, int DV>
-__device__ __forceinline__ void reduce_group(uint64_t* part, uint64_t item0, uint32_t ns,
+// The reducer's side of the exchange for one group (row, kv head, head group) whose ns <= B
+// partials start at item0; this workgroup is split `split`, its own per-wave state in s_acc /
+// s_ml. Output quads (4 elements) are taken by SUB consecutive threads each; sub-thread r takes
+// the splits r, r + SUB, ... and loads their acc quad and (m, l) word, reloading until no word
+// reads kClear (its own split comes from its waves, computed while the loads are in flight).
+// The maximum M, the sum L of l * 2^(m - M) and the weighted acc sum are formed per thread in
+// split order and meet across the SUB threads in a fixed shuffle tree, so the result does not
+// depend on which workgroup reduces. Every word read is set back to kClear; the (m, l) words,
+// read by all quads of a head, after a barrier.
+template <int B, int SUB, int DV, int W>
+__device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32_t ns,
                                              uint32_t split, uint32_t nreal,
                                              const float (*s_acc)[16][DV],
                                              const float (*s_ml)[16][2], float* out, int* err) {
-  constexpr uint32_t kT = 64 * kDecodeWaves;
+  constexpr uint32_t kT = 64 * W;
+  constexpr uint32_t kQ4 = DV / 4;   // quads per head
+  constexpr int kI = B / SUB;        // splits one thread takes
+  static_assert(SUB == 1 || SUB == 2 || SUB == 4 || SUB == 8, "sub-threads per quad");
+  static_assert(kI <= 8, "splits per thread");
   const uint32_t tid = threadIdx.x;
-  const uint32_t E = nreal * DV;
-  auto words = [&](uint32_t o, uint32_t hs) JMA_INL {
-    return part + ((item0 + o + (o >= split ? 1u : 0u)) * 16 + hs) * (DV + 2);
+  const uint32_t E4 = nreal * kQ4;
+  const __amdgpu_buffer_rsrc_t rs = part_rsrc(part);
+  auto base = [&](uint32_t g, uint32_t hs) JMA_INL {  // byte offset of (split g, head slot hs)
+    return (uint32_t)(((item0 + g) * 16 + hs) * (DV + 4) * 4);
   };
+  const uint32_t r = tid % SUB;
   bool timed_out = false;
-  for (uint32_t j0 = 0; j0 < E; j0 += kT * kE) {
-    uint64_t xv[kE][B], mv[kE][B], lv[kE][B];
-    auto load = [&](int u, int s) JMA_INL {
-      const uint32_t j = min(j0 + tid + kT * u, E - 1);
-      uint64_t* w = words(min((uint32_t)s, ns - 2), j / DV);
-      xv[u][s] = poll_word(w + j % DV);
-      mv[u][s] = poll_word(w + DV);
-      lv[u][s] = poll_word(w + DV + 1);
+  for (uint32_t q0 = 0; q0 < E4; q0 += kT / SUB) {
+    const uint32_t quad = q0 + tid / SUB;
+    const bool qok = quad < E4;
+    const uint32_t hs = qok ? quad / kQ4 : 0u, e = qok ? (quad % kQ4) * 4 : 0u;
+    auto needed = [&](int i) JMA_INL {
+      const uint32_t g = r + SUB * i;
+      return qok && g < ns && g != split;
     };
-    auto set = [&](int u, int s) JMA_INL {
-      return tag_set(xv[u][s]) && tag_set(mv[u][s]) && tag_set(lv[u][s]);
-    };
+    float4_t xv[kI], mv[kI];
 #pragma unroll
-    for (int u = 0; u < kE; ++u)
-#pragma unroll
-      for (int s = 0; s < B; ++s) load(u, s);
+    for (int i = 0; i < kI; ++i) {
+      const uint32_t w = base(r + SUB * i, hs);
+      xv[i] = needed(i) ? load_part(rs, w + e * 4) : float4_t{0.f, 0.f, 0.f, 0.f};
+      mv[i] = needed(i) ? load_part(rs, w + DV * 4) : float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    float mx, lw;  // this workgroup's own partial, while the loads are in flight
+    float4_t own;
+    wave_partial<DV, W>(s_acc, s_ml, hs, e, mx, lw, own);
     for (uint32_t spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
-      for (int u = 0; u < kE; ++u)
-#pragma unroll
-        for (int s = 0; s < B; ++s) ready &= set(u, s);
+      for (int i = 0; i < kI; ++i) ready &= written(xv[i]) && written(float4_t{mv[i][0], mv[i][1], mv[i][0], mv[i][1]});
       if (ready) break;
       if (spin == kSpinLimit) {
         timed_out = true;
         break;
       }
+      poll_barrier();
 #pragma unroll
-      for (int u = 0; u < kE; ++u)
-#pragma unroll
-        for (int s = 0; s < B; ++s)
-          if (!set(u, s)) load(u, s);
+      for (int i = 0; i < kI; ++i) {
+        if (!needed(i)) continue;
+        const uint32_t w = base(r + SUB * i, hs);
+        if (!written(xv[i])) xv[i] = load_part(rs, w + e * 4);
+        if (!written(float4_t{mv[i][0], mv[i][1], mv[i][0], mv[i][1]})) mv[i] = load_part(rs, w + DV * 4);
+      }
     }
+    // Per-thread maximum, then the maximum over the quad's SUB threads.
+    float m_i[kI];
+    float M = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kE; ++u) {
-      const uint32_t j = j0 + tid + kT * u;
-      if (j >= E) continue;
-      const uint32_t hs = j / DV, e = j % DV;
-      float mx, lo, ao;  // this workgroup's own partial
-      wave_partial<DV>(s_acc, s_ml, hs, e, mx, lo, ao);
-      float gm = mx;
+    for (int i = 0; i < kI; ++i) {
+      const uint32_t g = r + SUB * i;
+      m_i[i] = g == split ? mx : (g < ns ? mv[i][0] : -INFINITY);
+      M = fmaxf(M, m_i[i]);
+    }
+    if constexpr (SUB >= 2) M = fmaxf(M, __shfl_xor(M, 1));
+    if constexpr (SUB >= 4) M = fmaxf(M, __shfl_xor(M, 2));
+    if constexpr (SUB >= 8) M = fmaxf(M, __shfl_xor(M, 4));
+    const float mu = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f;
+    float4_t X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < B; ++s)
-        gm = (uint32_t)s < ns - 1 ? fmaxf(gm, __uint_as_float((uint32_t)mv[u][s])) : gm;
-      const float gmu = gm == -INFINITY ? 0.0f : gm;
-      float gl = 0.0f, ga = 0.0f;
-      bool own = false;
+    for (int i = 0; i < kI; ++i) {
+      const uint32_t g = r + SUB * i;
+      if (g >= ns) continue;
+      const float wg = __builtin_amdgcn_exp2f(m_i[i] - mu);
+      const float lg = g == split ? lw : mv[i][1];
+      const float4_t xg = g == split ? own : xv[i];
+      L = fmaf(lg, wg, L);
 #pragma unroll
-      for (int s = 0; s < B; ++s) {
-        if (!own && (uint32_t)s == split) {
-          own = true;
-          const float f = __builtin_amdgcn_exp2f(mx - gmu);
-          gl = fmaf(lo, f, gl);
-          ga = fmaf(ao, f, ga);
-        }
-        if ((uint32_t)s < ns - 1) {
-          const float f = __builtin_amdgcn_exp2f(__uint_as_float((uint32_t)mv[u][s]) - gmu);
-          gl = fmaf(__uint_as_float((uint32_t)lv[u][s]), f, gl);
-          ga = fmaf(__uint_as_float((uint32_t)xv[u][s]), f, ga);
-          clear_word(words(s, hs) + e);
-        }
-      }
-      if (!own) {
-        const float f = __builtin_amdgcn_exp2f(mx - gmu);
-        gl = fmaf(lo, f, gl);
-        ga = fmaf(ao, f, ga);
-      }
-      if (!(gl > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
-      out[j] = ga * (1.0f / gl);
+      for (int c = 0; c < 4; ++c) X[c] = fmaf(xg[c], wg, X[c]);
+      if (needed(i)) store_part(rs, base(g, hs) + e * 4, clear4());
+    }
+    if constexpr (SUB >= 2) {
+      L += __shfl_xor(L, 1);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) X[c] += __shfl_xor(X[c], 1);
+    }
+    if constexpr (SUB >= 4) {
+      L += __shfl_xor(L, 2);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) X[c] += __shfl_xor(X[c], 2);
+    }
+    if constexpr (SUB >= 8) {
+      L += __shfl_xor(L, 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) X[c] += __shfl_xor(X[c], 4);
+    }
+    if (qok && r == 0) {
+      if (!(L > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
+      *(float4_t*)(out + hs * DV + e) = X * (1.0f / L);
     }
   }
-  __syncthreads();
+  __syncthreads();  // every quad of every head has read its (m, l) words
   for (uint32_t k = tid; k < (ns - 1) * nreal; k += kT) {
-    uint64_t* w = words(k / nreal, k % nreal) + DV;
-    clear_word(w);
-    clear_word(w + 1);
+    const uint32_t o = k / nreal, hs = k % nreal;
+    store_part(rs, base(o + (o >= split ? 1u : 0u), hs) + DV * 4, clear4());
   }
   if (timed_out) atomicOr(err, 2);
 }
 
 // One workgroup = one work item (row, kv head, head group of <= 16 query heads, split); its
-// kDecodeWaves waves stride over the split's tiles. Scores are computed as S = K * Q^T on 16-row
+// decode_waves(DK) waves stride over the split's tiles. Scores are computed as S = K * Q^T on 16-row
 // blocks so lane (g, c) holds rows 4g+e of query head c: every lane works on a single head, the
 // online-softmax rescale is one factor per lane, and the score registers are already the B
 // operand of the PV product O^T = V^T * P.
@@ -439,11 +482,12 @@ __device__ __forceinline__ void reduce_group(uint64_t* part, uint64_t item0, uin
 //  - the cross-split reduction (counters): every workgroup of a (row, kv head, head group) takes
 //    an arrival ticket with one atomic at its start. The last to arrive becomes the reducer:
 //    every other workgroup of its group has started by then and so will finish. The others store
-//    their partial (m, l, acc) as tagged 64-bit words {value, 1} and exit without waiting; the
-//    reducer reads them back with device-coherent loads, reloading until every tag is set, then
-//    clears what it read (tag 0), so every partial word is clear again when the launch ends.
+//    their partial (acc, m, l) as plain words with device-coherent 16-byte stores and exit
+//    without waiting; the reducer reads them back with device-coherent loads, reloading until no
+//    word holds the not-written pattern, then writes that pattern back, so every partial word is
+//    clear again when the launch ends.
 template <typename KV, int DK, int DV, bool kSimple>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
   using TileT = Tile<KV, DK, DV>;
   constexpr uint32_t kBlk = TileT::kBlk;
@@ -451,7 +495,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   constexpr int kNv = DV / 16;        // output fragments per lane
   constexpr int kC = kF16 ? DK / 32 : DK / 16;
   constexpr int kQ = kF16 ? 8 : 4;    // q elements per lane per k-chunk
-  constexpr uint32_t kW = kDecodeWaves;
+  constexpr uint32_t kW = decode_waves(DK);
   __shared__ __attribute__((aligned(16))) float s_acc[kW][16][DV];
   __shared__ float s_ml[kW][16][2];
   __shared__ uint32_t s_ticket;
@@ -481,7 +525,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   JMA_GLOBAL const float *g_vn = (JMA_GLOBAL const float*)a.v_new;
   JMA_GLOBAL uint32_t* g_ctr = (JMA_GLOBAL uint32_t*)a.counters;
   JMA_GLOBAL float* g_out = (JMA_GLOBAL float*)a.out;
-  JMA_GLOBAL uint64_t* g_tag = (JMA_GLOBAL uint64_t*)a.part_tag;
+  JMA_GLOBAL float* g_tag = (JMA_GLOBAL float*)a.part_f;
   JMA_GLOBAL float* g_pacc = (JMA_GLOBAL float*)a.part_acc;
   JMA_GLOBAL float* g_pml = (JMA_GLOBAL float*)a.part_ml;
   JMA_GLOBAL int* g_err = (JMA_GLOBAL int*)a.err;
@@ -533,7 +577,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
   uint32_t* counters = (uint32_t*)g_ctr;
   float* out = (float*)g_out;
-  uint64_t* part_tag = (uint64_t*)g_tag;
+  float* part_f = (float*)g_tag;
   float* part_acc = (float*)g_pacc;
   float* part_ml = (float*)g_pml;
   int* err = (int*)g_err;
@@ -839,31 +883,43 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const uint64_t item0 = item - split;
   float* o_grp = out + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DV;
   if (reducer) {
-    if (ns <= 5) reduce_group<4, 4, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-    else if (ns <= 9) reduce_group<8, 2, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-    else if (ns <= 17) reduce_group<16, 1, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-    else reduce_group<32, 1, DV>(part_tag, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    // Sub-threads per quad: at least B / 8 (so a thread takes at most 8 splits), all of the
+    // workgroup's threads when the head group has few quads.
+    constexpr int kSubMax = kW;  // 64 * kW threads over >= 64 quads
+    const bool narrow = nreal * (DV / 4) * kSubMax <= 64 * kW;
+    if (ns <= 8) {
+      if (narrow) reduce_group<8, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<8, 1, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    } else if (ns <= 16) {
+      if (narrow) reduce_group<16, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<16, 2, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    } else {
+      if (narrow) reduce_group<32, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<32, 4, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    }
     return;
   }
-  for (uint32_t j = threadIdx.x; j < nreal * DV; j += 64 * kW) {
-    const uint32_t hs = j / DV, e = j % DV;
-    float mx, lw, aw;
-    wave_partial<DV>(s_acc, s_ml, hs, e, mx, lw, aw);
+  const __amdgpu_buffer_rsrc_t rs = part_rsrc(part_f);
+  for (uint32_t j = threadIdx.x; j < nreal * (DV / 4); j += 64 * kW) {
+    const uint32_t hs = j / (DV / 4), e = (j % (DV / 4)) * 4;
+    float mx, lw;
+    float4_t aw;
+    wave_partial<DV, kW>(s_acc, s_ml, hs, e, mx, lw, aw);
     if (ns == 1) {
       if (!(lw > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
-      o_grp[j] = aw * (1.0f / lw);
+      *(float4_t*)(o_grp + hs * DV + e) = aw * (1.0f / lw);
     } else if (!fused) {  // reduce_kernel combines the splits after this launch
-      part_acc[((uint64_t)item * 16 + hs) * DV + e] = aw;
+      *(float4_t*)(part_acc + ((uint64_t)item * 16 + hs) * DV + e) = aw;
       if (e == 0) {
         part_ml[((uint64_t)item * 16 + hs) * 2] = mx;
         part_ml[((uint64_t)item * 16 + hs) * 2 + 1] = lw;
       }
     } else {
-      uint64_t* pt = part_tag + ((uint64_t)item * 16 + hs) * (DV + 2);
-      __hip_atomic_store(pt + e, tagged(aw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t off = (uint32_t)(((uint64_t)item * 16 + hs) * (DV + 4) * 4);
+      store_part(rs, off + e * 4, float4_t{canon(aw[0]), canon(aw[1]), canon(aw[2]), canon(aw[3])});
       if (e == 0) {
-        __hip_atomic_store(pt + DV, tagged(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pt + DV + 1, tagged(lw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float c = __uint_as_float(kClear);
+        store_part(rs, off + DV * 4, float4_t{canon(mx), canon(lw), c, c});
       }
     }
   }
@@ -947,7 +1003,7 @@ bool decode_supported(bool f16, int dk, int dv) {
 
 template <typename KV, bool kSimple>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
-  const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * kDecodeWaves);
+  const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * decode_waves(d));
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {

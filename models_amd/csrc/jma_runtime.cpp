@@ -86,11 +86,11 @@ struct DeviceBuffer {
   }
 };
 
-// Grows `buf` to `need` bytes; a new allocation is zero-filled.
-void reserve_zeroed(DeviceBuffer& buf, size_t need, hipStream_t stream) {
+// Grows `buf` to `need` bytes; a new allocation has every byte set to `byte`.
+void reserve_filled(DeviceBuffer& buf, size_t need, int byte, hipStream_t stream) {
   if (need <= buf.bytes) return;
   buf.reserve(need, stream);
-  hip_check(hipMemsetAsync(buf.ptr, 0, buf.bytes, stream), "zero scratch");
+  hip_check(hipMemsetAsync(buf.ptr, byte, buf.bytes, stream), "fill scratch");
 }
 
 int env_int(const char* name, int fallback) {
@@ -105,9 +105,9 @@ struct jmodels_attn_context {
   int device = 0;
   hipStream_t stream = nullptr;
   int* d_err = nullptr;
-  DeviceBuffer part_acc, part_ml, part_tag, counters, qrot, stage_q, stage_k, stage_v, stage_out;
+  DeviceBuffer part_acc, part_ml, part_f, counters, qrot, stage_q, stage_k, stage_v, stage_out;
   int decode_target_blocks = 256;   // workgroups a decode launch aims for (256 CUs)
-  int tiles_per_wave = 2;           // minimum tiles each decode wave streams
+  int tiles_per_wave = 1;           // minimum tiles each decode wave streams
   bool unfused = false;             // JMA_UNFUSED=1: separate append and reduce kernels
 };
 
@@ -375,7 +375,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     units += (uint64_t)ntiles[i] * kv->hkv * a.hgroups;
   }
   const uint64_t target = (uint64_t)ctx->decode_target_blocks;
-  uint64_t tps = (uint64_t)jma::kDecodeWaves * ctx->tiles_per_wave;
+  uint64_t tps = (uint64_t)jma::decode_waves((int)kv->dk) * ctx->tiles_per_wave;
   tps = std::max<uint64_t>(tps, (units + target - 1) / target);
   tps = std::max<uint64_t>(tps, (max_tiles + jma::kMaxSplits - 1) / jma::kMaxSplits);
   a.tiles_per_split = (uint32_t)tps;
@@ -404,13 +404,13 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.part_acc = (float*)ctx->part_acc.ptr;
     a.part_ml = (float*)ctx->part_ml.ptr;
   } else if (any_split) {
-    // Arrival tickets start at zero and every tagged partial word starts clear; the reducing
+    // Arrival tickets start at zero and every partial word starts not-written; the reducing
     // workgroups restore both, so they are zeroed only when (re)allocated, never inside a launch
     // sequence a caller may capture.
-    reserve_zeroed(ctx->part_tag, (size_t)items * 16 * (kv->dv + 2) * sizeof(uint64_t), ctx->stream);
-    reserve_zeroed(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t),
+    reserve_filled(ctx->part_f, (size_t)items * 16 * (kv->dv + 4) * sizeof(float), 0xFF, ctx->stream);
+    reserve_filled(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t), 0,
                    ctx->stream);
-    a.part_tag = (uint64_t*)ctx->part_tag.ptr;
+    a.part_f = (float*)ctx->part_f.ptr;
     a.counters = (uint32_t*)ctx->counters.ptr;
   }
   hip_check(jma::launch_decode(a, kv->f16(), kv->dk, kv->dv, ctx->stream), "decode launch");
@@ -566,9 +566,9 @@ int32_t collect_errors(jmodels_attn_context* ctx) {
     int zero = 0;
     hip_check(hipMemcpy(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "reset error word");
     if (err & 2) {
-      // A reducer gave up waiting: tickets and tagged partials may be left set; clear them.
-      for (DeviceBuffer* b : {&ctx->part_tag, &ctx->counters})
-        if (b->ptr) hip_check(hipMemset(b->ptr, 0, b->bytes), "reset reduction scratch");
+      // A reducer gave up waiting: tickets and partial words may be left set; clear them.
+      if (ctx->part_f.ptr) hip_check(hipMemset(ctx->part_f.ptr, 0xFF, ctx->part_f.bytes), "reset partials");
+      if (ctx->counters.ptr) hip_check(hipMemset(ctx->counters.ptr, 0, ctx->counters.bytes), "reset tickets");
       fail(JMODELS_ATTN_DEVICE_ERROR, "cross-split reduction timed out waiting for a partial");
     }
     fail(JMODELS_ATTN_NON_FINITE, "softmax input contains NaN or positive infinity");
@@ -632,7 +632,7 @@ jmodels_attn_context* jmodels_attn_context_create(int32_t device) {
     auto* ctx = new jmodels_attn_context();
     ctx->device = device;
     ctx->decode_target_blocks = std::max(1, env_int("JMA_DECODE_TARGET_BLOCKS", 256));
-    ctx->tiles_per_wave = std::max(1, env_int("JMA_DECODE_TILES_PER_WAVE", 2));
+    ctx->tiles_per_wave = std::max(1, env_int("JMA_DECODE_TILES_PER_WAVE", 1));
     ctx->unfused = env_int("JMA_UNFUSED", 0) != 0;
     try {
       hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -654,7 +654,7 @@ int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx) {
   return guard([&] {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_tag, &ctx->counters, &ctx->qrot, &ctx->stage_q,
+    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_f, &ctx->counters, &ctx->qrot, &ctx->stage_q,
                             &ctx->stage_k, &ctx->stage_v, &ctx->stage_out})
       b->release();
     (void)hipFree(ctx->d_err);
