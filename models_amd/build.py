@@ -55,6 +55,13 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
     if verbose and errors:
         print("\n".join(errors))
+    # A kernel template whose host-side instantiation fails leaves its launch stub undefined; the
+    # shared library still links, so check for the library's own unresolved symbols here.
+    nm = subprocess.run(["nm", "-D", "--undefined-only", LIB_PATH + ".tmp"], capture_output=True, text=True)
+    own = [ln.split()[-1] for ln in nm.stdout.splitlines() if "jma" in ln or "jmodels" in ln]
+    if own:
+        os.remove(LIB_PATH + ".tmp")
+        raise RuntimeError(f"built library leaves its own symbols undefined: {own}")
     os.replace(LIB_PATH + ".tmp", LIB_PATH)
     return LIB_PATH
 

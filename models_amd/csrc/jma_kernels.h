@@ -101,8 +101,26 @@ struct PrefillArgs {
   uint32_t heads_per_stripe;  // query heads of one kv head sharing a stripe's 32 MFMA columns
   uint32_t rows_per_stripe;   // query rows of a stripe; rows * heads <= 32
   uint32_t head_groups;       // ceil(group / heads_per_stripe)
-  uint32_t row_blocks;        // set by launch_prefill
+  uint32_t row_blocks;        // set by plan_prefill
+  // The split_blocks longest row blocks (they run first) have their kv range cut in two halves,
+  // each a workgroup; the later of the two to arrive (ticket) merges them. part: [pair][half]
+  // [stripe][D / 8 chunks x 64 lanes + 32 columns] float4 words, every word 0xFFFFFFFF (not
+  // written) between launches; tickets: [pair], zero between launches.
+  uint32_t split_blocks;
+  float* part;
+  uint32_t* tickets;
 };
+
+// Launch plan of a prefill: row blocks, split blocks, the pairs of split workgroups and the bytes
+// of partial words they need. split_tiles >= 2 splits every block with at least that many kv
+// tiles; 0 or 1 never splits; -1 splits the blocks holding more than 1.5x the kv tiles an average
+// compute unit (of cus) runs, and at least 48: a split costs a second prologue and an exchange,
+// and pays only when the longest blocks would otherwise set the kernel's duration.
+struct PrefillPlan {
+  uint32_t row_blocks = 0, split_blocks = 0, pairs = 0;
+  size_t part_bytes = 0;
+};
+PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t cus);
 
 // Storage block (slots) of the transposed V layout.
 inline int v_block(bool f16) { return f16 ? 32 : 16; }

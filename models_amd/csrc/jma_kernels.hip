@@ -23,6 +23,7 @@
 namespace jma {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 // Lambdas over shared state must inline, or the captured state (accumulators included) would be
@@ -1045,6 +1046,16 @@ __device__ __forceinline__ uint32_t swap34(uint32_t i) {
   return (i & ~24u) | ((i & 8u) << 1) | ((i & 16u) >> 1);
 }
 
+// 16 bytes per lane from global memory straight into LDS (lane i's at lds + 16 i): a buffer load
+// over the rows at `base`, the lane's byte offset in a vector register and the tile's in a scalar
+// one. (The descriptor has a constant record count and is made here, at the use: otherwise the
+// compiler builds it in vector registers and wraps every load in a uniformity loop.)
+__device__ __forceinline__ void dma16(const void* base, _Float16* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFF0, 0x00020000),
+      (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 // Tile slot of score register e in lane half h.
 __device__ __forceinline__ uint32_t score_slot(int e, int h) {
   return 16u * ((e >> 2) & 1) + 8u * (e >> 3) + 4u * h + (e & 3);
@@ -1064,10 +1075,6 @@ __device__ __forceinline__ uint32_t swz_v(uint32_t r) { return ((r >> 1) ^ (r >>
 __device__ __forceinline__ float half_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float half_min(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float half_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -1091,6 +1098,85 @@ template <int D> struct Shape { static constexpr int S = D >= 256 ? 2 : 4, Q = 2
 
 }  // namespace pf
 
+// Finish of one half of a split row block. Each wave holds kCQ finished O^T chunks of its stripe
+// (chunks c0 .. c0 + kCQ - 1, unnormalised: weighted by 2^(m_r - M) over the kv groups) and its
+// columns' (M, L). The first half to arrive stores them as plain words ((M, L) once per stripe)
+// and exits; the second polls the other half's words until none reads kClear, combines the
+// halves in half order, (O0 e0 + O1 e1) / (L0 e0 + L1 e1) with e_h = 2^(M_h - max), stores the
+// output and clears the words, so the result does not depend on which half merges. The merge
+// decision is uniform over the workgroup.
+template <int D, int S, int kCQ>
+__device__ __forceinline__ void split_exchange(const PrefillArgs& a, uint32_t pair, uint32_t half,
+                                               bool merger, int s, uint32_t c0, bool post_ml,
+                                               int lane, int j, int h, bool col_ok, uint32_t crow,
+                                               uint32_t head, float m, float l,
+                                               const float4_t (&v)[kCQ]) {
+  constexpr int kC = D / 8;  // float4 chunks of O^T per lane and stripe
+  const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part);
+  auto base = [&](uint32_t hf) JMA_INL {
+    return (uint32_t)((((uint64_t)pair * 2 + hf) * S + s) * (kC * 64 + 32) * 16);
+  };
+  if (!merger) {
+    const uint32_t b = base(half);
+#pragma unroll
+    for (int i = 0; i < kCQ; ++i)
+      store_part(rs, b + ((c0 + i) * 64 + lane) * 16,
+                 float4_t{canon(v[i][0]), canon(v[i][1]), canon(v[i][2]), canon(v[i][3])});
+    if (post_ml && h == 0) {
+      const float cl = __uint_as_float(kClear);
+      store_part(rs, b + (kC * 64 + j) * 16, float4_t{canon(m), canon(l), cl, cl});
+    }
+    return;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&a.tickets[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t ob = base(1 - half);
+  float4_t x[kCQ];
+#pragma unroll
+  for (int i = 0; i < kCQ; ++i) x[i] = load_part(rs, ob + ((c0 + i) * 64 + lane) * 16);
+  float4_t mlv = load_part(rs, ob + (kC * 64 + j) * 16);
+  auto ml_ready = [&]() JMA_INL { return written(float4_t{mlv[0], mlv[1], mlv[0], mlv[1]}); };
+  bool timed_out = false;
+  for (uint32_t spin = 0;; ++spin) {
+    bool ready = ml_ready();
+#pragma unroll
+    for (int i = 0; i < kCQ; ++i) ready &= written(x[i]);
+    if (ready) break;
+    if (spin == kSpinLimit) {
+      timed_out = true;
+      break;
+    }
+    poll_barrier();
+    if (!ml_ready()) mlv = load_part(rs, ob + (kC * 64 + j) * 16);
+#pragma unroll
+    for (int i = 0; i < kCQ; ++i)
+      if (!written(x[i])) x[i] = load_part(rs, ob + ((c0 + i) * 64 + lane) * 16);
+  }
+  const float m0 = half == 0 ? m : mlv[0], l0 = half == 0 ? l : mlv[1];
+  const float m1 = half == 0 ? mlv[0] : m, l1 = half == 0 ? mlv[1] : l;
+  const float M = fmaxf(m0, m1);
+  const float e0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
+  const float e1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
+  const float L = fmaf(l1, e1, l0 * e0);
+  if (__ballot(col_ok && !(L > 0.0f && L < INFINITY)) != 0 && lane == 0) atomicOr(a.err, 1);
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
+#pragma unroll
+  for (int i = 0; i < kCQ; ++i) {
+    const uint32_t c = c0 + i;
+    const float4_t v0 = half == 0 ? v[i] : x[i], v1 = half == 0 ? x[i] : v[i];
+    float4_t r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = fmaf(v1[e], e1, v0[e] * e0) * inv;
+    if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = r;
+    store_part(rs, ob + (c * 64 + lane) * 16, clear4());
+  }
+  // Every wave of the stripe has read the (M, L) word before it is cleared.
+  __syncthreads();
+  if (post_ml && h == 0) store_part(rs, ob + (kC * 64 + j) * 16, clear4());
+  if (timed_out && lane == 0) atomicOr(a.err, 2);
+}
+
 // Workgroup = (kv head, head group, block of S stripes). A stripe is R query rows x Gz query heads
 // = 32 MFMA columns (R * Gz <= 32). Wave (s, q) owns stripe s and the kv tiles t0+q, t0+q+Q, ...
 // of the block's causal range: the Q waves of a stripe split its kv range, and the S waves of a kv
@@ -1104,11 +1190,13 @@ template <int D> struct Shape { static constexpr int S = D >= 256 ? 2 : 4, Q = 2
 //
 // Softmax keeps a per-column reference maximum m and rescales the accumulators only when a tile
 // maximum exceeds it by more than 8 (log2 units), so exponentials stay <= 256 and most steps skip
-// the rescale; the final normalisation divides by the sum of the same exponentials, so the result
-// is the softmax of the reference up to f16 rounding of q, k, v and p.
+// the rescale; the final normalisation divides by the sum of the same (f16-rounded) exponentials,
+// so the result is the softmax of the reference up to f16 rounding of q, k, v and p.
+// Up to D = 128 the kernel fits 256 registers per lane (two waves per SIMD), which also keeps
+// the matrix-op results in ordinary vector registers (no accumulation-register copies per tile).
 template <int D>
-__global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefill_kernel(
-    const PrefillArgs a) {
+__global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q)
+__attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const PrefillArgs a) {
   using namespace pf;
   constexpr int S = Shape<D>::S, Q = Shape<D>::Q;
   constexpr int kWaves = S * Q;
@@ -1135,11 +1223,22 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   __shared__ float2 s_ml[kWaves][32];
 
   // Kv heads vary fastest: consecutive workgroups land on different XCDs, so each XCD's L2 keeps
-  // the K/V of few kv heads. Row blocks run last-first (longest causal ranges first).
-  const uint32_t kvh = blockIdx.x % a.num_kv_heads;
-  const uint32_t rest = blockIdx.x / a.num_kv_heads;
+  // the K/V of few kv heads. Row blocks run last-first (longest causal ranges first); the
+  // split_blocks longest come first as two halves each.
+  const uint32_t n_split_items = 2 * a.split_blocks * a.head_groups * a.num_kv_heads;
+  const bool split = blockIdx.x < n_split_items;
+  const uint32_t b_item = split ? blockIdx.x : blockIdx.x - n_split_items;
+  const uint32_t kvh = b_item % a.num_kv_heads;
+  const uint32_t rest = b_item / a.num_kv_heads;
   const uint32_t hz = rest % a.head_groups;
-  const uint32_t rb = a.row_blocks - 1 - rest / a.head_groups;
+  const uint32_t half = split ? (rest / a.head_groups) % 2 : 0u;
+  const uint32_t rank = split ? rest / a.head_groups / 2 : a.split_blocks + rest / a.head_groups;
+  const uint32_t rb = a.row_blocks - 1 - rank;
+  const uint32_t pair = (rank * a.head_groups + hz) * a.num_kv_heads + kvh;
+  __shared__ uint32_t s_ticket;
+  uint32_t ticket = 0;  // arrival order of this half of a split pair, taken first
+  if (split && threadIdx.x == 0)
+    ticket = __hip_atomic_fetch_add(&a.tickets[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int s = wave % S, q = wave / S;
@@ -1160,9 +1259,13 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   const uint32_t cpos = a.start + crow;
   const uint32_t cfirst = first_visible(cpos, a.window);
 
-  // Kv tiles of the block, and the part of them this wave's stripe sees.
-  const uint32_t t0 = first_visible(a.start + b_row0, a.window) / 32;
-  const uint32_t t1 = (a.start + b_row1) / 32 + 1;
+  // Kv tiles of the block (of its half, for a split block), and the part of them this wave's
+  // stripe sees.
+  const uint32_t bt0 = first_visible(a.start + b_row0, a.window) / 32;
+  const uint32_t bt1 = (a.start + b_row1) / 32 + 1;
+  const uint32_t tmid = bt0 + (bt1 - bt0 + 1) / 2;
+  const uint32_t t0 = split && half == 1 ? tmid : bt0;
+  const uint32_t t1 = split && half == 0 ? tmid : bt1;
   const uint32_t steps = (t1 - t0 + Q - 1) / Q;
   const uint32_t w_last = a.start + row_last;
   const uint32_t w_first_late = first_visible(w_last, a.window);
@@ -1171,47 +1274,47 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
                           (uint64_t)kvh * a.kv.cap * D;
   const _Float16* vbase = (const _Float16*)a.kv.v + a.seq * a.kv.seq_stride_v + a.kv.layer_off_v +
                           (uint64_t)kvh * a.kv.cap * D;
-  // Element offsets inside a tile of the 16 bytes this lane stages per chunk. A direct-to-LDS load
+  // Byte offsets inside a tile of the 16 bytes this lane stages per chunk. A direct-to-LDS load
   // writes lane i's 16 bytes at chunk base + 16 i, so the LDS swizzle is applied on the global side.
   uint32_t koff[kCPW], voff[kCPW];
 #pragma unroll
   for (int i = 0; i < kCPW; ++i) {
     const uint32_t c = s + S * i;
     const uint32_t rk = c * (512 / D) + lane / kNC;
-    koff[i] = rk * D + 8 * ((lane % kNC) ^ swz_k<D>(rk));
+    koff[i] = 2 * (rk * D + 8 * ((lane % kNC) ^ swz_k<D>(rk)));
     const uint32_t rv = c * 16 + lane / 4;
-    voff[i] = rv * 32 + 8 * ((lane % 4) ^ swz_v(rv));
+    voff[i] = 2 * (rv * 32 + 8 * ((lane % 4) ^ swz_v(rv)));
   }
   auto has_tile = [&](uint32_t k) JMA_INL { return k < steps && t0 + k * Q + q < t1; };
-  // Whether every column of the stripe sees all of step k's tile (no mask needed).
+  // Whether every column of the stripe sees all of step k's tile (no mask needed). A tile at or
+  // past t1 (the last step of a kv group, or the other half's range of a split block) is masked.
   auto full = [&](uint32_t k) JMA_INL {
     const uint32_t p0 = 32 * (t0 + k * Q + q);
-    return p0 + 31 <= a.start + row0 && p0 >= w_first_late;
+    return p0 + 31 <= a.start + row0 && p0 >= w_first_late && p0 < 32 * t1;
   };
-  // First slot of step k's tile. Positions of a non-ring cache are below its capacity, and a ring
-  // holds the whole visible range, so one conditional subtraction wraps (no division, no branch).
-  const uint32_t slot_base = (32 * (t0 + q)) % a.kv.cap;
-  auto slot0_of = [&](uint32_t k) JMA_INL {
-    const uint32_t x = slot_base + 32 * Q * k;
-    return x >= a.kv.cap ? x - a.kv.cap : x;
+  // Byte offset (in the kv head's rows) of step k's tile. A step past the group's last tile loads
+  // that tile again (its scores are masked), and a group without tiles loads slot 0, so every
+  // wave issues the same number of loads each step. Positions of a non-ring cache are below its
+  // capacity, and a ring holds the whole visible range, so one conditional subtraction wraps.
+  const bool g_has = t0 + q < t1;
+  const uint32_t g_last = g_has ? (t1 - 1 - t0 - q) / Q : 0u;
+  const uint32_t cap_bytes = a.kv.cap * (2 * D);
+  const uint32_t base_bytes = g_has ? ((32 * (t0 + q)) % a.kv.cap) * (2 * D) : 0u;
+  auto tile_off = [&](uint32_t k) JMA_INL {
+    const uint32_t x = base_bytes + min(k, g_last) * (32 * Q * 2 * D);
+    return x >= cap_bytes ? x - cap_bytes : x;
   };
   // This wave's chunk i of step k's K tile or V tile into LDS array `arr` (the group's tiles sit
-  // q tiles into the stage). A step that has no tile for this group loads slot 0 instead, into a
-  // stage nothing reads, so every wave issues the same number of loads each step.
-  auto tile_slot = [&](uint32_t k) JMA_INL { return has_tile(k) ? slot0_of(k) : 0u; };
+  // q tiles into the stage).
   auto dma_k = [&](uint32_t k, _Float16* arr, int i) JMA_INL {
     const uint32_t c = s + S * i;
     if (c >= (uint32_t)kChunks) return;
-    __builtin_amdgcn_global_load_lds(
-        (const void*)(kbase + (uint64_t)tile_slot(k) * D + koff[i]),
-        (__attribute__((address_space(3))) void*)(arr + q * kT + 512 * c), 16, 0, 0);
+    pf::dma16(kbase, arr + q * kT + 512 * c, koff[i], tile_off(k));
   };
   auto dma_v = [&](uint32_t k, _Float16* arr, int i) JMA_INL {
     const uint32_t c = s + S * i;
     if (c >= (uint32_t)kChunks) return;
-    __builtin_amdgcn_global_load_lds(
-        (const void*)(vbase + (uint64_t)tile_slot(k) * D + voff[i]),
-        (__attribute__((address_space(3))) void*)(arr + Q * kT + q * kT + 512 * c), 16, 0, 0);
+    pf::dma16(vbase, arr + Q * kT + q * kT + 512 * c, voff[i], tile_off(k));
   };
   auto arr_of = [&](auto idx) JMA_INL -> _Float16* {
     constexpr int i = decltype(idx)::value % N;
@@ -1232,21 +1335,26 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   }
 
   // Q^T operands: 8 consecutive dims of this lane's column per k-step, scaled by
-  // scale * log2(e) and rounded to f16.
+  // scale * log2(e) and rounded to f16. A scaled element beyond the f16 range (where the
+  // reference's f32 scores stay finite) or infinite is reported like a non-finite score; a NaN
+  // element makes its column's scores NaN, which the final normalisation reports.
   half8_t qf[kKS];
   {
     const float* qrow = a.q + ((uint64_t)crow * a.num_heads + head) * D + 8 * h;
     const float qs = col_ok ? a.qscale : 0.0f;
+    float qmax = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
       const float4_t x0 = *(const float4_t*)(qrow + 16 * ks);
       const float4_t x1 = *(const float4_t*)(qrow + 16 * ks + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
+        qmax = fmaxf(qmax, fmaxf(fabsf(x0[e] * qs), fabsf(x1[e] * qs)));
         qf[ks][e] = (_Float16)(x0[e] * qs);
         qf[ks][4 + e] = (_Float16)(x1[e] * qs);
       }
     }
+    if (__ballot(col_ok && !(qmax < 65520.0f)) != 0 && lane == 0) atomicOr(a.err, 1);
   }
 
   float16_t o[kNb];
@@ -1254,18 +1362,23 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   for (int nb = 0; nb < kNb; ++nb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[nb][e] = 0.0f;
-  float m = -INFINITY, l = 0.0f, mn = INFINITY;
+  // l accumulates in two chains (l, lb), summed at the end. negm holds -m (0 while m is -inf) in
+  // every element: the initial accumulators of each score tile.
+  float m = -INFINITY, l = 0.0f, lb = 0.0f;
+  float16_t negm;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) negm[e] = 0.0f;
   const uint32_t kr = swap34(j);
 
   // LDS reads are issued in batches of up to 8 ahead of the matrix ops that consume them: with
   // eight waves and the direct-to-LDS traffic sharing the LDS, one read's latency is several
   // hundred cycles, and a read-use-read chain would serialise on it.
   constexpr int kBatch = kKS < 8 ? kKS : 8;
-  // S^T of one tile; `issue(i)` runs after the i-th matrix op, to spread loads between them.
+  // S^T of one tile minus the reference maximum of each column (the accumulators start at -m, or
+  // at 0 before the first tile): the tile's exponentials need no subtraction. `issue(i)` runs
+  // after the i-th matrix op, to spread loads between them.
   auto qk = [&](const _Float16* sk, auto issue) JMA_INL {
-    float16_t sc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+    float16_t sc = negm;
 #pragma unroll
     for (int ks0 = 0; ks0 < kKS; ks0 += kBatch) {
       half8_t kf[kBatch];
@@ -1282,50 +1395,56 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     }
     return sc;
   };
-  // Masks step k's scores (positions outside [first, position] of each column become -inf),
-  // returns the per-column tile maximum and tracks the minimum valid score.
+  // Masks step k's (shifted) scores (positions outside [first, position] of each column become
+  // -inf) and returns the per-column tile maximum.
   auto mask_max = [&](float16_t& sc, uint32_t k, bool whole) JMA_INL {
     float tmax = -INFINITY;
     if (whole) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        tmax = fmaxf(tmax, sc[e]);
-        mn = fminf(mn, sc[e]);
-      }
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
     } else {
-      const uint32_t p0 = 32 * (t0 + k * Q + q);
+      const uint32_t p0 = 32 * (t0 + k * Q + q), pend = 32 * t1;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const uint32_t p = p0 + score_slot(e, h);
-        const bool ok = p >= cfirst && p <= cpos;
-        mn = fminf(mn, ok ? sc[e] : INFINITY);
+        const bool ok = p >= cfirst && p <= cpos && p < pend;
         sc[e] = ok ? sc[e] : -INFINITY;
         tmax = fmaxf(tmax, sc[e]);
       }
     }
     return half_max(tmax);
   };
-  // Raises the reference maximum when a tile maximum exceeds it by more than 8.
-  auto rescale = [&](float tmax) JMA_INL {
-    if (__ballot(tmax > m + 8.0f) != 0) {
-      const bool up = tmax > m + 8.0f;
-      const float alpha = up ? __builtin_amdgcn_exp2f(m - tmax) : 1.0f;
-      m = up ? tmax : m;
+  // Raises the reference maximum when the tile's maximum exceeds it by more than 8 (tmax is the
+  // shifted tile's maximum, so the test is tmax > 8; any tile that has a visible score raises it
+  // from -inf), and shifts the tile to the new maximum.
+  auto rescale = [&](float16_t& sc, float tmax) JMA_INL {
+    const bool up = m == -INFINITY ? tmax > -INFINITY : tmax > 8.0f;
+    if (__ballot(up) != 0) {
+      const float alpha = !up ? 1.0f : (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-tmax));
+      const float delta = up ? tmax : 0.0f;
+      m = up ? (m == -INFINITY ? 0.0f : m) + tmax : m;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) negm[e] = m == -INFINITY ? 0.0f : -m;
       l *= alpha;
+      lb *= alpha;
 #pragma unroll
       for (int nb = 0; nb < kNb; ++nb) o[nb] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] -= delta;
     }
   };
+  // Exponentials of a shifted tile, rounded to f16 for the PV product; l sums the rounded values
+  // (dot products with (1, 1), f32 accumulation).
   auto exp_tile = [&](const float16_t& sc, half8_t* pf) JMA_INL {
-    const float mu = m == -INFINITY ? 0.0f : m;
-    float ps = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float p = __builtin_amdgcn_exp2f(sc[e] - mu);
-      ps += p;
-      pf[e >> 3][e & 7] = (_Float16)p;
+    for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(sc[e]);
+    const half2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const half2_t pr = {pf[i >> 2][2 * (i & 3)], pf[i >> 2][2 * (i & 3) + 1]};
+      if (i & 1) lb = __builtin_amdgcn_fdot2(pr, one, lb, false);
+      else l = __builtin_amdgcn_fdot2(pr, one, l, false);
     }
-    l += ps;
   };
   auto pv = [&](const _Float16* sv, const half8_t* pf) JMA_INL {
     constexpr int kNbB = kBatch / 2;  // dv blocks per batch of reads
@@ -1372,8 +1491,10 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   auto mask_step = [&](float16_t& sc, uint32_t k) JMA_INL {
     return full(k) ? mask_max(sc, k, true) : mask_max(sc, k, false);
   };
-  float16_t scur = qk(lx + q * kT, no_issue);
-  rescale(mask_step(scur, 0));
+  // Score tiles alternate between two register sets (even steps finish sa and compute sb).
+  float16_t sa = qk(lx + q * kT, no_issue), sb;
+  rescale(sa, mask_step(sa, 0));
+  static_assert(N % 2 == 0, "the unrolled steps alternate the score registers");
 
   // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
   // before tile k+1's scores are computed.
@@ -1384,6 +1505,8 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   // visible tiles and the occasional rescale branch.
   auto step = [&](uint32_t k, auto kp) JMA_INL {
     constexpr int P = decltype(kp)::value;
+    float16_t& scur = P % 2 == 0 ? sa : sb;
+    float16_t& snxt = P % 2 == 0 ? sb : sa;
     wait_barrier(std::integral_constant<int, (N - 2) * kDmaPerStep>{});
     _Float16* const dst = arr_of(std::integral_constant<int, P>{});
     const _Float16* const ksrc = arr_of(std::integral_constant<int, P + 1>{}) + q * kT;
@@ -1396,24 +1519,25 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
         dma_v(k + N - 1, dst, ks / kEvery);
       }
     };
-    float16_t snxt;
     if constexpr (kOverlap) {
       // QK^T of tile k+1 overlaps the exponentials of tile k.
       snxt = qk(ksrc, spread);
       exp_tile(scur, pf);
       pv(vsrc, pf);
-      __builtin_amdgcn_sched_group_barrier(0x100, kKS, 0);
+      // Order: all K and V^T operand reads, then the QK^T matrix ops each followed by a share of
+      // the exponentials, then the PV matrix ops.
+      __builtin_amdgcn_sched_group_barrier(0x100, kKS + 2 * kNb, 0);
       static_for<kKS>([&](auto) JMA_INL {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
       });
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNb, 0);
     } else {
       exp_tile(scur, pf);
       pv(vsrc, pf);
       snxt = qk(ksrc, spread);
     }
-    rescale(mask_step(snxt, k + 1));
-    scur = snxt;
+    rescale(snxt, mask_step(snxt, k + 1));
   };
   // (The last copies are guarded inside the loop: remainder copies after it would double the
   // code the register allocator spans and spill.)
@@ -1426,11 +1550,10 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
   // the q-th of its O^T chunks. Every wave posts (m, l) and, for each other kv group r, the
   // chunks wave r finishes; then it combines its own chunks (from registers) with the Q - 1
   // posted ones, in kv-group order, weighted by exp2(m_r - M) / L.
-  l = half_sum(l);
-  mn = half_min(mn);
+  l = half_sum(l + lb);
   // Every wave is done with the tile stages the exchange overwrites, and no load is in flight.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  if (split && threadIdx.x == 0) s_ticket = ticket;
   constexpr int kCQ = kC / Q;  // chunks one wave finishes
   // Posted chunks of stripe s: [source group][destination slot][kCQ][64 lanes] float4, in lx for
   // even stripes and ly for odd ones (each holds Q * (Q - 1) * kCQ KB <= one LDS array).
@@ -1461,12 +1584,13 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
     });
   }
   __syncthreads();
-  // Weights of the kv groups of this lane's column: exp2(m_r - M) / L.
+  // Weights of the kv groups of this lane's column: 2^(m_r - M), divided by L unless the block is
+  // split (the halves are normalised together).
   float wr[Q];
-  float L = l;
+  float M = m, L = l;
   if constexpr (Q > 1) {
     float mr[Q], lr[Q];
-    float M = -INFINITY;
+    M = -INFINITY;
 #pragma unroll
     for (int r = 0; r < Q; ++r) {
       const float2 v = r == q ? float2{m, l} : s_ml[r * S + s][j];
@@ -1480,15 +1604,17 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
       wr[r] = mr[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mr[r] - M);
       L = fmaf(lr[r], wr[r], L);
     }
+  } else {
+    wr[0] = 1.0f;
+  }
+  if (!split) {
+    const bool bad = col_ok && !(L > 0.0f && L < INFINITY);
+    if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
 #pragma unroll
     for (int r = 0; r < Q; ++r) wr[r] *= inv;
-  } else {
-    wr[0] = L > 0.0f ? 1.0f / L : 0.0f;
   }
-  const bool bad = col_ok && (mn == -INFINITY || !(L > 0.0f && L < INFINITY));
-  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
-  float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
+  float4_t fin[kCQ];  // this wave's finished chunks q * kCQ ..
   static_for<Q>([&](auto qq) JMA_INL {
     constexpr int own = decltype(qq)::value;
     if (own == q) {
@@ -1502,10 +1628,21 @@ __global__ __launch_bounds__(64 * pf::Shape<D>::S * pf::Shape<D>::Q) void prefil
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = fmaf(x[i], wr[r], v[i]);
         }
-        if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = v;
+        fin[idx.value] = v;
       });
     }
   });
+  if (split) {
+    split_exchange<D, S, kCQ>(a, pair, half, s_ticket != 0, s, (uint32_t)q * kCQ, q == 0, lane, j,
+                              h, col_ok, crow, head, M, L, fin);
+    return;
+  }
+  float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
+#pragma unroll
+  for (int i = 0; i < kCQ; ++i) {
+    const uint32_t c = (uint32_t)q * kCQ + i;
+    if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = fin[i];
+  }
 }
 
 bool prefill_supported(int dk, int dv) {
@@ -1513,13 +1650,56 @@ bool prefill_supported(int dk, int dv) {
 }
 
 template <int D>
+PrefillPlan plan_prefill_t(const PrefillArgs& a, int split_tiles, uint32_t cus) {
+  constexpr int S = pf::Shape<D>::S;
+  PrefillPlan p;
+  const uint32_t rows_per_block = S * a.rows_per_stripe;
+  p.row_blocks = (a.n + rows_per_block - 1) / rows_per_block;
+  const uint64_t per_block = (uint64_t)a.head_groups * a.num_kv_heads;  // workgroups per row block
+  auto tiles_of = [&](uint32_t rb) {  // kv tiles row block rb sees
+    const uint32_t r0 = rb * rows_per_block, r1 = std::min(r0 + rows_per_block, a.n) - 1;
+    const uint32_t w = a.window, p0 = a.start + r0;
+    const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
+    return (a.start + r1) / 32 + 1 - first / 32;
+  };
+  uint32_t min_tiles = (uint32_t)std::max(split_tiles, 2);
+  if (split_tiles < 0) {
+    // Automatic: a block is split when it holds more than 1.5x the tiles the average compute unit
+    // runs, and at least 48 (the exchange of the halves' partials, through device-coherent
+    // memory, costs about as much as 12 tiles): otherwise the longest blocks set the duration.
+    uint64_t total = 0;
+    for (uint32_t rb = 0; rb < p.row_blocks; ++rb) total += tiles_of(rb);
+    const uint64_t per_cu = total * per_block / std::max<uint32_t>(cus, 1);
+    min_tiles = (uint32_t)std::max<uint64_t>(48, per_cu * 3 / 2 + 1);
+  }
+  if (split_tiles < 0 || split_tiles >= 2) {
+    // Split the longest blocks, from the last one down.
+    while (p.split_blocks < p.row_blocks && tiles_of(p.row_blocks - 1 - p.split_blocks) >= min_tiles)
+      ++p.split_blocks;
+  }
+  p.pairs = p.split_blocks * (uint32_t)per_block;
+  p.part_bytes = (size_t)p.pairs * 2 * S * ((D / 8) * 64 + 32) * 16;
+  return p;
+}
+
+PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t cus) {
+  switch (dk) {
+    case 32: return plan_prefill_t<32>(a, split_tiles, cus);
+    case 64: return plan_prefill_t<64>(a, split_tiles, cus);
+    case 128: return plan_prefill_t<128>(a, split_tiles, cus);
+    case 256: return plan_prefill_t<256>(a, split_tiles, cus);
+    default: return PrefillPlan{};
+  }
+}
+
+template <int D>
 hipError_t launch_prefill_t(PrefillArgs a, hipStream_t stream) {
   constexpr int S = pf::Shape<D>::S, Q = pf::Shape<D>::Q;
-  const uint32_t rows_per_block = S * a.rows_per_stripe;
-  a.row_blocks = (a.n + rows_per_block - 1) / rows_per_block;
-  const uint64_t blocks = (uint64_t)a.row_blocks * a.head_groups * a.num_kv_heads;
+  const uint64_t blocks = ((uint64_t)a.row_blocks + a.split_blocks) * a.head_groups * a.num_kv_heads;
   if (blocks == 0) return hipSuccess;
-  if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+  if (blocks > 0x7fffffffu || a.split_blocks > a.row_blocks) return hipErrorInvalidValue;
+  if ((uint64_t)a.kv.cap * D * 2 > 0x7fffffffu) return hipErrorInvalidValue;  // 32-bit tile offsets
+  if (a.split_blocks > 0 && (a.part == nullptr || a.tickets == nullptr)) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_kernel<D>), dim3((uint32_t)blocks), dim3(64 * S * Q), 0, stream, a);
   return hipGetLastError();
 }

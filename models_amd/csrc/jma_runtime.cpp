@@ -105,9 +105,11 @@ struct jmodels_attn_context {
   int device = 0;
   hipStream_t stream = nullptr;
   int* d_err = nullptr;
-  DeviceBuffer part_acc, part_ml, part_f, counters, qrot, stage_q, stage_k, stage_v, stage_out;
+  DeviceBuffer part_acc, part_ml, part_f, counters, pf_part, pf_tickets, qrot, stage_q, stage_k, stage_v, stage_out;
   int decode_target_blocks = 256;   // workgroups a decode launch aims for (256 CUs)
   int tiles_per_wave = 1;           // minimum tiles each decode wave streams
+  int prefill_split_tiles = -1;     // split prefill row blocks of this many kv tiles; -1: automatic
+  uint32_t cus = 256;               // compute units of the device
   bool unfused = false;             // JMA_UNFUSED=1: separate append and reduce kernels
 };
 
@@ -509,6 +511,16 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.heads_per_stripe = std::min<uint32_t>(lc.group, 32);
     a.rows_per_stripe = 32 / a.heads_per_stripe;
     a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
+    const jma::PrefillPlan plan = jma::plan_prefill(a, (int)kv->dk, ctx->prefill_split_tiles, ctx->cus);
+    a.row_blocks = plan.row_blocks;
+    a.split_blocks = plan.split_blocks;
+    if (plan.pairs > 0) {
+      // Tickets start at zero and partial words not-written; the merging workgroups restore both.
+      reserve_filled(ctx->pf_part, plan.part_bytes, 0xFF, ctx->stream);
+      reserve_filled(ctx->pf_tickets, (size_t)plan.pairs * sizeof(uint32_t), 0, ctx->stream);
+      a.part = (float*)ctx->pf_part.ptr;
+      a.tickets = (uint32_t*)ctx->pf_tickets.ptr;
+    }
     hip_check(jma::launch_prefill(a, (int)kv->dk, (int)kv->dv, ctx->stream), "prefill launch");
     return;
   }
@@ -567,8 +579,10 @@ int32_t collect_errors(jmodels_attn_context* ctx) {
     hip_check(hipMemcpy(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "reset error word");
     if (err & 2) {
       // A reducer gave up waiting: tickets and partial words may be left set; clear them.
-      if (ctx->part_f.ptr) hip_check(hipMemset(ctx->part_f.ptr, 0xFF, ctx->part_f.bytes), "reset partials");
-      if (ctx->counters.ptr) hip_check(hipMemset(ctx->counters.ptr, 0, ctx->counters.bytes), "reset tickets");
+      for (DeviceBuffer* b : {&ctx->part_f, &ctx->pf_part})
+        if (b->ptr) hip_check(hipMemset(b->ptr, 0xFF, b->bytes), "reset partials");
+      for (DeviceBuffer* b : {&ctx->counters, &ctx->pf_tickets})
+        if (b->ptr) hip_check(hipMemset(b->ptr, 0, b->bytes), "reset tickets");
       fail(JMODELS_ATTN_DEVICE_ERROR, "cross-split reduction timed out waiting for a partial");
     }
     fail(JMODELS_ATTN_NON_FINITE, "softmax input contains NaN or positive infinity");
@@ -633,6 +647,8 @@ jmodels_attn_context* jmodels_attn_context_create(int32_t device) {
     ctx->device = device;
     ctx->decode_target_blocks = std::max(1, env_int("JMA_DECODE_TARGET_BLOCKS", 256));
     ctx->tiles_per_wave = std::max(1, env_int("JMA_DECODE_TILES_PER_WAVE", 1));
+    ctx->prefill_split_tiles = std::max(-1, env_int("JMA_PREFILL_SPLIT_TILES", -1));
+    ctx->cus = (uint32_t)std::max(1, prop.multiProcessorCount);
     ctx->unfused = env_int("JMA_UNFUSED", 0) != 0;
     try {
       hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -654,7 +670,7 @@ int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx) {
   return guard([&] {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_f, &ctx->counters, &ctx->qrot, &ctx->stage_q,
+    for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_f, &ctx->counters, &ctx->pf_part, &ctx->pf_tickets, &ctx->qrot, &ctx->stage_q,
                             &ctx->stage_k, &ctx->stage_v, &ctx->stage_out})
       b->release();
     (void)hipFree(ctx->d_err);

@@ -383,6 +383,45 @@ def test_prefill_chunked_and_windowed_matches_oracle(hip):
     rope.close()
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_prefill_split_blocks_match_oracle(monkeypatch, d):
+    """Row blocks whose kv range is split between two workgroups (the second to arrive merges the
+    halves through not-written words) against the oracle, for every split threshold
+    (JMA_PREFILL_SPLIT_TILES: 0 never splits, 2 splits every block of two or more kv tiles, 32 the
+    longest, -1 splits while the grid underfills the device), causal and windowed, a chunk start,
+    a group of 3 (ragged stripes) and ragged tails."""
+    hq, hkv, theta = 12, 4, 1e4
+    scale = A.default_scale(d)
+    n1, n2 = 150, 1061
+    n, cap = n1 + n2, 1280
+    q = normal(21, f"ps/q{d}", (n, hq * d))
+    k = normal(21, f"ps/k{d}", (n, hkv * d))
+    v = normal(21, f"ps/v{d}", (n, hkv * d))
+    for window in (0, 700):
+        ref = OracleKv(1, cap, hkv * d, hkv * d, half_precision=True)
+        r1, _, _ = ref.prefill_layer(0, 0, q[:n1], k[:n1], v[:n1], hq, hkv, d, d, theta, 1.0,
+                                     True, scale, window=window)
+        r2, _, _ = ref.prefill_layer(0, n1, q[n1:], k[n1:], v[n1:], hq, hkv, d, d, theta, 1.0,
+                                     True, scale, window=window)
+        for split in ("0", "2", "32", "-1"):
+            monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", split)
+            lib = A.HipAttentionLibrary(0)
+            try:
+                rope = lib.rotary_table(d, theta, 1.0, max_positions=cap)
+                kv = lib.kv_cache(1, cap, hkv, d, d, half_precision=True)
+                layer = A.AttentionLayer(0, hq, sliding_window=window, neox=True, rope=rope)
+                for rep in range(2):  # the second pass reuses the restored words and tickets
+                    g1 = kv.prefill(layer, 0, q[:n1], k[:n1], v[:n1])
+                    g2 = kv.prefill(layer, n1, q[n1:], k[n1:], v[n1:])
+                    assert_f16_close(g1, r1, f"d {d} window {window} split {split} chunk 1")
+                    assert_f16_close(g2, r2, f"d {d} window {window} split {split} chunk 2")
+                kv.close()
+                rope.close()
+            finally:
+                lib.close()
+            _say(f"d {d} window {window} split {split} ok")
+
+
 # ------------------------------------------------------------------ C4: ragged batched decode
 
 def test_c4_ragged_decode_reduced(hip):
