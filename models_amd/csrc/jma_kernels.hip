@@ -1100,21 +1100,29 @@ template <int D> struct Shape { static constexpr int S = D >= 256 ? 2 : 4, Q = 2
 
 // Finish of one half of a split row block. Each wave holds kCQ finished O^T chunks of its stripe
 // (chunks c0 .. c0 + kCQ - 1, unnormalised: weighted by 2^(m_r - M) over the kv groups) and its
-// columns' (M, L). The first half to arrive stores them as plain words ((M, L) once per stripe)
-// and exits; the second polls the other half's words until none reads kClear, combines the
-// halves in half order, (O0 e0 + O1 e1) / (L0 e0 + L1 e1) with e_h = 2^(M_h - max), stores the
-// output and clears the words, so the result does not depend on which half merges. The merge
-// decision is uniform over the workgroup.
-template <int D, int S, int kCQ>
+// columns' (M, L). The first half to arrive stores them as plain words ((M, L) once per stripe,
+// by the stripe's wave of kv group 0), waits for the stores, sets its wave's flag word and exits.
+// The second polls the one or two flags its wave needs (one word each: bulk polling of the data
+// words would load the whole partial per round), loads the other half's words until none reads
+// kClear (they already hold data once the flag is set), combines the halves in half order,
+// (O0 e0 + O1 e1) / (L0 e0 + L1 e1) with e_h = 2^(M_h - max), stores the output and clears the
+// words and flags, so the result does not depend on which half merges. The merge decision is
+// uniform over the workgroup.
+template <int D, int S, int kWaves, int kCQ>
 __device__ __forceinline__ void split_exchange(const PrefillArgs& a, uint32_t pair, uint32_t half,
-                                               bool merger, int s, uint32_t c0, bool post_ml,
-                                               int lane, int j, int h, bool col_ok, uint32_t crow,
-                                               uint32_t head, float m, float l,
+                                               bool merger, int s, int wave, uint32_t c0,
+                                               bool post_ml, int lane, int j, int h, bool col_ok,
+                                               uint32_t crow, uint32_t head, float m, float l,
                                                const float4_t (&v)[kCQ]) {
   constexpr int kC = D / 8;  // float4 chunks of O^T per lane and stripe
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part);
   auto base = [&](uint32_t hf) JMA_INL {
     return (uint32_t)((((uint64_t)pair * 2 + hf) * S + s) * (kC * 64 + 32) * 16);
+  };
+  // Flag words follow the partials of every pair: [pair][half][wave], 16 bytes each.
+  const uint64_t pairs = (uint64_t)a.split_blocks * a.head_groups * a.num_kv_heads;
+  auto flag = [&](uint32_t hf, int w) JMA_INL {
+    return (uint32_t)(pairs * 2 * S * (kC * 64 + 32) * 16 + (((uint64_t)pair * 2 + hf) * kWaves + w) * 16);
   };
   if (!merger) {
     const uint32_t b = base(half);
@@ -1126,18 +1134,33 @@ __device__ __forceinline__ void split_exchange(const PrefillArgs& a, uint32_t pa
       const float cl = __uint_as_float(kClear);
       store_part(rs, b + (kC * 64 + j) * 16, float4_t{canon(m), canon(l), cl, cl});
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) store_part(rs, flag(half, wave), float4_t{0.f, 0.f, 0.f, 0.f});
     return;
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&a.tickets[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t ob = base(1 - half);
+  bool timed_out = false;
+  {
+    const uint32_t f_own = flag(1 - half, wave), f_ml = flag(1 - half, s);  // wave s posts (M, L)
+    float4_t f1 = load_part(rs, f_own), f0 = load_part(rs, f_ml);
+    for (uint32_t spin = 0; !(written(f1) && written(f0)); ++spin) {
+      if (spin == kSpinLimit) {
+        timed_out = true;
+        break;
+      }
+      poll_barrier();
+      f1 = load_part(rs, f_own);
+      f0 = load_part(rs, f_ml);
+    }
+  }
   float4_t x[kCQ];
 #pragma unroll
   for (int i = 0; i < kCQ; ++i) x[i] = load_part(rs, ob + ((c0 + i) * 64 + lane) * 16);
   float4_t mlv = load_part(rs, ob + (kC * 64 + j) * 16);
   auto ml_ready = [&]() JMA_INL { return written(float4_t{mlv[0], mlv[1], mlv[0], mlv[1]}); };
-  bool timed_out = false;
-  for (uint32_t spin = 0;; ++spin) {
+  for (uint32_t spin = 0; !timed_out; ++spin) {
     bool ready = ml_ready();
 #pragma unroll
     for (int i = 0; i < kCQ; ++i) ready &= written(x[i]);
@@ -1171,9 +1194,10 @@ __device__ __forceinline__ void split_exchange(const PrefillArgs& a, uint32_t pa
     if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = r;
     store_part(rs, ob + (c * 64 + lane) * 16, clear4());
   }
-  // Every wave of the stripe has read the (M, L) word before it is cleared.
+  // Every wave of the stripe has read the (M, L) word and the flags before they are cleared.
   __syncthreads();
   if (post_ml && h == 0) store_part(rs, ob + (kC * 64 + j) * 16, clear4());
+  if (lane == 0) store_part(rs, flag(1 - half, wave), clear4());
   if (timed_out && lane == 0) atomicOr(a.err, 2);
 }
 
@@ -1633,8 +1657,8 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     }
   });
   if (split) {
-    split_exchange<D, S, kCQ>(a, pair, half, s_ticket != 0, s, (uint32_t)q * kCQ, q == 0, lane, j,
-                              h, col_ok, crow, head, M, L, fin);
+    split_exchange<D, S, kWaves, kCQ>(a, pair, half, s_ticket != 0, s, wave, (uint32_t)q * kCQ,
+                                      q == 0, lane, j, h, col_ok, crow, head, M, L, fin);
     return;
   }
   float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
@@ -1678,7 +1702,7 @@ PrefillPlan plan_prefill_t(const PrefillArgs& a, int split_tiles, uint32_t cus) 
       ++p.split_blocks;
   }
   p.pairs = p.split_blocks * (uint32_t)per_block;
-  p.part_bytes = (size_t)p.pairs * 2 * S * ((D / 8) * 64 + 32) * 16;
+  p.part_bytes = (size_t)p.pairs * 2 * (S * ((D / 8) * 64 + 32) + S * pf::Shape<D>::Q) * 16;
   return p;
 }
 
