@@ -1231,19 +1231,18 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   constexpr int kCPW = (kChunks + S - 1) / S;    // chunks of a tile one wave of its group loads
   constexpr int kNC = D / 8;                     // 16-byte chunks per K row
   constexpr int kC = 4 * kNb;                    // float4 chunks of O^T held per lane
-  constexpr int kArr = 2 * Q * kT;               // halves per LDS array: one K and one V stage
   static_assert(Q == 1 || Q == 2 || Q == 4, "kv groups per stripe");
-  // N stages: loads run N-1 steps ahead of use (every wave issues the same number of loads per
-  // step, so the wait can count them). Three stages measured slower than two on C3-sized work
-  // (more live registers for one more step of lookahead), so two are used.
-  constexpr int N = 2;
-  constexpr int kDmaPerStep = 2 * kCPW;          // K and V loads one wave issues per step
-  // Array i holds K stage i and V stage (i - 1) mod N. Step k loads K(k+N) and V(k+N-1) into
-  // array k mod N and reads K(k+1) and V(k) from array (k+1) mod N; as distinct variables, the
-  // compiler sees that the loads in flight do not alias the reads and adds no waits for them.
+  // T tiles per barrier. An LDS array holds, for each kv group, T consecutive K tiles and T V
+  // tiles. Two arrays alternate: barrier-step m reads array (m + 1) mod 2 — K tiles Tm+1 .. Tm+T
+  // and V tiles Tm .. Tm+T-1, so step k = Tm + j reads K(k+1) and V(k) from sub-slot j — while
+  // step k loads K(k+T+1) and V(k+T) into sub-slot j of array m mod 2. As distinct variables,
+  // the compiler sees that the loads in flight do not alias the reads and adds no waits for them.
+  // Two tiles per barrier halve the per-barrier costs (the wait for the slowest wave, the first
+  // LDS read after it); at d = 256 two arrays of one tile already take 128 KB.
+  constexpr int T = D >= 256 ? 1 : 2;
+  constexpr int kArr = 2 * T * Q * kT;           // halves per LDS array
   __shared__ __attribute__((aligned(16))) _Float16 lx[kArr];
   __shared__ __attribute__((aligned(16))) _Float16 ly[kArr];
-  __shared__ __attribute__((aligned(16))) _Float16 lz[N == 3 ? kArr : 8];  // (third stage)
   __shared__ float2 s_ml[kWaves][32];
 
   // Kv heads vary fastest: consecutive workgroups land on different XCDs, so each XCD's L2 keeps
@@ -1328,21 +1327,22 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     const uint32_t x = base_bytes + min(k, g_last) * (32 * Q * 2 * D);
     return x >= cap_bytes ? x - cap_bytes : x;
   };
-  // This wave's chunk i of step k's K tile or V tile into LDS array `arr` (the group's tiles sit
-  // q tiles into the stage).
-  auto dma_k = [&](uint32_t k, _Float16* arr, int i) JMA_INL {
+  // Where sub-slot j of this wave's kv group sits in an LDS array, for K and for V.
+  auto k_slot = [&](_Float16* arr, int j) JMA_INL { return arr + (j * Q + q) * kT; };
+  auto v_slot = [&](_Float16* arr, int j) JMA_INL { return arr + T * Q * kT + (j * Q + q) * kT; };
+  // This wave's chunk i of step k's K tile or V tile into sub-slot j of LDS array `arr`.
+  auto dma_k = [&](uint32_t k, _Float16* arr, int j, int i) JMA_INL {
     const uint32_t c = s + S * i;
     if (c >= (uint32_t)kChunks) return;
-    pf::dma16(kbase, arr + q * kT + 512 * c, koff[i], tile_off(k));
+    pf::dma16(kbase, k_slot(arr, j) + 512 * c, koff[i], tile_off(k));
   };
-  auto dma_v = [&](uint32_t k, _Float16* arr, int i) JMA_INL {
+  auto dma_v = [&](uint32_t k, _Float16* arr, int j, int i) JMA_INL {
     const uint32_t c = s + S * i;
     if (c >= (uint32_t)kChunks) return;
-    pf::dma16(vbase, arr + Q * kT + q * kT + 512 * c, voff[i], tile_off(k));
+    pf::dma16(vbase, v_slot(arr, j) + 512 * c, voff[i], tile_off(k));
   };
   auto arr_of = [&](auto idx) JMA_INL -> _Float16* {
-    constexpr int i = decltype(idx)::value % N;
-    return i == 0 ? lx : (i == 1 ? ly : lz);
+    return decltype(idx)::value % 2 == 0 ? lx : ly;
   };
   // Waits until at most `outstanding` of this wave's loads are in flight, then barrier. (The
   // barrier is bare: __syncthreads() would also wait for the loads still meant to be in flight.)
@@ -1352,10 +1352,11 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
 
-  // The first K tile goes out before the Q loads, so the two latencies overlap.
+  // The first K tile goes out (to sub-slot 0 of array 0) before the Q loads, so the two latencies
+  // overlap.
   if (has_tile(0)) {
 #pragma unroll
-    for (int i = 0; i < kCPW; ++i) dma_k(0, lx, i);
+    for (int i = 0; i < kCPW; ++i) dma_k(0, lx, 0, i);
   }
 
   // Q^T operands: 8 consecutive dims of this lane's column per k-step, scaled by
@@ -1494,19 +1495,19 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   // V stages start zeroed: a step whose tile this wave does not see still runs its PV product,
   // with p = 0, and 0 * (anything the stage held) must be 0. Only cache data (finite) or zeros
   // ever reach a V stage.
-  for (int i = threadIdx.x; i < Q * kT / 8; i += 64 * kWaves) {
-    *(half8_t*)(lx + Q * kT + 8 * i) = half8_t{};
-    *(half8_t*)(ly + Q * kT + 8 * i) = half8_t{};
+  for (int i = threadIdx.x; i < T * Q * kT / 8; i += 64 * kWaves) {
+    *(half8_t*)(lx + T * Q * kT + 8 * i) = half8_t{};
+    *(half8_t*)(ly + T * Q * kT + 8 * i) = half8_t{};
   }
-  // Prologue: K(0) ready; the loads of "steps" 1-N .. -1 go out (K(j+1) and V(j) into array
-  // j+1); scores of step 0 (masked, maximum taken, accumulators scaled for it).
+  // Prologue: K(0) ready; the loads for barrier-step 0 go out (K(1) .. K(T) and V(0) .. V(T-1)
+  // into array 1); scores of step 0 (masked, maximum taken, accumulators scaled for it).
   wait_barrier(std::integral_constant<int, 0>{});
-  static_for<N - 1>([&](auto jj) JMA_INL {
+  static_for<T>([&](auto jj) JMA_INL {
     constexpr int jv = decltype(jj)::value;
 #pragma unroll
     for (int i = 0; i < kCPW; ++i) {
-      dma_k(jv + 1, arr_of(std::integral_constant<int, jv + 1>{}), i);
-      dma_v(jv, arr_of(std::integral_constant<int, jv + 1>{}), i);
+      dma_k(jv + 1, ly, jv, i);
+      dma_v(jv, ly, jv, i);
     }
   });
   // Masks step k's scores when some column does not see all of the tile (a tile this wave does
@@ -1516,31 +1517,32 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     return full(k) ? mask_max(sc, k, true) : mask_max(sc, k, false);
   };
   // Score tiles alternate between two register sets (even steps finish sa and compute sb).
-  float16_t sa = qk(lx + q * kT, no_issue), sb;
+  float16_t sa = qk(k_slot(lx, 0), no_issue), sb;
   rescale(sa, mask_step(sa, 0));
-  static_assert(N % 2 == 0, "the unrolled steps alternate the score registers");
 
   // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
   // before tile k+1's scores are computed.
   constexpr bool kOverlap = D <= 128;
-  // Step k (P = k mod N, fixed per unrolled copy): K(k+1) and V(k) are ready after the barrier;
-  // K(k+N) and V(k+N-1) are loaded into the array that K(k) and V(k-1) held. Every step runs
-  // the same code (one path, no register shuffling between paths); only the masking of partly
-  // visible tiles and the occasional rescale branch.
+  // Step k (P = k mod 2T, fixed per unrolled copy; sub-step j = P mod T of barrier-step m, whose
+  // parity is P / T): after the barrier that opens the barrier-step, K(k+1) and V(k) are ready
+  // in array (m + 1) mod 2; K(k+T+1) and V(k+T) are loaded into array m mod 2. Every step runs
+  // the same code; only the masking of partly visible tiles and the occasional rescale branch.
   auto step = [&](uint32_t k, auto kp) JMA_INL {
     constexpr int P = decltype(kp)::value;
+    constexpr int j = P % T;
     float16_t& scur = P % 2 == 0 ? sa : sb;
     float16_t& snxt = P % 2 == 0 ? sb : sa;
-    wait_barrier(std::integral_constant<int, (N - 2) * kDmaPerStep>{});
-    _Float16* const dst = arr_of(std::integral_constant<int, P>{});
-    const _Float16* const ksrc = arr_of(std::integral_constant<int, P + 1>{}) + q * kT;
-    const _Float16* const vsrc = arr_of(std::integral_constant<int, P + 1>{}) + Q * kT + q * kT;
+    if constexpr (j == 0) wait_barrier(std::integral_constant<int, 0>{});
+    _Float16* const dst = arr_of(std::integral_constant<int, P / T>{});
+    _Float16* const src = arr_of(std::integral_constant<int, P / T + 1>{});
+    const _Float16* const ksrc = k_slot(src, j);
+    const _Float16* const vsrc = v_slot(src, j);
     half8_t pf[2];
     auto spread = [&](int ks) JMA_INL {
       constexpr int kEvery = kKS / kCPW;
       if (ks % kEvery == 0) {
-        dma_k(k + N, dst, ks / kEvery);
-        dma_v(k + N - 1, dst, ks / kEvery);
+        dma_k(k + T + 1, dst, j, ks / kEvery);
+        dma_v(k + T, dst, j, ks / kEvery);
       }
     };
     if constexpr (kOverlap) {
@@ -1565,8 +1567,8 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   };
   // (The last copies are guarded inside the loop: remainder copies after it would double the
   // code the register allocator spans and spill.)
-  for (uint32_t k = 0; k < steps; k += N)
-    static_for<N>([&](auto pp) JMA_INL {
+  for (uint32_t k = 0; k < steps; k += 2 * T)
+    static_for<2 * T>([&](auto pp) JMA_INL {
       if (k + decltype(pp)::value < steps) step(k + decltype(pp)::value, pp);
     });
 
