@@ -14,7 +14,9 @@ Printed: one JSON line with
              over its average duration from HIP events bracketing the timed replays on the
              context stream, against 8 TB/s
   cpu_baseline  the CPU oracle (C restatement of backend-java's loop) on a bounded sample,
-             1 core, in the same unit
+             1 core, in the same unit (backend-java's decode attention is single-threaded); its
+             all_cores field runs the same loop on batches of independent layer-steps over
+             (layer-step, kv head) units on up to 16 threads (the GPU box's CPU share)
 and, as extra fields, us/token and the C3 prefill (S 2048, 24/8 heads, d 128) TFLOP/s.
 """
 
@@ -223,7 +225,26 @@ def cpu_baseline_c2(material, budget_s: float):
         if time.perf_counter() - t >= budget_s and runs >= 3:
             break
     per = (time.perf_counter() - t) / runs
-    return dict(seconds_per_layer_step=per, runs=runs, bytes=decode_bytes(p, hkv, d))
+    return dict(seconds_per_layer_step=per, runs=runs, bytes=decode_bytes(p, hkv, d),
+                q_rot=q_rot, keys=keys, values=values, scale=scale)
+
+
+def cpu_baseline_c2_all_cores(cpu, material, budget_s: float, threads: int):
+    """The same layer-step on `threads` threads: batches of 16 independent layer-steps (the 16
+    layers of one token), split over (layer-step, kv head) units, until about budget_s seconds."""
+    from oracle import oracle
+    _, _, _, p, hq, hkv, d, _ = material
+    batch = 16
+    qs, ks, vs = [cpu["q_rot"]] * batch, [cpu["keys"]] * batch, [cpu["values"]] * batch
+    runs = 0
+    t = time.perf_counter()
+    while True:
+        oracle.gqa_rows_batch(qs, ks, vs, hq, hkv, d, d, cpu["scale"], threads=threads)
+        runs += 1
+        if time.perf_counter() - t >= budget_s and runs >= 2:
+            break
+    per = (time.perf_counter() - t) / (runs * batch)
+    return dict(seconds_per_layer_step=per, runs=runs * batch)
 
 
 def main() -> int:
@@ -339,6 +360,15 @@ def main() -> int:
                       f"(backend-java groupedQueryAttention restated in C, oracle/), same "
                       f"algorithmic byte count as the GPU figure",
             "us_per_token": round(cpu["seconds_per_layer_step"] * 16 * 1e6, 1),
+        }
+        threads = max(1, min(16, os.cpu_count() or 1))
+        allc = cpu_baseline_c2_all_cores(cpu, c2["cpu_material"], args.cpu_seconds / 2, threads)
+        result["cpu_baseline"]["all_cores"] = {
+            "value": round(cpu["bytes"] / allc["seconds_per_layer_step"] / 1e9, 4),
+            "cores": threads,
+            "sample": f"{allc['runs']} C2 layer-steps at position {c2['cpu_material'][3]} in "
+                      f"batches of 16, (layer-step, kv head) units over {threads} threads",
+            "us_per_token": round(allc["seconds_per_layer_step"] * 16 * 1e6, 1),
         }
     print(json.dumps(result), flush=True)
     return 0
