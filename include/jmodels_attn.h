@@ -62,6 +62,7 @@ extern "C" {
 #define JMODELS_ATTN_CAP_RING_LAYERS (1ull << 5)     /* LayeredKvCache RING retention */
 #define JMODELS_ATTN_CAP_DEVICE_POINTERS (1ull << 6) /* *_device entry points */
 #define JMODELS_ATTN_CAP_QK_NORM (1ull << 7)         /* per-head RMS norm of q and k before RoPE */
+#define JMODELS_ATTN_CAP_VALUE_NORM (1ull << 8)      /* unweighted per-head RMS norm of v (Gemma 4) */
 
 /* KV storage element types. F16 stores IEEE binary16 (round to nearest even), which widens to
  * exactly Float.float16ToFloat(Float.floatToFloat16(x)) — the reference's half-precision KV
@@ -87,7 +88,8 @@ typedef struct jmodels_attn_norm jmodels_attn_norm;
  *   rope            NULL = this layer applies no RoPE (LlamaConfig.usesRope false)
  *   qk_norm         NULL = no QK-norm; else each q and k head is RMS-normalised with the
  *                   object's weights before RoPE (normalizeHead, BJ/llama/LlamaForwardPass.java:
- *                   1070-1083, 1672-1676) */
+ *                   1070-1083, 1672-1676), and each v head without a weight when the object
+ *                   was made with JMODELS_ATTN_NORM_VALUE_RMS */
 typedef struct jmodels_attn_layer {
   uint32_t layer;
   uint32_t num_heads;
@@ -144,6 +146,17 @@ JMODELS_ATTN_API int32_t jmodels_attn_rope_destroy(jmodels_attn_rope* rope);
 JMODELS_ATTN_API int32_t jmodels_attn_norm_create(jmodels_attn_context* ctx, uint32_t head_dim,
                                  const float* q_weight, const float* k_weight, float eps,
                                  jmodels_attn_norm** norm_out);
+/* jmodels_attn_norm_create with flags. JMODELS_ATTN_NORM_VALUE_RMS also normalises each value
+ * head without a weight before it is stored, as Gemma4ForwardPass does (BJ/gemma4/
+ * Gemma4ForwardPass.java:990-996): Gemma4Math.normalizeWithoutWeight (BJ/gemma4/Gemma4Math.java:
+ * 38-55), v * (float)(1 / sqrt(sum(v^2) / head_dim + eps)) with the mean and eps added in float
+ * and the square root and reciprocal in double; eps must then be finite and > 0, and head_dim must
+ * also equal the cache's value_length. Gemma 4 layers without a value projection pass the raw
+ * keys as v (BJ/gemma4/Gemma4ForwardPass.java:966-968). Unknown flag bits: INVALID_SHAPE. */
+#define JMODELS_ATTN_NORM_VALUE_RMS 1u
+JMODELS_ATTN_API int32_t jmodels_attn_norm_create_ex(jmodels_attn_context* ctx, uint32_t head_dim,
+                                    const float* q_weight, const float* k_weight, float eps,
+                                    uint32_t flags, jmodels_attn_norm** norm_out);
 JMODELS_ATTN_API int32_t jmodels_attn_norm_destroy(jmodels_attn_norm* norm);
 
 /* ---------------------------------------------------------------- KV cache */

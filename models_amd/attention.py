@@ -51,6 +51,9 @@ CAP_SLIDING_WINDOW = 1 << 4
 CAP_RING_LAYERS = 1 << 5
 CAP_DEVICE_POINTERS = 1 << 6
 CAP_QK_NORM = 1 << 7
+CAP_VALUE_NORM = 1 << 8
+
+NORM_VALUE_RMS = 1
 
 KV_F32 = 0
 KV_F16 = 1
@@ -65,7 +68,8 @@ EXPORTS = (
     "jmodels_attn_append", "jmodels_attn_attend", "jmodels_attn_decode", "jmodels_attn_prefill",
     "jmodels_attn_append_device", "jmodels_attn_attend_device", "jmodels_attn_decode_device",
     "jmodels_attn_prefill_device", "jmodels_attn_attend_causal",
-    "jmodels_attn_attend_causal_device", "jmodels_attn_norm_create", "jmodels_attn_norm_destroy",
+    "jmodels_attn_attend_causal_device", "jmodels_attn_norm_create", "jmodels_attn_norm_create_ex",
+    "jmodels_attn_norm_destroy",
 )
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -116,6 +120,7 @@ def _declare(lib: ctypes.CDLL) -> None:
                                             ctypes.POINTER(_vp)]),
         "jmodels_attn_rope_destroy": (_i32, [_vp]),
         "jmodels_attn_norm_create": (_i32, [_vp, _u32, _vp, _vp, _cf, ctypes.POINTER(_vp)]),
+        "jmodels_attn_norm_create_ex": (_i32, [_vp, _u32, _vp, _vp, _cf, _u32, ctypes.POINTER(_vp)]),
         "jmodels_attn_norm_destroy": (_i32, [_vp]),
         "jmodels_attn_kv_create": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp,
                                           ctypes.POINTER(_vp)]),
@@ -245,8 +250,8 @@ class HipAttentionLibrary:
                               frequency_factors)
 
     def qk_norm(self, head_dim: int, q_weight=None, k_weight=None,
-                eps: float = 1e-6) -> "HipQkNorm":
-        return HipQkNorm(self, head_dim, q_weight, k_weight, eps)
+                eps: float = 1e-6, value_rms: bool = False) -> "HipQkNorm":
+        return HipQkNorm(self, head_dim, q_weight, k_weight, eps, value_rms)
 
     def kv_cache(self, num_layers: int, max_seq_len: int, num_kv_heads: int, key_length: int,
                  value_length: int, half_precision: bool = True, sequences: int = 1,
@@ -285,9 +290,12 @@ class HipRotaryTable:
 class HipQkNorm:
     """A layer's attn_q_norm / attn_k_norm weights (llama/LlamaWeights.java:99-101) in HBM; each q
     and k head is RMS-normalised with them before RoPE (LlamaForwardPass.normalizeHead, :1672-1676).
-    A missing weight (None) leaves that side unnormalised, as an empty weight array does."""
+    A missing weight (None) leaves that side unnormalised, as an empty weight array does. With
+    value_rms, each value head is also RMS-normalised without a weight before it is stored
+    (Gemma4ForwardPass, gemma4/Gemma4ForwardPass.java:990-996; Gemma4Math.normalizeWithoutWeight)."""
 
-    def __init__(self, owner: HipAttentionLibrary, head_dim: int, q_weight, k_weight, eps: float):
+    def __init__(self, owner: HipAttentionLibrary, head_dim: int, q_weight, k_weight, eps: float,
+                 value_rms: bool = False):
         self.owner = owner
         qw = None if q_weight is None else _f32(q_weight)
         kw = None if k_weight is None else _f32(k_weight)
@@ -295,11 +303,11 @@ class HipQkNorm:
             if w is not None and w.size != head_dim:
                 raise ValueError(f"norm weight has {w.size} elements, head_dim is {head_dim}")
         out = _vp()
-        owner.check(owner.lib.jmodels_attn_norm_create(
+        owner.check(owner.lib.jmodels_attn_norm_create_ex(
             owner.ctx, head_dim, None if qw is None else _ptr(qw), None if kw is None else _ptr(kw),
-            eps, ctypes.byref(out)), "norm_create")
+            eps, NORM_VALUE_RMS if value_rms else 0, ctypes.byref(out)), "norm_create")
         self.handle = out.value
-        self.head_dim, self.eps = head_dim, eps
+        self.head_dim, self.eps, self.value_rms = head_dim, eps, value_rms
 
     def close(self) -> None:
         if getattr(self, "handle", None):

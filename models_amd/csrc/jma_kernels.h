@@ -55,6 +55,7 @@ struct AppendArgs {
   const float* q_norm_w;    // [dk] QK-norm weights applied before RoPE; null = none
   const float* k_norm_w;
   float norm_eps;
+  uint32_t v_norm;          // 1: each v head RMS-normalised without a weight before it is stored
   RowList rows;
 };
 

@@ -84,6 +84,21 @@ __device__ __forceinline__ void head_rms_norm(const float* x, uint32_t d, const 
   y1 = y1 * scale * w[e1];
 }
 
+// Unweighted RMS norm of one value head before it is stored (Gemma4Math.normalizeWithoutWeight,
+// gemma4/Gemma4Math.java:38-55, applied at gemma4/Gemma4ForwardPass.java:990-996): sumSq of the
+// head in order, inverse = (float)(1 / sqrt(sumSq / d + eps)) with the mean and eps added in float
+// and the square root and reciprocal in double, element = x * inverse. Every thread of the head
+// computes the same sum, so the stored values are the oracle's bit for bit.
+__device__ __forceinline__ void value_rms_norm(const float* x, uint32_t d, float eps, float& y0,
+                                               float& y1) {
+#pragma clang fp contract(off)
+  float ss = 0.0f;
+  for (uint32_t i = 0; i < d; ++i) ss = ss + x[i] * x[i];
+  const float inverse = (float)(1.0 / sqrt((double)(ss / (float)d + eps)));
+  y0 = y0 * inverse;
+  y1 = y1 * inverse;
+}
+
 // One thread per element pair of a row: a RoPE pair of q or k (or a pass-through pair beyond the
 // rotary dims), or two V elements. Every load a thread needs is independent of the others, so a
 // row costs one memory round trip.
@@ -135,8 +150,9 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const AppendArgs a) {
   }
   const uint32_t wi = w - q_pairs - k_pairs;
   const uint32_t h = wi / half_v, d = 2 * (wi % half_v);
-  const float* x = a.v + ((uint64_t)row * a.num_kv_heads + h) * a.dv + d;
-  const float v0 = x[0], v1 = x[1];
+  const float* vh = a.v + ((uint64_t)row * a.num_kv_heads + h) * a.dv;
+  float v0 = vh[d], v1 = vh[d + 1];
+  if (a.v_norm) value_rms_norm(vh, a.dv, a.norm_eps, v0, v1);
   const uint32_t blk = slot / kBlk, r = slot % kBlk;
   const uint32_t s = kF16 ? perm32(r) : r;
   KV* vb = (KV*)a.kv.v + seq * a.kv.seq_stride_v + a.kv.layer_off_v +

@@ -126,6 +126,7 @@ struct jmodels_attn_norm {
   float eps = 0.0f;
   float* d_q = nullptr;  // null: q heads are not normalised
   float* d_k = nullptr;
+  bool v_rms = false;    // v heads are RMS-normalised without a weight (Gemma 4)
 };
 
 struct jmodels_attn_kv {
@@ -241,7 +242,9 @@ LayerCall resolve_layer(const jmodels_attn_kv* kv, const jmodels_attn_layer* p) 
     require(c.norm->ctx == kv->ctx, JMODELS_ATTN_INVALID_SHAPE, "qk-norm belongs to another context");
     require(c.norm->head_dim == kv->dk, JMODELS_ATTN_INVALID_SHAPE,
             "qk-norm head_dim differs from key_length");
-    if (!c.norm->d_q && !c.norm->d_k) c.norm = nullptr;
+    require(!c.norm->v_rms || c.norm->head_dim == kv->dv, JMODELS_ATTN_INVALID_SHAPE,
+            "value norm head_dim differs from value_length");
+    if (!c.norm->d_q && !c.norm->d_k && !c.norm->v_rms) c.norm = nullptr;
   }
   return c;
 }
@@ -326,6 +329,7 @@ void run_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall&
     a.q_norm_w = lc.norm->d_q;
     a.k_norm_w = lc.norm->d_k;
     a.norm_eps = lc.norm->eps;
+    a.v_norm = lc.norm->v_rms ? 1u : 0u;
   }
   a.rows = rows;
   hip_check(jma::launch_append(a, kv->f16(), ctx->stream), "rope_append launch");
@@ -612,7 +616,8 @@ uint32_t jmodels_attn_abi_version(void) { return JMODELS_ATTN_ABI_VERSION; }
 uint64_t jmodels_attn_capabilities(void) {
   return JMODELS_ATTN_CAP_DECODE_F32 | JMODELS_ATTN_CAP_DECODE_F16 | JMODELS_ATTN_CAP_PREFILL_MFMA |
          JMODELS_ATTN_CAP_RAGGED_DECODE | JMODELS_ATTN_CAP_SLIDING_WINDOW |
-         JMODELS_ATTN_CAP_RING_LAYERS | JMODELS_ATTN_CAP_DEVICE_POINTERS | JMODELS_ATTN_CAP_QK_NORM;
+         JMODELS_ATTN_CAP_RING_LAYERS | JMODELS_ATTN_CAP_DEVICE_POINTERS | JMODELS_ATTN_CAP_QK_NORM |
+         JMODELS_ATTN_CAP_VALUE_NORM;
 }
 
 const char* jmodels_attn_status_name(int32_t status) {
@@ -768,17 +773,28 @@ int32_t jmodels_attn_rope_destroy(jmodels_attn_rope* rope) {
 
 int32_t jmodels_attn_norm_create(jmodels_attn_context* ctx, uint32_t head_dim, const float* q_weight,
                                  const float* k_weight, float eps, jmodels_attn_norm** norm_out) {
+  return jmodels_attn_norm_create_ex(ctx, head_dim, q_weight, k_weight, eps, 0u, norm_out);
+}
+
+int32_t jmodels_attn_norm_create_ex(jmodels_attn_context* ctx, uint32_t head_dim,
+                                    const float* q_weight, const float* k_weight, float eps,
+                                    uint32_t flags, jmodels_attn_norm** norm_out) {
   return guard([&] {
     check_ctx(ctx);
     require(norm_out != nullptr, JMODELS_ATTN_NULL_POINTER, "norm_out is null");
     *norm_out = nullptr;
     require(head_dim > 0 && head_dim <= 4096, JMODELS_ATTN_INVALID_SHAPE, "head_dim must be in [1, 4096]");
     require(isfinite(eps) && eps >= 0.0f, JMODELS_ATTN_INVALID_SHAPE, "eps must be finite and >= 0");
+    require((flags & ~JMODELS_ATTN_NORM_VALUE_RMS) == 0, JMODELS_ATTN_INVALID_SHAPE, "unknown norm flags");
+    const bool v_rms = (flags & JMODELS_ATTN_NORM_VALUE_RMS) != 0;
+    // Gemma4Math.normalizeWithoutWeight rejects eps that is not finite and > 0 (:47-49).
+    require(!v_rms || eps > 0.0f, JMODELS_ATTN_INVALID_SHAPE, "value norm eps must be > 0");
     hip_check(hipSetDevice(ctx->device), "hipSetDevice");
     auto* norm = new jmodels_attn_norm();
     norm->ctx = ctx;
     norm->head_dim = head_dim;
     norm->eps = eps;
+    norm->v_rms = v_rms;
     const size_t bytes = (size_t)head_dim * sizeof(float);
     try {
       if (q_weight) {

@@ -171,6 +171,18 @@ int jmo_softmax(float* x, int size) {
   return JMO_OK;
 }
 
+int jmo_value_rms_norm(float* out, const float* in, int length, float eps) {
+  /* Gemma4Math.normalizeWithoutWeight (gemma4/Gemma4Math.java:38-55): sumSquares as a float dot
+   * product (sequential here; vectors-core's lane order is unpinned), inverse =
+   * (float)(1.0 / Math.sqrt(sumSquares / length + eps)) with the mean and the epsilon added in
+   * float and the square root and reciprocal in double, then out = in * inverse. */
+  if (length <= 0 || !(eps > 0.0f) || !isfinite(eps)) return JMO_ILLEGAL_ARGUMENT;
+  float sum_sq = jmo_dot(in, in, length);
+  float inverse = (float)(1.0 / sqrt((double)(sum_sq / (float)length + eps)));
+  for (int i = 0; i < length; i++) out[i] = in[i] * inverse;
+  return JMO_OK;
+}
+
 float jmo_dot(const float* a, const float* b, int n) {
   float sum = 0.0f;
   for (int i = 0; i < n; i++) sum += a[i] * b[i];

@@ -72,6 +72,9 @@ void jmo_qk_norm_heads(float* x, int heads, int head_dim, const float* weight, f
 /* VectorUtil.dotProduct restated as a sequential float sum (vectors-core is not vendored, so its
  * lane order is unpinned; see oracle.py). */
 float jmo_dot(const float* a, const float* b, int n);
+/* Gemma4Math.normalizeWithoutWeight (gemma4/Gemma4Math.java:38-55); ILLEGAL_ARGUMENT for
+ * length <= 0 or eps not finite and > 0. out may equal in. */
+int jmo_value_rms_norm(float* out, const float* in, int length, float eps);
 
 /* ---------------------------------------------------------------- KvCache (linear, growing) */
 

@@ -87,6 +87,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "jmo_rms_norm": (None, [_f32p, _f32p, _f32p, c_int, c_float]),
         "jmo_qk_norm_heads": (None, [_f32p, c_int, c_int, _f32p, c_float]),
         "jmo_dot": (c_float, [_f32p, _f32p, c_int]),
+        "jmo_value_rms_norm": (c_int, [_f32p, _f32p, c_int, c_float]),
         "jmo_kv_create": (c_void, [c_int, c_int, c_int, c_int, c_int]),
         "jmo_kv_destroy": (None, [c_void]),
         "jmo_kv_store": (c_int, [c_void, c_int, c_int, _f32p, _f32p]),
@@ -233,6 +234,26 @@ def qk_norm_heads(x, heads: int, head_dim: int, weight, eps: float) -> np.ndarra
     assert v.size == heads * head_dim and w.size == head_dim
     lib().jmo_qk_norm_heads(_ptr(v), heads, head_dim, _ptr(w), eps)
     return v
+
+
+def value_rms_norm(x, eps: float, offset: int = 0, length: int = None) -> np.ndarray:
+    """Gemma4Math.normalizeWithoutWeight over x[offset:offset+length] (a copy of x; the rest
+    unchanged)."""
+    v = _f32(x).copy()
+    length = v.size - offset if length is None else length
+    seg = v[offset:offset + length].copy()
+    _check(lib().jmo_value_rms_norm(_ptr(seg), _ptr(seg), length, eps), "value_rms_norm")
+    v[offset:offset + length] = seg
+    return v
+
+
+def value_rms_heads(x, heads: int, head_dim: int, eps: float) -> np.ndarray:
+    """normalizeWithoutWeight applied to each of ``heads`` consecutive heads (a copy of x), as
+    Gemma4ForwardPass does to every value head (gemma4/Gemma4ForwardPass.java:990-996)."""
+    v = _f32(x).reshape(-1)
+    assert v.size == heads * head_dim
+    return np.concatenate([value_rms_norm(v[h * head_dim:(h + 1) * head_dim], eps)
+                           for h in range(heads)])
 
 
 def attention_start(position: int, window: int) -> int:

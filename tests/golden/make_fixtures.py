@@ -307,6 +307,18 @@ def rms_norm_cases():
     ]
 
 
+def value_norm_cases():
+    # Gemma4MathTest (gemma4/Gemma4MathTest.java:28-38): normalizeWithoutWeight over values[1..2]
+    # of {99, 3, 4, 98} with eps 1e-6; the neighbours stay untouched.
+    return [
+        {"name": "normalizesAnUnweightedHeadInPlaceWithoutTouchingAdjacentValues",
+         "src": "gemma4/Gemma4MathTest.java:28-38",
+         "values": [99.0, 3.0, 4.0, 98.0], "offset": 1, "length": 2, "eps": 1e-6,
+         "expect_equal": [[0, 99.0], [3, 98.0]],
+         "expect_close": [[1, 0.8485281, 1e-6], [2, 1.1313708, 1e-6]]},
+    ]
+
+
 def window_cases():
     # EncoderAttentionWindowTest CausalWindow (GEMMA3, window 512, pattern 6): layer 0 slides,
     # layer 5 is global (:37-40, 128-145); LlamaConfig.usesSlidingWindow (:157-162).
@@ -339,6 +351,7 @@ def main():
         "rope": rope_cases(),
         "softmax": softmax_cases(),
         "rms_norm": rms_norm_cases(),
+        "value_norm": value_norm_cases(),
         "attention_start": window_cases(),
         "sliding_layers": sliding_layers(),
     }

@@ -49,7 +49,8 @@ def test_abi_version_and_capabilities(lib):
     assert lib.jmodels_attn_abi_version() == A.ABI_VERSION == 2
     caps = lib.jmodels_attn_capabilities()
     for bit in (A.CAP_DECODE_F32, A.CAP_DECODE_F16, A.CAP_PREFILL_MFMA, A.CAP_RAGGED_DECODE,
-                A.CAP_SLIDING_WINDOW, A.CAP_RING_LAYERS, A.CAP_DEVICE_POINTERS, A.CAP_QK_NORM):
+                A.CAP_SLIDING_WINDOW, A.CAP_RING_LAYERS, A.CAP_DEVICE_POINTERS, A.CAP_QK_NORM,
+                A.CAP_VALUE_NORM):
         assert caps & bit
 
 
@@ -67,6 +68,9 @@ def test_null_handles_are_rejected_without_a_gpu(lib):
     assert lib.jmodels_attn_rope_destroy(None) == A.NULL_POINTER
     assert lib.jmodels_attn_kv_destroy(None) == A.NULL_POINTER
     assert lib.jmodels_attn_norm_destroy(None) == A.NULL_POINTER
+    h = ctypes.c_void_p()
+    assert lib.jmodels_attn_norm_create_ex(None, 64, None, None, 1e-6, A.NORM_VALUE_RMS,
+                                           ctypes.byref(h)) == A.NULL_POINTER
     out_h = ctypes.c_void_p()
     assert lib.jmodels_attn_norm_create(None, 128, None, None, 1e-6, ctypes.byref(out_h)) == \
         A.NULL_POINTER

@@ -214,6 +214,69 @@ def test_qk_norm_prefill_then_decode(hip, half):
         rope.close()
 
 
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("d", [128, 256])
+def test_gemma4_value_norm_prefill_then_decode(hip, half, d):
+    """Gemma-4-shaped layer (Gemma4ForwardPass.executeLayer, gemma4/Gemma4ForwardPass.java:955-1006):
+    q and k heads RMS-normalised with weights, every v head RMS-normalised without a weight
+    (Gemma4Math.normalizeWithoutWeight), NeoX RoPE, scale 1.0; a layer without a value projection
+    passes the raw keys as v (:966-968). 200 prior rows through the prefill, then 3 decode steps,
+    against the oracle fed the host-normalised q, k and v; the stored K and V rows are the
+    oracle's bit for bit."""
+    hq, hkv, prior, steps, theta, eps = 8, 2, 200, 3, 1e6, 1e-6
+    n = prior + steps
+    close = assert_f16_close if half else assert_f32_close
+    for k_as_v in (False, True):
+        q = normal(14, f"g4/q{d}", (n, hq * d))
+        k = normal(14, f"g4/k{d}", (n, hkv * d))
+        v = k.copy() if k_as_v else normal(14, f"g4/v{d}", (n, hkv * d))
+        wq = normal(14, f"g4/wq{d}", (d,)) * 0.2 + 1.0
+        wk = normal(14, f"g4/wk{d}", (d,)) * 0.2 + 1.0
+        qn = _qk_norm_rows(q, hq, d, wq, eps)
+        kn = _qk_norm_rows(k, hkv, d, wk, eps)
+        vn = np.stack([oracle.value_rms_heads(row, hkv, d, eps) for row in v])
+        ref = OracleKv(1, 512, hkv * d, hkv * d, half_precision=half)
+        ref_prefill, _, _ = ref.prefill_layer(0, 0, qn[:prior], kn[:prior], vn[:prior], hq, hkv,
+                                              d, d, theta, 1.0, True, 1.0)
+        ref_dec = [ref.decode_layer(0, prior + s, qn[prior + s], kn[prior + s], vn[prior + s], hq,
+                                    hkv, d, d, theta, 1.0, True, 1.0)[0] for s in range(steps)]
+        rope = hip.rotary_table(d, theta, 1.0, max_positions=512)
+        kv = hip.kv_cache(1, 512, hkv, d, d, half_precision=half)
+        norm = hip.qk_norm(d, wq, wk, eps, value_rms=True)
+        try:
+            layer = A.AttentionLayer(0, hq, neox=True, scale=1.0, rope=rope, qk_norm=norm)
+            got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior])
+            e = [close(got_prefill, ref_prefill, f"Gemma-4 prefill d {d} k_as_v {k_as_v}")]
+            for s in range(steps):
+                got = kv.decode(layer, [prior + s], q[prior + s], k[prior + s], v[prior + s])
+                e.append(close(got, ref_dec[s], f"Gemma-4 decode d {d} step {s}"))
+            _say(f"Gemma-4 d={d} half={half} k_as_v={k_as_v} errors " + " ".join(f"{x:.2e}" for x in e))
+            np.testing.assert_array_equal(kv.key_slice(0, 0, n), ref.key_slice(0, 0, n))
+            np.testing.assert_array_equal(kv.value_slice(0, 0, n), ref.value_slice(0, 0, n))
+        finally:
+            norm.close()
+            kv.close()
+            rope.close()
+
+
+def test_value_norm_rejects_bad_shapes(hip):
+    """normalizeWithoutWeight rejects eps <= 0 (gemma4/Gemma4Math.java:47-49); the value norm's
+    head_dim must equal the cache's value_length."""
+    with pytest.raises(A.AttentionStatusError) as info:
+        hip.qk_norm(64, None, None, 0.0, value_rms=True)
+    assert info.value.status == A.INVALID_SHAPE
+    norm = hip.qk_norm(64, None, None, 1e-6, value_rms=True)
+    kv = hip.kv_cache(1, 8, 1, 64, 128, half_precision=False)
+    try:
+        layer = A.AttentionLayer(0, 1, qk_norm=norm)
+        with pytest.raises(A.AttentionStatusError) as info:
+            kv.append(layer, [0], np.ones(64), np.ones(64), np.ones(128))
+        assert info.value.status == A.INVALID_SHAPE
+    finally:
+        kv.close()
+        norm.close()
+
+
 def test_qk_norm_rejects_bad_weights(hip):
     with pytest.raises(ValueError):
         hip.qk_norm(64, np.ones(32), None)

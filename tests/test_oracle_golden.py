@@ -226,3 +226,14 @@ def test_rms_norm_known_answers(oracle, known_answers):
         out = oracle.rms_norm(case["x"], case["weight"], case["eps"])
         for i, want, tol in case["expect_close"]:
             assert abs(float(out[i]) - want) <= tol, (case["name"], i, out[i], want)
+
+
+def test_value_norm_known_answers(oracle, known_answers):
+    # Gemma4MathTest.normalizesAnUnweightedHeadInPlaceWithoutTouchingAdjacentValues
+    # (gemma4/Gemma4MathTest.java:28-38).
+    for case in known_answers["value_norm"]:
+        out = oracle.value_rms_norm(case["values"], case["eps"], case["offset"], case["length"])
+        for i, want in case["expect_equal"]:
+            assert float(out[i]) == want, (case["name"], i)
+        for i, want, tol in case["expect_close"]:
+            assert abs(float(out[i]) - want) <= tol, (case["name"], i, out[i], want)

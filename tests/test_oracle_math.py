@@ -245,3 +245,27 @@ def test_rms_norm_against_float64_and_in_place(oracle):
         np.testing.assert_array_equal(out[:d], got)  # in place (per head) == out of place
         np.testing.assert_allclose(out[d:2 * d], got, rtol=4e-6)  # scale invariance
         np.testing.assert_array_equal(out[2 * d:], np.zeros(d, np.float32))
+
+
+def test_value_rms_norm_against_float64_and_rejections(oracle):
+    # normalizeWithoutWeight: x / sqrt(mean(x^2) + eps) with no weight, computed in float64; the
+    # oracle's float sum and its double reciprocal stay within a few ulp. A weight applied, a wrong
+    # divisor or a missing eps fails this; eps <= 0 or non-finite is rejected as the reference's
+    # IllegalArgumentException (gemma4/Gemma4Math.java:47-49).
+    rng = np.random.default_rng(6)
+    for d in (2, 16, 64, 128, 256):
+        x = rng.standard_normal(d).astype(np.float32) * 3
+        ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6)
+        got = oracle.value_rms_norm(x, 1e-6)
+        np.testing.assert_allclose(got, ref, rtol=4e-6, atol=0)
+        heads = np.concatenate([x, 2 * x, np.zeros(d, np.float32)])
+        out = oracle.value_rms_heads(heads, 3, d, 1e-6)
+        np.testing.assert_array_equal(out[:d], got)
+        np.testing.assert_allclose(out[d:2 * d], got, rtol=4e-6)  # scale invariance
+        np.testing.assert_array_equal(out[2 * d:], np.zeros(d, np.float32))
+    # A large eps dominates: x / sqrt(eps) for a small x.
+    x = np.full(4, 1e-3, np.float32)
+    np.testing.assert_allclose(oracle.value_rms_norm(x, 1.0), x / np.sqrt(1.0 + 1e-6), rtol=1e-6)
+    for eps in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(oracle.OracleError):
+            oracle.value_rms_norm(np.ones(4, np.float32), eps)
