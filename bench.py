@@ -17,7 +17,8 @@ Printed: one JSON line with
              1 core, in the same unit (backend-java's decode attention is single-threaded); its
              all_cores field runs the same loop on batches of independent layer-steps over
              (layer-step, kv head) units on up to 16 threads (the GPU box's CPU share)
-and, as extra fields, us/token and the C3 prefill (S 2048, 24/8 heads, d 128) TFLOP/s.
+and, as extra fields, us/token, the C3 prefill (S 2048, 24/8 heads, d 128) TFLOP/s and the C4
+ragged decode (64 sessions up to 16384 positions, one launch) GB/s.
 """
 
 from __future__ import annotations
@@ -206,6 +207,52 @@ def run_c3(hip, A, rt, synth, reps: int = 10):
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
 
 
+def run_c4(hip, A, rt, synth, reps: int = 10):
+    """C4 ragged decode attention at full size: 64 sessions, KV lengths drawn
+    uniformly from [256, 16384], 12 Q / 2 KV heads, d 128, NeoX theta 1e6, f16 KV. The cache is
+    filled once; the timed launches are the split-K attention of one query row per session over
+    its L visible positions (`attend_device`, the new token's append excluded), inputs resident."""
+    hq, hkv, d, B, theta = 12, 2, 128, 64, 1e6
+    lens = [int(x) for x in synth.uniform_int(4, "bench/c4/len", B, 256, 16384)]
+    maxlen = max(lens)
+    qd, kd = hq * d, hkv * d
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=maxlen)
+    kv = hip.kv_cache(1, maxlen, hkv, d, d, half_precision=True, sequences=B)
+    layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+    zq = rt.DeviceArray(maxlen * qd)
+    zq.zero()
+    dk, dv = rt.DeviceArray(maxlen * kd), rt.DeviceArray(maxlen * kd)
+    t0 = time.time()
+    for s, L in enumerate(lens):
+        dk.upload(synth.normal(4, f"bench/c4/k{s}", (L, kd)))
+        dv.upload(synth.normal(4, f"bench/c4/v{s}", (L, kd)))
+        kv.append_device(layer, np.full(L, s, np.uint32), np.arange(L), zq.ptr, L * qd,
+                         dk.ptr, L * kd, dv.ptr, L * kd)
+    hip.synchronize()
+    log(f"C4 cache filled ({sum(lens)} rows, {time.time() - t0:.1f}s)")
+    dq = rt.DeviceArray(B * qd)
+    dq.upload(synth.normal(4, "bench/c4/q", (B, qd)))
+    dout = rt.DeviceArray(B * qd)
+    seqs, pos = np.arange(B), np.array(lens) - 1
+    for _ in range(2):
+        kv.attend_device(layer, seqs, pos, dq.ptr, B * qd, dout.ptr, B * qd)
+    hip.synchronize()
+    stream = hip.stream()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(stream)
+    for _ in range(reps):
+        kv.attend_device(layer, seqs, pos, dq.ptr, B * qd, dout.ptr, B * qd)
+    e1.record(stream)
+    hip.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    nbytes = 2 * sum(lens) * hkv * d * 2
+    for buf in (zq, dk, dv, dq, dout):
+        buf.free()
+    kv.close()
+    rope.close()
+    return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, rows=sum(lens))
+
+
 def cpu_baseline_c2(material, budget_s: float):
     """backend-java's decode attention restated in C (oracle/), one thread, on repeated C2
     layer-steps at the last decoded position until about budget_s seconds of CPU work ran."""
@@ -255,6 +302,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill figure")
+    ap.add_argument("--no-c4", action="store_true", help="skip the C4 ragged decode figure")
+    ap.add_argument("--c4-only", action="store_true",
+                    help="profiling aid: run only the C4 ragged decode measurement, print its figures")
     ap.add_argument("--prefill-only", action="store_true",
                     help="profiling aid: run only the C3 prefill measurement, print its figures")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -288,6 +338,11 @@ def main() -> int:
         print(json.dumps({"prefill_us": round(c3["ms"] * 1e3, 2), "tflops": round(c3["tflops"], 2),
                           "flops": c3["flops"]}), flush=True)
         return 0
+    if args.c4_only:
+        c4 = run_c4(hip, A, rt, synth)
+        print(json.dumps({"c4_us": round(c4["ms"] * 1e3, 2), "gbs": round(c4["gbs"], 1),
+                          "bytes": c4["bytes"]}), flush=True)
+        return 0
     c2 = run_c2(hip, A, rt, synth, args.steps, args.warmup)
     log(f"C2: {args.steps} steps in {c2['elapsed'] * 1e3:.2f} ms; decode kernel "
         f"{c2['timed_kernel_ms'] * 1e3:.2f} us per launch in the timed replays, "
@@ -296,6 +351,10 @@ def main() -> int:
     if not args.no_prefill:
         c3 = run_c3(hip, A, rt, synth)
         log(f"C3 prefill: {c3['ms'] * 1e3:.1f} us, {c3['tflops']:.1f} TFLOP/s")
+    c4 = None
+    if not args.no_c4:
+        c4 = run_c4(hip, A, rt, synth)
+        log(f"C4 ragged decode: {c4['ms'] * 1e3:.1f} us, {c4['gbs']:.0f} GB/s")
     hip.close()
 
     value = c2["algo_bytes"] / c2["elapsed"] / 1e9
@@ -347,6 +406,16 @@ def main() -> int:
             "us": round(c3["ms"] * 1e3, 2),
             "frac_of_f16_mfma_peak": round(c3["tflops"] / F16_MFMA_PEAK_TFLOPS, 4),
             "flops": c3["flops"],
+        }
+    if c4 is not None:
+        result["ragged_decode"] = {
+            "workload": "C4 Qwen2.5-1.5B-shaped ragged decode attention: 64 sessions, KV lengths "
+                        "U[256, 16384], 12 Q / 2 KV heads, d 128, f16 KV, one query row each",
+            "gbs": round(c4["gbs"], 1),
+            "us": round(c4["ms"] * 1e3, 2),
+            "frac_of_hbm_peak": round(c4["gbs"] / HBM_PEAK_GBS, 4),
+            "bytes": c4["bytes"],
+            "kv_rows": c4["rows"],
         }
     if not args.no_cpu:
         cpu = cpu_baseline_c2(c2["cpu_material"], args.cpu_seconds)

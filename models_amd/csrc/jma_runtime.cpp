@@ -106,7 +106,7 @@ struct jmodels_attn_context {
   hipStream_t stream = nullptr;
   int* d_err = nullptr;
   DeviceBuffer part_acc, part_ml, part_f, counters, pf_part, pf_tickets, qrot, stage_q, stage_k, stage_v, stage_out;
-  int decode_target_blocks = 256;   // workgroups a decode launch aims for (256 CUs)
+  int decode_target_blocks = 512;   // workgroups a decode launch aims for (two per CU)
   int tiles_per_wave = 1;           // minimum tiles each decode wave streams
   int prefill_split_tiles = -1;     // split prefill row blocks of this many kv tiles; -1: automatic
   uint32_t cus = 256;               // compute units of the device
@@ -650,7 +650,7 @@ jmodels_attn_context* jmodels_attn_context_create(int32_t device) {
     hip_check(hipSetDevice(device), "hipSetDevice");
     auto* ctx = new jmodels_attn_context();
     ctx->device = device;
-    ctx->decode_target_blocks = std::max(1, env_int("JMA_DECODE_TARGET_BLOCKS", 256));
+    ctx->decode_target_blocks = std::max(1, env_int("JMA_DECODE_TARGET_BLOCKS", 512));
     ctx->tiles_per_wave = std::max(1, env_int("JMA_DECODE_TILES_PER_WAVE", 1));
     ctx->prefill_split_tiles = std::max(-1, env_int("JMA_PREFILL_SPLIT_TILES", -1));
     ctx->cus = (uint32_t)std::max(1, prop.multiProcessorCount);
