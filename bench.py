@@ -17,8 +17,9 @@ Printed: one JSON line with
              1 core, in the same unit (backend-java's decode attention is single-threaded); its
              all_cores field runs the same loop on batches of independent layer-steps over
              (layer-step, kv head) units on up to 16 threads (the GPU box's CPU share)
-and, as extra fields, us/token, the C3 prefill (S 2048, 24/8 heads, d 128) TFLOP/s and the C4
-ragged decode (64 sessions up to 16384 positions, one launch) GB/s.
+and, as extra fields, us/token, the C3 prefill (S 2048, 24/8 heads, d 128) TFLOP/s, the C4
+ragged decode (64 sessions up to 16384 positions, one launch) GB/s and the C5 long-context
+decode (26 layers, 32k context, sliding-window rings) GB/s and us/token.
 """
 
 from __future__ import annotations
@@ -253,6 +254,90 @@ def run_c4(hip, A, rt, synth, reps: int = 10):
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, rows=sum(lens))
 
 
+def run_c5(hip, A, rt, synth, steps: int = 64, warmup: int = 4):
+    """C5 Gemma-3-1B-shaped long-context decode at full size: 4 Q / 1 KV heads (MQA),
+    d 256, NeoX RoPE (theta 1e6 on the global layers 5, 11, 17, 23, 1e4 on the sliding ones), f16
+    KV, 26 layers in the 5 sliding (window 512) : 1 global pattern, 32704 prior positions, 64
+    decode steps. The sliding layers keep LayeredKvCache RING retention of window + 64 slots and
+    are filled with the last 512 prior positions (all their window reads); the global layers hold
+    all 32704. A step is one token through the 26 layers (one fused decode launch each), replayed
+    from per-token HIP graphs with inputs resident in HBM, as for C2."""
+    hq, hkv, d, prior, layers, w = 4, 1, 256, 32704, 26, 512
+    n = prior + steps
+    qd, kd = hq * d, hkv * d
+    sliding = [A.uses_sliding_window(l, 6, w) for l in range(layers)]
+    rope_swa = hip.rotary_table(d, 1e4, 1.0, max_positions=n)
+    rope_glb = hip.rotary_table(d, 1e6, 1.0, max_positions=n)
+    ring_cap = w + steps
+    kv = hip.kv_cache(layers, n, hkv, d, d, half_precision=True,
+                      ring_capacity=[ring_cap if sl else 0 for sl in sliding])
+    lp = [A.AttentionLayer(l, hq, sliding_window=w if sliding[l] else 0, neox=True,
+                           rope=rope_swa if sliding[l] else rope_glb) for l in range(layers)]
+    zq = rt.DeviceArray(prior * qd)
+    zq.zero()
+    dk, dv = rt.DeviceArray(n * kd), rt.DeviceArray(n * kd)
+    t0 = time.time()
+    for l in range(layers):
+        first = prior - w if sliding[l] else 0
+        rows = prior - first
+        dk.upload(synth.normal(5, f"bench/c5/k{l}", (rows, kd)))
+        dv.upload(synth.normal(5, f"bench/c5/v{l}", (rows, kd)))
+        kv.append_device(lp[l], np.zeros(rows, np.uint32), np.arange(first, prior), zq.ptr,
+                         rows * qd, dk.ptr, rows * kd, dv.ptr, rows * kd)
+    hip.synchronize()
+    log(f"C5 cache filled ({time.time() - t0:.1f}s)")
+    zq.free()
+    # Per layer and step: q, the new k and v rows.
+    dq = rt.DeviceArray(layers * steps * qd)
+    dkn, dvn = rt.DeviceArray(layers * steps * kd), rt.DeviceArray(layers * steps * kd)
+    dq.upload(synth.normal(5, "bench/c5/q", (layers, steps, qd)))
+    dkn.upload(synth.normal(5, "bench/c5/kn", (layers, steps, kd)))
+    dvn.upload(synth.normal(5, "bench/c5/vn", (layers, steps, kd)))
+    dout = rt.DeviceArray(layers * steps * qd)
+    stream = hip.stream()
+
+    def token(st):
+        p = prior + st
+        for l in range(layers):
+            i = l * steps + st
+            kv.decode_device(lp[l], [0], [p], dq.at(i * qd), qd, dkn.at(i * kd), kd,
+                             dvn.at(i * kd), kd, dout.at(i * qd), qd)
+
+    for st in range(steps):  # eager pass: allocates every scratch buffer the graphs need
+        token(st)
+    hip.synchronize()
+    kv.discard_from(prior)
+    graphs = [rt.Graph(stream, lambda st=st: token(st)) for st in range(steps)]
+    kv.discard_from(prior)
+    for st in range(warmup):
+        graphs[st].launch()
+    hip.synchronize()
+    rt.device_synchronize()
+    ev0, ev1 = rt.Event(), rt.Event()
+    t = time.perf_counter()
+    ev0.record(stream)
+    for st in range(steps):
+        graphs[st].launch()
+    ev1.record(stream)
+    rt.device_synchronize()
+    elapsed = time.perf_counter() - t
+    gpu_ms = ev0.elapsed_ms(ev1)
+    nbytes = 0
+    for st in range(steps):
+        p = prior + st
+        for l in range(layers):
+            nbytes += 2 * (min(p + 1, w) if sliding[l] else p + 1) * hkv * d * 2
+    for g in graphs:
+        g.destroy()
+    for buf in (dk, dv, dq, dkn, dvn, dout):
+        buf.free()
+    kv.close()
+    rope_swa.close()
+    rope_glb.close()
+    return dict(elapsed=elapsed, gpu_ms=gpu_ms, bytes=nbytes, steps=steps,
+                us_per_token=elapsed / steps * 1e6, gbs=nbytes / elapsed / 1e9)
+
+
 def cpu_baseline_c2(material, budget_s: float):
     """backend-java's decode attention restated in C (oracle/), one thread, on repeated C2
     layer-steps at the last decoded position until about budget_s seconds of CPU work ran."""
@@ -303,6 +388,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the C3 prefill figure")
     ap.add_argument("--no-c4", action="store_true", help="skip the C4 ragged decode figure")
+    ap.add_argument("--no-c5", action="store_true", help="skip the C5 long-context decode figure")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="profiling aid: run only the C5 long-context decode measurement")
     ap.add_argument("--c4-only", action="store_true",
                     help="profiling aid: run only the C4 ragged decode measurement, print its figures")
     ap.add_argument("--prefill-only", action="store_true",
@@ -338,6 +426,11 @@ def main() -> int:
         print(json.dumps({"prefill_us": round(c3["ms"] * 1e3, 2), "tflops": round(c3["tflops"], 2),
                           "flops": c3["flops"]}), flush=True)
         return 0
+    if args.c5_only:
+        c5 = run_c5(hip, A, rt, synth)
+        print(json.dumps({"c5_us_per_token": round(c5["us_per_token"], 2), "gbs": round(c5["gbs"], 1),
+                          "bytes_per_token": c5["bytes"] // c5["steps"]}), flush=True)
+        return 0
     if args.c4_only:
         c4 = run_c4(hip, A, rt, synth)
         print(json.dumps({"c4_us": round(c4["ms"] * 1e3, 2), "gbs": round(c4["gbs"], 1),
@@ -355,6 +448,10 @@ def main() -> int:
     if not args.no_c4:
         c4 = run_c4(hip, A, rt, synth)
         log(f"C4 ragged decode: {c4['ms'] * 1e3:.1f} us, {c4['gbs']:.0f} GB/s")
+    c5 = None
+    if not args.no_c5:
+        c5 = run_c5(hip, A, rt, synth)
+        log(f"C5 long-context decode: {c5['us_per_token']:.1f} us/token, {c5['gbs']:.0f} GB/s")
     hip.close()
 
     value = c2["algo_bytes"] / c2["elapsed"] / 1e9
@@ -416,6 +513,15 @@ def main() -> int:
             "frac_of_hbm_peak": round(c4["gbs"] / HBM_PEAK_GBS, 4),
             "bytes": c4["bytes"],
             "kv_rows": c4["rows"],
+        }
+    if c5 is not None:
+        result["long_context_decode"] = {
+            "workload": "C5 Gemma-3-1B-shaped decode: 4 Q / 1 KV heads, d 256, f16 KV, 26 layers "
+                        "(5 sliding window 512 rings : 1 global), context 32704..32767, 64 steps",
+            "gbs": round(c5["gbs"], 1),
+            "us_per_token": round(c5["us_per_token"], 2),
+            "frac_of_hbm_peak": round(c5["gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_token": c5["bytes"] // c5["steps"],
         }
     if not args.no_cpu:
         cpu = cpu_baseline_c2(c2["cpu_material"], args.cpu_seconds)
