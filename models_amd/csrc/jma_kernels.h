@@ -14,8 +14,11 @@ constexpr int kMaxRows = 128;
 // combine in LDS. Two waves per SIMD hide each other's instruction latency; at dk = 256 two tile
 // buffers take half the register file, so one wave per SIMD.
 constexpr int decode_waves(int dk) { return dk >= 256 ? 4 : 8; }
-// Most splits one decode row may be cut into; the cross-split reduction loads them all at once.
+// Most splits one decode row may be cut into when the decode kernel reduces them itself (the
+// reducing workgroup loads every split's partial); and when a separate reduce_kernel does
+// (partials in part_acc / part_ml, reduced by one workgroup per head and 64 output elements).
 constexpr int kMaxSplits = 32;
+constexpr int kMaxWideSplits = 1024;
 
 // Where one layer's K and V live. K: [sequence][layer][kv head][slot][key_length] row-major.
 // V: [sequence][layer][kv head][slot / B][value_length][B] (B = 32 for f16, 16 for f32), the

@@ -944,14 +944,22 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
 
 // ================================================================ kernel 4: cross-split reduce
 
-// One wave per (row, query head): out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the
-// row's splits (at most kMaxSplits). Every split's partial is loaded before any is used (indices
-// past the last split are clamped to it and weighted 0), so the reduction costs one round trip.
+// One workgroup of 16 waves per (row, query head, 64-element chunk of the head's output): out =
+// sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to kMaxWideSplits.
+// Thread t loads split t's (m, l): one round trip for all of them; the workgroup agrees on M and
+// on the weights 2^(m_s - M) (kept in LDS) and sums l in a fixed tree. Wave w then sums its
+// splits w, w + 16, ... in order, with all of their loads issued before the first is used, and
+// the sixteen sums are added in wave order: the result is the same on every run for a plan.
 template <int DV>
-__global__ __launch_bounds__(64) void reduce_kernel(const DecodeArgs a) {
-  constexpr int kJ = (DV + 63) / 64;  // output elements per lane
-  const uint32_t row = blockIdx.x / a.num_heads;
-  const uint32_t head = blockIdx.x % a.num_heads;
+__global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
+  constexpr uint32_t kChunks = (DV + 63) / 64;
+  constexpr int kWaves = 16;
+  constexpr int kAhead = kMaxWideSplits / kWaves;  // splits one wave sums at most
+  __shared__ float s_w[kMaxWideSplits];
+  __shared__ float s_m[kWaves], s_l[kWaves], s_x[kWaves][64];
+  const uint32_t chunk = blockIdx.x % kChunks;
+  const uint32_t row = blockIdx.x / kChunks / a.num_heads;
+  const uint32_t head = blockIdx.x / kChunks % a.num_heads;
   const uint32_t hkv = a.num_heads / a.group;
   const uint32_t ns = a.ns_uniform ? a.ns_uniform : a.nsplit[row];
   if (ns == 1) return;
@@ -960,47 +968,59 @@ __global__ __launch_bounds__(64) void reduce_kernel(const DecodeArgs a) {
   const uint32_t hl = head % a.group;
   const uint32_t hg = hl / 16, c16 = hl % 16;
   const uint64_t base = row_item + ((uint64_t)kvh * a.hgroups + hg) * ns;
-  const int lane = threadIdx.x;
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  float m[kMaxSplits], lw[kMaxSplits], x[kMaxSplits][kJ];
+  // Weights: thread t takes split t.
+  float2 ml = {-INFINITY, 0.0f};
+  if (tid < ns) ml = *(const float2*)(a.part_ml + ((base + tid) * 16 + c16) * 2);
+  float mw = ml.x;
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
-    const uint64_t it = base + min((uint32_t)s, ns - 1);
-    const float2 ml = *(const float2*)(a.part_ml + (it * 16 + c16) * 2);
-    m[s] = ml.x;
-    lw[s] = ml.y;
+  for (int o = 32; o >= 1; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
+  if (lane == 0) s_m[wave] = mw;
+  __syncthreads();
+  float M = s_m[0];
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int d = min(lane + 64 * j, DV - 1);
-      x[s][j] = a.part_acc[(it * 16 + c16) * DV + d];
-    }
+  for (int i = 1; i < kWaves; ++i) M = fmaxf(M, s_m[i]);
+  const float mu = M == -INFINITY ? 0.0f : M;
+  const float wt = tid < ns ? __builtin_amdgcn_exp2f(ml.x - mu) : 0.0f;
+  if (tid < ns) s_w[tid] = wt;
+  float lw = tid < ns ? ml.y * wt : 0.0f;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lw += __shfl_xor(lw, o);
+  if (lane == 0) s_l[wave] = lw;
+  __syncthreads();
+
+  // Weighted sums of this chunk: wave w takes splits w, w + 16, ...
+  const uint32_t d = chunk * 64 + lane;
+  const uint32_t dl = d < DV ? d : DV - 1;  // lanes past the head load a valid element
+  float xv[kAhead];
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i) {
+    const uint32_t sp = wave + kWaves * i;
+    xv[i] = sp < ns ? a.part_acc[((base + sp) * 16 + c16) * DV + dl] : 0.0f;
   }
-  float mx = -INFINITY;
+  float X = 0.0f;
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) mx = (uint32_t)s < ns ? fmaxf(mx, m[s]) : mx;
-  const float mu = mx == -INFINITY ? 0.0f : mx;
-  float l = 0.0f, sum[kJ];
-#pragma unroll
-  for (int j = 0; j < kJ; ++j) sum[j] = 0.0f;
-#pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
-    const float w = (uint32_t)s < ns ? __builtin_amdgcn_exp2f(m[s] - mu) : 0.0f;
-    l = fmaf(lw[s], w, l);
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) sum[j] = fmaf(x[s][j], w, sum[j]);
+  for (int i = 0; i < kAhead; ++i) {
+    const uint32_t sp = wave + kWaves * i;
+    if (sp < ns) X = fmaf(xv[i], s_w[sp], X);
   }
-  if (!(l > 0.0f) && lane == 0) atomicOr(a.err, 1);  // all -inf, or a NaN / +inf score
-  const float inv = 1.0f / l;
-  float* o = a.out + ((uint64_t)row * a.num_heads + head) * DV;
+  s_x[wave][lane] = X;
+  __syncthreads();
+  if (wave != 0) return;
+  float lt = 0.0f, xt = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kJ; ++j) {
-    const int d = lane + 64 * j;
-    if (d < DV) o[d] = sum[j] * inv;
+  for (int i = 0; i < kWaves; ++i) {
+    lt += s_l[i];
+    xt += s_x[i][lane];
   }
+  if (!(lt > 0.0f) && lane == 0 && chunk == 0) atomicOr(a.err, 1);  // all -inf, NaN or +inf
+  if (d < DV) a.out[((uint64_t)row * a.num_heads + head) * DV + d] = xt * (1.0f / lt);
 }
 
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream) {
-  const dim3 grid(a.rows.count * a.num_heads), block(64);
+  const uint32_t chunks = (uint32_t)((dv + 63) / 64);
+  const dim3 grid(a.rows.count * a.num_heads * chunks), block(1024);
   switch (dv) {
     case 16: hipLaunchKernelGGL(reduce_kernel<16>, grid, block, 0, stream, a); break;
     case 32: hipLaunchKernelGGL(reduce_kernel<32>, grid, block, 0, stream, a); break;

@@ -337,7 +337,11 @@ void run_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall&
 
 // Split planning for one launch of <= kMaxRows rows. Every workgroup of the launch streams
 // tiles_per_split tiles: at least tiles_per_wave per wave, raised until the launch is near the
-// workgroup target, and high enough that no row needs more than kMaxSplits splits.
+// workgroup target, and high enough that no row needs more than kMaxSplits splits (the decode
+// kernel then reduces the splits itself). When that cap would leave the launch with fewer than a
+// quarter of the target workgroups (few long rows: one sequence at a long context and few KV
+// heads), the rows are cut wider, up to kMaxWideSplits splits, and reduce_kernel combines them
+// in a second launch.
 // New rows handed to the decode kernel to rotate and append itself (all null: rows are cached).
 struct FusedAppend {
   const float* k = nullptr;
@@ -383,7 +387,16 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   const uint64_t target = (uint64_t)ctx->decode_target_blocks;
   uint64_t tps = (uint64_t)jma::decode_waves((int)kv->dk) * ctx->tiles_per_wave;
   tps = std::max<uint64_t>(tps, (units + target - 1) / target);
-  tps = std::max<uint64_t>(tps, (max_tiles + jma::kMaxSplits - 1) / jma::kMaxSplits);
+  const uint64_t tps_fused = std::max<uint64_t>(tps, (max_tiles + jma::kMaxSplits - 1) / jma::kMaxSplits);
+  bool wide = false;
+  if (tps_fused > tps && !ctx->unfused) {
+    uint64_t fused_items = 0;
+    for (uint32_t i = 0; i < rows.count; ++i)
+      fused_items += (ntiles[i] + tps_fused - 1) / tps_fused * kv->hkv * a.hgroups;
+    wide = fused_items * 4 < target;
+  }
+  tps = wide ? std::max<uint64_t>(tps, (max_tiles + jma::kMaxWideSplits - 1) / jma::kMaxWideSplits)
+             : tps_fused;
   a.tiles_per_split = (uint32_t)tps;
   uint32_t items = 0;
   bool any_split = false;
@@ -404,7 +417,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.k_base = (char*)a.kv.k + (a.kv.seq_stride_k * rows.seq0 + a.kv.layer_off_k) * es;
     a.v_base = (char*)a.kv.v + (a.kv.seq_stride_v * rows.seq0 + a.kv.layer_off_v) * es;
   }
-  if (any_split && ctx->unfused) {
+  if (any_split && (ctx->unfused || wide)) {
     ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream);
     ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream);
     a.part_acc = (float*)ctx->part_acc.ptr;

@@ -785,6 +785,41 @@ def test_split_plans_and_fusion_agree(hip, monkeypatch, neox):
             np.testing.assert_array_equal(rows[variant][s][1], rows[0][s][1])
 
 
+@pytest.mark.parametrize("half,d", [(True, 256), (True, 128), (False, 128)])
+def test_wide_split_decode_matches_oracle(hip, half, d):
+    """Few long rows (MQA, one KV head, contexts up to 16384): the 32-split cap of the fused
+    reduction would leave most CUs idle, so the plan cuts the rows into up to 1024 splits and
+    reduce_kernel combines them in a second launch. Ragged rows (one long, one short, one at a
+    tile boundary) with the new token appended by the decode kernel, against the oracle's GQA
+    over the read-back cache."""
+    hq, hkv, theta = 4, 1, 1e6
+    scale = A.default_scale(d)
+    lens = [16383 if half else 8191, 300, 4096]
+    B = len(lens)
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=max(lens) + 1)
+    kv = hip.kv_cache(1, max(lens) + 1, hkv, d, d, half_precision=half, sequences=B)
+    close = assert_f16_close if half else assert_f32_close
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        for s_, L in enumerate(lens):
+            kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32),
+                      normal(15, f"wide/k{s_}", (L, hkv * d)), normal(15, f"wide/v{s_}", (L, hkv * d)),
+                      sequences=np.full(L, s_))
+        qn = normal(15, "wide/qn", (B, hq * d))
+        kn = normal(15, "wide/kn", (B, hkv * d))
+        vn = normal(15, "wide/vn", (B, hkv * d))
+        got = kv.decode(layer, lens, qn, kn, vn, sequences=np.arange(B)).reshape(B, -1)
+        for s_, L in enumerate(lens):
+            keys, values = kv.read(0, 0, L + 1, sequence=s_)
+            q_rot = rope_rows(qn[s_:s_ + 1], [L], hq, d, d, theta, True, check_against_oracle=False)
+            want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
+            err = close(got[s_], want, f"wide split d {d} session {s_} (L={L})")
+            _say(f"wide split half={half} d={d} L={L} err {err:.2e}")
+    finally:
+        kv.close()
+        rope.close()
+
+
 def test_graph_replays_match_eager_decode(hip):
     """Per-token HIP graphs of decode_device (as the benchmark replays them): every replay, with
     eager work and synchronizations in between, reproduces the eager outputs exactly."""
