@@ -306,6 +306,7 @@ def run_c5(hip, A, rt, synth, steps: int = 64, warmup: int = 4):
     for st in range(steps):  # eager pass: allocates every scratch buffer the graphs need
         token(st)
     hip.synchronize()
+    eager_out = dout.download()
     kv.discard_from(prior)
     graphs = [rt.Graph(stream, lambda st=st: token(st)) for st in range(steps)]
     kv.discard_from(prior)
@@ -322,6 +323,8 @@ def run_c5(hip, A, rt, synth, steps: int = 64, warmup: int = 4):
     rt.device_synchronize()
     elapsed = time.perf_counter() - t
     gpu_ms = ev0.elapsed_ms(ev1)
+    if not np.array_equal(dout.download(), eager_out):
+        raise RuntimeError("C5 graph replay differs from the eager decode")
     nbytes = 0
     for st in range(steps):
         p = prior + st
