@@ -820,6 +820,40 @@ def test_wide_split_decode_matches_oracle(hip, half, d):
         rope.close()
 
 
+def test_wide_split_on_a_ring_layer_matches_oracle(hip):
+    """A wide plan on a RING layer (LayeredKvCache retention, capacity 16384, window 12000) at a
+    position past the first wrap (20000): the 375 visible tiles are cut into wide splits whose
+    slots wrap inside the ring; against the oracle's GQA over the window read back from the
+    ring, and the stored row bit-exact."""
+    hq, hkv, d, theta, cap, w, p = 4, 1, 128, 1e6, 16384, 12000, 20000
+    scale = A.default_scale(d)
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=p + 1)
+    kv = hip.kv_cache(1, p + 1, hkv, d, d, half_precision=True, ring_capacity=[cap])
+    try:
+        layer = A.AttentionLayer(0, hq, sliding_window=w, neox=True, rope=rope)
+        chunk = cap - w
+        for start in range(0, p, chunk):
+            stop = min(p, start + chunk)
+            kv.append(layer, np.arange(start, stop), np.zeros((stop - start, hq * d), np.float32),
+                      normal(17, f"wring/k{start}", (stop - start, hkv * d)),
+                      normal(17, f"wring/v{start}", (stop - start, hkv * d)))
+        qn = normal(17, "wring/qn", (1, hq * d))
+        kn = normal(17, "wring/kn", (1, hkv * d))
+        vn = normal(17, "wring/vn", (1, hkv * d))
+        got = kv.decode(layer, [p], qn, kn, vn).reshape(-1)
+        first = p - w + 1
+        keys, values = kv.read(0, first, p + 1)
+        k_new = oracle.f16_round(rope_rows(kn, [p], hkv, d, d, theta, True, check_against_oracle=False))
+        np.testing.assert_array_equal(keys.reshape(w, -1)[-1], k_new[0])
+        q_rot = rope_rows(qn, [p], hq, d, d, theta, True, check_against_oracle=False)
+        want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
+        err = assert_f16_close(got, want, "wide split on a ring layer")
+        _say(f"wide split ring err {err:.2e}")
+    finally:
+        kv.close()
+        rope.close()
+
+
 def test_graph_replays_match_eager_decode(hip):
     """Per-token HIP graphs of decode_device (as the benchmark replays them): every replay, with
     eager work and synchronizations in between, reproduces the eager outputs exactly."""
