@@ -1344,7 +1344,6 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     const uint32_t rv = c * 16 + lane / 4;
     voff[i] = 2 * (rv * 32 + 8 * ((lane % 4) ^ swz_v(rv)));
   }
-  auto has_tile = [&](uint32_t k) JMA_INL { return k < steps && t0 + k * Q + q < t1; };
   // Whether every column of the stripe sees all of step k's tile (no mask needed). A tile at or
   // past t1 (the last step of a kv group, or the other half's range of a split block) is masked.
   auto full = [&](uint32_t k) JMA_INL {
@@ -1389,11 +1388,10 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   };
 
   // The first K tile goes out (to sub-slot 0 of array 0) before the Q loads, so the two latencies
-  // overlap.
-  if (has_tile(0)) {
+  // overlap. A group without tiles loads slot 0 like its later steps: every K stage holds cache
+  // data, never stale LDS contents.
 #pragma unroll
-    for (int i = 0; i < kCPW; ++i) dma_k(0, lx, 0, i);
-  }
+  for (int i = 0; i < kCPW; ++i) dma_k(0, lx, 0, i);
 
   // Q^T operands: 8 consecutive dims of this lane's column per k-step, scaled by
   // scale * log2(e) and rounded to f16. A scaled element beyond the f16 range (where the
@@ -1613,8 +1611,10 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   // chunks wave r finishes; then it combines its own chunks (from registers) with the Q - 1
   // posted ones, in kv-group order, weighted by exp2(m_r - M) / L.
   l = half_sum(l + lb);
-  // Every wave is done with the tile stages the exchange overwrites, and no load is in flight.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // The exchange overwrites the tile stages: every wave's operand reads and tile loads (the last
+  // steps still load clamped tiles) must be complete first, in all waves, since waves leave the
+  // loop up to a step apart.
+  wait_barrier(std::integral_constant<int, 0>{});
   if (split && threadIdx.x == 0) s_ticket = ticket;
   constexpr int kCQ = kC / Q;  // chunks one wave finishes
   // Posted chunks of stripe s: [source group][destination slot][kCQ][64 lanes] float4, in lx for
