@@ -225,6 +225,15 @@ struct Tile<float, DK, DV> {
   }
 };
 
+// v with each 32-bit word ANDed with the matching word of keep.
+__device__ __forceinline__ half8_t keep_bits(half8_t v, const uint32_t* keep) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  u32x4_t u = __builtin_bit_cast(u32x4_t, v);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) u[w] &= keep[w];
+  return __builtin_bit_cast(half8_t, u);
+}
+
 __device__ __forceinline__ uint64_t pack2(float lo, float hi) {
   return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
 }
@@ -803,12 +812,22 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[e] = sc[e];
     }
-    // Only the first and last tiles of the visible range hold masked rows.
+    // Only the first and last tiles of the visible range hold masked rows. Their value elements
+    // (element i of each V operand is the position of score i) are cleared too, through the
+    // bit masks vkeep (one per 32-bit word of an operand): a masked slot may hold anything (a
+    // discarded tail, an old ring slot, a value that overflowed f16), and 0 * inf would reach the
+    // result.
+    uint32_t vkeep[4] = {~0u, ~0u, ~0u, ~0u};
     if (p0 < first || p0 + kBlk - 1 > pos) {
 #pragma unroll
       for (int i = 0; i < kNs; ++i) {
         const uint32_t p = kF16 ? p0 + 16 * (i >> 2) + 4 * g + (i & 3) : p0 + 4 * g + i;
-        s[i] = p >= first && p <= pos ? s[i] : -INFINITY;
+        const bool ok = p >= first && p <= pos;
+        s[i] = ok ? s[i] : -INFINITY;
+        if (!ok) {
+          if constexpr (kF16) vkeep[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+          else vkeep[i] = 0u;
+        }
       }
     }
     float mt = s[0];
@@ -846,15 +865,17 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
       }
 #pragma unroll
       for (int n = 0; n < kNv; ++n) {
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.v[n], phi, acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.v[n], plo, acc[n], 0, 0, 0);
+        const half8_t vn = keep_bits(cur.v[n], vkeep);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vn, phi, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vn, plo, acc[n], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int n = 0; n < kNv; ++n) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.v[n][e], p[e], acc[n], 0, 0, 0);
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              __uint_as_float(__float_as_uint(cur.v[n][e]) & vkeep[e]), p[e], acc[n], 0, 0, 0);
       }
     }
   };
@@ -1295,6 +1316,8 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   const uint32_t rb = a.row_blocks - 1 - rank;
   const uint32_t pair = (rank * a.head_groups + hz) * a.num_kv_heads + kvh;
   __shared__ uint32_t s_ticket;
+  __shared__ uint32_t s_rerun;  // set when the block needs the robust pass
+  if (threadIdx.x == 0) s_rerun = 0u;
   uint32_t ticket = 0;  // arrival order of this half of a split pair, taken first
   if (split && threadIdx.x == 0)
     ticket = __hip_atomic_fetch_add(&a.tickets[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1327,6 +1350,7 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   const uint32_t t1 = split && half == 0 ? tmid : bt1;
   const uint32_t steps = (t1 - t0 + Q - 1) / Q;
   const uint32_t w_last = a.start + row_last;
+  const uint32_t w_first_early = first_visible(a.start + row0, a.window);
   const uint32_t w_first_late = first_visible(w_last, a.window);
 
   const _Float16* kbase = (const _Float16*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
@@ -1416,28 +1440,49 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     if (__ballot(col_ok && !(qmax < 65520.0f)) != 0 && lane == 0) atomicOr(a.err, 1);
   }
 
+  // Softmax state, set up by each pass: l accumulates in two chains (l, lb), summed at the end;
+  // negm holds -m (0 while m is -inf) in every element: the initial accumulators of each score
+  // tile.
   float16_t o[kNb];
-#pragma unroll
-  for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[nb][e] = 0.0f;
-  // l accumulates in two chains (l, lb), summed at the end. negm holds -m (0 while m is -inf) in
-  // every element: the initial accumulators of each score tile.
-  float m = -INFINITY, l = 0.0f, lb = 0.0f;
+  float m, l, lb;
   float16_t negm;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) negm[e] = 0.0f;
   const uint32_t kr = swap34(j);
 
   // LDS reads are issued in batches of up to 8 ahead of the matrix ops that consume them: with
   // eight waves and the direct-to-LDS traffic sharing the LDS, one read's latency is several
   // hundred cycles, and a read-use-read chain would serialise on it.
   constexpr int kBatch = kKS < 8 ? kKS : 8;
-  // S^T of one tile minus the reference maximum of each column (the accumulators start at -m, or
+  // Two passes share the code below. The fast pass masks a partly visible tile through the
+  // accumulators its first QK^T op starts from: kMaskFloor (-2^100) at the positions a column
+  // does not see (outside [first, position], or past t1), so no score is masked after the matrix
+  // ops and masked and unmasked tiles share all the code after the first op. Any score the ops
+  // add stays below half the floor (its exponential is 0, and a column maximum under half the
+  // floor reads as -inf) as long as the keys there are finite. The cache may hold anything at
+  // positions a row does not see (a discarded tail, an old ring slot, a value that overflowed
+  // f16), and there an infinite key or value turns the column's state non-finite (-2^100 + inf,
+  // 0 * inf). A workgroup whose valid columns end the fast pass with a non-finite state runs its
+  // block again in the robust pass, which masks scores after the products (select) and zeroes
+  // the value operands at positions no column of the wave sees, so those positions never reach
+  // a result, as in the reference; a state still non-finite then is the reference's too.
+  constexpr float kMaskFloor = -0x1p100f;
+  auto masked_init = [&](uint32_t k) JMA_INL {
+    const uint32_t p0 = 32 * (t0 + k * Q + q), pend = 32 * t1;
+    float16_t mi;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t p = p0 + score_slot(e, h);
+      mi[e] = p >= cfirst && p <= cpos && p < pend ? negm[e] : kMaskFloor;
+    }
+    return mi;
+  };
+  // S^T of tile k minus the reference maximum of each column (the accumulators start at -m, or
   // at 0 before the first tile): the tile's exponentials need no subtraction. `issue(i)` runs
   // after the i-th matrix op, to spread loads between them.
-  auto qk = [&](const _Float16* sk, auto issue) JMA_INL {
-    float16_t sc = negm;
+  auto qk = [&](const _Float16* sk, uint32_t k, auto robust, auto issue) JMA_INL {
+    const bool masked = !decltype(robust)::value && !full(k);
+    float16_t mi;
+    if (masked) mi = masked_init(k);
+    float16_t sc;
 #pragma unroll
     for (int ks0 = 0; ks0 < kKS; ks0 += kBatch) {
       half8_t kf[kBatch];
@@ -1448,30 +1493,43 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
       }
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[ks0 + i], sc, 0, 0, 0);
+        if (ks0 + i == 0) {
+          if (masked) sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[0], mi, 0, 0, 0);
+          else sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[0], negm, 0, 0, 0);
+        } else {
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qf[ks0 + i], sc, 0, 0, 0);
+        }
         issue(ks0 + i);
       }
     }
     return sc;
   };
-  // Masks step k's (shifted) scores (positions outside [first, position] of each column become
-  // -inf) and returns the per-column tile maximum.
-  auto mask_max = [&](float16_t& sc, uint32_t k, bool whole) JMA_INL {
+  // The per-column maximum of tile k's (shifted) scores, -inf when the column sees none of them.
+  // The robust pass masks the scores here (positions outside [first, position] of each column,
+  // or past t1, become -inf).
+  auto tile_max = [&](float16_t& sc, uint32_t k, auto robust) JMA_INL {
     float tmax = -INFINITY;
-    if (whole) {
+    if constexpr (decltype(robust)::value) {
+      if (full(k)) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+      } else {
+        const uint32_t p0 = 32 * (t0 + k * Q + q), pend = 32 * t1;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t p = p0 + score_slot(e, h);
+          const bool ok = p >= cfirst && p <= cpos && p < pend;
+          sc[e] = ok ? sc[e] : -INFINITY;
+          tmax = fmaxf(tmax, sc[e]);
+        }
+      }
+      return half_max(tmax);
+    } else {
 #pragma unroll
       for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-    } else {
-      const uint32_t p0 = 32 * (t0 + k * Q + q), pend = 32 * t1;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t p = p0 + score_slot(e, h);
-        const bool ok = p >= cfirst && p <= cpos && p < pend;
-        sc[e] = ok ? sc[e] : -INFINITY;
-        tmax = fmaxf(tmax, sc[e]);
-      }
+      tmax = half_max(tmax);
+      return tmax < 0.5f * kMaskFloor ? -INFINITY : tmax;
     }
-    return half_max(tmax);
   };
   // Raises the reference maximum when the tile's maximum exceeds it by more than 8 (tmax is the
   // shifted tile's maximum, so the test is tmax > 8; any tile that has a visible score raises it
@@ -1505,8 +1563,22 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
       else l = __builtin_amdgcn_fdot2(pr, one, l, false);
     }
   };
-  auto pv = [&](const _Float16* sv, const half8_t* pf) JMA_INL {
+  // O^T += V^T P for tile k. Element t of operand b holds the key of score register 8b + t (the
+  // f16 V blocks are stored in that order); the robust pass zeroes the elements at positions no
+  // column of this wave sees.
+  auto pv = [&](const _Float16* sv, const half8_t* pf, uint32_t k, auto robust) JMA_INL {
     constexpr int kNbB = kBatch / 2;  // dv blocks per batch of reads
+    bool keep[2][8];
+    if constexpr (decltype(robust)::value) {
+      const uint32_t p0 = 32 * (t0 + k * Q + q);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const uint32_t p = p0 + score_slot(8 * b + t, h);
+          keep[b][t] = p >= w_first_early && p <= w_last;
+        }
+    }
 #pragma unroll
     for (int nb0 = 0; nb0 < kNb; nb0 += kNbB) {
       half8_t vf[kNbB][2];
@@ -1516,6 +1588,10 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
         for (int b = 0; b < 2; ++b) {
           const uint32_t vr = 32 * (nb0 + i) + j;
           vf[i][b] = *(const half8_t*)(sv + vr * 32 + 8 * ((2 * b + h) ^ swz_v(vr)));
+          if constexpr (decltype(robust)::value) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) vf[i][b][t] = keep[b][t] ? vf[i][b][t] : (_Float16)0.0f;
+          }
         }
 #pragma unroll
       for (int i = 0; i < kNbB; ++i)
@@ -1525,10 +1601,24 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     }
   };
   auto no_issue = [](int) JMA_INL {};
+  // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
+  // before tile k+1's scores are computed.
+  constexpr bool kOverlap = D <= 128;
 
+  // One pass over the block's tiles (K(0) already on its way to sub-slot 0 of array 0).
+  auto run = [&](auto robust) JMA_INL {
+#pragma unroll
+  for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[nb][e] = 0.0f;
+  m = -INFINITY;
+  l = 0.0f;
+  lb = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) negm[e] = 0.0f;
   // V stages start zeroed: a step whose tile this wave does not see still runs its PV product,
-  // with p = 0, and 0 * (anything the stage held) must be 0. Only cache data (finite) or zeros
-  // ever reach a V stage.
+  // with p = 0, and 0 * (anything the stage held) must be 0. Only cache data or zeros ever reach
+  // a V stage.
   for (int i = threadIdx.x; i < T * Q * kT / 8; i += 64 * kWaves) {
     *(half8_t*)(lx + T * Q * kT + 8 * i) = half8_t{};
     *(half8_t*)(ly + T * Q * kT + 8 * i) = half8_t{};
@@ -1544,19 +1634,11 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
       dma_v(jv, ly, jv, i);
     }
   });
-  // Masks step k's scores when some column does not see all of the tile (a tile this wave does
-  // not see at all, or one that does not exist, is masked completely: its stale scores become
-  // -inf, so its exponentials are 0). Returns the column maximum.
-  auto mask_step = [&](float16_t& sc, uint32_t k) JMA_INL {
-    return full(k) ? mask_max(sc, k, true) : mask_max(sc, k, false);
-  };
-  // Score tiles alternate between two register sets (even steps finish sa and compute sb).
-  float16_t sa = qk(k_slot(lx, 0), no_issue), sb;
-  rescale(sa, mask_step(sa, 0));
+  // Score tiles alternate between two register sets (even steps finish sa and compute sb). A
+  // tile this wave does not see at all, or one that does not exist, is masked completely.
+  float16_t sa = qk(k_slot(lx, 0), 0, robust, no_issue), sb;
+  rescale(sa, tile_max(sa, 0, robust));
 
-  // At D = 256 the accumulators leave no registers for two live score tiles: tile k is finished
-  // before tile k+1's scores are computed.
-  constexpr bool kOverlap = D <= 128;
   // Step k (P = k mod 2T, fixed per unrolled copy; sub-step j = P mod T of barrier-step m, whose
   // parity is P / T): after the barrier that opens the barrier-step, K(k+1) and V(k) are ready
   // in array (m + 1) mod 2; K(k+T+1) and V(k+T) are loaded into array m mod 2. Every step runs
@@ -1581,9 +1663,9 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     };
     if constexpr (kOverlap) {
       // QK^T of tile k+1 overlaps the exponentials of tile k.
-      snxt = qk(ksrc, spread);
+      snxt = qk(ksrc, k + 1, robust, spread);
       exp_tile(scur, pf);
-      pv(vsrc, pf);
+      pv(vsrc, pf, k, robust);
       // Order: all K and V^T operand reads, then the QK^T matrix ops each followed by a share of
       // the exponentials, then the PV matrix ops.
       __builtin_amdgcn_sched_group_barrier(0x100, kKS + 2 * kNb, 0);
@@ -1594,10 +1676,10 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
       __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNb, 0);
     } else {
       exp_tile(scur, pf);
-      pv(vsrc, pf);
-      snxt = qk(ksrc, spread);
+      pv(vsrc, pf, k, robust);
+      snxt = qk(ksrc, k + 1, robust, spread);
     }
-    rescale(snxt, mask_step(snxt, k + 1));
+    rescale(snxt, tile_max(snxt, k + 1, robust));
   };
   // (The last copies are guarded inside the loop: remainder copies after it would double the
   // code the register allocator spans and spill.)
@@ -1605,16 +1687,36 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     static_for<2 * T>([&](auto pp) JMA_INL {
       if (k + decltype(pp)::value < steps) step(k + decltype(pp)::value, pp);
     });
+  };
+
+  run(std::false_type{});
+  {
+    // A valid column whose state is not finite (NaN or +inf in l, m or the accumulators) asks
+    // for the robust pass.
+    float osum = 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) osum += o[nb][e];
+    const bool bad = col_ok && !(l + lb < INFINITY && m < INFINITY && fabsf(osum) < INFINITY);
+    if (__ballot(bad) != 0 && lane == 0) s_rerun = 1u;
+  }
+  // Every wave's operand reads and tile loads (the last steps still load clamped tiles) are
+  // complete before a second pass or the exchange below overwrites the tile stages, since waves
+  // leave the loop up to a step apart.
+  wait_barrier(std::integral_constant<int, 0>{});
+  if (s_rerun != 0u) {
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) dma_k(0, lx, 0, i);
+    run(std::true_type{});
+    wait_barrier(std::integral_constant<int, 0>{});
+  }
 
   // Merge the kv-group partials of each stripe in one LDS exchange: wave q of a stripe finishes
   // the q-th of its O^T chunks. Every wave posts (m, l) and, for each other kv group r, the
   // chunks wave r finishes; then it combines its own chunks (from registers) with the Q - 1
   // posted ones, in kv-group order, weighted by exp2(m_r - M) / L.
   l = half_sum(l + lb);
-  // The exchange overwrites the tile stages: every wave's operand reads and tile loads (the last
-  // steps still load clamped tiles) must be complete first, in all waves, since waves leave the
-  // loop up to a step apart.
-  wait_barrier(std::integral_constant<int, 0>{});
   if (split && threadIdx.x == 0) s_ticket = ticket;
   constexpr int kCQ = kC / Q;  // chunks one wave finishes
   // Posted chunks of stripe s: [source group][destination slot][kCQ][64 lanes] float4, in lx for
