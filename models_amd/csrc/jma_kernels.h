@@ -84,6 +84,13 @@ struct DecodeArgs {
   uint32_t num_heads, group, hgroups, window;
   uint32_t num_kv_heads;
   uint32_t pairs, neox, rope_q;  // rope_q: q is raw and the kernel rotates it
+  // QK-norm of a fused decode: per-head RMS-norm weights for raw q (used when rope_q) and the new
+  // k rows, applied before RoPE (null = none); v_norm: the new v rows are RMS-normalised without a
+  // weight before they are stored.
+  const float* q_norm_w;
+  const float* k_norm_w;
+  float norm_eps;
+  uint32_t v_norm;
   uint32_t tiles_per_split;
   uint32_t total_items;
   uint32_t max_splits;  // splits of the row with the most; the grid is (max_splits, kv heads *

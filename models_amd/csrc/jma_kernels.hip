@@ -73,13 +73,18 @@ __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float
 // eps) in double, scale = 1 / rms, element = x * scale * w, each operation rounded on its own.
 // Every thread of the head computes the same sum (the head row is in L1), so the result is the
 // oracle's bit for bit; it replaces the pair's values y0 = x[e0], y1 = x[e1].
-__device__ __forceinline__ void head_rms_norm(const float* x, uint32_t d, const float* w, float eps,
-                                              uint32_t e0, uint32_t e1, float& y0, float& y1) {
+__device__ __forceinline__ float head_rms_scale(const float* x, uint32_t d, float eps) {
 #pragma clang fp contract(off)
   float ss = 0.0f;
   for (uint32_t i = 0; i < d; ++i) ss = ss + x[i] * x[i];
   const float rms = (float)sqrt((double)(ss / (float)d + eps));
-  const float scale = 1.0f / rms;
+  return 1.0f / rms;
+}
+
+__device__ __forceinline__ void head_rms_norm(const float* x, uint32_t d, const float* w, float eps,
+                                              uint32_t e0, uint32_t e1, float& y0, float& y1) {
+#pragma clang fp contract(off)
+  const float scale = head_rms_scale(x, d, eps);
   y0 = y0 * scale * w[e0];
   y1 = y1 * scale * w[e1];
 }
@@ -528,6 +533,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
   __shared__ __attribute__((aligned(16))) KV s_new_k[DK];  // the appended row, rotated
   __shared__ KV s_new_v[DV];
   __shared__ __attribute__((aligned(16))) float s_q[16][DK + 4];  // q rows, padded against bank conflicts
+  __shared__ float s_qn[16];  // QK-norm scale of each raw q head
 
   // The grid is (split, kv head * head groups + head group, row). Every scalar argument the
   // kernel uses, the row's own table entries included, is fetched in one batch: left to itself
@@ -662,6 +668,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
       const bool rot = cs != nullptr && j < pairs;
       const uint32_t e0 = rot && neox ? j : 2 * j, e1 = rot && neox ? j + pairs : 2 * j + 1;
       float y0 = kx[e0], y1 = kx[e1], fc = 1.0f, fs = 0.0f;
+      // QK-norm of the head before RoPE, as the append kernel applies it.
+      if (a.k_norm_w != nullptr) head_rms_norm(kx, DK, a.k_norm_w, a.norm_eps, e0, e1, y0, y1);
       if (cs != nullptr) {
         fc = cs[rot ? j : 0u];
         fs = sn[rot ? j : 0u];
@@ -675,7 +683,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
       }
     } else if (tid < DK / 2 + DV / 2) {
       const uint32_t d = 2 * (tid - DK / 2);
-      const float v0 = vx[d], v1 = vx[d + 1];
+      float v0 = vx[d], v1 = vx[d + 1];
+      if (a.v_norm != 0u) value_rms_norm(vx, DV, a.norm_eps, v0, v1);
       s_new_v[d] = (KV)v0;
       s_new_v[d + 1] = (KV)v1;
       if (hg == 0) {
@@ -721,12 +730,25 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
         fs[it] = sn[rot[it] ? j : 0u];
       }
     }
+    // Raw q of a QK-norm layer: each head's scale (one thread per head, the append kernel's
+    // arithmetic), then every element times that scale and its weight, before RoPE.
+    const float* qw = rope_q != 0 ? (const float*)a.q_norm_w : nullptr;
+    if (qw != nullptr) {
+      if (threadIdx.x < nreal) s_qn[threadIdx.x] = head_rms_scale(qg + threadIdx.x * DK, DK, a.norm_eps);
+      __syncthreads();
+    }
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       if (threadIdx.x + 64 * kW * it >= nq) continue;
       float u0 = y0[it], u1 = y1[it];
-      if (rot[it]) rotate_pair(u0, u1, fc[it], fs[it]);
       const uint32_t hs = e0[it] / DK;
+      if (qw != nullptr) {
+#pragma clang fp contract(off)
+        const float sc = s_qn[hs];
+        u0 = u0 * sc * qw[e0[it] - hs * DK];
+        u1 = u1 * sc * qw[e1[it] - hs * DK];
+      }
+      if (rot[it]) rotate_pair(u0, u1, fc[it], fs[it]);
       s_q[hs][e0[it] - hs * DK] = u0 * qscale;
       s_q[hs][e1[it] - hs * DK] = u1 * qscale;
     }

@@ -346,7 +346,7 @@ void run_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall&
 struct FusedAppend {
   const float* k = nullptr;
   const float* v = nullptr;
-  bool rope_q = false;  // q is raw: the kernel applies the layer's RoPE
+  bool rope_q = false;  // q is raw: the kernel applies the layer's QK-norm and RoPE
 };
 
 void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
@@ -374,6 +374,14 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.pairs = lc.rope->pairs;
   }
   a.neox = lc.neox;
+  if (lc.norm) {
+    if (fa.rope_q) a.q_norm_w = lc.norm->d_q;
+    if (fa.k) {
+      a.k_norm_w = lc.norm->d_k;
+      a.v_norm = lc.norm->v_rms ? 1u : 0u;
+    }
+    a.norm_eps = lc.norm->eps;
+  }
   std::vector<uint32_t> ntiles(rows.count);
   uint64_t units = 0;
   uint32_t max_tiles = 0;
@@ -437,11 +445,11 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     hip_check(jma::launch_reduce(a, kv->dv, ctx->stream), "reduce launch");
 }
 
-// The decode kernel rotates q and appends the new rows itself when its RoPE chunks line up with
-// the rotary pairs (a multiple of 8 pairs) and the context does not ask for separate kernels.
-// QK-norm layers take the append kernel (it normalises each head before RoPE), then attention.
+// The decode kernel normalises (QK-norm, value norm), rotates q and appends the new rows itself
+// when its RoPE chunks line up with the rotary pairs (a multiple of 8 pairs) and the context does
+// not ask for separate kernels.
 bool can_fuse_decode(const jmodels_attn_context* ctx, const LayerCall& lc) {
-  if (ctx->unfused || lc.norm != nullptr) return false;
+  if (ctx->unfused) return false;
   return lc.rope == nullptr || lc.rope->pairs % 8 == 0;
 }
 
@@ -1213,7 +1221,7 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
         FusedAppend fa;
         fa.k = dk + base * kdim;
         fa.v = dv + base * vdim;
-        fa.rope_q = lc.rope != nullptr;
+        fa.rope_q = lc.rope != nullptr || lc.norm != nullptr;
         run_attend_rows(ctx, kv, lc, rows, dq + base * qdim, dout + base * odim, fa);
       }
       for (uint32_t i = 0; i < count; ++i) kv->mark(sequences[i], lc.layer, positions[i]);

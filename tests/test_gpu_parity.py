@@ -176,17 +176,19 @@ def test_append_qk_norm_is_bit_exact(hip, half, neox, sides):
 
 
 @pytest.mark.parametrize("half", [False, True])
-def test_qk_norm_prefill_then_decode(hip, half):
+@pytest.mark.parametrize("sides", ["both", "k_only"])
+def test_qk_norm_prefill_then_decode(hip, half, sides):
     """Qwen3-shaped layer with attn_q_norm / attn_k_norm (16 Q / 8 KV heads, d 128, NeoX theta 1e6):
-    300 prior rows through the MFMA prefill, then 3 decode steps (QK-norm layers take the unfused
-    append + split-K decode path). The oracle normalises q and k the same way before its own RoPE."""
+    300 prior rows through the MFMA prefill, then 3 decode steps (one fused launch each: QK-norm,
+    RoPE, append and attention). The oracle normalises q and k the same way before its own RoPE;
+    with only a k weight, q passes through unnormalised."""
     hq, hkv, d, prior, steps, theta, eps = 16, 8, 128, 300, 3, 1e6, 1e-6
     n = prior + steps
     scale = A.default_scale(d)
     q = normal(13, "qnd/q", (n, hq * d))
     k = normal(13, "qnd/k", (n, hkv * d))
     v = normal(13, "qnd/v", (n, hkv * d))
-    wq = normal(13, "qnd/wq", (d,)) * 0.2 + 1.0
+    wq = None if sides == "k_only" else normal(13, "qnd/wq", (d,)) * 0.2 + 1.0
     wk = normal(13, "qnd/wk", (d,)) * 0.2 + 1.0
     qn = _qk_norm_rows(q, hq, d, wq, eps)
     kn = _qk_norm_rows(k, hkv, d, wk, eps)
