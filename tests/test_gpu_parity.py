@@ -487,16 +487,17 @@ def test_prefill_split_blocks_match_oracle(monkeypatch, d):
             _say(f"d {d} window {window} split {split} ok")
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("which", ["k", "v"])
 @pytest.mark.parametrize("window", [0, 20])
-def test_prefill_ignores_rows_it_does_not_see(hip, window, which):
+def test_prefill_ignores_rows_it_does_not_see(hip, window, which, d):
     """Positions a row does not see never reach its result, whatever the cache holds there: 48
     rows are appended with key (or value) row 45 (and, windowed, row 3) overflowing f16 to
     infinity, positions 40.. are discarded (the slots keep their contents), and rows 40..43 are
     prefilled again, then position 44 decoded. Their causal (and window) ranges exclude the
     infinite rows, which share kv tiles with rows they do see; the reference's results are
     finite."""
-    hq, hkv, d, theta, cap = 8, 2, 128, 1e4, 128
+    hq, hkv, theta, cap = 8, 2, 1e4, 128
     scale = A.default_scale(d)
     q = normal(22, "nf/q", (48, hq * d))
     k = normal(22, "nf/k", (48, hkv * d))
@@ -523,13 +524,13 @@ def test_prefill_ignores_rows_it_does_not_see(hip, window, which):
         assert not np.all(np.isfinite(stored))
         kv.discard_from(40)
         got = kv.prefill(layer, 40, q2, k2, v2)
-        assert_f16_close(got, want, f"{which} window {window} prefill")
+        assert_f16_close(got, want, f"d {d} {which} window {window} prefill")
         # and a decode step at 44, whose kv tile still holds the infinite row 45
         q3, k3, v3 = (normal(22, f"nf/{t}3", (hq * d if t == "q" else hkv * d,)) for t in "qkv")
         want3, _, _ = ref.decode_layer(0, 44, q3, k3, v3, hq, hkv, d, d, theta, 1.0, True, scale,
                                        window=window)
         got3 = kv.decode(layer, [44], q3, k3, v3)
-        assert_f16_close(got3, want3, f"{which} window {window} decode")
+        assert_f16_close(got3, want3, f"d {d} {which} window {window} decode")
     finally:
         kv.close()
         rope.close()
