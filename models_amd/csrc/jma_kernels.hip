@@ -517,7 +517,9 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 //    without waiting; the reducer reads them back with device-coherent loads, reloading until no
 //    word holds the not-written pattern, then writes that pattern back, so every partial word is
 //    clear again when the launch ends.
-template <typename KV, int DK, int DV, bool kSimple>
+// kOne: the plan gives every wave at most one tile (tiles_per_split <= waves), so the second tile
+// buffer is never needed (at head dim 256 two buffers are the whole register file).
+template <typename KV, int DK, int DV, bool kSimple, bool kOne>
 __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
   using TileT = Tile<KV, DK, DV>;
@@ -650,7 +652,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
   uint32_t t = s_t0 + wave;
   TileT ta, tb;
   if (t < s_t1) ta.load(kb, vb, slot0_of(t), c16, g);
-  if (kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
+  if constexpr (!kOne)
+    if (kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
 
   // Fused append. The new row's tile is the last of the row's last split: the row is rotated
   // into LDS, from where the wave owning that tile patches it into its registers, and the head
@@ -753,7 +756,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
       s_q[hs][e1[it] - hs * DK] = u1 * qscale;
     }
   }
-  if (!kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
+  if constexpr (!kOne)
+    if (!kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
   __syncthreads();  // q (and the appended row) are in LDS
 
   // Q operand (B of S = K Q^T); the padding head lanes hold zeros.
@@ -908,19 +912,24 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
   using no_patch = std::integral_constant<bool, false>;
   using with_patch = std::integral_constant<bool, true>;
   const uint32_t t_stop = patch_wave ? t_new : s_t1;
-  for (;;) {
-    if (t >= t_stop) break;
-    step(ta, t, no_patch{});
-    if (t + 2 * kW < s_t1) ta.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
-    t += kW;
-    if (t >= t_stop) break;
-    step(tb, t, no_patch{});
-    if (t + 2 * kW < s_t1) tb.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
-    t += kW;
-  }
-  if (patch_wave) {
-    if (((t_new - s_t0 - wave) / kW) % 2 == 0) step(ta, t_new, with_patch{});
-    else step(tb, t_new, with_patch{});
+  if constexpr (kOne) {
+    if (t < t_stop) step(ta, t, no_patch{});
+    if (patch_wave) step(ta, t_new, with_patch{});
+  } else {
+    for (;;) {
+      if (t >= t_stop) break;
+      step(ta, t, no_patch{});
+      if (t + 2 * kW < s_t1) ta.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
+      t += kW;
+      if (t >= t_stop) break;
+      step(tb, t, no_patch{});
+      if (t + 2 * kW < s_t1) tb.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
+      t += kW;
+    }
+    if (patch_wave) {
+      if (((t_new - s_t0 - wave) / kW) % 2 == 0) step(ta, t_new, with_patch{});
+      else step(tb, t_new, with_patch{});
+    }
   }
 
   l = wave_sum_groups(l);
@@ -1087,14 +1096,20 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple, false>), grid, block, 0, stream, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple>), grid, block, 0, stream, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple>), grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple>), grid, block, 0, stream, a); break;
-    case 256: hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple>), grid, block, 0, stream, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple, false>), grid, block, 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple, false>), grid, block, 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple, false>), grid, block, 0, stream, a); break;
+    case 256:
+      // One tile per wave (the long-context plans cut this fine) needs one tile buffer only.
+      if (a.tiles_per_split <= (uint32_t)decode_waves(256))
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

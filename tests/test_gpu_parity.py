@@ -791,13 +791,15 @@ def test_attend_causal_equals_prefill(hip):
         rope.close()
 
 
+@pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("neox", [False, True])
-def test_split_plans_and_fusion_agree(hip, monkeypatch, neox):
+def test_split_plans_and_fusion_agree(hip, monkeypatch, neox, d):
     """Split-K invariance and fusion equivalence on a ragged multi-session decode batch: many
     splits (one tile per wave, up to 32 splits) or one split per row, with RoPE + append + split
     reduction fused into the decode kernel or run as separate kernels (JMA_UNFUSED=1), change only
-    the summation order; the appended cache rows are bit-identical."""
-    hq, hkv, d, theta, B = 8, 2, 64, 1e4, 5
+    the summation order; the appended cache rows are bit-identical. At head dim 256 the plans of
+    one tile per wave run the single-tile-buffer kernel instance, the others the two-buffer one."""
+    hq, hkv, theta, B = 8, 2, 1e4, 5
     lens = [40, 700, 1333, 2048, 97]
     outs, rows = [], []
     for env in ({"JMA_DECODE_TILES_PER_WAVE": "1", "JMA_DECODE_TARGET_BLOCKS": "4096"},
