@@ -491,6 +491,22 @@ def test_prefill_split_blocks_match_oracle(monkeypatch, d):
 @pytest.mark.parametrize("which", ["k", "v"])
 @pytest.mark.parametrize("window", [0, 20])
 def test_prefill_ignores_rows_it_does_not_see(hip, window, which, d):
+    _nonfinite_rows_case(hip, window, which, d)
+
+
+@pytest.mark.parametrize("which", ["k", "v"])
+def test_split_prefill_ignores_rows_it_does_not_see(monkeypatch, which):
+    """The same with every row block of two or more kv tiles split between two workgroups
+    (JMA_PREFILL_SPLIT_TILES=2): a half that repeats its pass still meets its partner."""
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
+    lib = A.HipAttentionLibrary(0)
+    try:
+        _nonfinite_rows_case(lib, 0, which, 128)
+    finally:
+        lib.close()
+
+
+def _nonfinite_rows_case(hip, window, which, d):
     """Positions a row does not see never reach its result, whatever the cache holds there: 48
     rows are appended with key (or value) row 45 (and, windowed, row 3) overflowing f16 to
     infinity, positions 40.. are discarded (the slots keep their contents), and rows 40..43 are
