@@ -1485,10 +1485,11 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   float16_t negm;
   const uint32_t kr = swap34(j);
 
-  // LDS reads are issued in batches of up to 8 ahead of the matrix ops that consume them: with
+  // LDS reads are issued in batches of up to 4 ahead of the matrix ops that consume them: with
   // eight waves and the direct-to-LDS traffic sharing the LDS, one read's latency is several
-  // hundred cycles, and a read-use-read chain would serialise on it.
-  constexpr int kBatch = kKS < 8 ? kKS : 8;
+  // hundred cycles, and a read-use-read chain would serialise on it. (Batches of 8 measured ~1%
+  // slower on C3.)
+  constexpr int kBatch = kKS < 4 ? kKS : 4;
   // Two passes share the code below. The fast pass masks a partly visible tile through the
   // accumulators its first QK^T op starts from: kMaskFloor (-2^100) at the positions a column
   // does not see (outside [first, position], or past t1), so no score is masked after the matrix
