@@ -16,7 +16,13 @@
  *   - host-buffer calls are synchronous: they return once outputs are visible to the host;
  *   - *_device calls take device pointers and are asynchronous on the context stream; errors
  *     detected by kernels are reported by jmodels_attn_context_synchronize;
- *   - outputs must not alias inputs (RS:535-539).
+ *   - outputs must not alias inputs (RS:535-539);
+ *   - *_device calls may be captured into a HIP graph on the context stream. A context keeps
+ *     grow-only scratch memory (split partials, arrival tickets, rotated queries) sized by the
+ *     largest launch plan seen so far; a call whose plan needs more while the stream is being
+ *     captured returns NOT_CAPTURABLE and enqueues nothing, so run each shape once outside the
+ *     capture first. Scratch that is outgrown later stays allocated until the context is
+ *     destroyed, so graphs captured earlier remain valid.
  *
  * Ownership change vs the reference: the library owns the KV cache, resident in HBM and
  * appended in place; Java holds an opaque handle instead of float[] buffers.
@@ -52,6 +58,11 @@ extern "C" {
                                             BJ/cache/LayeredKvCache.java:192-197) */
 #define JMODELS_ATTN_NON_FINITE 8        /* an attention score was NaN or +inf; TensorOps.softmax
                                             rejects those (BJ/ops/TensorOps.java:1256-1269) */
+#define JMODELS_ATTN_NOT_CAPTURABLE 9    /* the call needs more context scratch memory than was
+                                            allocated so far, and the context stream is being
+                                            captured into a graph: nothing was enqueued. Make the
+                                            same call once outside the capture first (no
+                                            counterpart in the reference, which has no graphs) */
 
 /* Capability bits (RS:59-77 style). */
 #define JMODELS_ATTN_CAP_DECODE_F32 (1ull << 0)      /* f32 KV split-K decode */

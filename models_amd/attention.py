@@ -42,6 +42,7 @@ DEVICE_ERROR = 5
 OUT_OF_RANGE = 6
 UNAVAILABLE = 7
 NON_FINITE = 8
+NOT_CAPTURABLE = 9
 
 CAP_DECODE_F32 = 1 << 0
 CAP_DECODE_F16 = 1 << 1

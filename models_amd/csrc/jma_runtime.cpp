@@ -62,35 +62,55 @@ int32_t guard(F&& body) {
 
 uint64_t round_up(uint64_t x, uint64_t m) { return (x + m - 1) / m * m; }
 
-// Grow-only device buffer owned by a context.
+// Fails with NOT_CAPTURABLE when `stream` is being captured into a graph: a call that would
+// allocate, fill or wait there must first run once outside the capture.
+void require_not_capturing(hipStream_t stream, const char* what) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  hip_check(hipStreamIsCapturing(stream, &status), "hipStreamIsCapturing");
+  if (status != hipStreamCaptureStatusNone)
+    fail(JMODELS_ATTN_NOT_CAPTURABLE,
+         std::string(what) + " needs more scratch memory than this context holds while its stream "
+                             "is being captured; make the same call once outside the capture first");
+}
+
+// Grow-only device buffer owned by a context. A buffer it outgrows is retired, not freed, until
+// the context is destroyed: graphs captured earlier keep the old address in their kernel
+// arguments and may still be replayed. Sizes at least double, so the retired buffers together
+// never exceed the current one.
 struct DeviceBuffer {
   void* ptr = nullptr;
   size_t bytes = 0;
-  // Regrowth waits for `stream` so no queued kernel still reads the old allocation.
-  void reserve(size_t need, hipStream_t stream) {
+  std::vector<void*> retired;
+  // Growth is refused while `stream` is being captured; otherwise it waits for `stream` (its
+  // kernels may still use the old allocation, whose contents callers may copy).
+  void reserve(size_t need, hipStream_t stream, const char* what = "scratch") {
     if (need <= bytes) return;
-    if (ptr) {
-      hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
-      hip_check(hipFree(ptr), "hipFree");
-    }
-    ptr = nullptr;
-    bytes = 0;
-    size_t grow = std::max(need, (size_t)1 << 16);
-    hip_check(hipMalloc(&ptr, grow), "hipMalloc scratch");
+    require_not_capturing(stream, what);
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    const size_t grow = std::max({need, 2 * bytes, (size_t)1 << 16});
+    void* fresh = nullptr;
+    hip_check(hipMalloc(&fresh, grow), "hipMalloc scratch");
+    if (ptr) retired.push_back(ptr);
+    ptr = fresh;
     bytes = grow;
   }
   void release() {
+    for (void* p : retired) (void)hipFree(p);
+    retired.clear();
     if (ptr) (void)hipFree(ptr);
     ptr = nullptr;
     bytes = 0;
   }
 };
 
-// Grows `buf` to `need` bytes; a new allocation has every byte set to `byte`.
-void reserve_filled(DeviceBuffer& buf, size_t need, int byte, hipStream_t stream) {
+// Grows `buf` to `need` bytes; a new allocation has every byte set to `byte` (synchronously, so
+// no fill is ever recorded into a caller's graph).
+void reserve_filled(DeviceBuffer& buf, size_t need, int byte, hipStream_t stream,
+                    const char* what = "scratch") {
   if (need <= buf.bytes) return;
-  buf.reserve(need, stream);
+  buf.reserve(need, stream, what);
   hip_check(hipMemsetAsync(buf.ptr, byte, buf.bytes, stream), "fill scratch");
+  hip_check(hipStreamSynchronize(stream), "fill scratch");
 }
 
 int env_int(const char* name, int fallback) {
@@ -426,17 +446,18 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.v_base = (char*)a.kv.v + (a.kv.seq_stride_v * rows.seq0 + a.kv.layer_off_v) * es;
   }
   if (any_split && (ctx->unfused || wide)) {
-    ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream);
-    ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream);
+    ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream, "decode partials");
+    ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream, "decode partials");
     a.part_acc = (float*)ctx->part_acc.ptr;
     a.part_ml = (float*)ctx->part_ml.ptr;
   } else if (any_split) {
     // Arrival tickets start at zero and every partial word starts not-written; the reducing
     // workgroups restore both, so they are zeroed only when (re)allocated, never inside a launch
     // sequence a caller may capture.
-    reserve_filled(ctx->part_f, (size_t)items * 16 * (kv->dv + 4) * sizeof(float), 0xFF, ctx->stream);
+    reserve_filled(ctx->part_f, (size_t)items * 16 * (kv->dv + 4) * sizeof(float), 0xFF, ctx->stream,
+                   "decode split exchange");
     reserve_filled(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t), 0,
-                   ctx->stream);
+                   ctx->stream, "decode split exchange");
     a.part_f = (float*)ctx->part_f.ptr;
     a.counters = (uint32_t*)ctx->counters.ptr;
   }
@@ -541,8 +562,9 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.split_blocks = plan.split_blocks;
     if (plan.pairs > 0) {
       // Tickets start at zero and partial words not-written; the merging workgroups restore both.
-      reserve_filled(ctx->pf_part, plan.part_bytes, 0xFF, ctx->stream);
-      reserve_filled(ctx->pf_tickets, (size_t)plan.pairs * sizeof(uint32_t), 0, ctx->stream);
+      reserve_filled(ctx->pf_part, plan.part_bytes, 0xFF, ctx->stream, "prefill split exchange");
+      reserve_filled(ctx->pf_tickets, (size_t)plan.pairs * sizeof(uint32_t), 0, ctx->stream,
+                     "prefill split exchange");
       a.part = (float*)ctx->pf_part.ptr;
       a.tickets = (uint32_t*)ctx->pf_tickets.ptr;
     }
@@ -583,7 +605,7 @@ void prefill_impl(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCal
   const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
   if (!(kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv))) check_decode_shape(kv);
   validate_causal(kv, lc, sequence, start, n, false);
-  ctx->qrot.reserve((size_t)n * qdim * sizeof(float), ctx->stream);
+  ctx->qrot.reserve((size_t)n * qdim * sizeof(float), ctx->stream, "prefill rotated queries");
   // One launch appends every row: consecutive positions of one sequence need no row table.
   jma::RowList rows{};
   rows.count = n;
@@ -652,6 +674,7 @@ const char* jmodels_attn_status_name(int32_t status) {
     case JMODELS_ATTN_OUT_OF_RANGE: return "OUT_OF_RANGE";
     case JMODELS_ATTN_UNAVAILABLE: return "UNAVAILABLE";
     case JMODELS_ATTN_NON_FINITE: return "NON_FINITE";
+    case JMODELS_ATTN_NOT_CAPTURABLE: return "NOT_CAPTURABLE";
     default: return "UNKNOWN";
   }
 }
@@ -1226,7 +1249,7 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
       }
       for (uint32_t i = 0; i < count; ++i) kv->mark(sequences[i], lc.layer, positions[i]);
     } else {
-      ctx->qrot.reserve(qn * sizeof(float), ctx->stream);
+      ctx->qrot.reserve(qn * sizeof(float), ctx->stream, "decode rotated queries");
       float* qrot = (float*)ctx->qrot.ptr;
       append_rows(ctx, kv, lc, count, sequences, positions, dq, dk, dv, qrot);
       run_attend(ctx, kv, lc, count, sequences, positions, qrot, dout);

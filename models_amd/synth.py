@@ -14,6 +14,8 @@ host (Python here, Java later) can reproduce bit for bit:
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -51,14 +53,36 @@ def words(seed: int, tag: str, count: int, offset: int = 0) -> np.ndarray:
         return _mix(key + idx * _GOLDEN)
 
 
-def normal(seed: int, tag: str, shape) -> np.ndarray:
-    """float32 N(0,1) array of ``shape`` from stream (seed, tag)."""
-    n = int(np.prod(shape)) if np.ndim(shape) else int(shape)
-    w = words(seed, tag, 2 * n)
+_CHUNK = 1 << 20  # values per chunk when a large array is generated on several threads
+
+
+def _normal_into(out: np.ndarray, key: np.uint64, start: int) -> None:
+    """Values start .. start + out.size of the stream with key ``key``, written into ``out``."""
+    n = out.size
+    with np.errstate(over="ignore"):
+        idx = np.arange(2 * start + 1, 2 * (start + n) + 1, dtype=np.uint64)
+        w = _mix(key + idx * _GOLDEN)
     u1 = ((w[0::2] >> np.uint64(11)).astype(np.float64) + 1.0) * (2.0 ** -53)
     u2 = (w[1::2] >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
-    z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
-    return z.astype(np.float32).reshape(shape)
+    out[:] = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+
+
+def normal(seed: int, tag: str, shape) -> np.ndarray:
+    """float32 N(0,1) array of ``shape`` from stream (seed, tag). Large arrays are produced in
+    chunks on up to 16 threads (numpy releases the GIL); every value depends only on its index, so
+    the result is the same as one pass."""
+    n = int(np.prod(shape)) if np.ndim(shape) else int(shape)
+    key = stream_key(seed, tag)
+    out = np.empty(n, np.float32)
+    if n <= _CHUNK:
+        _normal_into(out, key, 0)
+        return out.reshape(shape)
+    from concurrent.futures import ThreadPoolExecutor
+    starts = range(0, n, _CHUNK)
+    workers = max(1, min(16, os.cpu_count() or 1, len(starts)))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(lambda s0: _normal_into(out[s0:s0 + _CHUNK], key, s0), starts))
+    return out.reshape(shape)
 
 
 def uniform_int(seed: int, tag: str, count: int, low: int, high: int) -> np.ndarray:

@@ -57,7 +57,7 @@ def test_abi_version_and_capabilities(lib):
 def test_status_names(lib):
     # NativeKernelLibrary.statusName analogue: codes 0-4 keep backend-native's meaning.
     names = {0: "OK", 1: "NULL_POINTER", 2: "INVALID_SHAPE", 3: "BUFFER_TOO_SMALL", 4: "PANIC",
-             5: "DEVICE_ERROR", 6: "OUT_OF_RANGE", 7: "UNAVAILABLE", 8: "NON_FINITE",
+             5: "DEVICE_ERROR", 6: "OUT_OF_RANGE", 7: "UNAVAILABLE", 8: "NON_FINITE", 9: "NOT_CAPTURABLE",
              99: "UNKNOWN"}
     for code, name in names.items():
         assert lib.jmodels_attn_status_name(code).decode() == name

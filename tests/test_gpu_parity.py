@@ -2,8 +2,10 @@
 
 Bars (from the path's contract): KV-cache contents, RoPE outputs, window bounds and positions are
 bit-exact; attention outputs are within max-abs 1e-3 with f32 KV and normwise relative 2e-2 with
-f16 KV. Configs C1-C5 are the five BASELINE workloads; sizes the oracle cannot finish in seconds
-are reduced, and the full sizes are covered by spot checks and size-independent properties."""
+f16 KV (per (row, head) output vector). Configs C1-C5 are the five BASELINE workloads, each run at
+its configured size against the oracle (C2's 16 x 128 layer-steps by oracle spot checks plus
+size-independent properties: replay idempotence and bit-exact appended rows); reduced variants
+exercise the host-buffer entry points and edge cases."""
 
 import math
 import sys
@@ -204,10 +206,10 @@ def test_qk_norm_prefill_then_decode(hip, half, sides):
     try:
         layer = A.AttentionLayer(0, hq, neox=True, rope=rope, qk_norm=norm)
         got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior])
-        e = [close(got_prefill, ref_prefill, "QK-norm prefill")]
+        e = [close(got_prefill, ref_prefill, "QK-norm prefill", head_dim=d)]
         for s in range(steps):
             got = kv.decode(layer, [prior + s], q[prior + s], k[prior + s], v[prior + s])
-            e.append(close(got, ref_dec[s], f"QK-norm decode step {s}"))
+            e.append(close(got, ref_dec[s], f"QK-norm decode step {s}", head_dim=d))
         _say(f"QK-norm half={half} errors " + " ".join(f"{x:.2e}" for x in e))
         np.testing.assert_array_equal(kv.key_slice(0, 0, n), ref.key_slice(0, 0, n))
     finally:
@@ -248,10 +250,10 @@ def test_gemma4_value_norm_prefill_then_decode(hip, half, d):
         try:
             layer = A.AttentionLayer(0, hq, neox=True, scale=1.0, rope=rope, qk_norm=norm)
             got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior])
-            e = [close(got_prefill, ref_prefill, f"Gemma-4 prefill d {d} k_as_v {k_as_v}")]
+            e = [close(got_prefill, ref_prefill, f"Gemma-4 prefill d {d} k_as_v {k_as_v}", head_dim=d)]
             for s in range(steps):
                 got = kv.decode(layer, [prior + s], q[prior + s], k[prior + s], v[prior + s])
-                e.append(close(got, ref_dec[s], f"Gemma-4 decode d {d} step {s}"))
+                e.append(close(got, ref_dec[s], f"Gemma-4 decode d {d} step {s}", head_dim=d))
             _say(f"Gemma-4 d={d} half={half} k_as_v={k_as_v} errors " + " ".join(f"{x:.2e}" for x in e))
             np.testing.assert_array_equal(kv.key_slice(0, 0, n), ref.key_slice(0, 0, n))
             np.testing.assert_array_equal(kv.value_slice(0, 0, n), ref.value_slice(0, 0, n))
@@ -336,8 +338,8 @@ def test_c1_qwen3_decode_f32(hip):
         layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
         got_prefill = kv.prefill(layer, 0, q[:prior], k[:prior], v[:prior])
         got = kv.decode(layer, [prior], q[prior], k[prior], v[prior])
-        e1 = assert_f32_close(got_prefill, ref_prefill, "C1 prefill rows")
-        e2 = assert_f32_close(got, ref_out, "C1 decode")
+        e1 = assert_f32_close(got_prefill, ref_prefill, "C1 prefill rows", head_dim=d)
+        e2 = assert_f32_close(got, ref_out, "C1 decode", head_dim=d)
         _say(f"C1 max abs err prefill {e1:.2e} decode {e2:.2e}")
         np.testing.assert_array_equal(kv.key_slice(0, 0, prior + 1), ref.key_slice(0, 0, prior + 1))
         np.testing.assert_array_equal(kv.value_slice(0, 0, prior + 1),
@@ -371,13 +373,13 @@ def test_c2_llama_decode_f16_reduced(hip):
             q_rot = rope_rows(q, range(n), hq, d, d, theta, False)
             for row in (0, 1, 31, 32, 500, prior - 1):
                 want = ref.gqa(0, row, q_rot[row], hq, hkv, d, d, scale)
-                assert_f16_close(got_prefill[row], want, f"C2 prefill row {row}")
+                assert_f16_close(got_prefill[row], want, f"C2 prefill row {row}", head_dim=d)
             for s in range(steps):
                 p = prior + s
                 got = kv.decode(layer, [p], q[p], k[p], v[p])
                 want, _, _ = ref.decode_layer(0, p, q[p], k[p], v[p], hq, hkv, d, d, theta, 1.0,
                                               False, scale)
-                rel = assert_f16_close(got, want, f"C2 layer {l} step {s}")
+                rel = assert_f16_close(got, want, f"C2 layer {l} step {s}", head_dim=d)
             _say(f"C2 layer {l} last-step normwise rel err {rel:.2e}")
             np.testing.assert_array_equal(kv.key_slice(l, 0, n), ref.key_slice(0, 0, n))
             np.testing.assert_array_equal(kv.value_slice(l, 0, n), ref.value_slice(0, 0, n))
@@ -412,7 +414,7 @@ def test_c3_llama_prefill_f16_full(hip):
         outs = oracle.gqa_rows_batch([q_rot[r] for r in rows], [keys[:r + 1] for r in rows],
                                      [values[:r + 1] for r in rows], hq, hkv, d, d, scale,
                                      threads=16)
-        rel = assert_f16_close(got, np.stack(outs), "C3 prefill")
+        rel = assert_f16_close(got, np.stack(outs), "C3 prefill", head_dim=d)
         _say(f"C3 normwise rel err {rel:.2e}")
     finally:
         kv.close()
@@ -441,14 +443,14 @@ def test_prefill_chunked_and_windowed_matches_oracle(hip):
             layer = A.AttentionLayer(0, hq, sliding_window=window, neox=True, rope=rope)
             g1 = kv.prefill(layer, 0, q[:n1], k[:n1], v[:n1])
             g2 = kv.prefill(layer, n1, q[n1:], k[n1:], v[n1:])
-            assert_f16_close(g1, r1, f"chunk 1 window {window}")
-            assert_f16_close(g2, r2, f"chunk 2 window {window}")
+            assert_f16_close(g1, r1, f"chunk 1 window {window}", head_dim=d)
+            assert_f16_close(g2, r2, f"chunk 2 window {window}", head_dim=d)
         finally:
             kv.close()
     rope.close()
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 def test_prefill_split_blocks_match_oracle(monkeypatch, d):
     """Row blocks whose kv range is split between two workgroups (the second to arrive merges the
     halves through not-written words) against the oracle, for every split threshold
@@ -478,13 +480,46 @@ def test_prefill_split_blocks_match_oracle(monkeypatch, d):
                 for rep in range(2):  # the second pass reuses the restored words and tickets
                     g1 = kv.prefill(layer, 0, q[:n1], k[:n1], v[:n1])
                     g2 = kv.prefill(layer, n1, q[n1:], k[n1:], v[n1:])
-                    assert_f16_close(g1, r1, f"d {d} window {window} split {split} chunk 1")
-                    assert_f16_close(g2, r2, f"d {d} window {window} split {split} chunk 2")
+                    assert_f16_close(g1, r1, f"d {d} window {window} split {split} chunk 1", head_dim=d)
+                    assert_f16_close(g2, r2, f"d {d} window {window} split {split} chunk 2", head_dim=d)
                 kv.close()
                 rope.close()
             finally:
                 lib.close()
             _say(f"d {d} window {window} split {split} ok")
+
+
+def test_gemma3_prefill_2048_automatic_split(hip):
+    """A Gemma-3-shaped 2048-row prefill (4 Q / 1 KV heads, d 256, NeoX theta 1e6) under the
+    automatic plan: row blocks hold 2 stripes of 8 rows x 4 heads, and the 34 longest (>= 48 kv
+    tiles against an average of 16 per compute unit) have their kv range split between two
+    workgroups that merge through the partial-word exchange. Every row against the oracle over
+    the read-back cache; K bit-exact."""
+    hq, hkv, d, S, theta = 4, 1, 256, 2048, 1e6
+    scale = A.default_scale(d)
+    q = normal(23, "g3p/q", (S, hq * d))
+    k = normal(23, "g3p/k", (S, hkv * d))
+    v = normal(23, "g3p/v", (S, hkv * d))
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=S)
+    kv = hip.kv_cache(1, S, hkv, d, d, half_precision=True)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        got = kv.prefill(layer, 0, q, k, v).reshape(S, hq * d)
+        got2 = kv.attend_causal(layer, 0, rope_rows(q, range(S), hq, d, d, theta, True)).reshape(S, -1)
+        np.testing.assert_array_equal(got2, got)  # the exchange words and tickets were restored
+        keys, values = kv.read(0, 0, S)
+        keys, values = keys.reshape(S, -1), values.reshape(S, -1)
+        np.testing.assert_array_equal(keys, oracle.f16_round(rope_rows(k, range(S), hkv, d, d,
+                                                                        theta, True)))
+        q_rot = rope_rows(q, range(S), hq, d, d, theta, True)
+        outs = oracle.gqa_rows_batch([q_rot[r] for r in range(S)], [keys[:r + 1] for r in range(S)],
+                                     [values[:r + 1] for r in range(S)], hq, hkv, d, d, scale,
+                                     threads=16)
+        rel = assert_f16_close(got, np.stack(outs), "Gemma-3 2048-row prefill", head_dim=d)
+        _say(f"Gemma-3 2048-row prefill normwise rel err {rel:.2e}")
+    finally:
+        kv.close()
+        rope.close()
 
 
 @pytest.mark.parametrize("d", [64, 128, 256])
@@ -494,14 +529,15 @@ def test_prefill_ignores_rows_it_does_not_see(hip, window, which, d):
     _nonfinite_rows_case(hip, window, which, d)
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("which", ["k", "v"])
-def test_split_prefill_ignores_rows_it_does_not_see(monkeypatch, which):
+def test_split_prefill_ignores_rows_it_does_not_see(monkeypatch, which, d):
     """The same with every row block of two or more kv tiles split between two workgroups
     (JMA_PREFILL_SPLIT_TILES=2): a half that repeats its pass still meets its partner."""
     monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
     lib = A.HipAttentionLibrary(0)
     try:
-        _nonfinite_rows_case(lib, 0, which, 128)
+        _nonfinite_rows_case(lib, 0, which, d)
     finally:
         lib.close()
 
@@ -540,13 +576,13 @@ def _nonfinite_rows_case(hip, window, which, d):
         assert not np.all(np.isfinite(stored))
         kv.discard_from(40)
         got = kv.prefill(layer, 40, q2, k2, v2)
-        assert_f16_close(got, want, f"d {d} {which} window {window} prefill")
+        assert_f16_close(got, want, f"d {d} {which} window {window} prefill", head_dim=d)
         # and a decode step at 44, whose kv tile still holds the infinite row 45
         q3, k3, v3 = (normal(22, f"nf/{t}3", (hq * d if t == "q" else hkv * d,)) for t in "qkv")
         want3, _, _ = ref.decode_layer(0, 44, q3, k3, v3, hq, hkv, d, d, theta, 1.0, True, scale,
                                        window=window)
         got3 = kv.decode(layer, [44], q3, k3, v3)
-        assert_f16_close(got3, want3, f"d {d} {which} window {window} decode")
+        assert_f16_close(got3, want3, f"d {d} {which} window {window} decode", head_dim=d)
     finally:
         kv.close()
         rope.close()
@@ -582,9 +618,76 @@ def test_c4_ragged_decode_reduced(hip):
                                                check_against_oracle=False))
             np.testing.assert_array_equal(keys.reshape(L + 1, -1)[L], k_new[0])
             want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
-            worst = max(worst, assert_f16_close(got[s], want, f"C4 session {s} (L={L})"))
+            worst = max(worst, assert_f16_close(got[s], want, f"C4 session {s} (L={L})", head_dim=d))
         _say(f"C4 worst normwise rel err {worst:.2e}")
     finally:
+        kv.close()
+        rope.close()
+
+
+def test_c4_ragged_decode_full_size(hip):
+    """BASELINE configs[3] at its configured size: 64 sessions whose KV lengths are the
+    benchmark's draw (U[256, 16384], seed 4, 480k cached rows), 12 Q / 2 KV heads, d 128, NeoX
+    theta 1e6, f16 KV, one new token per session in one fused decode launch (RoPE, append,
+    split-K attention, cross-split reduction). Every session against the oracle's GQA over the
+    read-back cache (attendIndependentSessions, llama/LlamaForwardPass.java:793-839); the appended
+    rows bit-exact; the longest and shortest sessions' whole caches bit-exact."""
+    from models_amd.hip_runtime import DeviceArray
+    hq, hkv, d, theta, B = 12, 2, 128, 1e6, 64
+    scale = A.default_scale(d)
+    lens = [int(x) for x in synth.uniform_int(4, "bench/c4/len", B, 256, 16384)]
+    maxlen = max(lens) + 1
+    qd, kd = hq * d, hkv * d
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=maxlen)
+    kv = hip.kv_cache(1, maxlen, hkv, d, d, half_precision=True, sequences=B)
+    zq = DeviceArray(maxlen * qd)
+    zq.zero()
+    dk, dv = DeviceArray(maxlen * kd), DeviceArray(maxlen * kd)
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        k_host = {}
+        check_full = {int(np.argmax(lens)), int(np.argmin(lens))}
+        for s, L in enumerate(lens):
+            k = normal(4, f"c4full/k{s}", (L, kd))
+            v = normal(4, f"c4full/v{s}", (L, kd))
+            if s in check_full:
+                k_host[s] = (k, v)
+            dk.upload(k)
+            dv.upload(v)
+            kv.append_device(layer, np.full(L, s, np.uint32), np.arange(L), zq.ptr, L * qd,
+                             dk.ptr, L * kd, dv.ptr, L * kd)
+        hip.synchronize()
+        _say(f"C4 full: {sum(lens)} rows cached")
+        qn = normal(4, "c4full/qn", (B, qd))
+        kn = normal(4, "c4full/kn", (B, kd))
+        vn = normal(4, "c4full/vn", (B, kd))
+        got = kv.decode(layer, lens, qn, kn, vn, sequences=np.arange(B)).reshape(B, -1)
+        q_rot = rope_rows(qn, lens, hq, d, d, theta, True)
+        k_new = oracle.f16_round(rope_rows(kn, lens, hkv, d, d, theta, True))
+        qs, ks, vs = [], [], []
+        for s, L in enumerate(lens):
+            keys, values = kv.read(0, 0, L + 1, sequence=s)
+            keys, values = keys.reshape(L + 1, kd), values.reshape(L + 1, kd)
+            np.testing.assert_array_equal(keys[L], k_new[s])
+            np.testing.assert_array_equal(values[L], oracle.f16_round(vn[s]))
+            if s in check_full:
+                k, v = k_host[s]
+                k_ref = oracle.f16_round(rope_rows(k, range(L), hkv, d, d, theta, True,
+                                                   check_against_oracle=False))
+                np.testing.assert_array_equal(keys[:L], k_ref)
+                np.testing.assert_array_equal(values[:L], oracle.f16_round(v))
+            qs.append(q_rot[s])
+            ks.append(keys)
+            vs.append(values)
+        outs = oracle.gqa_rows_batch(qs, ks, vs, hq, hkv, d, d, scale, threads=16)
+        worst = 0.0
+        for s, L in enumerate(lens):
+            worst = max(worst, assert_f16_close(got[s], outs[s], f"C4 full session {s} (L={L})",
+                                                head_dim=d))
+        _say(f"C4 full worst normwise rel err {worst:.2e}")
+    finally:
+        for buf in (zq, dk, dv):
+            buf.free()
         kv.close()
         rope.close()
 
@@ -628,12 +731,83 @@ def test_c5_gemma3_sliding_window_reduced(hip, ring):
                 got = kv.decode(layer, [p], q[p], k[p], v[p])
                 want, _, _ = ref.decode_layer(0, p, q[p], k[p], v[p], hq, hkv, d, d, theta, 1.0,
                                               True, scale, window=window)
-                rel = assert_f16_close(got, want, f"C5 layer {l} step {s}")
+                rel = assert_f16_close(got, want, f"C5 layer {l} step {s}", head_dim=d)
             _say(f"C5 ring={ring} layer {l} ({'swa' if sliding[l] else 'global'}) rel {rel:.2e}")
             if ring and sliding[l]:
                 assert not kv.contains(l, 0) and kv.contains(l, n - 1)
                 assert kv.contains(l, n - 544) and not kv.contains(l, n - 545)
     finally:
+        kv.close()
+        rope_swa.close()
+        rope_glb.close()
+
+
+def test_c5_gemma3_long_context_full_size(hip):
+    """BASELINE configs[4] at its configured size: 4 Q / 1 KV heads (MQA), d 256, NeoX RoPE
+    (theta 1e4 on sliding layers, 1e6 on the global layers 5, 11, 17, 23), f16 KV, 26 layers in
+    the 5 sliding (window 512) : 1 global pattern (LlamaConfig.usesSlidingWindow and
+    attentionStartPosition, llama/LlamaConfig.java:157-162, 184-195), 32704 prior positions and 3
+    decode steps. Sliding layers keep LayeredKvCache RING retention of 544 slots (window + one
+    32-row chunk) holding their last 512 prior positions; the global layers hold all 32704 and
+    run the wide split plans. Every layer and step against the oracle's GQA over the window read
+    back from the device, with the appended rows bit-exact."""
+    from models_amd.hip_runtime import DeviceArray
+    hq, hkv, d, prior, steps, layers, w, ring = 4, 1, 256, 32704, 3, 26, 512, 544
+    scale = A.default_scale(d)
+    n = prior + steps
+    qd, kd = hq * d, hkv * d
+    sliding = [A.uses_sliding_window(l, 6, w) for l in range(layers)]
+    assert [l for l in range(layers) if not sliding[l]] == [5, 11, 17, 23]
+    rope_swa = hip.rotary_table(d, 1e4, 1.0, max_positions=n)
+    rope_glb = hip.rotary_table(d, 1e6, 1.0, max_positions=n)
+    kv = hip.kv_cache(layers, n, hkv, d, d, half_precision=True,
+                      ring_capacity=[ring if sl else 0 for sl in sliding])
+    zq = DeviceArray(prior * qd)
+    zq.zero()
+    dk, dv = DeviceArray(prior * kd), DeviceArray(prior * kd)
+    try:
+        lp = [A.AttentionLayer(l, hq, sliding_window=w if sliding[l] else 0, neox=True,
+                               rope=rope_swa if sliding[l] else rope_glb) for l in range(layers)]
+        for l in range(layers):
+            first = prior - w if sliding[l] else 0
+            rows = prior - first
+            dk.upload(normal(5, f"c5full/k{l}", (rows, kd)))
+            dv.upload(normal(5, f"c5full/v{l}", (rows, kd)))
+            kv.append_device(lp[l], np.zeros(rows, np.uint32), np.arange(first, prior), zq.ptr,
+                             rows * qd, dk.ptr, rows * kd, dv.ptr, rows * kd)
+        hip.synchronize()
+        _say("C5 full: caches filled")
+        q = normal(5, "c5full/q", (layers, steps, qd))
+        kn = normal(5, "c5full/kn", (layers, steps, kd))
+        vn = normal(5, "c5full/vn", (layers, steps, kd))
+        worst = {True: 0.0, False: 0.0}
+        for st in range(steps):
+            p = prior + st
+            outs = [kv.decode(lp[l], [p], q[l, st], kn[l, st], vn[l, st]) for l in range(layers)]
+            qs, ks, vs = [], [], []
+            for l in range(layers):
+                theta = 1e4 if sliding[l] else 1e6
+                first = A.attention_start_position(p, w if sliding[l] else 0)
+                keys, values = kv.read(l, first, p + 1)
+                keys, values = keys.reshape(-1, kd), values.reshape(-1, kd)
+                k_new = oracle.f16_round(rope_rows(kn[l, st:st + 1], [p], hkv, d, d, theta, True,
+                                                   check_against_oracle=(l < 6 and st == 0)))
+                np.testing.assert_array_equal(keys[-1], k_new[0])
+                np.testing.assert_array_equal(values[-1], oracle.f16_round(vn[l, st]))
+                qs.append(rope_rows(q[l, st:st + 1], [p], hq, d, d, theta, True,
+                                    check_against_oracle=(l < 6 and st == 0))[0])
+                ks.append(keys)
+                vs.append(values)
+            want = oracle.gqa_rows_batch(qs, ks, vs, hq, hkv, d, d, scale, threads=16)
+            for l in range(layers):
+                rel = assert_f16_close(outs[l], want[l], f"C5 full layer {l} step {st}", head_dim=d)
+                worst[sliding[l]] = max(worst[sliding[l]], rel)
+            # the ring holds what was stored and nothing older
+            assert kv.contains(0, prior - w) and not kv.contains(0, prior - w - 1)
+        _say(f"C5 full worst normwise rel err: sliding {worst[True]:.2e}, global {worst[False]:.2e}")
+    finally:
+        for buf in (zq, dk, dv):
+            buf.free()
         kv.close()
         rope_swa.close()
         rope_glb.close()
@@ -775,7 +949,7 @@ def test_c2_full_size_spot_checks_and_properties(hip):
                 q_rot = rope_rows(q_host[l, s:s + 1], [p], hq, d, d, theta, False)
                 want = oracle.gqa_rows(q_rot[0], keys[:p + 1], values[:p + 1], hq, hkv, d, d,
                                        scale)
-                rel = assert_f16_close(first[l, s], want, f"C2 full layer {l} step {s}")
+                rel = assert_f16_close(first[l, s], want, f"C2 full layer {l} step {s}", head_dim=d)
                 _say(f"C2 full layer {l} step {s} rel {rel:.2e}")
     finally:
         for buf in (zeros_q, dq, dk, dv, dout):
@@ -882,7 +1056,7 @@ def test_wide_split_decode_matches_oracle(hip, half, d):
             keys, values = kv.read(0, 0, L + 1, sequence=s_)
             q_rot = rope_rows(qn[s_:s_ + 1], [L], hq, d, d, theta, True, check_against_oracle=False)
             want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
-            err = close(got[s_], want, f"wide split d {d} session {s_} (L={L})")
+            err = close(got[s_], want, f"wide split d {d} session {s_} (L={L})", head_dim=d)
             _say(f"wide split half={half} d={d} L={L} err {err:.2e}")
     finally:
         kv.close()
@@ -916,7 +1090,7 @@ def test_wide_split_on_a_ring_layer_matches_oracle(hip):
         np.testing.assert_array_equal(keys.reshape(w, -1)[-1], k_new[0])
         q_rot = rope_rows(qn, [p], hq, d, d, theta, True, check_against_oracle=False)
         want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
-        err = assert_f16_close(got, want, "wide split on a ring layer")
+        err = assert_f16_close(got, want, "wide split on a ring layer", head_dim=d)
         _say(f"wide split ring err {err:.2e}")
     finally:
         kv.close()
@@ -979,3 +1153,104 @@ def test_graph_replays_match_eager_decode(hip):
             b.free()
         kv.close()
         rope.close()
+
+
+def test_scratch_growth_and_graph_capture(hip):
+    """Scratch memory and graph capture. (1) In a fresh context, the first wide-plan decode
+    (one long MQA row: partials for up to 1024 splits) issued while the context stream is being
+    captured is refused with NOT_CAPTURABLE, enqueues nothing and records no position; the same
+    call then runs eagerly, and a graph captured after it replays the eager result exactly.
+    (2) A graph captured with the scratch of a short-context plan still replays its own eager
+    result after a longer-context call has grown that scratch (the outgrown buffer stays alive)."""
+    import ctypes
+    from models_amd import hip_runtime as rt
+    lib = A.HipAttentionLibrary(0)
+    bufs, graphs = [], []
+    try:
+        stream = lib.stream()
+        h = rt.hip()
+        # (1) wide plan: 1 KV head, 8191 cached positions
+        hq, hkv, d, L = 4, 1, 128, 8191
+        rope = lib.rotary_table(d, 1e6, 1.0, max_positions=L + 1)
+        kv = lib.kv_cache(1, L + 1, hkv, d, d, half_precision=True)
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32),
+                  normal(31, "cap/k", (L, hkv * d)), normal(31, "cap/v", (L, hkv * d)))
+        dq = rt.DeviceArray.from_host(normal(31, "cap/q", (hq * d,)))
+        dk = rt.DeviceArray.from_host(normal(31, "cap/kn", (hkv * d,)))
+        dv = rt.DeviceArray.from_host(normal(31, "cap/vn", (hkv * d,)))
+        dout = rt.DeviceArray(hq * d)
+        bufs += [dq, dk, dv, dout]
+
+        def call():
+            kv.decode_device(layer, [0], [L], dq.ptr, hq * d, dk.ptr, hkv * d, dv.ptr, hkv * d,
+                             dout.ptr, hq * d)
+
+        rt.check(h.hipStreamBeginCapture(stream, rt.Graph.RELAXED), "hipStreamBeginCapture")
+        try:
+            with pytest.raises(A.AttentionStatusError) as e:
+                call()
+        finally:
+            g = ctypes.c_void_p()
+            rt.check(h.hipStreamEndCapture(stream, ctypes.byref(g)), "hipStreamEndCapture")
+            h.hipGraphDestroy(g)
+        assert e.value.status == A.NOT_CAPTURABLE, e.value
+        assert not kv.contains(0, L)
+        dout.zero()
+        call()
+        lib.synchronize()
+        eager = dout.download()
+        assert np.all(np.isfinite(eager)) and np.any(eager)
+        kv.discard_from(L)
+        graphs.append(rt.Graph(stream, call))
+        kv.discard_from(L)
+        for replay in range(3):
+            dout.zero()
+            graphs[-1].launch()
+            lib.synchronize()
+            np.testing.assert_array_equal(dout.download(), eager, err_msg=f"wide replay {replay}")
+        kv.close()
+        rope.close()
+
+        # (2) fused split exchange: 8 KV heads, a short row then a long one in another session
+        hq, hkv, d = 8, 8, 128
+        lens = [1000, 8000]
+        rope = lib.rotary_table(d, 1e6, 1.0, max_positions=max(lens) + 1)
+        kv = lib.kv_cache(1, max(lens) + 1, hkv, d, d, half_precision=True, sequences=2)
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        for s, n in enumerate(lens):
+            kv.append(layer, np.arange(n), np.zeros((n, hq * d), np.float32),
+                      normal(32, f"grow/k{s}", (n, hkv * d)), normal(32, f"grow/v{s}", (n, hkv * d)),
+                      sequences=np.full(n, s))
+        ins = [[rt.DeviceArray.from_host(normal(32, f"grow/{t}{s}", (hq * d if t == "q" else hkv * d,)))
+                for t in "qkv"] for s in range(2)]
+        outs = [rt.DeviceArray(hq * d) for _ in range(2)]
+        bufs += [b for row in ins for b in row] + outs
+
+        def call_s(s):
+            q, k, v = ins[s]
+            kv.decode_device(layer, [s], [lens[s]], q.ptr, hq * d, k.ptr, hkv * d, v.ptr, hkv * d,
+                             outs[s].ptr, hq * d)
+
+        call_s(0)
+        lib.synchronize()
+        eager0 = outs[0].download()
+        kv.discard_from(lens[0], sequence=0)
+        graphs.append(rt.Graph(stream, lambda: call_s(0)))
+        kv.discard_from(lens[0], sequence=0)
+        call_s(1)  # a wider plan: the exchange scratch grows here
+        lib.synchronize()
+        assert np.all(np.isfinite(outs[1].download()))
+        for replay in range(3):
+            outs[0].zero()
+            graphs[-1].launch()
+            lib.synchronize()
+            np.testing.assert_array_equal(outs[0].download(), eager0, err_msg=f"replay {replay}")
+        kv.close()
+        rope.close()
+    finally:
+        for g in graphs:
+            g.destroy()
+        for b in bufs:
+            b.free()
+        lib.close()
