@@ -276,6 +276,23 @@ JMODELS_ATTN_API int32_t jmodels_attn_decode_device(jmodels_attn_context* ctx, j
                                    const float* q, uint64_t q_elements, const float* k,
                                    uint64_t k_elements, const float* v, uint64_t v_elements,
                                    float* out, uint64_t out_elements);
+/* jmodels_attn_decode_device without any device allocation. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Instead of the context's grow-only
+ * scratch it uses one fixed array per GPU, a file-scope device array of 41 MiB (64 KiB of arrival
+ * tickets, 16 MiB of fused split partials, 16 MiB + 1 MiB of partials for the separate reduction,
+ * 8 MiB of rotated queries) that each GPU the library runs on holds until the process ends. A
+ * launch plan needing more than a region holds is refused with BUFFER_TOO_SMALL before anything
+ * is enqueued. Every call on a GPU shares that GPU's array, whatever the context: calls that
+ * overlap on one GPU (two contexts' streams, or two threads) race. Sequential calls are safe:
+ * each launch leaves the exchange regions as it found them. */
+JMODELS_ATTN_API int32_t jmodels_attn_decode_device_noalloc(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                           const jmodels_attn_layer* layer, uint32_t count,
+                                           const uint32_t* sequences, const uint32_t* positions,
+                                           const float* q, uint64_t q_elements, const float* k,
+                                           uint64_t k_elements, const float* v,
+                                           uint64_t v_elements, float* out,
+                                           uint64_t out_elements);
 JMODELS_ATTN_API int32_t jmodels_attn_attend_causal_device(jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
                                           const jmodels_attn_layer* layer, uint32_t sequence,
                                           uint32_t start, uint32_t n, const float* q,

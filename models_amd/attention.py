@@ -70,7 +70,7 @@ EXPORTS = (
     "jmodels_attn_append_device", "jmodels_attn_attend_device", "jmodels_attn_decode_device",
     "jmodels_attn_prefill_device", "jmodels_attn_attend_causal",
     "jmodels_attn_attend_causal_device", "jmodels_attn_norm_create", "jmodels_attn_norm_create_ex",
-    "jmodels_attn_norm_destroy",
+    "jmodels_attn_norm_destroy", "jmodels_attn_decode_device_noalloc",
 )
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -138,7 +138,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         sig[name] = (_i32, rows + [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _u64])
     for name in ("jmodels_attn_attend", "jmodels_attn_attend_device"):
         sig[name] = (_i32, rows + [_vp, _u64, _vp, _u64])
-    for name in ("jmodels_attn_decode", "jmodels_attn_decode_device"):
+    for name in ("jmodels_attn_decode", "jmodels_attn_decode_device",
+                 "jmodels_attn_decode_device_noalloc"):
         sig[name] = (_i32, rows + [_vp, _u64, _vp, _u64, _vp, _u64, _vp, _u64])
     for name in ("jmodels_attn_attend_causal", "jmodels_attn_attend_causal_device"):
         sig[name] = (_i32, [_vp, _vp, _LP, _u32, _u32, _u32, _vp, _u64, _vp, _u64])
@@ -518,6 +519,18 @@ class HipKvCache:
             o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
             pos.ctypes.data_as(_u32p), q_ptr, q_elems, k_ptr, k_elems, v_ptr, v_elems, out_ptr,
             out_elems), "decode_device")
+
+    def decode_device_noalloc(self, layer: AttentionLayer, sequences, positions, q_ptr: int,
+                              q_elems: int, k_ptr: int, k_elems: int, v_ptr: int, v_elems: int,
+                              out_ptr: int, out_elems: int) -> None:
+        """decode_device on the GPU's fixed scratch: allocates no device memory."""
+        seq, pos = self._rows(sequences, positions)
+        st = layer.struct()
+        o = self.owner
+        o.check(o.lib.jmodels_attn_decode_device_noalloc(
+            o.ctx, self.handle, ctypes.byref(st), seq.size, seq.ctypes.data_as(_u32p),
+            pos.ctypes.data_as(_u32p), q_ptr, q_elems, k_ptr, k_elems, v_ptr, v_elems, out_ptr,
+            out_elems), "decode_device_noalloc")
 
     def attend_device(self, layer: AttentionLayer, sequences, positions, q_ptr: int,
                       q_elems: int, out_ptr: int, out_elems: int) -> None:

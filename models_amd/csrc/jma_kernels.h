@@ -136,6 +136,25 @@ PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t
 // Storage block (slots) of the transposed V layout.
 inline int v_block(bool f16) { return f16 ? 32 : 16; }
 
+// Fixed device scratch of the allocation-free decode entry point: one file-scope array per GPU
+// (in jma_kernels.hip), split into the regions a decode launch may need. Every call on a GPU
+// shares its GPU's array; the split exchange leaves the exchange regions as it found them
+// (tickets zero, partial words not-written), so they are prepared once per device.
+struct FixedScratch {
+  uint32_t* counters = nullptr;  // arrival tickets, zero between launches
+  float* part_f = nullptr;       // fused split partials, every word 0xFFFFFFFF between launches
+  float* part_acc = nullptr;     // partials combined by reduce_kernel
+  float* part_ml = nullptr;
+  float* qrot = nullptr;         // rotated queries of the separate-kernel path
+  size_t counters_bytes = 0, part_f_bytes = 0, part_acc_bytes = 0, part_ml_bytes = 0, qrot_bytes = 0;
+};
+// Looks up the array's device address on `device` (which must be current) the first time it is
+// asked for that device, prepares the exchange regions there with fill kernels on `stream` and
+// waits for them; later calls return the cached addresses.
+hipError_t fixed_scratch(int device, hipStream_t stream, FixedScratch* out);
+// Restores the exchange regions of `device`'s array (after a reducer gave up waiting).
+hipError_t fixed_scratch_reset(const FixedScratch& s, hipStream_t stream);
+
 bool decode_supported(bool f16, int dk, int dv);
 bool prefill_supported(int dk, int dv);
 

@@ -16,6 +16,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "jma_kernels.h"
@@ -1082,6 +1084,72 @@ hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream) {
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// ================================================================ fixed scratch
+
+// The allocation-free decode entry point's scratch: a file-scope device array (each GPU the
+// library runs on holds its own copy until the process ends). Host code never uses the array's
+// name as an address: fixed_scratch() resolves the device address with hipGetSymbolAddress once
+// per device and hands out that pointer.
+constexpr size_t kFixedCounterBytes = size_t(64) << 10;
+constexpr size_t kFixedPartFBytes = size_t(16) << 20;
+constexpr size_t kFixedPartAccBytes = size_t(16) << 20;
+constexpr size_t kFixedPartMlBytes = size_t(1) << 20;
+constexpr size_t kFixedQrotBytes = size_t(8) << 20;
+constexpr size_t kFixedBytes =
+    kFixedCounterBytes + kFixedPartFBytes + kFixedPartAccBytes + kFixedPartMlBytes + kFixedQrotBytes;
+static __device__ __align__(256) unsigned char scratch[kFixedBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_fixed_mutex;
+static FixedScratch g_fixed[kMaxDevices];
+static bool g_fixed_ready[kMaxDevices];
+
+__global__ __launch_bounds__(256) void fill_words_kernel(uint32_t* p, uint32_t value, uint64_t words) {
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (uint64_t)gridDim.x * 256)
+    p[i] = value;
+}
+
+static hipError_t fill_words(void* p, uint32_t value, size_t bytes, hipStream_t stream) {
+  const uint64_t words = bytes / 4;
+  const uint32_t blocks = (uint32_t)std::min<uint64_t>((words + 255) / 256, 2048);
+  hipLaunchKernelGGL(fill_words_kernel, dim3(blocks), dim3(256), 0, stream, (uint32_t*)p, value, words);
+  return hipGetLastError();
+}
+
+hipError_t fixed_scratch_reset(const FixedScratch& s, hipStream_t stream) {
+  hipError_t e = fill_words(s.counters, 0u, s.counters_bytes, stream);
+  if (e == hipSuccess) e = fill_words(s.part_f, 0xFFFFFFFFu, s.part_f_bytes, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  return e;
+}
+
+hipError_t fixed_scratch(int device, hipStream_t stream, FixedScratch* out) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_fixed_mutex);
+  if (!g_fixed_ready[device]) {
+    unsigned char* base = nullptr;
+    hipError_t e = hipGetSymbolAddress((void**)&base, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    FixedScratch s;
+    s.counters = (uint32_t*)base;
+    s.counters_bytes = kFixedCounterBytes;
+    s.part_f = (float*)(base + kFixedCounterBytes);
+    s.part_f_bytes = kFixedPartFBytes;
+    s.part_acc = (float*)(base + kFixedCounterBytes + kFixedPartFBytes);
+    s.part_acc_bytes = kFixedPartAccBytes;
+    s.part_ml = (float*)(base + kFixedCounterBytes + kFixedPartFBytes + kFixedPartAccBytes);
+    s.part_ml_bytes = kFixedPartMlBytes;
+    s.qrot = (float*)(base + kFixedCounterBytes + kFixedPartFBytes + kFixedPartAccBytes + kFixedPartMlBytes);
+    s.qrot_bytes = kFixedQrotBytes;
+    e = fixed_scratch_reset(s, stream);
+    if (e != hipSuccess) return e;
+    g_fixed[device] = s;
+    g_fixed_ready[device] = true;
+  }
+  *out = g_fixed[device];
+  return hipSuccess;
 }
 
 bool decode_supported(bool f16, int dk, int dv) {

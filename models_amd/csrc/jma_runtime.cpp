@@ -131,6 +131,7 @@ struct jmodels_attn_context {
   int prefill_split_tiles = -1;     // split prefill row blocks of this many kv tiles; -1: automatic
   uint32_t cus = 256;               // compute units of the device
   bool unfused = false;             // JMA_UNFUSED=1: separate append and reduce kernels
+  jma::FixedScratch fixed;          // the device's fixed scratch (allocation-free decode)
 };
 
 struct jmodels_attn_rope {
@@ -369,9 +370,12 @@ struct FusedAppend {
   bool rope_q = false;  // q is raw: the kernel applies the layer's QK-norm and RoPE
 };
 
+// fixed: null = the context's grow-only scratch; else the device's fixed scratch, and a plan
+// that needs more than it holds is refused (BUFFER_TOO_SMALL) before anything is enqueued.
 void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
                      const jma::RowList& rows, const float* q, float* out,
-                     const FusedAppend& fa = FusedAppend()) {
+                     const FusedAppend& fa = FusedAppend(),
+                     const jma::FixedScratch* fixed = nullptr) {
   const uint32_t blk = (uint32_t)jma::v_block(kv->f16());
   jma::DecodeArgs a{};
   a.kv = kv->view(lc.layer);
@@ -445,21 +449,43 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.k_base = (char*)a.kv.k + (a.kv.seq_stride_k * rows.seq0 + a.kv.layer_off_k) * es;
     a.v_base = (char*)a.kv.v + (a.kv.seq_stride_v * rows.seq0 + a.kv.layer_off_v) * es;
   }
+  auto fits = [&](size_t need, size_t have, const char* what) {
+    require(need <= have, JMODELS_ATTN_BUFFER_TOO_SMALL,
+            std::string("the launch plan needs ") + std::to_string(need) + " bytes of " + what +
+                ", the fixed scratch holds " + std::to_string(have));
+  };
   if (any_split && (ctx->unfused || wide)) {
-    ctx->part_acc.reserve((size_t)items * 16 * kv->dv * sizeof(float), ctx->stream, "decode partials");
-    ctx->part_ml.reserve((size_t)items * 16 * 2 * sizeof(float), ctx->stream, "decode partials");
-    a.part_acc = (float*)ctx->part_acc.ptr;
-    a.part_ml = (float*)ctx->part_ml.ptr;
+    const size_t acc_b = (size_t)items * 16 * kv->dv * sizeof(float);
+    const size_t ml_b = (size_t)items * 16 * 2 * sizeof(float);
+    if (fixed) {
+      fits(acc_b, fixed->part_acc_bytes, "split partials");
+      fits(ml_b, fixed->part_ml_bytes, "split maxima and sums");
+      a.part_acc = fixed->part_acc;
+      a.part_ml = fixed->part_ml;
+    } else {
+      ctx->part_acc.reserve(acc_b, ctx->stream, "decode partials");
+      ctx->part_ml.reserve(ml_b, ctx->stream, "decode partials");
+      a.part_acc = (float*)ctx->part_acc.ptr;
+      a.part_ml = (float*)ctx->part_ml.ptr;
+    }
   } else if (any_split) {
     // Arrival tickets start at zero and every partial word starts not-written; the reducing
     // workgroups restore both, so they are zeroed only when (re)allocated, never inside a launch
     // sequence a caller may capture.
-    reserve_filled(ctx->part_f, (size_t)items * 16 * (kv->dv + 4) * sizeof(float), 0xFF, ctx->stream,
-                   "decode split exchange");
-    reserve_filled(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t), 0,
-                   ctx->stream, "decode split exchange");
-    a.part_f = (float*)ctx->part_f.ptr;
-    a.counters = (uint32_t*)ctx->counters.ptr;
+    const size_t part_b = (size_t)items * 16 * (kv->dv + 4) * sizeof(float);
+    const size_t ctr_b = (size_t)rows.count * kv->hkv * a.hgroups * sizeof(uint32_t);
+    if (fixed) {
+      fits(part_b, fixed->part_f_bytes, "split exchange partials");
+      fits(ctr_b, fixed->counters_bytes, "arrival tickets");
+      a.part_f = fixed->part_f;
+      a.counters = fixed->counters;
+    } else {
+      reserve_filled(ctx->part_f, part_b, 0xFF, ctx->stream, "decode split exchange");
+      reserve_filled(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t), 0,
+                     ctx->stream, "decode split exchange");
+      a.part_f = (float*)ctx->part_f.ptr;
+      a.counters = (uint32_t*)ctx->counters.ptr;
+    }
   }
   hip_check(jma::launch_decode(a, kv->f16(), kv->dk, kv->dv, ctx->stream), "decode launch");
   if (any_split && a.counters == nullptr)
@@ -476,13 +502,13 @@ bool can_fuse_decode(const jmodels_attn_context* ctx, const LayerCall& lc) {
 
 void run_attend(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
                 uint32_t count, const uint32_t* sequences, const uint32_t* positions,
-                const float* q, float* out) {
+                const float* q, float* out, const jma::FixedScratch* fixed = nullptr) {
   const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
   const uint64_t odim = (uint64_t)lc.num_heads * kv->dv;
   for (uint32_t base = 0; base < count; base += jma::kMaxRows) {
     const uint32_t n = std::min<uint32_t>(jma::kMaxRows, count - base);
     jma::RowList rows = make_rows(n, sequences + base, positions + base);
-    run_attend_rows(ctx, kv, lc, rows, q + base * qdim, out + base * odim);
+    run_attend_rows(ctx, kv, lc, rows, q + base * qdim, out + base * odim, FusedAppend(), fixed);
   }
 }
 
@@ -630,6 +656,7 @@ int32_t collect_errors(jmodels_attn_context* ctx) {
         if (b->ptr) hip_check(hipMemset(b->ptr, 0xFF, b->bytes), "reset partials");
       for (DeviceBuffer* b : {&ctx->counters, &ctx->pf_tickets})
         if (b->ptr) hip_check(hipMemset(b->ptr, 0, b->bytes), "reset tickets");
+      hip_check(jma::fixed_scratch_reset(ctx->fixed, ctx->stream), "reset fixed scratch");
       fail(JMODELS_ATTN_DEVICE_ERROR, "cross-split reduction timed out waiting for a partial");
     }
     fail(JMODELS_ATTN_NON_FINITE, "softmax input contains NaN or positive infinity");
@@ -703,6 +730,9 @@ jmodels_attn_context* jmodels_attn_context_create(int32_t device) {
       hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
       hip_check(hipMalloc(&ctx->d_err, sizeof(int)), "hipMalloc error word");
       hip_check(hipMemset(ctx->d_err, 0, sizeof(int)), "hipMemset error word");
+      // The device's fixed scratch: its address, and its exchange regions prepared, once per
+      // device (the allocation-free entry point then allocates nothing).
+      hip_check(jma::fixed_scratch(device, ctx->stream, &ctx->fixed), "fixed scratch");
     } catch (...) {
       if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
       if (ctx->d_err) (void)hipFree(ctx->d_err);
@@ -1189,12 +1219,14 @@ static int32_t attend_entry(bool device, jmodels_attn_context* ctx, const jmodel
   });
 }
 
+// fixed: null = the context's grow-only scratch; else the device's fixed scratch (device
+// pointers only), with plans that need more refused before anything is enqueued.
 static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn_kv* kv,
                             const jmodels_attn_layer* layer, uint32_t count,
                             const uint32_t* sequences, const uint32_t* positions, const float* q,
                             uint64_t q_elements, const float* k, uint64_t k_elements,
                             const float* v, uint64_t v_elements, float* out,
-                            uint64_t out_elements) {
+                            uint64_t out_elements, const jma::FixedScratch* fixed = nullptr) {
   return guard([&] {
     common_checks(ctx, kv);
     check_decode_shape(kv);
@@ -1245,14 +1277,22 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
         fa.k = dk + base * kdim;
         fa.v = dv + base * vdim;
         fa.rope_q = lc.rope != nullptr || lc.norm != nullptr;
-        run_attend_rows(ctx, kv, lc, rows, dq + base * qdim, dout + base * odim, fa);
+        run_attend_rows(ctx, kv, lc, rows, dq + base * qdim, dout + base * odim, fa, fixed);
       }
       for (uint32_t i = 0; i < count; ++i) kv->mark(sequences[i], lc.layer, positions[i]);
     } else {
-      ctx->qrot.reserve(qn * sizeof(float), ctx->stream, "decode rotated queries");
-      float* qrot = (float*)ctx->qrot.ptr;
+      float* qrot = nullptr;
+      if (fixed) {
+        require(qn * sizeof(float) <= fixed->qrot_bytes, JMODELS_ATTN_BUFFER_TOO_SMALL,
+                "the rotated queries need " + std::to_string(qn * sizeof(float)) +
+                    " bytes, the fixed scratch holds " + std::to_string(fixed->qrot_bytes));
+        qrot = fixed->qrot;
+      } else {
+        ctx->qrot.reserve(qn * sizeof(float), ctx->stream, "decode rotated queries");
+        qrot = (float*)ctx->qrot.ptr;
+      }
       append_rows(ctx, kv, lc, count, sequences, positions, dq, dk, dv, qrot);
-      run_attend(ctx, kv, lc, count, sequences, positions, qrot, dout);
+      run_attend(ctx, kv, lc, count, sequences, positions, qrot, dout, fixed);
     }
     if (device) return;
     hip_check(hipMemcpyAsync(out, dout, on * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
@@ -1414,6 +1454,18 @@ int32_t jmodels_attn_decode_device(jmodels_attn_context* ctx, jmodels_attn_kv* k
                                    float* out, uint64_t out_elements) {
   return decode_entry(true, ctx, kv, layer, count, sequences, positions, q, q_elements, k,
                       k_elements, v, v_elements, out, out_elements);
+}
+
+int32_t jmodels_attn_decode_device_noalloc(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
+                                           const jmodels_attn_layer* layer, uint32_t count,
+                                           const uint32_t* sequences, const uint32_t* positions,
+                                           const float* q, uint64_t q_elements, const float* k,
+                                           uint64_t k_elements, const float* v,
+                                           uint64_t v_elements, float* out,
+                                           uint64_t out_elements) {
+  if (!ctx) return JMODELS_ATTN_NULL_POINTER;
+  return decode_entry(true, ctx, kv, layer, count, sequences, positions, q, q_elements, k,
+                      k_elements, v, v_elements, out, out_elements, &ctx->fixed);
 }
 
 int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
