@@ -181,18 +181,49 @@ hipError_t launch_append(const AppendArgs& a, bool f16, hipStream_t stream) {
 
 // ================================================================ kernel 2: split-K decode
 
+// Cross-lane exchanges in vector ALU instructions rather than LDS permutes (an LDS round trip
+// each). v_permlane16_swap with both operands x leaves, in its two results, the rows {0, 0, 2, 2}
+// and {1, 1, 3, 3} of x (rows of 16 lanes); v_permlane32_swap leaves rows {0, 1, 0, 1} and
+// {2, 3, 2, 3}. Combining the two results pairs every lane with its partner 16 (or 32) lanes
+// away, and since a + b == b + a exactly, both partners hold the same bits afterwards.
+__device__ __forceinline__ void swap16(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap32(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float wave_max_groups(float x) {
   // max over the four 16-lane groups that hold the same query head
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  float a, b;
+  swap16(x, a, b);
+  x = fmaxf(a, b);
+  swap32(x, a, b);
+  return fmaxf(a, b);
 }
 
 __device__ __forceinline__ float wave_sum_groups(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  float a, b;
+  swap16(x, a, b);
+  x = a + b;
+  swap32(x, a, b);
+  return a + b;
 }
+
+// DPP lane exchanges inside groups of 8 consecutive lanes: partner lane i ^ 1, i ^ 2, and
+// 7 - i within each half row (which, once the quads hold equal values, pairs quad 0 with quad 1
+// as i ^ 4 would).
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror
 
 // Fragments of one tile (kBlk positions) of K and V for one lane, in matrix-core operand order.
 template <typename KV, int DK, int DV>
@@ -346,6 +377,14 @@ __device__ __forceinline__ float4_t clear4() {
   return float4_t{c, c, c, c};
 }
 
+// Writes the not-written pattern back over a word group the reducer has read. Nobody reads it
+// again in this launch, and the release at the end of the kernel writes it back to memory
+// before the next launch starts, so a plain store suffices: it is acknowledged by the L2
+// instead of after a write-through to memory, which shortens the kernel's tail.
+__device__ __forceinline__ void clear_part(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(clear4(), rs, off, 0, 0);
+}
+
 // Polls of one reducer before it gives up and reports a reduction timeout (error bit 1). Each
 // poll waits one memory round trip, so this bounds the wait at seconds; it is reached only if a
 // producer of the group never stores, which the ticket order rules out.
@@ -420,6 +459,9 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
     float mx, lw;  // this workgroup's own partial, while the loads are in flight
     float4_t own;
     wave_partial<DV, W>(s_acc, s_ml, hs, e, mx, lw, own);
+    // Keep that work ahead of the first wait for the loads (left alone, the compiler sinks it
+    // behind the wait, where it lengthens the reducer's tail).
+    asm volatile("" ::"v"(mx), "v"(lw), "v"(own[0]), "v"(own[1]), "v"(own[2]), "v"(own[3]));
     for (uint32_t spin = 0;; ++spin) {
       bool ready = true;
 #pragma unroll
@@ -447,9 +489,9 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
       m_i[i] = g == split ? mx : (g < ns ? mv[i][0] : -INFINITY);
       M = fmaxf(M, m_i[i]);
     }
-    if constexpr (SUB >= 2) M = fmaxf(M, __shfl_xor(M, 1));
-    if constexpr (SUB >= 4) M = fmaxf(M, __shfl_xor(M, 2));
-    if constexpr (SUB >= 8) M = fmaxf(M, __shfl_xor(M, 4));
+    if constexpr (SUB >= 2) M = fmaxf(M, dpp<kDppXor1>(M));
+    if constexpr (SUB >= 4) M = fmaxf(M, dpp<kDppXor2>(M));
+    if constexpr (SUB >= 8) M = fmaxf(M, dpp<kDppHalfMirror>(M));
     const float mu = M == -INFINITY ? 0.0f : M;
     float L = 0.0f;
     float4_t X = {0.f, 0.f, 0.f, 0.f};
@@ -463,22 +505,22 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
       L = fmaf(lg, wg, L);
 #pragma unroll
       for (int c = 0; c < 4; ++c) X[c] = fmaf(xg[c], wg, X[c]);
-      if (needed(i)) store_part(rs, base(g, hs) + e * 4, clear4());
+      if (needed(i)) clear_part(rs, base(g, hs) + e * 4);
     }
     if constexpr (SUB >= 2) {
-      L += __shfl_xor(L, 1);
+      L += dpp<kDppXor1>(L);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) X[c] += __shfl_xor(X[c], 1);
+      for (int c = 0; c < 4; ++c) X[c] += dpp<kDppXor1>(X[c]);
     }
     if constexpr (SUB >= 4) {
-      L += __shfl_xor(L, 2);
+      L += dpp<kDppXor2>(L);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) X[c] += __shfl_xor(X[c], 2);
+      for (int c = 0; c < 4; ++c) X[c] += dpp<kDppXor2>(X[c]);
     }
     if constexpr (SUB >= 8) {
-      L += __shfl_xor(L, 4);
+      L += dpp<kDppHalfMirror>(L);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) X[c] += __shfl_xor(X[c], 4);
+      for (int c = 0; c < 4; ++c) X[c] += dpp<kDppHalfMirror>(X[c]);
     }
     if (qok && r == 0) {
       if (!(L > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
@@ -488,7 +530,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
   __syncthreads();  // every quad of every head has read its (m, l) words
   for (uint32_t k = tid; k < (ns - 1) * nreal; k += kT) {
     const uint32_t o = k / nreal, hs = k % nreal;
-    store_part(rs, base(o + (o >= split ? 1u : 0u), hs) + DV * 4, clear4());
+    clear_part(rs, base(o + (o >= split ? 1u : 0u), hs) + DV * 4);
   }
   if (timed_out) atomicOr(err, 2);
 }

@@ -121,13 +121,14 @@ def test_noalloc_decode_matches_decode_device():
 
 
 def test_noalloc_refuses_plans_beyond_the_fixed_scratch(monkeypatch):
-    """128 sessions x 8 KV heads x 5 splits (a 100000-workgroup target keeps splits at 4 tiles)
-    need 85 MB of partial words, beyond the 16 MiB region: refused, nothing enqueued or recorded;
-    decode_device itself grows its scratch and runs the same call."""
+    """128 sessions x 8 KV heads x 5 splits (a 100000-workgroup target keeps splits at 4 tiles) of
+    4 query heads x 256 elements need tens of MB of split partials, beyond the fixed scratch:
+    refused, nothing enqueued or recorded; decode_device itself grows its scratch and runs the
+    same call."""
     monkeypatch.setenv("JMA_DECODE_TARGET_BLOCKS", "100000")
     lib = A.HipAttentionLibrary(0)
     try:
-        hq, hkv, d, B, n = 8, 8, 256, 128, 544
+        hq, hkv, d, B, n = 32, 8, 256, 128, 544
         rope = lib.rotary_table(d, 1e4, 1.0, max_positions=n + 1)
         kv = lib.kv_cache(1, n + 1, hkv, d, d, half_precision=True, sequences=B)
         layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
