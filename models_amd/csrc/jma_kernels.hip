@@ -563,8 +563,15 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 //    clear again when the launch ends.
 // kOne: the plan gives every wave at most one tile (tiles_per_split <= waves), so the second tile
 // buffer is never needed (at head dim 256 two buffers are the whole register file).
+// The leading scalar arguments are what the kSimple instance needs to address its first tiles
+// (the layer's K / V base for the sequence, the first row's position, the window, tiles per split
+// and the slot capacity). The library is built with kernel-argument preloading, so they arrive in
+// scalar registers at wave start and the first tile loads do not wait for a kernel-argument
+// load; the other instances pass zeros there and read everything from `a`.
 template <typename KV, int DK, int DV, bool kSimple, bool kOne>
-__global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
+    const void* p_kb, const void* p_vb, uint32_t p_start, uint32_t p_window, uint32_t p_tps,
+    uint32_t p_cap, const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
   using TileT = Tile<KV, DK, DV>;
   constexpr uint32_t kBlk = TileT::kBlk;
@@ -610,17 +617,18 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
   uint32_t ns, item, hg, kvh, seq, pos;
   KV *kb, *vb;
   if constexpr (kSimple) {
-    JMA_GLOBAL KV* g_kb = (JMA_GLOBAL KV*)a.k_base;
-    JMA_GLOBAL KV* g_vb = (JMA_GLOBAL KV*)a.v_base;
-    asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hkv), "+s"(ns_uniform), "+s"(rows_start),
-                 "+s"(window), "+s"(tps), "+s"(cap), "+s"(pairs), "+s"(neox), "+s"(rope_q),
-                 "+s"(qscale), "+s"(g_kb), "+s"(g_vb));
-    asm volatile("" : "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn), "+s"(g_ctr),
-                 "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
-    ns = ns_uniform;
+    // Only the preloaded arguments here: the rest are fetched after the first tile loads issue.
+    JMA_GLOBAL KV* g_kb = (JMA_GLOBAL KV*)p_kb;
+    JMA_GLOBAL KV* g_vb = (JMA_GLOBAL KV*)p_vb;
+    asm volatile("" : "+s"(g_kb), "+s"(g_vb), "+s"(p_start), "+s"(p_window), "+s"(p_tps), "+s"(p_cap));
+    rows_start = p_start;
+    window = p_window;
+    tps = p_tps;
+    cap = p_cap;
+    ns = 0;
+    item = 0;
     hg = 0;
     kvh = rest;
-    item = (row * hkv + kvh) * ns + split;
     seq = 0;
     pos = rows_start + row;
     ring = 0;
@@ -651,22 +659,6 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
     kb = (KV*)g_k + seq * seq_stride_k + layer_off_k + (uint64_t)kvh * cap * DK;
     vb = (KV*)g_v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV;
   }
-  const float *q_in = (const float*)g_q, *cos_t = (const float*)g_cos, *sin_t = (const float*)g_sin;
-  const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
-  uint32_t* counters = (uint32_t*)g_ctr;
-  float* out = (float*)g_out;
-  float* part_f = (float*)g_tag;
-  float* part_acc = (float*)g_pacc;
-  float* part_ml = (float*)g_pml;
-  int* err = (int*)g_err;
-
-  const bool fused = ns > 1 && counters != nullptr;
-  const uint64_t gid = ((uint64_t)row * hkv + kvh) * hgroups + hg;
-  // Arrival ticket first: its round trip overlaps the tile loads.
-  uint32_t ticket = 0;
-  if (fused && threadIdx.x == 0)
-    ticket = __hip_atomic_fetch_add(&counters[gid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
   const uint32_t first = first_visible(pos, window);
   const uint32_t t_begin = first / kBlk, t_end = pos / kBlk + 1;
   const uint32_t s_t0 = t_begin + split * tps;
@@ -680,10 +672,6 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
   const int g = lane >> 4;
   const int c16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t hl = hg * 16 + c16;
-  const bool head_ok = hl < group;
-  const float* cs = cos_t ? cos_t + (uint64_t)pos * pairs : nullptr;
-  const float* sn = cos_t ? sin_t + (uint64_t)pos * pairs : nullptr;
 
   auto slot0_of = [&](uint32_t t) JMA_INL {
     const uint32_t x = slot_base + (t - s_t0) * kBlk;
@@ -698,6 +686,37 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(const Dec
   if (t < s_t1) ta.load(kb, vb, slot0_of(t), c16, g);
   if constexpr (!kOne)
     if (kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
+
+  if constexpr (kSimple) {
+    // The remaining arguments, in one batch, once the first tile loads are issued.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+s"(num_heads), "+s"(group), "+s"(hkv), "+s"(ns_uniform), "+s"(pairs),
+                 "+s"(neox), "+s"(rope_q), "+s"(qscale));
+    asm volatile("" : "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn), "+s"(g_ctr),
+                 "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
+    ns = ns_uniform;
+    item = (row * hkv + kvh) * ns + split;
+  }
+  const float *q_in = (const float*)g_q, *cos_t = (const float*)g_cos, *sin_t = (const float*)g_sin;
+  const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
+  uint32_t* counters = (uint32_t*)g_ctr;
+  float* out = (float*)g_out;
+  float* part_f = (float*)g_tag;
+  float* part_acc = (float*)g_pacc;
+  float* part_ml = (float*)g_pml;
+  int* err = (int*)g_err;
+
+  const bool fused = ns > 1 && counters != nullptr;
+  const uint64_t gid = ((uint64_t)row * hkv + kvh) * hgroups + hg;
+  // Arrival ticket: its round trip overlaps the tile loads.
+  uint32_t ticket = 0;
+  if (fused && threadIdx.x == 0)
+    ticket = __hip_atomic_fetch_add(&counters[gid], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  const uint32_t hl = hg * 16 + c16;
+  const bool head_ok = hl < group;
+  const float* cs = cos_t ? cos_t + (uint64_t)pos * pairs : nullptr;
+  const float* sn = cos_t ? sin_t + (uint64_t)pos * pairs : nullptr;
 
   // Fused append. The new row's tile is the last of the row's last split: the row is rotated
   // into LDS, from where the wave owning that tile patches it into its registers, and the head
@@ -1203,22 +1222,27 @@ bool decode_supported(bool f16, int dk, int dv) {
 template <typename KV, bool kSimple>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
   const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * decode_waves(d));
+  // Preloaded leading arguments of the kSimple instance (zeros for the general one).
+  const void* kb = kSimple ? a.k_base : nullptr;
+  const void* vb = kSimple ? a.v_base : nullptr;
+  const uint32_t start = kSimple ? a.rows.start : 0u, window = kSimple ? a.window : 0u;
+  const uint32_t tps = kSimple ? a.tiles_per_split : 0u, cap = kSimple ? a.kv.cap : 0u;
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple, false>), grid, block, 0, stream, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple, false>), grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple, false>), grid, block, 0, stream, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a); break;
     case 256:
       // One tile per wave (the long-context plans cut this fine) needs one tile buffer only.
       if (a.tiles_per_split <= (uint32_t)decode_waves(256))
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a);
       else
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a);
       break;
     default: return hipErrorInvalidValue;
   }
