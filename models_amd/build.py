@@ -30,9 +30,9 @@ HIPCC_FLAGS = [
     # atomic's result right after issuing it, which puts a memory round trip in front of the
     # decode kernel's tile loads
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
-    # the decode kernel's six leading scalar arguments arrive in SGPRs at wave start (kernels
+    # the decode kernel's seven leading scalar arguments arrive in SGPRs at wave start (kernels
     # whose first argument is a struct preload nothing)
-    "-mllvm", "-amdgpu-kernarg-preload-count=6",
+    "-mllvm", "-amdgpu-kernarg-preload-count=7",
     "-Wall",
     "-Wno-unused-result",
 ]

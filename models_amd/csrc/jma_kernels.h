@@ -78,8 +78,8 @@ struct DecodeArgs {
   int* err;             // bit 0: non-finite score seen
   KvView kv;
   void* k_base;         // non-null: the rows are contiguous positions of one sequence, every row
-  void* v_base;         // has the same split count, one head group, LINEAR layer; the layer's
-                        // K / V base for that sequence (the kernel then skips the general indexing)
+  void* v_base;         // has the same split count, one head group; the layer's K / V base for
+                        // that sequence (the kernel then skips the general indexing)
   float qscale;         // score scale * log2(e), folded into q
   uint32_t num_heads, group, hgroups, window;
   uint32_t num_kv_heads;

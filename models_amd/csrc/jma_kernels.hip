@@ -571,7 +571,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 template <typename KV, int DK, int DV, bool kSimple, bool kOne>
 __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     const void* p_kb, const void* p_vb, uint32_t p_start, uint32_t p_window, uint32_t p_tps,
-    uint32_t p_cap, const DecodeArgs a) {
+    uint32_t p_cap, uint32_t p_ring, const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
   using TileT = Tile<KV, DK, DV>;
   constexpr uint32_t kBlk = TileT::kBlk;
@@ -592,8 +592,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   // kernel uses, the row's own table entries included, is fetched in one batch: left to itself
   // the compiler loads each right before its use, behind its own wait, and a scalar load costs
   // about half a vector memory round trip here. kSimple (contiguous rows of one sequence, equal
-  // split counts, one head group, a LINEAR layer) takes its cache base from the host and needs
-  // almost no address arithmetic before the first tile load.
+  // split counts, one head group) takes its cache base from the host and needs almost no address
+  // arithmetic before the first tile load.
   const uint32_t split = blockIdx.x, rest = blockIdx.y, row = blockIdx.z;
   uint32_t num_heads = a.num_heads, group = a.group, hgroups = a.hgroups, hkv = a.num_kv_heads;
   uint32_t ns_uniform = a.ns_uniform, rows_contig = a.rows.contiguous;
@@ -620,7 +620,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     // Only the preloaded arguments here: the rest are fetched after the first tile loads issue.
     JMA_GLOBAL KV* g_kb = (JMA_GLOBAL KV*)p_kb;
     JMA_GLOBAL KV* g_vb = (JMA_GLOBAL KV*)p_vb;
-    asm volatile("" : "+s"(g_kb), "+s"(g_vb), "+s"(p_start), "+s"(p_window), "+s"(p_tps), "+s"(p_cap));
+    asm volatile("" : "+s"(g_kb), "+s"(g_vb), "+s"(p_start), "+s"(p_window), "+s"(p_tps), "+s"(p_cap),
+                 "+s"(p_ring));
     rows_start = p_start;
     window = p_window;
     tps = p_tps;
@@ -631,7 +632,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     kvh = rest;
     seq = 0;
     pos = rows_start + row;
-    ring = 0;
+    ring = p_ring;
     hgroups = 1;
     kb = (KV*)g_kb + (uint64_t)kvh * cap * DK;
     vb = (KV*)g_vb + (uint64_t)kvh * cap * DV;
@@ -666,7 +667,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   // Ring layers: the split's first tile slot, then consecutive tiles wrap at most once (a
   // split spans fewer positions than the ring holds).
   uint32_t slot_base = s_t0 * kBlk;
-  if (!kSimple && ring) slot_base %= cap;
+  if (ring) slot_base %= cap;
 
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -675,7 +676,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 
   auto slot0_of = [&](uint32_t t) JMA_INL {
     const uint32_t x = slot_base + (t - s_t0) * kBlk;
-    return !kSimple && ring && x >= cap ? x - cap : x;
+    return ring && x >= cap ? x - cap : x;
   };
 
   // The first two tiles of this wave are in flight before anything else is loaded (at head
@@ -1227,22 +1228,23 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
   const void* vb = kSimple ? a.v_base : nullptr;
   const uint32_t start = kSimple ? a.rows.start : 0u, window = kSimple ? a.window : 0u;
   const uint32_t tps = kSimple ? a.tiles_per_split : 0u, cap = kSimple ? a.kv.cap : 0u;
+  const uint32_t ring = kSimple ? a.kv.ring : 0u;
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
     case 256:
       // One tile per wave (the long-context plans cut this fine) needs one tile buffer only.
       if (a.tiles_per_split <= (uint32_t)decode_waves(256))
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       else
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     default: return hipErrorInvalidValue;
   }

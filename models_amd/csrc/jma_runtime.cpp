@@ -444,7 +444,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   a.item_start[rows.count] = items;
   a.total_items = items;
   a.ns_uniform = uniform ? a.nsplit[0] : 0u;
-  if (uniform && rows.contiguous && a.hgroups == 1 && !a.kv.ring) {
+  if (uniform && rows.contiguous && a.hgroups == 1) {
     const size_t es = kv->f16() ? 2 : 4;
     a.k_base = (char*)a.kv.k + (a.kv.seq_stride_k * rows.seq0 + a.kv.layer_off_k) * es;
     a.v_base = (char*)a.kv.v + (a.kv.seq_stride_v * rows.seq0 + a.kv.layer_off_v) * es;
