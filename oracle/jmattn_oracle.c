@@ -788,6 +788,53 @@ int jmo_prefill_layer(jmo_kv* kv, int layer, int start, int n, int window, float
   return status;
 }
 
+/* ---------------------------------------------------------------- 8-lane timing variant */
+
+/* A dot product in eight partial sums (lane j accumulates elements i with i % 8 == j, then the
+ * lanes are added pairwise: (0+4, 1+5, 2+6, 3+7), then (0+2, 1+3), then (0+1)), followed by the
+ * scalar tail: the shape of a Vector API reduction over 256-bit float vectors, which the compiler
+ * turns into AVX2 code. Used only to time a vectorised CPU baseline; parity is pinned on the
+ * sequential jmo_dot. */
+static float dot8(const float* a, const float* b, int n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int j = 0; j < 8; j++) acc[j] += a[i + j] * b[i + j];
+  for (int j = 0; j < 4; j++) acc[j] += acc[j + 4];
+  acc[0] += acc[2];
+  acc[1] += acc[3];
+  float sum = acc[0] + acc[1];
+  for (; i < n; i++) sum += a[i] * b[i];
+  return sum;
+}
+
+static int gqa_core8(const float* q, const float* keys, const float* values, int rows,
+                     int key_row_stride, int value_row_stride, int num_heads, int num_kv_heads,
+                     int key_length, int value_length, float scale, float* out, float* scores) {
+  /* gqa_core with dot8 for the scores; the weighted V sum is element-wise (no reduction), so
+   * the compiler vectorises it as written. */
+  if (num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || rows <= 0) return JMO_ILLEGAL_ARGUMENT;
+  int group = num_heads / num_kv_heads;
+  memset(out, 0, sizeof(float) * (size_t)num_heads * value_length);
+  for (int head = 0; head < num_heads; head++) {
+    int kv_head = head / group;
+    const float* qh = q + (int64_t)head * key_length;
+    for (int r = 0; r < rows; r++) {
+      const float* krow = keys + (int64_t)r * key_row_stride + (int64_t)kv_head * key_length;
+      scores[r] = dot8(qh, krow, key_length) * scale;
+    }
+    int status = jmo_softmax(scores, rows);
+    if (status != JMO_OK) return status;
+    float* oh = out + (int64_t)head * value_length;
+    for (int r = 0; r < rows; r++) {
+      const float* vrow = values + (int64_t)r * value_row_stride + (int64_t)kv_head * value_length;
+      float p = scores[r];
+      for (int i = 0; i < value_length; i++) oh[i] += p * vrow[i];
+    }
+  }
+  return JMO_OK;
+}
+
 /* ---------------------------------------------------------------- threaded baseline */
 
 typedef struct {
@@ -800,6 +847,7 @@ typedef struct {
   int key_row_stride, value_row_stride, num_heads, num_kv_heads, key_length, value_length;
   float scale;
   float* const* out;
+  int lanes8;
   int status;
 } jmo_batch_job;
 
@@ -815,7 +863,7 @@ static void* batch_worker(void* arg) {
     int s = unit / job->num_kv_heads;
     int kvh = unit % job->num_kv_heads;
     /* one kv head, its `group` query heads: a 1-kv-head GQA over offset views */
-    int status = gqa_core(job->q[s] + (int64_t)kvh * group * job->key_length,
+    int status = (job->lanes8 ? gqa_core8 : gqa_core)(job->q[s] + (int64_t)kvh * group * job->key_length,
                           job->keys[s] + (int64_t)kvh * job->key_length,
                           job->values[s] + (int64_t)kvh * job->value_length, job->rows[s],
                           job->key_row_stride, job->value_row_stride, group, 1, job->key_length,
@@ -829,10 +877,11 @@ static void* batch_worker(void* arg) {
   return NULL;
 }
 
-int jmo_gqa_rows_batch(int count, const float* const* q, const float* const* keys,
-                       const float* const* values, const int* rows, int key_row_stride,
-                       int value_row_stride, int num_heads, int num_kv_heads, int key_length,
-                       int value_length, float scale, float* const* out, int threads) {
+static int gqa_rows_batch(int count, const float* const* q, const float* const* keys,
+                          const float* const* values, const int* rows, int key_row_stride,
+                          int value_row_stride, int num_heads, int num_kv_heads, int key_length,
+                          int value_length, float scale, float* const* out, int threads,
+                          int lanes8) {
   if (count <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return JMO_ILLEGAL_ARGUMENT;
   if (threads < 1) threads = 1;
   int units = count * num_kv_heads;
@@ -856,6 +905,7 @@ int jmo_gqa_rows_batch(int count, const float* const* q, const float* const* key
     j->value_length = value_length;
     j->scale = scale;
     j->out = out;
+    j->lanes8 = lanes8;
     j->status = JMO_OK;
     if (threads == 1) {
       batch_worker(j);
@@ -871,4 +921,20 @@ int jmo_gqa_rows_batch(int count, const float* const* q, const float* const* key
   free(tids);
   free(jobs);
   return status;
+}
+
+int jmo_gqa_rows_batch(int count, const float* const* q, const float* const* keys,
+                       const float* const* values, const int* rows, int key_row_stride,
+                       int value_row_stride, int num_heads, int num_kv_heads, int key_length,
+                       int value_length, float scale, float* const* out, int threads) {
+  return gqa_rows_batch(count, q, keys, values, rows, key_row_stride, value_row_stride, num_heads,
+                        num_kv_heads, key_length, value_length, scale, out, threads, 0);
+}
+
+int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* keys,
+                        const float* const* values, const int* rows, int key_row_stride,
+                        int value_row_stride, int num_heads, int num_kv_heads, int key_length,
+                        int value_length, float scale, float* const* out, int threads) {
+  return gqa_rows_batch(count, q, keys, values, rows, key_row_stride, value_row_stride, num_heads,
+                        num_kv_heads, key_length, value_length, scale, out, threads, 1);
 }

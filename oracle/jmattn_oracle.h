@@ -176,6 +176,12 @@ int jmo_gqa_rows_batch(int count, const float* const* q, const float* const* key
                        const float* const* values, const int* rows, int key_row_stride,
                        int value_row_stride, int num_heads, int num_kv_heads, int key_length,
                        int value_length, float scale, float* const* out, int threads);
+/* jmo_gqa_rows_batch with dot products in eight partial sums (a vectorised loop, timing only:
+ * the bench's vectorised CPU baseline; parity is pinned on the sequential variant). */
+int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* keys,
+                       const float* const* values, const int* rows, int key_row_stride,
+                       int value_row_stride, int num_heads, int num_kv_heads, int key_length,
+                       int value_length, float scale, float* const* out, int threads);
 
 #ifdef __cplusplus
 }

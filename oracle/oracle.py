@@ -137,6 +137,9 @@ def _declare(L: ctypes.CDLL) -> None:
         "jmo_gqa_rows_batch": (c_int, [c_int, ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
                                        ctypes.POINTER(_f32p), _i32p, c_int, c_int, c_int, c_int,
                                        c_int, c_int, c_float, ctypes.POINTER(_f32p), c_int]),
+        "jmo_gqa_rows_batch8": (c_int, [c_int, ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
+                                       ctypes.POINTER(_f32p), _i32p, c_int, c_int, c_int, c_int,
+                                       c_int, c_int, c_float, ctypes.POINTER(_f32p), c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -494,8 +497,9 @@ def gqa_rows(q, keys, values, num_heads: int, num_kv_heads: int, key_length: int
 
 
 def gqa_rows_batch(qs, keys_list, values_list, num_heads, num_kv_heads, key_length,
-                   value_length, scale, threads=1):
-    """Independent sequences, work split over (sequence, kv head) units on ``threads`` threads."""
+                   value_length, scale, threads=1, lanes8=False):
+    """Independent sequences, work split over (sequence, kv head) units on ``threads`` threads.
+    lanes8: dot products in eight partial sums (vectorised; timing only, not the parity oracle)."""
     n = len(qs)
     qs = [_f32(q) for q in qs]
     ks = [_f32(k) for k in keys_list]
@@ -503,7 +507,8 @@ def gqa_rows_batch(qs, keys_list, values_list, num_heads, num_kv_heads, key_leng
     outs = [np.empty(num_heads * value_length, np.float32) for _ in range(n)]
     rows = (ctypes.c_int * n)(*[k.size // (num_kv_heads * key_length) for k in ks])
     P = _f32p * n
-    _check(lib().jmo_gqa_rows_batch(n, P(*[_ptr(a) for a in qs]), P(*[_ptr(a) for a in ks]),
+    fn = lib().jmo_gqa_rows_batch8 if lanes8 else lib().jmo_gqa_rows_batch
+    _check(fn(n, P(*[_ptr(a) for a in qs]), P(*[_ptr(a) for a in ks]),
                                     P(*[_ptr(a) for a in vs]), rows, num_kv_heads * key_length,
                                     num_kv_heads * value_length, num_heads, num_kv_heads,
                                     key_length, value_length, scale,
