@@ -43,10 +43,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix
 # HBM bytes per decode launch on C2 measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# (bench.py --no-cpu --no-prefill --steps 8 --warmup 2), each scaled by what the counter reads
-# for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4487.5 KiB x 2.0 + 620.5 KiB. Recorded with
-# its commands in profiles/decode_c2.md; counters cannot be read from inside this process.
-DECODE_TRAFFIC_BYTES = round((4487.5 * 2.0 + 620.5) * 1024)
+# (bench.py --no-cpu --no-prefill --no-c1 --no-c4 --no-c5 --steps 8 --warmup 2), each scaled by
+# what the counter reads for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4406.3 KiB x 2.0 +
+# 316.6 KiB. Recorded with its commands in profiles/decode_c2.md; counters cannot be read from
+# inside this process.
+DECODE_TRAFFIC_BYTES = round((4406.3 * 2.0 + 316.6) * 1024)
 
 
 def log(msg: str) -> None:
