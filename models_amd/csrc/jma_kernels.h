@@ -5,20 +5,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace jma {
+#include "jma_plan.h"
 
-// Rows handled by one launch when their (sequence, position) pairs are passed as kernel
-// arguments; larger batches are split into several launches by the runtime.
-constexpr int kMaxRows = 128;
-// Waves per decode workgroup at head dimension dk: the waves of one workgroup share a split and
-// combine in LDS. Two waves per SIMD hide each other's instruction latency; at dk = 256 two tile
-// buffers take half the register file, so one wave per SIMD.
-constexpr int decode_waves(int dk) { return dk >= 256 ? 4 : 8; }
-// Most splits one decode row may be cut into when the decode kernel reduces them itself (the
-// reducing workgroup loads every split's partial); and when a separate reduce_kernel does
-// (partials in part_acc / part_ml, reduced by one workgroup per head and 64 output elements).
-constexpr int kMaxSplits = 32;
-constexpr int kMaxWideSplits = 1024;
+namespace jma {
 
 // Where one layer's K and V live. K: [sequence][layer][kv head][slot][key_length] row-major.
 // V: [sequence][layer][kv head][slot / B][value_length][B] (B = 32 for f16, 16 for f32), the
@@ -101,6 +90,9 @@ struct DecodeArgs {
   uint32_t nsplit[kMaxRows];
 };
 
+// Kernel arguments travel in the kernarg segment, at most 4 KiB.
+static_assert(sizeof(DecodeArgs) <= 4096, "DecodeArgs exceeds the kernel argument limit");
+
 struct PrefillArgs {
   KvView kv;
   const float* q;       // [n][num_heads][dk], rotated
@@ -132,9 +124,6 @@ struct PrefillPlan {
   size_t part_bytes = 0;
 };
 PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t cus);
-
-// Storage block (slots) of the transposed V layout.
-inline int v_block(bool f16) { return f16 ? 32 : 16; }
 
 // Fixed device scratch of the allocation-free decode entry point: one file-scope array per GPU
 // (in jma_kernels.hip), split into the regions a decode launch may need. Every call on a GPU

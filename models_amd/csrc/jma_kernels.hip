@@ -52,11 +52,6 @@ __device__ __forceinline__ uint32_t row_position(const RowList& r, uint32_t i) {
   return r.contiguous ? r.start + i : r.pos[i];
 }
 
-__device__ __forceinline__ uint32_t first_visible(uint32_t position, uint32_t window) {
-  // LlamaConfig.attentionStartPosition, causal branch (llama/LlamaConfig.java:184-195).
-  return (window == 0 || position + 1 <= window) ? 0u : position + 1 - window;
-}
-
 // ================================================================ kernel 1: RoPE + append
 
 // One RoPE pair rotated exactly as TensorOps.rotatePair / rotateSplitPair compute it
@@ -437,7 +432,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
   const uint32_t E4 = nreal * kQ4;
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(part);
   auto base = [&](uint32_t g, uint32_t hs) JMA_INL {  // byte offset of (split g, head slot hs)
-    return (uint32_t)(((item0 + g) * 16 + hs) * (DV + 4) * 4);
+    return (uint32_t)(fused_part_float(item0 + g, hs, DV, 0) * 4);
   };
   const uint32_t r = tid % SUB;
   bool timed_out = false;
@@ -652,7 +647,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
                  "+s"(g_err));
     ns = ns_uniform ? ns_uniform : r_ns;
     if (split >= ns) return;  // a listed row with fewer splits than the grid's widest row
-    item = ns_uniform ? (row * hkv * hgroups + rest) * ns + split : r_item0 + rest * ns + split;
+    item = group_item0(ns_uniform, r_item0, row, hkv, hgroups, rest, ns) + split;
     hg = hgroups == 1 ? 0u : rest % hgroups;
     kvh = hgroups == 1 ? rest : rest / hgroups;
     seq = rows_contig ? rows_seq0 : r_seq;
@@ -696,7 +691,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     asm volatile("" : "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn), "+s"(g_ctr),
                  "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
     ns = ns_uniform;
-    item = (row * hkv + kvh) * ns + split;
+    item = group_item0(ns, 0, row, hkv, 1, kvh, ns) + split;
   }
   const float *q_in = (const float*)g_q, *cos_t = (const float*)g_cos, *sin_t = (const float*)g_sin;
   const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
@@ -708,7 +703,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   int* err = (int*)g_err;
 
   const bool fused = ns > 1 && counters != nullptr;
-  const uint64_t gid = ((uint64_t)row * hkv + kvh) * hgroups + hg;
+  const uint64_t gid = group_counter(row, hkv, kvh, hgroups, hg);
   // Arrival ticket: its round trip overlaps the tile loads.
   uint32_t ticket = 0;
   if (fused && threadIdx.x == 0)
@@ -1042,13 +1037,13 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
       if (!(lw > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
       *(float4_t*)(o_grp + hs * DV + e) = aw * (1.0f / lw);
     } else if (!fused) {  // reduce_kernel combines the splits after this launch
-      *(float4_t*)(part_acc + ((uint64_t)item * 16 + hs) * DV + e) = aw;
+      *(float4_t*)(part_acc + sep_acc_float(item, hs, DV, e)) = aw;
       if (e == 0) {
-        part_ml[((uint64_t)item * 16 + hs) * 2] = mx;
-        part_ml[((uint64_t)item * 16 + hs) * 2 + 1] = lw;
+        part_ml[sep_ml_float(item, hs)] = mx;
+        part_ml[sep_ml_float(item, hs) + 1] = lw;
       }
     } else {
-      const uint32_t off = (uint32_t)(((uint64_t)item * 16 + hs) * (DV + 4) * 4);
+      const uint32_t off = (uint32_t)(fused_part_float(item, hs, DV, 0) * 4);
       store_part(rs, off + e * 4, float4_t{canon(aw[0]), canon(aw[1]), canon(aw[2]), canon(aw[3])});
       if (e == 0) {
         const float c = __uint_as_float(kClear);
@@ -1079,16 +1074,16 @@ __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
   const uint32_t hkv = a.num_heads / a.group;
   const uint32_t ns = a.ns_uniform ? a.ns_uniform : a.nsplit[row];
   if (ns == 1) return;
-  const uint32_t row_item = a.ns_uniform ? row * hkv * a.hgroups * ns : a.item_start[row];
   const uint32_t kvh = head / a.group;
   const uint32_t hl = head % a.group;
   const uint32_t hg = hl / 16, c16 = hl % 16;
-  const uint64_t base = row_item + ((uint64_t)kvh * a.hgroups + hg) * ns;
+  const uint64_t base = group_item0(a.ns_uniform, a.item_start[row], row, hkv, a.hgroups,
+                                    kvh * a.hgroups + hg, ns);
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
   // Weights: thread t takes split t.
   float2 ml = {-INFINITY, 0.0f};
-  if (tid < ns) ml = *(const float2*)(a.part_ml + ((base + tid) * 16 + c16) * 2);
+  if (tid < ns) ml = *(const float2*)(a.part_ml + sep_ml_float(base + tid, c16));
   float mw = ml.x;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
@@ -1113,7 +1108,7 @@ __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < kAhead; ++i) {
     const uint32_t sp = wave + kWaves * i;
-    xv[i] = sp < ns ? a.part_acc[((base + sp) * 16 + c16) * DV + dl] : 0.0f;
+    xv[i] = sp < ns ? a.part_acc[sep_acc_float(base + sp, c16, DV, dl)] : 0.0f;
   }
   float X = 0.0f;
 #pragma unroll

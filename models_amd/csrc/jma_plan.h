@@ -1,0 +1,136 @@
+// Decode launch planning and the index formulas of the decode split exchange, shared by the host
+// runtime (jma_runtime.cpp), the kernels (jma_kernels.hip) and a CPU bounds check
+// (tests/plan_check.cpp). Plain C++: no HIP types, so it also builds with g++ alone.
+#pragma once
+
+#include <stdint.h>
+
+#include <algorithm>
+
+#if defined(__HIPCC__)
+#define JMA_HD __host__ __device__ inline
+#else
+#define JMA_HD inline
+#endif
+
+namespace jma {
+
+// Rows handled by one launch when their (sequence, position) pairs are passed as kernel
+// arguments; larger batches are split into several launches by the runtime.
+constexpr int kMaxRows = 128;
+// Waves per decode workgroup at head dimension dk: the waves of one workgroup share a split and
+// combine in LDS. Two waves per SIMD hide each other's instruction latency; at dk = 256 two tile
+// buffers take half the register file, so one wave per SIMD.
+constexpr int decode_waves(int dk) { return dk >= 256 ? 4 : 8; }
+// Most splits one decode row may be cut into when the decode kernel reduces them itself (the
+// reducing workgroup loads every split's partial); and when a separate reduce_kernel does
+// (partials in part_acc / part_ml, reduced by one workgroup per head and 64 output elements).
+constexpr int kMaxSplits = 32;
+constexpr int kMaxWideSplits = 1024;
+// Query heads one decode workgroup serves (the 16 MFMA columns); partial buffers reserve this
+// many head slots per work item.
+constexpr int kHeadSlots = 16;
+
+// Storage block (slots) of the transposed V layout.
+JMA_HD int v_block(bool f16) { return f16 ? 32 : 16; }
+
+JMA_HD uint32_t first_visible(uint32_t position, uint32_t window) {
+  // LlamaConfig.attentionStartPosition, causal branch (llama/LlamaConfig.java:184-195).
+  return (window == 0 || position + 1 <= window) ? 0u : position + 1 - window;
+}
+
+// First work item of the group (row, rest = kv head * head groups + head group) whose ns splits
+// are items item0 .. item0 + ns - 1. ns_uniform > 0: every row has ns_uniform splits; else row
+// `row` starts at item_start_row.
+JMA_HD uint64_t group_item0(uint32_t ns_uniform, uint32_t item_start_row, uint32_t row,
+                            uint32_t hkv, uint32_t hgroups, uint32_t rest, uint32_t ns) {
+  return ns_uniform ? ((uint64_t)row * hkv * hgroups + rest) * ns
+                    : (uint64_t)item_start_row + (uint64_t)rest * ns;
+}
+
+// Arrival-ticket counter of a group: [row][kv head][head group].
+JMA_HD uint64_t group_counter(uint32_t row, uint32_t hkv, uint32_t kvh, uint32_t hgroups, uint32_t hg) {
+  return ((uint64_t)row * hkv + kvh) * hgroups + hg;
+}
+
+// Fused exchange: float index of element e (e < dv; e = dv is m, dv + 1 is l) of head slot hs of
+// work item `item`; each (item, head slot) holds dv + 4 floats.
+JMA_HD uint64_t fused_part_float(uint64_t item, uint32_t hs, uint32_t dv, uint32_t e) {
+  return (item * kHeadSlots + hs) * (dv + 4) + e;
+}
+// Separate reduction: element e of head slot hs of item in part_acc, and its (m, l) in part_ml.
+JMA_HD uint64_t sep_acc_float(uint64_t item, uint32_t hs, uint32_t dv, uint32_t e) {
+  return (item * kHeadSlots + hs) * dv + e;
+}
+JMA_HD uint64_t sep_ml_float(uint64_t item, uint32_t hs) { return (item * kHeadSlots + hs) * 2; }
+
+// Split plan of one decode launch of `count` <= kMaxRows rows at positions[]: every workgroup
+// streams tiles_per_split tiles, at least tiles_per_wave per wave, raised until the launch is near
+// target_blocks workgroups and no row needs more than kMaxSplits splits (the decode kernel then
+// reduces the splits itself). When that cap would leave the launch with fewer than a quarter of
+// the target workgroups (few long rows: one sequence at a long context with few KV heads), rows
+// are cut wider, up to kMaxWideSplits splits, and reduce_kernel combines them (`separate`); a
+// context running separate kernels (`unfused`) always does.
+struct DecodePlan {
+  uint32_t hgroups = 0, tiles_per_split = 0, total_items = 0, max_splits = 0, ns_uniform = 0;
+  bool any_split = false, separate = false;
+  uint32_t nsplit[kMaxRows] = {};
+  uint32_t item_start[kMaxRows + 1] = {};
+  uint64_t part_f_bytes = 0, counter_bytes = 0, acc_bytes = 0, ml_bytes = 0;
+};
+
+inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_t window,
+                              uint32_t hkv, uint32_t group, int dk, int dv, bool f16,
+                              int target_blocks, int tiles_per_wave, bool unfused) {
+  DecodePlan p;
+  const uint32_t blk = (uint32_t)v_block(f16);
+  p.hgroups = (group + kHeadSlots - 1) / kHeadSlots;
+  uint32_t ntiles[kMaxRows];
+  uint64_t units = 0;
+  uint32_t max_tiles = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint32_t pos = positions[i];
+    const uint32_t first = first_visible(pos, window);
+    ntiles[i] = pos / blk - first / blk + 1;
+    max_tiles = std::max(max_tiles, ntiles[i]);
+    units += (uint64_t)ntiles[i] * hkv * p.hgroups;
+  }
+  const uint64_t target = (uint64_t)std::max(target_blocks, 1);
+  uint64_t tps = (uint64_t)decode_waves(dk) * (uint64_t)std::max(tiles_per_wave, 1);
+  tps = std::max<uint64_t>(tps, (units + target - 1) / target);
+  const uint64_t tps_fused = std::max<uint64_t>(tps, (max_tiles + kMaxSplits - 1) / kMaxSplits);
+  bool wide = false;
+  if (tps_fused > tps && !unfused) {
+    uint64_t fused_items = 0;
+    for (uint32_t i = 0; i < count; ++i)
+      fused_items += (ntiles[i] + tps_fused - 1) / tps_fused * hkv * p.hgroups;
+    wide = fused_items * 4 < target;
+  }
+  tps = wide ? std::max<uint64_t>(tps, (max_tiles + kMaxWideSplits - 1) / kMaxWideSplits)
+             : tps_fused;
+  p.tiles_per_split = (uint32_t)tps;
+  uint32_t items = 0;
+  bool uniform = true;
+  for (uint32_t i = 0; i < count; ++i) {
+    p.item_start[i] = items;
+    p.nsplit[i] = (uint32_t)((ntiles[i] + tps - 1) / tps);
+    p.any_split |= p.nsplit[i] > 1;
+    uniform &= p.nsplit[i] == p.nsplit[0];
+    p.max_splits = std::max(p.max_splits, p.nsplit[i]);
+    items += p.nsplit[i] * hkv * p.hgroups;
+  }
+  p.item_start[count] = items;
+  p.total_items = items;
+  p.ns_uniform = uniform ? p.nsplit[0] : 0u;
+  p.separate = p.any_split && (unfused || wide);
+  if (p.separate) {
+    p.acc_bytes = (uint64_t)items * kHeadSlots * dv * 4;
+    p.ml_bytes = (uint64_t)items * kHeadSlots * 2 * 4;
+  } else if (p.any_split) {
+    p.part_f_bytes = (uint64_t)items * kHeadSlots * (dv + 4) * 4;
+    p.counter_bytes = (uint64_t)count * hkv * p.hgroups * 4;
+  }
+  return p;
+}
+
+}  // namespace jma

@@ -270,10 +270,6 @@ LayerCall resolve_layer(const jmodels_attn_kv* kv, const jmodels_attn_layer* p) 
   return c;
 }
 
-uint32_t first_visible(uint32_t position, uint32_t window) {
-  return (window == 0 || position + 1 <= window) ? 0u : position + 1 - window;
-}
-
 void check_rows(const jmodels_attn_kv* kv, const LayerCall& lc, uint32_t count,
                 const uint32_t* sequences, const uint32_t* positions) {
   require(count > 0, JMODELS_ATTN_INVALID_SHAPE, "count must be > 0");
@@ -376,7 +372,6 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
                      const jma::RowList& rows, const float* q, float* out,
                      const FusedAppend& fa = FusedAppend(),
                      const jma::FixedScratch* fixed = nullptr) {
-  const uint32_t blk = (uint32_t)jma::v_block(kv->f16());
   jma::DecodeArgs a{};
   a.kv = kv->view(lc.layer);
   a.q = q;
@@ -385,7 +380,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   a.qscale = lc.scale * 1.4426950408889634f;
   a.num_heads = lc.num_heads;
   a.group = lc.group;
-  a.hgroups = (lc.group + 15) / 16;
+  a.hgroups = (lc.group + jma::kHeadSlots - 1) / jma::kHeadSlots;
   a.num_kv_heads = kv->hkv;
   a.window = lc.window;
   a.rows = rows;
@@ -406,44 +401,16 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     }
     a.norm_eps = lc.norm->eps;
   }
-  std::vector<uint32_t> ntiles(rows.count);
-  uint64_t units = 0;
-  uint32_t max_tiles = 0;
-  for (uint32_t i = 0; i < rows.count; ++i) {
-    const uint32_t pos = rows.pos[i];
-    const uint32_t first = first_visible(pos, lc.window);
-    ntiles[i] = pos / blk - first / blk + 1;
-    max_tiles = std::max(max_tiles, ntiles[i]);
-    units += (uint64_t)ntiles[i] * kv->hkv * a.hgroups;
-  }
-  const uint64_t target = (uint64_t)ctx->decode_target_blocks;
-  uint64_t tps = (uint64_t)jma::decode_waves((int)kv->dk) * ctx->tiles_per_wave;
-  tps = std::max<uint64_t>(tps, (units + target - 1) / target);
-  const uint64_t tps_fused = std::max<uint64_t>(tps, (max_tiles + jma::kMaxSplits - 1) / jma::kMaxSplits);
-  bool wide = false;
-  if (tps_fused > tps && !ctx->unfused) {
-    uint64_t fused_items = 0;
-    for (uint32_t i = 0; i < rows.count; ++i)
-      fused_items += (ntiles[i] + tps_fused - 1) / tps_fused * kv->hkv * a.hgroups;
-    wide = fused_items * 4 < target;
-  }
-  tps = wide ? std::max<uint64_t>(tps, (max_tiles + jma::kMaxWideSplits - 1) / jma::kMaxWideSplits)
-             : tps_fused;
-  a.tiles_per_split = (uint32_t)tps;
-  uint32_t items = 0;
-  bool any_split = false;
-  bool uniform = true;
-  for (uint32_t i = 0; i < rows.count; ++i) {
-    a.item_start[i] = items;
-    a.nsplit[i] = (uint32_t)((ntiles[i] + tps - 1) / tps);
-    any_split |= a.nsplit[i] > 1;
-    uniform &= a.nsplit[i] == a.nsplit[0];
-    a.max_splits = std::max(a.max_splits, a.nsplit[i]);
-    items += a.nsplit[i] * kv->hkv * a.hgroups;
-  }
-  a.item_start[rows.count] = items;
-  a.total_items = items;
-  a.ns_uniform = uniform ? a.nsplit[0] : 0u;
+  const jma::DecodePlan plan =
+      jma::plan_decode(rows.count, rows.pos, lc.window, kv->hkv, lc.group, (int)kv->dk, (int)kv->dv,
+                       kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave, ctx->unfused);
+  a.tiles_per_split = plan.tiles_per_split;
+  for (uint32_t i = 0; i <= rows.count; ++i) a.item_start[i] = plan.item_start[i];
+  for (uint32_t i = 0; i < rows.count; ++i) a.nsplit[i] = plan.nsplit[i];
+  a.max_splits = plan.max_splits;
+  a.total_items = plan.total_items;
+  a.ns_uniform = plan.ns_uniform;
+  const bool uniform = plan.ns_uniform != 0;
   if (uniform && rows.contiguous && a.hgroups == 1) {
     const size_t es = kv->f16() ? 2 : 4;
     a.k_base = (char*)a.kv.k + (a.kv.seq_stride_k * rows.seq0 + a.kv.layer_off_k) * es;
@@ -454,9 +421,8 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
             std::string("the launch plan needs ") + std::to_string(need) + " bytes of " + what +
                 ", the fixed scratch holds " + std::to_string(have));
   };
-  if (any_split && (ctx->unfused || wide)) {
-    const size_t acc_b = (size_t)items * 16 * kv->dv * sizeof(float);
-    const size_t ml_b = (size_t)items * 16 * 2 * sizeof(float);
+  if (plan.separate) {
+    const size_t acc_b = plan.acc_bytes, ml_b = plan.ml_bytes;
     if (fixed) {
       fits(acc_b, fixed->part_acc_bytes, "split partials");
       fits(ml_b, fixed->part_ml_bytes, "split maxima and sums");
@@ -468,12 +434,14 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
       a.part_acc = (float*)ctx->part_acc.ptr;
       a.part_ml = (float*)ctx->part_ml.ptr;
     }
-  } else if (any_split) {
+  } else if (plan.any_split) {
     // Arrival tickets start at zero and every partial word starts not-written; the reducing
     // workgroups restore both, so they are zeroed only when (re)allocated, never inside a launch
     // sequence a caller may capture.
-    const size_t part_b = (size_t)items * 16 * (kv->dv + 4) * sizeof(float);
-    const size_t ctr_b = (size_t)rows.count * kv->hkv * a.hgroups * sizeof(uint32_t);
+    const size_t part_b = plan.part_f_bytes, ctr_b = plan.counter_bytes;
+    // The exchange addresses its partials with 32-bit byte offsets (a buffer descriptor).
+    require(part_b <= 0x7FFFFFF0u, JMODELS_ATTN_INVALID_SHAPE,
+            "decode plan needs more than 2 GiB of split partials (lower JMA_DECODE_TARGET_BLOCKS)");
     if (fixed) {
       fits(part_b, fixed->part_f_bytes, "split exchange partials");
       fits(ctr_b, fixed->counters_bytes, "arrival tickets");
@@ -488,8 +456,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     }
   }
   hip_check(jma::launch_decode(a, kv->f16(), kv->dk, kv->dv, ctx->stream), "decode launch");
-  if (any_split && a.counters == nullptr)
-    hip_check(jma::launch_reduce(a, kv->dv, ctx->stream), "reduce launch");
+  if (plan.separate) hip_check(jma::launch_reduce(a, kv->dv, ctx->stream), "reduce launch");
 }
 
 // The decode kernel normalises (QK-norm, value norm), rotates q and appends the new rows itself
@@ -516,7 +483,7 @@ void validate_attend_ranges(const jmodels_attn_kv* kv, const LayerCall& lc, uint
                             const uint32_t* sequences, const uint32_t* positions) {
   for (uint32_t i = 0; i < count; ++i) {
     const uint32_t p = positions[i];
-    kv->require_range(sequences[i], lc.layer, first_visible(p, lc.window), p);
+    kv->require_range(sequences[i], lc.layer, jma::first_visible(p, lc.window), p);
   }
 }
 
@@ -615,7 +582,7 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
 // start .. start+n-1 see must be available, and a RING layer must hold them all at once.
 void validate_causal(const jmodels_attn_kv* kv, const LayerCall& lc, uint32_t sequence,
                      uint32_t start, uint32_t n, bool rows_cached) {
-  const uint32_t first = first_visible(start, lc.window);
+  const uint32_t first = jma::first_visible(start, lc.window);
   if (kv->ring[lc.layer]) {
     // Gemma4KvCache sizes rings as window + prefill chunk (gemma4/Gemma4KvCache.java:39).
     require(start + n - first <= kv->ring[lc.layer], JMODELS_ATTN_OUT_OF_RANGE,
@@ -1249,7 +1216,7 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
     // Everything the new rows will read, except the rows themselves, must already be cached.
     for (uint32_t i = 0; i < count; ++i) {
       const uint32_t p = positions[i];
-      const uint32_t first = first_visible(p, lc.window);
+      const uint32_t first = jma::first_visible(p, lc.window);
       if (kv->ring[lc.layer] && p - first + 1 > kv->ring[lc.layer])
         fail(JMODELS_ATTN_OUT_OF_RANGE, "attention range exceeds ring capacity " +
                                             std::to_string(kv->ring[lc.layer]));

@@ -1,0 +1,164 @@
+// CPU bounds check of the decode launch plans (built with g++ and AddressSanitizer /
+// UndefinedBehaviorSanitizer by tests/test_plan_cpu.py). For every configured decode shape it
+// plans the launch with the runtime's own planner (models_amd/csrc/jma_plan.h), then walks every
+// workgroup of the grid the way decode_kernel and reduce_kernel index their buffers (the same
+// index functions) and checks:
+//   - every (row, kv head, head group, split) work item is distinct and inside total_items;
+//   - a row's splits cover its visible kv tiles exactly once;
+//   - every partial word a producer writes or a reducer reads lies inside the planned buffer, the
+//     fused exchange within the 32-bit byte offsets its buffer descriptor takes;
+//   - arrival-ticket counters lie inside the planned counter buffer;
+//   - split counts stay within the fused (32) or separate (1024) caps;
+//   - the separate reduction (reduce_kernel) reads only items its row's groups own.
+// Prints one line per case and "ok" at the end; exits non-zero on the first failed check.
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <string>
+#include <vector>
+
+#include "jma_plan.h"
+
+using namespace jma;
+
+namespace {
+
+struct Case {
+  std::string name;
+  std::vector<uint32_t> pos;
+  uint32_t window, hkv, group;
+  int dk, dv;
+  bool f16;
+  int target, tiles_per_wave;
+  bool unfused;
+  uint32_t ring;  // ring capacity of the layer, 0 = linear
+};
+
+[[noreturn]] void die(const Case& c, const std::string& what) {
+  fprintf(stderr, "FAILED %s: %s\n", c.name.c_str(), what.c_str());
+  exit(1);
+}
+
+void check(const Case& c) {
+  const uint32_t count = (uint32_t)c.pos.size();
+  if (count == 0 || count > (uint32_t)kMaxRows) die(c, "row count");
+  const DecodePlan p = plan_decode(count, c.pos.data(), c.window, c.hkv, c.group, c.dk, c.dv, c.f16,
+                                   c.target, c.tiles_per_wave, c.unfused);
+  const uint32_t blk = (uint32_t)v_block(c.f16);
+  const uint32_t hgroups = p.hgroups;
+  if (hgroups != (c.group + kHeadSlots - 1) / kHeadSlots) die(c, "head groups");
+  if (p.part_f_bytes > 0x7FFFFFF0ull) die(c, "fused partials exceed 32-bit buffer offsets");
+  std::vector<int> owner(p.total_items, 0);
+  const uint64_t part_f_floats = p.part_f_bytes / 4, acc_floats = p.acc_bytes / 4;
+  const uint64_t ml_floats = p.ml_bytes / 4, counters = p.counter_bytes / 4;
+  for (uint32_t row = 0; row < count; ++row) {
+    const uint32_t ns = p.ns_uniform ? p.ns_uniform : p.nsplit[row];
+    if (ns != p.nsplit[row]) die(c, "uniform split count differs from the row's");
+    if (ns == 0 || ns > p.max_splits) die(c, "split count outside [1, max_splits]");
+    if (ns > (uint32_t)(p.separate ? kMaxWideSplits : kMaxSplits)) die(c, "split count above the cap");
+    const uint32_t pos = c.pos[row];
+    const uint32_t first = first_visible(pos, c.window);
+    if (c.ring && pos - first + 1 > c.ring) die(c, "window wider than the ring");
+    const uint32_t t_begin = first / blk, t_end = pos / blk + 1;
+    std::vector<int> seen(t_end - t_begin, 0);
+    for (uint32_t rest = 0; rest < c.hkv * hgroups; ++rest) {
+      const uint32_t kvh = rest / hgroups, hg = rest % hgroups;
+      const uint32_t nreal = std::min<uint32_t>(kHeadSlots, c.group - hg * kHeadSlots);
+      const uint64_t item0 = group_item0(p.ns_uniform, p.item_start[row], row, c.hkv, hgroups, rest, ns);
+      if (item0 + ns > p.total_items) die(c, "group items past total_items");
+      if (ns > 1 && !p.separate) {
+        const uint64_t gid = group_counter(row, c.hkv, kvh, hgroups, hg);
+        if (gid >= counters) die(c, "arrival ticket outside the counter buffer");
+      }
+      for (uint32_t split = 0; split < p.max_splits; ++split) {
+        if (split >= ns) continue;  // the kernel's early exit for rows with fewer splits
+        const uint64_t item = item0 + split;
+        if (owner[item]++) die(c, "work item shared by two workgroups");
+        const uint32_t s_t0 = t_begin + split * p.tiles_per_split;
+        const uint32_t s_t1 = std::min(s_t0 + p.tiles_per_split, t_end);
+        if (s_t0 >= s_t1) die(c, "a split without tiles");
+        if (rest == 0)
+          for (uint32_t t = s_t0; t < s_t1; ++t) seen[t - t_begin]++;
+        if (ns == 1) continue;
+        for (uint32_t hs = 0; hs < nreal; ++hs) {
+          if (p.separate) {
+            if (sep_acc_float(item, hs, c.dv, c.dv - 1) >= acc_floats) die(c, "part_acc index");
+            if (sep_ml_float(item, hs) + 1 >= ml_floats) die(c, "part_ml index");
+          } else {
+            // producer stores acc quads and the (m, l, pad, pad) word group; the reducer reads
+            // the same words of every split of the group
+            if (fused_part_float(item, hs, c.dv, c.dv + 3) >= part_f_floats) die(c, "part_f index");
+            if (fused_part_float(item, hs, c.dv, c.dv + 3) * 4 + 16 > 0x7FFFFFF0ull)
+              die(c, "part_f byte offset beyond the buffer descriptor");
+          }
+        }
+      }
+      if (p.separate && ns > 1) {
+        // reduce_kernel: one workgroup per (row, query head, 64-element chunk) reads the row's
+        // group base + split for split < ns
+        const uint64_t base = group_item0(p.ns_uniform, p.item_start[row], row, c.hkv, hgroups,
+                                          kvh * hgroups + hg, ns);
+        if (base != item0) die(c, "reduce_kernel group base differs from the producers'");
+        for (uint32_t hs = 0; hs < nreal; ++hs)
+          if (sep_acc_float(base + ns - 1, hs, c.dv, c.dv - 1) >= acc_floats) die(c, "reduce read");
+      }
+    }
+    for (uint32_t t = 0; t < seen.size(); ++t)
+      if (seen[t] != 1) die(c, "kv tile " + std::to_string(t_begin + t) + " covered " +
+                                   std::to_string(seen[t]) + " times");
+  }
+  for (uint64_t i = 0; i < p.total_items; ++i)
+    if (owner[i] != 1) die(c, "work item " + std::to_string(i) + " not written exactly once");
+  printf("%-44s rows %3u tiles/split %5u splits <= %4u items %7u %s %8.1f KiB\n", c.name.c_str(),
+         count, p.tiles_per_split, p.max_splits, p.total_items,
+         p.separate ? "separate" : (p.any_split ? "fused   " : "single  "),
+         (double)(p.separate ? p.acc_bytes + p.ml_bytes : p.part_f_bytes) / 1024.0);
+}
+
+// Deterministic ragged lengths (a 64-bit LCG), uniform on [lo, hi].
+std::vector<uint32_t> ragged(uint32_t n, uint32_t lo, uint32_t hi, uint64_t seed) {
+  std::vector<uint32_t> v(n);
+  uint64_t x = seed;
+  for (uint32_t i = 0; i < n; ++i) {
+    x = x * 6364136223846793005ull + 1442695040888963407ull;
+    v[i] = lo + (uint32_t)((x >> 33) % (hi - lo + 1));
+  }
+  return v;
+}
+
+std::vector<uint32_t> run(uint32_t start, uint32_t n) {
+  std::vector<uint32_t> v(n);
+  for (uint32_t i = 0; i < n; ++i) v[i] = start + i;
+  return v;
+}
+
+}  // namespace
+
+int main() {
+  std::vector<Case> cases;
+  // BASELINE configs at their configured sizes (one decode row per launch unless listed).
+  cases.push_back({"C1 f32 d128 16/8 @512", {512}, 0, 8, 2, 128, 128, false, 512, 1, false, 0});
+  for (uint32_t p : {4096u, 4159u, 4223u})
+    cases.push_back({"C2 f16 d64 32/8 @" + std::to_string(p), {p}, 0, 8, 4, 64, 64, true, 512, 1, false, 0});
+  cases.push_back({"C1 prefill rows (f32, listed)", run(0, 128), 0, 8, 2, 128, 128, false, 512, 1, false, 0});
+  cases.push_back({"C4 64 ragged U[256,16384] d128 12/2", ragged(64, 256, 16384, 4), 0, 2, 6, 128, 128, true, 512, 1, false, 0});
+  for (uint32_t p : {32704u, 32735u, 32767u}) {
+    cases.push_back({"C5 global d256 4/1 @" + std::to_string(p), {p}, 0, 1, 4, 256, 256, true, 512, 1, false, 0});
+    cases.push_back({"C5 sliding ring 544 w512 @" + std::to_string(p), {p}, 512, 1, 4, 256, 256, true, 512, 1, false, 544});
+  }
+  // Split-plan extremes the tests and tuning variables reach.
+  cases.push_back({"target 1 (one split per row)", ragged(5, 40, 2048, 13), 0, 2, 4, 64, 64, true, 1, 64, false, 0});
+  cases.push_back({"target 4096, 1 tile/wave", ragged(5, 40, 2048, 13), 0, 2, 4, 256, 256, true, 4096, 1, false, 0});
+  cases.push_back({"unfused (separate reduction)", ragged(5, 40, 2048, 13), 0, 2, 4, 64, 64, true, 4096, 1, true, 0});
+  cases.push_back({"wide: 16383 positions d256 MQA", {16383, 300, 4096}, 0, 1, 4, 256, 256, true, 512, 1, false, 0});
+  cases.push_back({"wide: ring 16384 w12000 @20000", {20000}, 12000, 1, 4, 128, 128, true, 512, 1, false, 16384});
+  cases.push_back({"two head groups (20 q heads / kv head)", ragged(7, 1, 9000, 3), 0, 2, 20, 128, 128, true, 512, 1, false, 0});
+  cases.push_back({"128 rows x 8 kv x 4 head groups, long", ragged(128, 60000, 65535, 9), 0, 8, 64, 128, 128, true, 512, 1, false, 0});
+  cases.push_back({"128 rows, target 100000", ragged(128, 544, 544, 1), 0, 8, 4, 256, 256, true, 100000, 1, false, 0});
+  cases.push_back({"single position 0", {0}, 0, 1, 1, 16, 16, false, 512, 1, false, 0});
+  cases.push_back({"1M context MQA d128", {1048575}, 0, 1, 8, 128, 128, true, 512, 1, false, 0});
+  for (const Case& c : cases) check(c);
+  printf("ok\n");
+  return 0;
+}

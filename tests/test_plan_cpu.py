@@ -1,0 +1,27 @@
+"""CPU bounds check of the decode launch plans: tests/plan_check.cpp, built with g++ and the
+address and undefined-behaviour sanitizers, plans every BASELINE decode shape (C1-C5 at their
+configured sizes, including C5's global layers with the wide split plan and its sliding-window
+ring layers) and extreme tuning settings with the runtime's own planner, then walks every
+workgroup's partial-buffer, counter and tile indexing with the kernels' own index functions."""
+
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_decode_plans_stay_in_bounds(tmp_path):
+    exe = tmp_path / "plan_check"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
+           "-fno-sanitize-recover=all", "-I", os.path.join(ROOT, "models_amd", "csrc"),
+           os.path.join(ROOT, "tests", "plan_check.cpp"), "-o", str(exe)]
+    build = subprocess.run(cmd, capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.strip().endswith("ok"), run.stdout
+    assert "C5 global d256 4/1 @32767" in run.stdout and "separate" in run.stdout
