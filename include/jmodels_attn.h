@@ -176,11 +176,35 @@ JMODELS_ATTN_API int32_t jmodels_attn_norm_destroy(jmodels_attn_norm* norm);
  * one backend-java KvCache, BJ/llama/LlamaForwardPass.java:412-416). Allocated at max_seq_len up
  * front (no growth copies; BJ/cache/KvCache.java:284-322 grows lazily instead).
  * ring_capacity: NULL, or num_layers entries where 0 = LINEAR and c > 0 = RING of c slots
- * (BJ/cache/LayeredKvCache.java:41-64); c must be a multiple of 32 and is capped at max_seq_len. */
+ * (BJ/cache/LayeredKvCache.java:41-64), any c > 0; c >= max_seq_len stores the layer linearly
+ * (physicalLimit = min(ringCapacity, maxSeqLen), :128-129). A ring's device storage is rounded
+ * up to a multiple of 32 slots; what it retains (contains, read, the window check) follows c. */
 JMODELS_ATTN_API int32_t jmodels_attn_kv_create(jmodels_attn_context* ctx, uint32_t sequences, uint32_t num_layers,
                                uint32_t max_seq_len, uint32_t num_kv_heads, uint32_t key_length,
                                uint32_t value_length, uint32_t dtype,
                                const uint32_t* ring_capacity, jmodels_attn_kv** kv_out);
+/* One layer of a layered cache: LayeredKvCache.LayerSpec (BJ/cache/LayeredKvCache.java:41-64)
+ * with keyDim = num_kv_heads * key_length and valueDim = num_kv_heads * value_length, as
+ * Gemma4KvCache builds them per layer (BJ/gemma4/Gemma4KvCache.java:39-47; head counts and
+ * head lengths per layer from Gemma4Config.numKvHeads / headDim, BJ/gemma4/Gemma4Config.java:
+ * 172-192). ring_capacity 0 = LINEAR, else RING of that many slots (any value > 0). */
+typedef struct jmodels_attn_layer_spec {
+  uint32_t num_kv_heads;
+  uint32_t key_length;
+  uint32_t value_length;
+  uint32_t ring_capacity;
+} jmodels_attn_layer_spec;
+
+/* LayeredKvCache constructor (BJ/cache/LayeredKvCache.java:124-156) for `sequences` sessions:
+ * num_layers specs, each layer with its own kv heads, key/value lengths and retention. Attention
+ * calls use the layer's own dimensions (jmodels_attn_layer.num_heads must be a multiple of that
+ * layer's num_kv_heads). Decode supports key_length == value_length in {32, 64, 128, 256, 512}
+ * (f16) or {16, ..., 512} (f32); the MFMA prefill key lengths up to 256, longer ones run the
+ * decode kernel per row. */
+JMODELS_ATTN_API int32_t jmodels_attn_kv_create_layered(jmodels_attn_context* ctx, uint32_t sequences,
+                                       uint32_t num_layers, uint32_t max_seq_len,
+                                       const jmodels_attn_layer_spec* specs, uint32_t dtype,
+                                       jmodels_attn_kv** kv_out);
 JMODELS_ATTN_API int32_t jmodels_attn_kv_destroy(jmodels_attn_kv* kv);
 /* KvCache.clear (BJ/cache/KvCache.java:156-158) for one sequence, or all when sequence < 0. */
 JMODELS_ATTN_API int32_t jmodels_attn_kv_clear(jmodels_attn_kv* kv, int32_t sequence);
@@ -190,7 +214,8 @@ JMODELS_ATTN_API int32_t jmodels_attn_kv_discard_from(jmodels_attn_kv* kv, uint3
 /* LayeredKvCache.contains (BJ/cache/LayeredKvCache.java:172-175): *out = 1 if available. */
 JMODELS_ATTN_API int32_t jmodels_attn_kv_contains(const jmodels_attn_kv* kv, uint32_t sequence, uint32_t layer,
                                  uint32_t position, int32_t* out);
-/* KvCache.store without RoPE (BJ/cache/KvCache.java:51-73): host vectors of key_dim/value_dim. */
+/* KvCache.store without RoPE (BJ/cache/KvCache.java:51-73): host vectors of the layer's
+ * key_dim/value_dim. */
 JMODELS_ATTN_API int32_t jmodels_attn_kv_store(jmodels_attn_context* ctx, jmodels_attn_kv* kv, uint32_t sequence,
                               uint32_t layer, uint32_t position, const float* key,
                               uint64_t key_elements, const float* value, uint64_t value_elements);

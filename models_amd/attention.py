@@ -71,6 +71,7 @@ EXPORTS = (
     "jmodels_attn_prefill_device", "jmodels_attn_attend_causal",
     "jmodels_attn_attend_causal_device", "jmodels_attn_norm_create", "jmodels_attn_norm_create_ex",
     "jmodels_attn_norm_destroy", "jmodels_attn_decode_device_noalloc",
+    "jmodels_attn_kv_create_layered",
 )
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -125,6 +126,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "jmodels_attn_norm_destroy": (_i32, [_vp]),
         "jmodels_attn_kv_create": (_i32, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _vp,
                                           ctypes.POINTER(_vp)]),
+        "jmodels_attn_kv_create_layered": (_i32, [_vp, _u32, _u32, _u32, _vp, _u32, ctypes.POINTER(_vp)]),
         "jmodels_attn_kv_destroy": (_i32, [_vp]),
         "jmodels_attn_kv_clear": (_i32, [_vp, _i32]),
         "jmodels_attn_kv_discard_from": (_i32, [_vp, _u32, _u32]),
@@ -258,8 +260,19 @@ class HipAttentionLibrary:
     def kv_cache(self, num_layers: int, max_seq_len: int, num_kv_heads: int, key_length: int,
                  value_length: int, half_precision: bool = True, sequences: int = 1,
                  ring_capacity: Optional[Sequence[int]] = None) -> "HipKvCache":
-        return HipKvCache(self, num_layers, max_seq_len, num_kv_heads, key_length, value_length,
-                          half_precision, sequences, ring_capacity)
+        """One shape for every layer (KvCache, or LayeredKvCache with ring_capacity)."""
+        rings = list(ring_capacity) if ring_capacity is not None else [0] * num_layers
+        if len(rings) != num_layers:
+            raise ValueError("ring_capacity needs one entry per layer")
+        specs = [LayerSpec(num_kv_heads, key_length, value_length, r) for r in rings]
+        return HipKvCache(self, specs, max_seq_len, half_precision, sequences, uniform=True)
+
+    def layered_kv_cache(self, specs: Sequence["LayerSpec"], max_seq_len: int,
+                         half_precision: bool = True, sequences: int = 1) -> "HipKvCache":
+        """LayeredKvCache(maxSeqLen, LayerSpec[]) (cache/LayeredKvCache.java:124-156): per-layer kv
+        heads, head lengths and retention, as Gemma4KvCache builds them
+        (gemma4/Gemma4KvCache.java:39-47)."""
+        return HipKvCache(self, list(specs), max_seq_len, half_precision, sequences, uniform=False)
 
 
 class HipRotaryTable:
@@ -335,29 +348,66 @@ class AttentionLayer:
                       self.qk_norm.handle if self.qk_norm is not None else None)
 
 
-class HipKvCache:
-    """Device-resident KV cache for ``sequences`` independent sessions (KvCache / LayeredKvCache)."""
+@dataclass(frozen=True)
+class LayerSpec:
+    """LayeredKvCache.LayerSpec (cache/LayeredKvCache.java:41-64) with keyDim = num_kv_heads *
+    key_length and valueDim = num_kv_heads * value_length; ring_capacity 0 = LINEAR."""
 
-    def __init__(self, owner: HipAttentionLibrary, num_layers: int, max_seq_len: int,
-                 num_kv_heads: int, key_length: int, value_length: int, half_precision: bool,
-                 sequences: int, ring_capacity: Optional[Sequence[int]]):
+    num_kv_heads: int
+    key_length: int
+    value_length: int
+    ring_capacity: int = 0
+
+    @property
+    def key_dim(self) -> int:
+        return self.num_kv_heads * self.key_length
+
+    @property
+    def value_dim(self) -> int:
+        return self.num_kv_heads * self.value_length
+
+
+class _LayerSpecC(ctypes.Structure):
+    _fields_ = [("num_kv_heads", ctypes.c_uint32), ("key_length", ctypes.c_uint32),
+                ("value_length", ctypes.c_uint32), ("ring_capacity", ctypes.c_uint32)]
+
+
+class HipKvCache:
+    """Device-resident KV cache for ``sequences`` independent sessions (KvCache / LayeredKvCache).
+    Shapes are per layer (``specs``); num_kv_heads, key_length, value_length, key_dim and
+    value_dim name layer 0's for caches of one shape."""
+
+    def __init__(self, owner: HipAttentionLibrary, specs: Sequence[LayerSpec], max_seq_len: int,
+                 half_precision: bool, sequences: int, uniform: bool):
         self.owner = owner
-        self.num_layers, self.max_seq_len = num_layers, max_seq_len
-        self.num_kv_heads, self.key_length, self.value_length = num_kv_heads, key_length, value_length
-        self.key_dim = num_kv_heads * key_length
-        self.value_dim = num_kv_heads * value_length
+        self.specs = list(specs)
+        self.num_layers, self.max_seq_len = len(self.specs), max_seq_len
+        first = self.specs[0]
+        self.num_kv_heads, self.key_length, self.value_length = (first.num_kv_heads, first.key_length,
+                                                                 first.value_length)
+        self.key_dim, self.value_dim = first.key_dim, first.value_dim
         self.sequences = sequences
         self.half_precision = half_precision
-        ring = None
-        if ring_capacity is not None:
-            if len(ring_capacity) != num_layers:
-                raise ValueError("ring_capacity needs one entry per layer")
-            ring = (ctypes.c_uint32 * num_layers)(*ring_capacity)
         out = _vp()
-        owner.check(owner.lib.jmodels_attn_kv_create(
-            owner.ctx, sequences, num_layers, max_seq_len, num_kv_heads, key_length, value_length,
-            KV_F16 if half_precision else KV_F32, ring, ctypes.byref(out)), "kv_create")
+        dtype = KV_F16 if half_precision else KV_F32
+        if uniform:
+            ring = (ctypes.c_uint32 * self.num_layers)(*[sp.ring_capacity for sp in self.specs])
+            owner.check(owner.lib.jmodels_attn_kv_create(
+                owner.ctx, sequences, self.num_layers, max_seq_len, first.num_kv_heads,
+                first.key_length, first.value_length, dtype, ring, ctypes.byref(out)), "kv_create")
+        else:
+            arr = (_LayerSpecC * self.num_layers)(
+                *[_LayerSpecC(sp.num_kv_heads, sp.key_length, sp.value_length, sp.ring_capacity)
+                  for sp in self.specs])
+            owner.check(owner.lib.jmodels_attn_kv_create_layered(
+                owner.ctx, sequences, self.num_layers, max_seq_len, arr, dtype, ctypes.byref(out)),
+                "kv_create_layered")
         self.handle = out.value
+
+    def spec(self, layer: int) -> LayerSpec:
+        """Layer ``layer``'s shape; for a layer outside the cache, layer 0's, so that the call
+        reaches the library and fails there with its OUT_OF_RANGE status."""
+        return self.specs[layer] if 0 <= layer < self.num_layers else self.specs[0]
 
     def close(self) -> None:
         if getattr(self, "handle", None):
@@ -369,18 +419,20 @@ class HipKvCache:
     def store(self, layer: int, position: int, key, value, sequence: int = 0) -> None:
         k = _f32(key)
         v = _f32(value)
-        if k.size != self.key_dim:
-            raise ValueError(f"key.length must equal {self.key_dim}: {k.size}")
-        if v.size != self.value_dim:
-            raise ValueError(f"value.length must equal {self.value_dim}: {v.size}")
+        sp = self.spec(layer)
+        if k.size != sp.key_dim:
+            raise ValueError(f"key.length must equal {sp.key_dim}: {k.size}")
+        if v.size != sp.value_dim:
+            raise ValueError(f"value.length must equal {sp.value_dim}: {v.size}")
         o = self.owner
         o.check(o.lib.jmodels_attn_kv_store(o.ctx, self.handle, sequence, layer, position,
                                             _ptr(k), k.size, _ptr(v), v.size), "kv_store")
 
     def read(self, layer: int, frm: int, to: int, sequence: int = 0):
         n = max(to - frm, 0)
-        keys = np.empty(n * self.key_dim, np.float32)
-        values = np.empty(n * self.value_dim, np.float32)
+        sp = self.spec(layer)
+        keys = np.empty(n * sp.key_dim, np.float32)
+        values = np.empty(n * sp.value_dim, np.float32)
         o = self.owner
         o.check(o.lib.jmodels_attn_kv_read(o.ctx, self.handle, sequence, layer, frm, to,
                                            _ptr(keys), keys.size, _ptr(values), values.size),
@@ -425,7 +477,7 @@ class HipKvCache:
         return seq, pos
 
     def _check_heads(self, layer: AttentionLayer):
-        if layer.num_heads <= 0 or layer.num_heads % self.num_kv_heads:
+        if layer.num_heads <= 0 or layer.num_heads % self.spec(layer.layer).num_kv_heads:
             raise ValueError("numHeads must be divisible by numKvHeads")
 
     def append(self, layer: AttentionLayer, positions, q, k, v, sequences=None):
@@ -449,7 +501,7 @@ class HipKvCache:
         seq, pos = self._rows(np.zeros(np.size(positions)) if sequences is None else sequences,
                               positions)
         q = _f32(q)
-        out = np.empty(seq.size * layer.num_heads * self.value_length, np.float32)
+        out = np.empty(seq.size * layer.num_heads * self.spec(layer.layer).value_length, np.float32)
         st = layer.struct()
         o = self.owner
         o.check(o.lib.jmodels_attn_attend(
@@ -463,7 +515,7 @@ class HipKvCache:
         seq, pos = self._rows(np.zeros(np.size(positions)) if sequences is None else sequences,
                               positions)
         q, k, v = _f32(q), _f32(k), _f32(v)
-        out = np.empty(seq.size * layer.num_heads * self.value_length, np.float32)
+        out = np.empty(seq.size * layer.num_heads * self.spec(layer.layer).value_length, np.float32)
         st = layer.struct()
         o = self.owner
         o.check(o.lib.jmodels_attn_decode(
@@ -476,8 +528,9 @@ class HipKvCache:
         """Causal prefill of consecutive rows start .. start+n-1."""
         self._check_heads(layer)
         q, k, v = _f32(q), _f32(k), _f32(v)
-        n = q.size // (layer.num_heads * self.key_length)
-        out = np.empty(n * layer.num_heads * self.value_length, np.float32)
+        sp = self.spec(layer.layer)
+        n = q.size // (layer.num_heads * sp.key_length)
+        out = np.empty(n * layer.num_heads * sp.value_length, np.float32)
         st = layer.struct()
         o = self.owner
         o.check(o.lib.jmodels_attn_prefill(
@@ -489,8 +542,9 @@ class HipKvCache:
         """computeBatchedAttention: causal attention of cached rows start .. start+n-1."""
         self._check_heads(layer)
         q = _f32(q)
-        n = q.size // (layer.num_heads * self.key_length)
-        out = np.empty(n * layer.num_heads * self.value_length, np.float32)
+        sp = self.spec(layer.layer)
+        n = q.size // (layer.num_heads * sp.key_length)
+        out = np.empty(n * layer.num_heads * sp.value_length, np.float32)
         st = layer.struct()
         o = self.owner
         o.check(o.lib.jmodels_attn_attend_causal(

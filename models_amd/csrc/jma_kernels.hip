@@ -229,16 +229,22 @@ struct Tile<_Float16, DK, DV> {
   static constexpr uint32_t kBlk = 32;
   half8_t k[2][DK / 32];
   half8_t v[DV / 16];
-  __device__ __forceinline__ void load(const _Float16* kb, const _Float16* vb, uint32_t slot0,
-                                       int c16, int g) {
+  __device__ __forceinline__ void load_k(const _Float16* kb, uint32_t slot0, int c16, int g) {
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int c = 0; c < DK / 32; ++c)
         k[b][c] = *(const half8_t*)(kb + (uint64_t)(slot0 + 16 * b + c16) * DK + 32 * c + 8 * g);
+  }
+  __device__ __forceinline__ void load_v(const _Float16* vb, uint32_t slot0, int c16, int g) {
     const _Float16* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
 #pragma unroll
     for (int n = 0; n < DV / 16; ++n) v[n] = *(const half8_t*)(vblk + (16 * n + c16) * kBlk + 8 * g);
+  }
+  __device__ __forceinline__ void load(const _Float16* kb, const _Float16* vb, uint32_t slot0,
+                                       int c16, int g) {
+    load_k(kb, slot0, c16, g);
+    load_v(vb, slot0, c16, g);
   }
 };
 
@@ -247,14 +253,20 @@ struct Tile<float, DK, DV> {
   static constexpr uint32_t kBlk = 16;
   float4_t k[DK / 16];
   float4_t v[DV / 16];
-  __device__ __forceinline__ void load(const float* kb, const float* vb, uint32_t slot0, int c16,
-                                       int g) {
+  __device__ __forceinline__ void load_k(const float* kb, uint32_t slot0, int c16, int g) {
 #pragma unroll
     for (int c = 0; c < DK / 16; ++c)
       k[c] = *(const float4_t*)(kb + (uint64_t)(slot0 + c16) * DK + 16 * c + 4 * g);
+  }
+  __device__ __forceinline__ void load_v(const float* vb, uint32_t slot0, int c16, int g) {
     const float* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
 #pragma unroll
     for (int n = 0; n < DV / 16; ++n) v[n] = *(const float4_t*)(vblk + (16 * n + c16) * kBlk + 4 * g);
+  }
+  __device__ __forceinline__ void load(const float* kb, const float* vb, uint32_t slot0, int c16,
+                                       int g) {
+    load_k(kb, slot0, c16, g);
+    load_v(vb, slot0, c16, g);
   }
 };
 
@@ -575,12 +587,20 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   constexpr int kC = kF16 ? DK / 32 : DK / 16;
   constexpr int kQ = kF16 ? 8 : 4;    // q elements per lane per k-chunk
   constexpr uint32_t kW = decode_waves(DK);
-  __shared__ __attribute__((aligned(16))) float s_acc[kW][16][DV];
+  // kQLds (head dim 512): the q operands are read from LDS at every tile instead of being held in
+  // registers (16 heads x 512 elements as f16 hi + lo would take 128 registers per lane), and the
+  // q rows share their LDS with the waves' combine area, which is written only after every wave
+  // has left its tile loop.
+  constexpr bool kQLds = DK >= 512;
+  constexpr int kAccFloats = kW * 16 * DV, kQFloats = 16 * (DK + 4);
+  __shared__ __attribute__((aligned(16))) float s_acc_mem[kQLds && kQFloats > kAccFloats ? kQFloats : kAccFloats];
+  __shared__ __attribute__((aligned(16))) float s_q_mem[kQLds ? 4 : kQFloats];
+  float (*s_acc)[16][DV] = (float (*)[16][DV])s_acc_mem;
+  float (*s_q)[DK + 4] = (float (*)[DK + 4])(kQLds ? s_acc_mem : s_q_mem);  // q rows, padded against bank conflicts
   __shared__ float s_ml[kW][16][2];
   __shared__ uint32_t s_ticket;
   __shared__ __attribute__((aligned(16))) KV s_new_k[DK];  // the appended row, rotated
   __shared__ KV s_new_v[DV];
-  __shared__ __attribute__((aligned(16))) float s_q[16][DK + 4];  // q rows, padded against bank conflicts
   __shared__ float s_qn[16];  // QK-norm scale of each raw q head
 
   // The grid is (split, kv head * head groups + head group, row). Every scalar argument the
@@ -676,12 +696,19 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 
   // The first two tiles of this wave are in flight before anything else is loaded (at head
   // dimension 256 the second waits until q is prepared: two tiles are half the register file).
+  // At head dimension 512 a tile's K and V never share the registers: K is loaded here, V inside
+  // the step once the scores are formed.
   constexpr bool kEarly2 = DK <= 128;
+  constexpr bool kSplitKV = DK >= 512;
+  auto tile_load = [&](TileT& x, uint32_t tt) JMA_INL {
+    if constexpr (kSplitKV) x.load_k(kb, slot0_of(tt), c16, g);
+    else x.load(kb, vb, slot0_of(tt), c16, g);
+  };
   uint32_t t = s_t0 + wave;
   TileT ta, tb;
-  if (t < s_t1) ta.load(kb, vb, slot0_of(t), c16, g);
+  if (t < s_t1) tile_load(ta, t);
   if constexpr (!kOne)
-    if (kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
+    if (kEarly2 && t + kW < s_t1) tile_load(tb, t + kW);
 
   if constexpr (kSimple) {
     // The remaining arguments, in one batch, once the first tile loads are issued.
@@ -719,12 +746,16 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   // group 0 workgroup stores it to the cache (the next launches read it there).
   const bool append = k_new != nullptr && split == ns - 1;
   if (append) {
-    // One thread per K pair (rotated as rope_append_kernel rotates it) or V element pair; every
-    // load is issued before any is used.
+    // One thread per K pair (rotated as rope_append_kernel rotates it) or V element pair, the
+    // workgroup's threads taking DK / 2 + DV / 2 pairs in turn (two turns at head dimension 512).
     const uint32_t slot = ring ? pos % cap : pos;
     const float* kx = k_new + ((uint64_t)row * hkv + kvh) * DK;
     const float* vx = v_new + ((uint64_t)row * hkv + kvh) * DV;
-    const uint32_t tid = threadIdx.x;
+    constexpr uint32_t kPairs = DK / 2 + DV / 2;
+    constexpr uint32_t kTurns = (kPairs + 64 * kW - 1) / (64 * kW);
+#pragma unroll
+    for (uint32_t turn = 0; turn < kTurns; ++turn) {
+    const uint32_t tid = threadIdx.x + turn * 64 * kW;
     if (tid < DK / 2) {
       const uint32_t j = tid;
       const bool rot = cs != nullptr && j < pairs;
@@ -755,6 +786,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         vp[0] = (KV)v0;
         vp[kBlk] = (KV)v1;
       }
+    }
     }
   }
   // Lanes of the wave owning the new row's tile that hold that row: K lanes hold tile rows
@@ -816,14 +848,15 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     }
   }
   if constexpr (!kOne)
-    if (!kEarly2 && t + kW < s_t1) tb.load(kb, vb, slot0_of(t + kW), c16, g);
+    if (!kEarly2 && t + kW < s_t1) tile_load(tb, t + kW);
   __syncthreads();  // q (and the appended row) are in LDS
 
-  // Q operand (B of S = K Q^T); the padding head lanes hold zeros.
-  half8_t qhi[kF16 ? kC : 1], qlo[kF16 ? kC : 1];
-  float4_t qf[kF16 ? 1 : kC];
-#pragma unroll
-  for (int c = 0; c < kC; ++c) {
+  // Q operand (B of S = K Q^T); the padding head lanes hold zeros. kQLds: formed from LDS at each
+  // use by q_chunk instead.
+  constexpr int kCR = kQLds ? 1 : kC;  // chunks held in registers
+  half8_t qhi[kF16 ? kCR : 1], qlo[kF16 ? kCR : 1];
+  float4_t qf[kF16 ? 1 : kCR];
+  auto q_chunk = [&](int c, half8_t& hi, half8_t& lo, float4_t& f) JMA_INL {
     float x[kQ];
 #pragma unroll
     for (int i = 0; i < kQ; i += 4) {
@@ -835,10 +868,24 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     for (int e = 0; e < kQ; ++e) {
       if constexpr (kF16) {
         const _Float16 h = (_Float16)x[e];
-        qhi[c][e] = h;
-        qlo[c][e] = (_Float16)(x[e] - (float)h);
+        hi[e] = h;
+        lo[e] = (_Float16)(x[e] - (float)h);
       } else {
-        qf[c][e] = x[e];
+        f[e] = x[e];
+      }
+    }
+  };
+  if constexpr (!kQLds) {
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+      half8_t h, lo;
+      float4_t f;
+      q_chunk(c, h, lo, f);
+      if constexpr (kF16) {
+        qhi[c] = h;
+        qlo[c] = lo;
+      } else {
+        qf[c] = f;
       }
     }
   }
@@ -865,6 +912,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
           cur.k[c] = k_lane ? x : cur.k[c];
         }
       }
+    }
+    auto patch_v = [&]() JMA_INL {
       if (v_lane) {
 #pragma unroll
         for (int n = 0; n < kNv; ++n)
@@ -872,10 +921,29 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
           for (int e = 0; e < kQ; ++e)
             if ((uint32_t)e == v_at % (uint32_t)kQ) cur.v[n][e] = s_new_v[16 * n + c16];
       }
-    }
+    };
+    if constexpr (decltype(patch)::value && !kSplitKV) patch_v();
     const uint32_t p0 = tt * kBlk;
     float s[kNs];
-    if constexpr (kF16) {
+    if constexpr (kF16 && kQLds) {
+      // q chunk c is formed once from LDS and serves both 16-row halves of the tile.
+      float4_t sc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int c = 0; c < kC; ++c) {
+        half8_t qh, ql;
+        float4_t unused;
+        q_chunk(c, qh, ql, unused);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qh, sc[b], 0, 0, 0);
+          sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], ql, sc[b], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[4 * b + e] = sc[b][e];
+    } else if constexpr (kF16) {
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         float4_t sc = {0.f, 0.f, 0.f, 0.f};
@@ -890,12 +958,21 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     } else {
       float4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < kC; ++c)
+      for (int c = 0; c < kC; ++c) {
+        half8_t unused_h, unused_l;
+        float4_t qc;
+        if constexpr (kQLds) q_chunk(c, unused_h, unused_l, qc);
+        else qc = qf[c];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          sc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[c][e], qf[c][e], sc, 0, 0, 0);
+          sc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[c][e], qc[e], sc, 0, 0, 0);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[e] = sc[e];
+    }
+    if constexpr (kSplitKV) {  // V of this tile, now that K's registers are free
+      cur.load_v(vb, slot0_of(tt), c16, g);
+      if constexpr (decltype(patch)::value) patch_v();
     }
     // Only the first and last tiles of the visible range hold masked rows. Their value elements
     // (element i of each V operand is the position of score i) are cleared too, through the
@@ -971,18 +1048,28 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   using no_patch = std::integral_constant<bool, false>;
   using with_patch = std::integral_constant<bool, true>;
   const uint32_t t_stop = patch_wave ? t_new : s_t1;
-  if constexpr (kOne) {
+  if constexpr (kOne && DK < 512) {
+    // At most one tile per wave (the launch picks this instance only then).
     if (t < t_stop) step(ta, t, no_patch{});
+    if (patch_wave) step(ta, t_new, with_patch{});
+  } else if constexpr (kOne) {
+    // One tile buffer: a further tile of this wave is loaded once the buffer is consumed.
+    for (;;) {
+      if (t >= t_stop) break;
+      step(ta, t, no_patch{});
+      t += kW;
+      if (t < s_t1) tile_load(ta, t);
+    }
     if (patch_wave) step(ta, t_new, with_patch{});
   } else {
     for (;;) {
       if (t >= t_stop) break;
       step(ta, t, no_patch{});
-      if (t + 2 * kW < s_t1) ta.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
+      if (t + 2 * kW < s_t1) tile_load(ta, t + 2 * kW);
       t += kW;
       if (t >= t_stop) break;
       step(tb, t, no_patch{});
-      if (t + 2 * kW < s_t1) tb.load(kb, vb, slot0_of(t + 2 * kW), c16, g);
+      if (t + 2 * kW < s_t1) tile_load(tb, t + 2 * kW);
       t += kW;
     }
     if (patch_wave) {
@@ -992,6 +1079,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   }
 
   l = wave_sum_groups(l);
+  if constexpr (kQLds) __syncthreads();  // every wave is done with the q rows the combine area overlays
 
   // Every wave publishes its state; then one thread per (head, element) combines the waves.
   if (head_ok) {
@@ -1138,6 +1226,7 @@ hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream) {
     case 64: hipLaunchKernelGGL(reduce_kernel<64>, grid, block, 0, stream, a); break;
     case 128: hipLaunchKernelGGL(reduce_kernel<128>, grid, block, 0, stream, a); break;
     case 256: hipLaunchKernelGGL(reduce_kernel<256>, grid, block, 0, stream, a); break;
+    case 512: hipLaunchKernelGGL(reduce_kernel<512>, grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1211,8 +1300,8 @@ hipError_t fixed_scratch(int device, hipStream_t stream, FixedScratch* out) {
 
 bool decode_supported(bool f16, int dk, int dv) {
   if (dk != dv) return false;
-  if (f16) return dk == 32 || dk == 64 || dk == 128 || dk == 256;
-  return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256;
+  if (f16) return dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
+  return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
 }
 
 template <typename KV, bool kSimple>
@@ -1240,6 +1329,10 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
         hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       else
         hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+      break;
+    case 512:
+      // One tile buffer always: a tile is the whole register budget of a wave at this width.
+      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -152,9 +152,12 @@ struct jmodels_attn_norm {
 
 struct jmodels_attn_kv {
   jmodels_attn_context* ctx = nullptr;
-  uint32_t sequences = 0, layers = 0, max_seq_len = 0, hkv = 0, dk = 0, dv = 0, dtype = 0;
+  uint32_t sequences = 0, layers = 0, max_seq_len = 0, dtype = 0;
+  // per layer (LayeredKvCache.LayerSpec, BJ/cache/LayeredKvCache.java:41-64): kv heads, key and
+  // value lengths per head
+  std::vector<uint32_t> hkv_l, dk_l, dv_l;
   std::vector<uint32_t> ring;      // logical ring capacity per layer, 0 = linear
-  std::vector<uint32_t> cap;       // physical slots per layer
+  std::vector<uint32_t> cap;       // physical slots per layer (a ring's rounded up to 32)
   std::vector<uint64_t> layer_off_k, layer_off_v;
   uint64_t seq_stride_k = 0, seq_stride_v = 0;
   void* d_k = nullptr;
@@ -233,6 +236,7 @@ void check_ctx(const jmodels_attn_context* ctx) {
 
 struct LayerCall {
   uint32_t layer, num_heads, group, window, neox;
+  uint32_t hkv, dk, dv;  // the layer's kv heads and head lengths
   float scale;
   const jmodels_attn_rope* rope;
   const jmodels_attn_norm* norm;  // null or weights on neither side = no QK-norm
@@ -242,28 +246,31 @@ LayerCall resolve_layer(const jmodels_attn_kv* kv, const jmodels_attn_layer* p) 
   require(p != nullptr, JMODELS_ATTN_NULL_POINTER, "layer parameters are null");
   require(p->layer < kv->layers, JMODELS_ATTN_OUT_OF_RANGE,
           "layer out of range: " + std::to_string(p->layer));
-  require(p->num_heads > 0 && p->num_heads % kv->hkv == 0, JMODELS_ATTN_INVALID_SHAPE,
-          "num_heads must be a positive multiple of num_kv_heads");
   LayerCall c{};
   c.layer = p->layer;
+  c.hkv = kv->hkv_l[p->layer];
+  c.dk = kv->dk_l[p->layer];
+  c.dv = kv->dv_l[p->layer];
+  require(p->num_heads > 0 && p->num_heads % c.hkv == 0, JMODELS_ATTN_INVALID_SHAPE,
+          "num_heads must be a positive multiple of the layer's num_kv_heads");
   c.num_heads = p->num_heads;
-  c.group = p->num_heads / kv->hkv;
+  c.group = p->num_heads / c.hkv;
   c.window = p->sliding_window;
   c.neox = p->neox ? 1u : 0u;
   // LlamaForwardPass: scale = (float)(1.0 / Math.sqrt(keyLength)) (llama/LlamaForwardPass.java:1559)
-  c.scale = p->scale != 0.0f ? p->scale : (float)(1.0 / sqrt((double)kv->dk));
+  c.scale = p->scale != 0.0f ? p->scale : (float)(1.0 / sqrt((double)c.dk));
   require(isfinite(c.scale) && c.scale > 0.0f, JMODELS_ATTN_INVALID_SHAPE, "scale must be finite and > 0");
   c.rope = p->rope;
   if (c.rope) {
     require(c.rope->ctx == kv->ctx, JMODELS_ATTN_INVALID_SHAPE, "rope table belongs to another context");
-    require(c.rope->rotary_dim <= kv->dk, JMODELS_ATTN_INVALID_SHAPE, "rotary_dim exceeds key_length");
+    require(c.rope->rotary_dim <= c.dk, JMODELS_ATTN_INVALID_SHAPE, "rotary_dim exceeds key_length");
   }
   c.norm = p->qk_norm;
   if (c.norm) {
     require(c.norm->ctx == kv->ctx, JMODELS_ATTN_INVALID_SHAPE, "qk-norm belongs to another context");
-    require(c.norm->head_dim == kv->dk, JMODELS_ATTN_INVALID_SHAPE,
+    require(c.norm->head_dim == c.dk, JMODELS_ATTN_INVALID_SHAPE,
             "qk-norm head_dim differs from key_length");
-    require(!c.norm->v_rms || c.norm->head_dim == kv->dv, JMODELS_ATTN_INVALID_SHAPE,
+    require(!c.norm->v_rms || c.norm->head_dim == c.dv, JMODELS_ATTN_INVALID_SHAPE,
             "value norm head_dim differs from value_length");
     if (!c.norm->d_q && !c.norm->d_k && !c.norm->v_rms) c.norm = nullptr;
   }
@@ -315,8 +322,8 @@ jma::RowList make_rows(uint32_t count, const uint32_t* sequences, const uint32_t
   return r;
 }
 
-uint32_t append_blocks_per_row(uint32_t num_heads, const jmodels_attn_kv* kv) {
-  const uint32_t pairs = num_heads * kv->dk / 2 + kv->hkv * kv->dk / 2 + kv->hkv * kv->dv / 2;
+uint32_t append_blocks_per_row(uint32_t num_heads, uint32_t hkv, uint32_t dk, uint32_t dv) {
+  const uint32_t pairs = num_heads * dk / 2 + hkv * dk / 2 + hkv * dv / 2;
   return (pairs + 255) / 256;
 }
 
@@ -338,10 +345,10 @@ void run_append(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall&
   }
   a.neox = lc.neox;
   a.num_heads = lc.num_heads;
-  a.num_kv_heads = kv->hkv;
-  a.dk = kv->dk;
-  a.dv = kv->dv;
-  a.blocks_per_row = append_blocks_per_row(lc.num_heads, kv);
+  a.num_kv_heads = lc.hkv;
+  a.dk = lc.dk;
+  a.dv = lc.dv;
+  a.blocks_per_row = append_blocks_per_row(lc.num_heads, lc.hkv, lc.dk, lc.dv);
   if (lc.norm) {
     a.q_norm_w = lc.norm->d_q;
     a.k_norm_w = lc.norm->d_k;
@@ -381,7 +388,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   a.num_heads = lc.num_heads;
   a.group = lc.group;
   a.hgroups = (lc.group + jma::kHeadSlots - 1) / jma::kHeadSlots;
-  a.num_kv_heads = kv->hkv;
+  a.num_kv_heads = lc.hkv;
   a.window = lc.window;
   a.rows = rows;
   a.k_new = fa.k;
@@ -402,7 +409,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     a.norm_eps = lc.norm->eps;
   }
   const jma::DecodePlan plan =
-      jma::plan_decode(rows.count, rows.pos, lc.window, kv->hkv, lc.group, (int)kv->dk, (int)kv->dv,
+      jma::plan_decode(rows.count, rows.pos, lc.window, lc.hkv, lc.group, (int)lc.dk, (int)lc.dv,
                        kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave, ctx->unfused);
   a.tiles_per_split = plan.tiles_per_split;
   for (uint32_t i = 0; i <= rows.count; ++i) a.item_start[i] = plan.item_start[i];
@@ -449,14 +456,14 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
       a.counters = fixed->counters;
     } else {
       reserve_filled(ctx->part_f, part_b, 0xFF, ctx->stream, "decode split exchange");
-      reserve_filled(ctx->counters, (size_t)jma::kMaxRows * kv->hkv * a.hgroups * sizeof(uint32_t), 0,
+      reserve_filled(ctx->counters, (size_t)jma::kMaxRows * lc.hkv * a.hgroups * sizeof(uint32_t), 0,
                      ctx->stream, "decode split exchange");
       a.part_f = (float*)ctx->part_f.ptr;
       a.counters = (uint32_t*)ctx->counters.ptr;
     }
   }
-  hip_check(jma::launch_decode(a, kv->f16(), kv->dk, kv->dv, ctx->stream), "decode launch");
-  if (plan.separate) hip_check(jma::launch_reduce(a, kv->dv, ctx->stream), "reduce launch");
+  hip_check(jma::launch_decode(a, kv->f16(), lc.dk, lc.dv, ctx->stream), "decode launch");
+  if (plan.separate) hip_check(jma::launch_reduce(a, lc.dv, ctx->stream), "reduce launch");
 }
 
 // The decode kernel normalises (QK-norm, value norm), rotates q and appends the new rows itself
@@ -470,8 +477,8 @@ bool can_fuse_decode(const jmodels_attn_context* ctx, const LayerCall& lc) {
 void run_attend(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
                 uint32_t count, const uint32_t* sequences, const uint32_t* positions,
                 const float* q, float* out, const jma::FixedScratch* fixed = nullptr) {
-  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
-  const uint64_t odim = (uint64_t)lc.num_heads * kv->dv;
+  const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk;
+  const uint64_t odim = (uint64_t)lc.num_heads * lc.dv;
   for (uint32_t base = 0; base < count; base += jma::kMaxRows) {
     const uint32_t n = std::min<uint32_t>(jma::kMaxRows, count - base);
     jma::RowList rows = make_rows(n, sequences + base, positions + base);
@@ -490,13 +497,13 @@ void validate_attend_ranges(const jmodels_attn_kv* kv, const LayerCall& lc, uint
 void append_rows(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall& lc,
                  uint32_t count, const uint32_t* sequences, const uint32_t* positions,
                  const float* q, const float* k, const float* v, float* q_out) {
-  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
-  const uint64_t kdim = (uint64_t)kv->hkv * kv->dk;
-  const uint64_t vdim = (uint64_t)kv->hkv * kv->dv;
+  const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk;
+  const uint64_t kdim = (uint64_t)lc.hkv * lc.dk;
+  const uint64_t vdim = (uint64_t)lc.hkv * lc.dv;
   // One launch takes up to kMaxRows rows. On a RING layer two rows of one sequence may map to
-  // the same slot; such rows go to separate launches in row order, so the later store wins as
-  // with sequential KvCache.store calls.
-  const uint32_t ring = kv->ring[lc.layer];
+  // the same device slot (position % the physical capacity); such rows go to separate launches
+  // in row order, so the later store wins as with sequential KvCache.store calls.
+  const uint32_t ring = kv->ring[lc.layer] ? kv->cap[lc.layer] : 0u;
   std::vector<uint64_t> slots_in_launch;
   uint32_t base = 0;
   while (base < count) {
@@ -519,10 +526,10 @@ void append_rows(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall
   for (uint32_t i = 0; i < count; ++i) kv->mark(sequences[i], lc.layer, positions[i]);
 }
 
-void check_decode_shape(const jmodels_attn_kv* kv) {
-  require(jma::decode_supported(kv->f16(), (int)kv->dk, (int)kv->dv), JMODELS_ATTN_INVALID_SHAPE,
-          "unsupported head dims for decode: key_length " + std::to_string(kv->dk) +
-              ", value_length " + std::to_string(kv->dv));
+void check_decode_shape(const jmodels_attn_kv* kv, const LayerCall& lc) {
+  require(jma::decode_supported(kv->f16(), (int)lc.dk, (int)lc.dv), JMODELS_ATTN_INVALID_SHAPE,
+          "unsupported head dims for decode: key_length " + std::to_string(lc.dk) +
+              ", value_length " + std::to_string(lc.dv));
 }
 
 // Causal attention of rows start .. start+n-1 whose K/V are cached and whose rotated queries are
@@ -531,9 +538,9 @@ void check_decode_shape(const jmodels_attn_kv* kv) {
 // decode kernel over chunks of listed rows.
 void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
                         uint32_t sequence, uint32_t start, uint32_t n, const float* q, float* out) {
-  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
-  const uint64_t odim = (uint64_t)lc.num_heads * kv->dv;
-  if (kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv)) {
+  const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk;
+  const uint64_t odim = (uint64_t)lc.num_heads * lc.dv;
+  if (kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv)) {
     jma::PrefillArgs a{};
     a.kv = kv->view(lc.layer);
     a.q = q;
@@ -545,12 +552,12 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.seq = sequence;
     a.window = lc.window;
     a.num_heads = lc.num_heads;
-    a.num_kv_heads = kv->hkv;
+    a.num_kv_heads = lc.hkv;
     a.group = lc.group;
     a.heads_per_stripe = std::min<uint32_t>(lc.group, 32);
     a.rows_per_stripe = 32 / a.heads_per_stripe;
     a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
-    const jma::PrefillPlan plan = jma::plan_prefill(a, (int)kv->dk, ctx->prefill_split_tiles, ctx->cus);
+    const jma::PrefillPlan plan = jma::plan_prefill(a, (int)lc.dk, ctx->prefill_split_tiles, ctx->cus);
     a.row_blocks = plan.row_blocks;
     a.split_blocks = plan.split_blocks;
     if (plan.pairs > 0) {
@@ -561,10 +568,10 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
       a.part = (float*)ctx->pf_part.ptr;
       a.tickets = (uint32_t*)ctx->pf_tickets.ptr;
     }
-    hip_check(jma::launch_prefill(a, (int)kv->dk, (int)kv->dv, ctx->stream), "prefill launch");
+    hip_check(jma::launch_prefill(a, (int)lc.dk, (int)lc.dv, ctx->stream), "prefill launch");
     return;
   }
-  check_decode_shape(kv);
+  check_decode_shape(kv, lc);
   for (uint32_t base = 0; base < n; base += jma::kMaxRows) {
     const uint32_t m = std::min<uint32_t>(jma::kMaxRows, n - base);
     jma::RowList rows{};
@@ -595,8 +602,8 @@ void validate_causal(const jmodels_attn_kv* kv, const LayerCall& lc, uint32_t se
 void prefill_impl(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCall& lc,
                   uint32_t sequence, uint32_t start, uint32_t n, const float* q, const float* k,
                   const float* v, float* out) {
-  const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk;
-  if (!(kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv))) check_decode_shape(kv);
+  const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk;
+  if (!(kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv))) check_decode_shape(kv, lc);
   validate_causal(kv, lc, sequence, start, n, false);
   ctx->qrot.reserve((size_t)n * qdim * sizeof(float), ctx->stream, "prefill rotated queries");
   // One launch appends every row: consecutive positions of one sequence need no row table.
@@ -867,77 +874,107 @@ int32_t jmodels_attn_norm_destroy(jmodels_attn_norm* norm) {
   });
 }
 
+// Creates a cache from per-layer specs (LayeredKvCache(maxSeqLen, LayerSpec[]),
+// BJ/cache/LayeredKvCache.java:35-64, 124-156): per layer its kv heads, key and value lengths and
+// ring capacity (0 = LINEAR). A RING layer keeps the reference's retention in the host
+// bookkeeping (slot = position % ring, a newer position evicts the one ring positions before it)
+// while its device storage rounds the ring up to a multiple of 32 slots (the kernels' 32-row
+// tiles then never wrap inside a tile); the device slot of a position is position % that
+// physical capacity, which holds every position the logical ring retains.
+static void create_layered(jmodels_attn_context* ctx, uint32_t sequences, uint32_t num_layers,
+                           uint32_t max_seq_len, const jmodels_attn_layer_spec* specs,
+                           uint32_t dtype, jmodels_attn_kv** kv_out) {
+  check_ctx(ctx);
+  require(kv_out != nullptr && specs != nullptr, JMODELS_ATTN_NULL_POINTER, "kv_out or specs is null");
+  *kv_out = nullptr;
+  require(sequences > 0 && num_layers > 0 && max_seq_len > 0, JMODELS_ATTN_INVALID_SHAPE,
+          "cache dimensions must be > 0");
+  require(dtype == JMODELS_ATTN_KV_F32 || dtype == JMODELS_ATTN_KV_F16, JMODELS_ATTN_INVALID_SHAPE,
+          "dtype must be JMODELS_ATTN_KV_F32 or JMODELS_ATTN_KV_F16");
+  auto kv = std::make_unique<jmodels_attn_kv>();
+  kv->ctx = ctx;
+  kv->sequences = sequences;
+  kv->layers = num_layers;
+  kv->max_seq_len = max_seq_len;
+  kv->dtype = dtype;
+  kv->hkv_l.assign(num_layers, 0);
+  kv->dk_l.assign(num_layers, 0);
+  kv->dv_l.assign(num_layers, 0);
+  kv->ring.assign(num_layers, 0);
+  kv->cap.assign(num_layers, 0);
+  kv->layer_off_k.assign(num_layers, 0);
+  kv->layer_off_v.assign(num_layers, 0);
+  uint64_t off_k = 0, off_v = 0;
+  for (uint32_t l = 0; l < num_layers; ++l) {
+    const jmodels_attn_layer_spec& sp = specs[l];
+    const std::string at = " (layer " + std::to_string(l) + ")";
+    require(sp.num_kv_heads > 0 && sp.key_length > 0 && sp.value_length > 0,
+            JMODELS_ATTN_INVALID_SHAPE, "layer dimensions must be > 0" + at);
+    require(sp.key_length % 16 == 0 && sp.value_length % 16 == 0, JMODELS_ATTN_INVALID_SHAPE,
+            "key_length and value_length must be multiples of 16" + at);
+    require(sp.num_kv_heads <= 4096 && sp.key_length <= 4096 && sp.value_length <= 4096,
+            JMODELS_ATTN_INVALID_SHAPE, "layer dimensions exceed 4096" + at);
+    kv->hkv_l[l] = sp.num_kv_heads;
+    kv->dk_l[l] = sp.key_length;
+    kv->dv_l[l] = sp.value_length;
+    uint32_t r = sp.ring_capacity;
+    // LayeredKvCache physicalLimit = min(ringCapacity, maxSeqLen) (cache/LayeredKvCache.java:128-129);
+    // a ring at least as long as the context never wraps, so it is stored linearly.
+    if (r >= max_seq_len) r = 0;
+    kv->ring[l] = r;
+    kv->cap[l] = (uint32_t)round_up(r ? r : max_seq_len, 32);
+    kv->layer_off_k[l] = off_k;
+    kv->layer_off_v[l] = off_v;
+    off_k += (uint64_t)sp.num_kv_heads * kv->cap[l] * sp.key_length;
+    off_v += (uint64_t)sp.num_kv_heads * kv->cap[l] * sp.value_length;
+  }
+  kv->seq_stride_k = off_k;
+  kv->seq_stride_v = off_v;
+  const uint64_t kbytes = off_k * sequences * kv->elem();
+  const uint64_t vbytes = off_v * sequences * kv->elem();
+  kv->bytes = kbytes + vbytes;
+  set_device(ctx);
+  hip_check(hipMalloc(&kv->d_k, kbytes), "hipMalloc K cache");
+  if (hipMalloc(&kv->d_v, vbytes) != hipSuccess) {
+    (void)hipFree(kv->d_k);
+    fail(JMODELS_ATTN_DEVICE_ERROR, "hipMalloc V cache failed");
+  }
+  // Zero fill: rows past a sequence's end are masked, and zeros keep 0 * V finite.
+  hip_check(hipMemsetAsync(kv->d_k, 0, kbytes, ctx->stream), "zero K cache");
+  hip_check(hipMemsetAsync(kv->d_v, 0, vbytes, ctx->stream), "zero V cache");
+  hip_check(hipStreamSynchronize(ctx->stream), "zero cache");
+  const size_t n = (size_t)sequences * num_layers;
+  kv->populated.resize(n);
+  kv->positions.resize(n);
+  kv->contiguous_end.assign(n, 0);
+  for (uint32_t s = 0; s < sequences; ++s)
+    for (uint32_t l = 0; l < num_layers; ++l) {
+      if (kv->ring[l]) kv->positions[kv->idx(s, l)].assign(kv->ring[l], -1);
+      else kv->populated[kv->idx(s, l)].assign((max_seq_len + 63) / 64, 0);
+    }
+  *kv_out = kv.release();
+}
+
 int32_t jmodels_attn_kv_create(jmodels_attn_context* ctx, uint32_t sequences, uint32_t num_layers,
                                uint32_t max_seq_len, uint32_t num_kv_heads, uint32_t key_length,
                                uint32_t value_length, uint32_t dtype,
                                const uint32_t* ring_capacity, jmodels_attn_kv** kv_out) {
   return guard([&] {
-    check_ctx(ctx);
-    require(kv_out != nullptr, JMODELS_ATTN_NULL_POINTER, "kv_out is null");
-    *kv_out = nullptr;
-    require(sequences > 0 && num_layers > 0 && max_seq_len > 0 && num_kv_heads > 0 &&
-                key_length > 0 && value_length > 0,
-            JMODELS_ATTN_INVALID_SHAPE, "cache dimensions must be > 0");
-    require(dtype == JMODELS_ATTN_KV_F32 || dtype == JMODELS_ATTN_KV_F16, JMODELS_ATTN_INVALID_SHAPE,
-            "dtype must be JMODELS_ATTN_KV_F32 or JMODELS_ATTN_KV_F16");
-    require(key_length % 16 == 0 && value_length % 16 == 0, JMODELS_ATTN_INVALID_SHAPE,
-            "key_length and value_length must be multiples of 16");
-    auto kv = std::make_unique<jmodels_attn_kv>();
-    kv->ctx = ctx;
-    kv->sequences = sequences;
-    kv->layers = num_layers;
-    kv->max_seq_len = max_seq_len;
-    kv->hkv = num_kv_heads;
-    kv->dk = key_length;
-    kv->dv = value_length;
-    kv->dtype = dtype;
-    const uint32_t blk = (uint32_t)jma::v_block(dtype == JMODELS_ATTN_KV_F16);
-    kv->ring.assign(num_layers, 0);
-    kv->cap.assign(num_layers, 0);
-    kv->layer_off_k.assign(num_layers, 0);
-    kv->layer_off_v.assign(num_layers, 0);
-    uint64_t off_k = 0, off_v = 0;
-    for (uint32_t l = 0; l < num_layers; ++l) {
-      uint32_t r = ring_capacity ? ring_capacity[l] : 0;
-      // LayeredKvCache physicalLimit = min(ringCapacity, maxSeqLen) (cache/LayeredKvCache.java:128-129);
-      // a ring at least as long as the context never wraps, so it is stored linearly.
-      if (r >= max_seq_len) r = 0;
-      require(r % 32 == 0, JMODELS_ATTN_INVALID_SHAPE,
-              "ring capacity must be a multiple of 32: " + std::to_string(r));
-      kv->ring[l] = r;
-      kv->cap[l] = r ? r : (uint32_t)round_up(max_seq_len, 32);
-      (void)blk;
-      kv->layer_off_k[l] = off_k;
-      kv->layer_off_v[l] = off_v;
-      off_k += (uint64_t)num_kv_heads * kv->cap[l] * key_length;
-      off_v += (uint64_t)num_kv_heads * kv->cap[l] * value_length;
-    }
-    kv->seq_stride_k = off_k;
-    kv->seq_stride_v = off_v;
-    const uint64_t kbytes = off_k * sequences * kv->elem();
-    const uint64_t vbytes = off_v * sequences * kv->elem();
-    kv->bytes = kbytes + vbytes;
-    set_device(ctx);
-    hip_check(hipMalloc(&kv->d_k, kbytes), "hipMalloc K cache");
-    if (hipMalloc(&kv->d_v, vbytes) != hipSuccess) {
-      (void)hipFree(kv->d_k);
-      fail(JMODELS_ATTN_DEVICE_ERROR, "hipMalloc V cache failed");
-    }
-    // Zero fill: rows past a sequence's end are masked, and zeros keep 0 * V finite.
-    hip_check(hipMemsetAsync(kv->d_k, 0, kbytes, ctx->stream), "zero K cache");
-    hip_check(hipMemsetAsync(kv->d_v, 0, vbytes, ctx->stream), "zero V cache");
-    hip_check(hipStreamSynchronize(ctx->stream), "zero cache");
-    const size_t n = (size_t)sequences * num_layers;
-    kv->populated.resize(n);
-    kv->positions.resize(n);
-    kv->contiguous_end.assign(n, 0);
-    for (uint32_t s = 0; s < sequences; ++s)
-      for (uint32_t l = 0; l < num_layers; ++l) {
-        if (kv->ring[l]) kv->positions[kv->idx(s, l)].assign(kv->ring[l], -1);
-        else kv->populated[kv->idx(s, l)].assign((max_seq_len + 63) / 64, 0);
-      }
-    *kv_out = kv.release();
+    require(num_layers > 0 && num_layers <= (1u << 20), JMODELS_ATTN_INVALID_SHAPE,
+            "num_layers must be in [1, 2^20]");
+    std::vector<jmodels_attn_layer_spec> specs(num_layers);
+    for (uint32_t l = 0; l < num_layers; ++l)
+      specs[l] = jmodels_attn_layer_spec{num_kv_heads, key_length, value_length,
+                                         ring_capacity ? ring_capacity[l] : 0u};
+    create_layered(ctx, sequences, num_layers, max_seq_len, specs.data(), dtype, kv_out);
   });
+}
+
+int32_t jmodels_attn_kv_create_layered(jmodels_attn_context* ctx, uint32_t sequences,
+                                       uint32_t num_layers, uint32_t max_seq_len,
+                                       const jmodels_attn_layer_spec* specs, uint32_t dtype,
+                                       jmodels_attn_kv** kv_out) {
+  return guard([&] { create_layered(ctx, sequences, num_layers, max_seq_len, specs, dtype, kv_out); });
 }
 
 int32_t jmodels_attn_kv_destroy(jmodels_attn_kv* kv) {
@@ -1017,15 +1054,11 @@ int32_t jmodels_attn_kv_store(jmodels_attn_context* ctx, jmodels_attn_kv* kv, ui
     require(sequence < kv->sequences, JMODELS_ATTN_OUT_OF_RANGE, "sequence out of range");
     require(position < kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
             "position out of range: " + std::to_string(position));
-    const uint64_t kdim = (uint64_t)kv->hkv * kv->dk, vdim = (uint64_t)kv->hkv * kv->dv;
+    const uint32_t hkv = kv->hkv_l[layer], key_len = kv->dk_l[layer], value_len = kv->dv_l[layer];
+    const uint64_t kdim = (uint64_t)hkv * key_len, vdim = (uint64_t)hkv * value_len;
     check_elems(key_elements, kdim, "key");
     check_elems(value_elements, vdim, "value");
     set_device(ctx);
-    LayerCall lc{};
-    lc.layer = layer;
-    lc.num_heads = kv->hkv;
-    lc.group = 1;
-    lc.rope = nullptr;
     float* dk = stage(ctx->stage_k, key, kdim, ctx->stream);
     float* dv = stage(ctx->stage_v, value, vdim, ctx->stream);
     // q is unused by a store: point it at k with zero query heads' worth of work.
@@ -1036,10 +1069,10 @@ int32_t jmodels_attn_kv_store(jmodels_attn_context* ctx, jmodels_attn_kv* kv, ui
     a.k = dk;
     a.v = dv;
     a.num_heads = 0;
-    a.num_kv_heads = kv->hkv;
-    a.dk = kv->dk;
-    a.dv = kv->dv;
-    a.blocks_per_row = append_blocks_per_row(0, kv);
+    a.num_kv_heads = hkv;
+    a.dk = key_len;
+    a.dv = value_len;
+    a.blocks_per_row = append_blocks_per_row(0, hkv, key_len, value_len);
     a.rows = rows;
     hip_check(jma::launch_append(a, kv->f16(), ctx->stream), "store launch");
     hip_check(hipStreamSynchronize(ctx->stream), "store");
@@ -1059,21 +1092,20 @@ int32_t jmodels_attn_kv_read(jmodels_attn_context* ctx, const jmodels_attn_kv* k
     require(from <= to && to <= kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
             "invalid position range: [" + std::to_string(from) + ", " + std::to_string(to) + ")");
     const uint32_t n = to - from;
-    const uint64_t kdim = (uint64_t)kv->hkv * kv->dk, vdim = (uint64_t)kv->hkv * kv->dv;
+    const uint32_t hkv = kv->hkv_l[layer], key_len = kv->dk_l[layer], value_len = kv->dv_l[layer];
+    const uint64_t kdim = (uint64_t)hkv * key_len, vdim = (uint64_t)hkv * value_len;
     if (keys) check_elems(key_elements, n * kdim, "keys");
     if (values) check_elems(value_elements, n * vdim, "values");
     if (n == 0) return;
-    for (uint32_t p = from; p < to; ++p) {
-      if (!kv->available(sequence, layer, p))
-        fail(JMODELS_ATTN_UNAVAILABLE, "cache position " + std::to_string(p) + " for layer " +
-                                           std::to_string(layer) + " is not populated");
-    }
+    // A ring layer rejects a range wider than its capacity before it looks at positions
+    // (LayeredKvCache.attentionView, cache/LayeredKvCache.java:178-197).
+    kv->require_range(sequence, layer, from, to - 1);
     set_device(ctx);
     hip_check(hipStreamSynchronize(ctx->stream), "read");
     const size_t es = kv->elem();
     const uint32_t cap = kv->cap[layer];
     const uint32_t blk = (uint32_t)jma::v_block(kv->f16());
-    const uint64_t kl = (uint64_t)kv->hkv * cap * kv->dk, vl = (uint64_t)kv->hkv * cap * kv->dv;
+    const uint64_t kl = (uint64_t)hkv * cap * key_len, vl = (uint64_t)hkv * cap * value_len;
     std::vector<unsigned char> hk(kl * es), hv(vl * es);
     const unsigned char* kbase = (const unsigned char*)kv->d_k +
                                  (sequence * kv->seq_stride_k + kv->layer_off_k[layer]) * es;
@@ -1095,15 +1127,15 @@ int32_t jmodels_attn_kv_read(jmodels_attn_context* ctx, const jmodels_attn_kv* k
       const uint32_t slot = kv->ring[layer] ? p % cap : p;
       const uint32_t r = slot % blk, b = slot / blk;
       const uint32_t s = kv->f16() ? 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u) : r;
-      for (uint32_t h = 0; h < kv->hkv; ++h) {
+      for (uint32_t h = 0; h < hkv; ++h) {
         if (keys)
-          for (uint32_t d = 0; d < kv->dk; ++d)
-            keys[(uint64_t)(p - from) * kdim + h * kv->dk + d] =
-                widen(hk.data(), ((uint64_t)h * cap + slot) * kv->dk + d);
+          for (uint32_t d = 0; d < key_len; ++d)
+            keys[(uint64_t)(p - from) * kdim + h * key_len + d] =
+                widen(hk.data(), ((uint64_t)h * cap + slot) * key_len + d);
         if (values)
-          for (uint32_t d = 0; d < kv->dv; ++d)
-            values[(uint64_t)(p - from) * vdim + h * kv->dv + d] =
-                widen(hv.data(), (uint64_t)h * cap * kv->dv + ((uint64_t)b * kv->dv + d) * blk + s);
+          for (uint32_t d = 0; d < value_len; ++d)
+            values[(uint64_t)(p - from) * vdim + h * value_len + d] =
+                widen(hv.data(), (uint64_t)h * cap * value_len + ((uint64_t)b * value_len + d) * blk + s);
       }
     }
   });
@@ -1135,10 +1167,10 @@ static int32_t append_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
     const LayerCall lc = resolve_layer(kv, layer);
     check_rows(kv, lc, count, sequences, positions);
     require(q && k && v, JMODELS_ATTN_NULL_POINTER, "q/k/v are null");
-    const uint64_t qn = (uint64_t)count * lc.num_heads * kv->dk;
+    const uint64_t qn = (uint64_t)count * lc.num_heads * lc.dk;
     check_elems(q_elements, qn, "q");
-    check_elems(k_elements, (uint64_t)count * kv->hkv * kv->dk, "k");
-    check_elems(v_elements, (uint64_t)count * kv->hkv * kv->dv, "v");
+    check_elems(k_elements, (uint64_t)count * lc.hkv * lc.dk, "k");
+    check_elems(v_elements, (uint64_t)count * lc.hkv * lc.dv, "v");
     if (q_rotated) check_elems(q_rotated_elements, qn, "q_rotated");
     set_device(ctx);
     if (device) {
@@ -1146,8 +1178,8 @@ static int32_t append_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
       return;
     }
     const float* dq = stage(ctx->stage_q, q, qn, ctx->stream);
-    const float* dk = stage(ctx->stage_k, k, (uint64_t)count * kv->hkv * kv->dk, ctx->stream);
-    const float* dv = stage(ctx->stage_v, v, (uint64_t)count * kv->hkv * kv->dv, ctx->stream);
+    const float* dk = stage(ctx->stage_k, k, (uint64_t)count * lc.hkv * lc.dk, ctx->stream);
+    const float* dv = stage(ctx->stage_v, v, (uint64_t)count * lc.hkv * lc.dv, ctx->stream);
     float* dqo = q_rotated ? stage<float>(ctx->stage_out, nullptr, qn, ctx->stream) : nullptr;
     append_rows(ctx, kv, lc, count, sequences, positions, dq, dk, dv, dqo);
     if (q_rotated)
@@ -1163,12 +1195,12 @@ static int32_t attend_entry(bool device, jmodels_attn_context* ctx, const jmodel
                             uint64_t q_elements, float* out, uint64_t out_elements) {
   return guard([&] {
     common_checks(ctx, kv);
-    check_decode_shape(kv);
     const LayerCall lc = resolve_layer(kv, layer);
+    check_decode_shape(kv, lc);
     check_rows(kv, lc, count, sequences, positions);
     require(q && out, JMODELS_ATTN_NULL_POINTER, "q/out are null");
-    const uint64_t qn = (uint64_t)count * lc.num_heads * kv->dk;
-    const uint64_t on = (uint64_t)count * lc.num_heads * kv->dv;
+    const uint64_t qn = (uint64_t)count * lc.num_heads * lc.dk;
+    const uint64_t on = (uint64_t)count * lc.num_heads * lc.dv;
     check_elems(q_elements, qn, "q");
     check_elems(out_elements, on, "out");
     validate_attend_ranges(kv, lc, count, sequences, positions);
@@ -1196,14 +1228,14 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
                             uint64_t out_elements, const jma::FixedScratch* fixed = nullptr) {
   return guard([&] {
     common_checks(ctx, kv);
-    check_decode_shape(kv);
     const LayerCall lc = resolve_layer(kv, layer);
+    check_decode_shape(kv, lc);
     check_rows(kv, lc, count, sequences, positions);
     require(q && k && v && out, JMODELS_ATTN_NULL_POINTER, "q/k/v/out are null");
-    const uint64_t qn = (uint64_t)count * lc.num_heads * kv->dk;
-    const uint64_t kn = (uint64_t)count * kv->hkv * kv->dk;
-    const uint64_t vn = (uint64_t)count * kv->hkv * kv->dv;
-    const uint64_t on = (uint64_t)count * lc.num_heads * kv->dv;
+    const uint64_t qn = (uint64_t)count * lc.num_heads * lc.dk;
+    const uint64_t kn = (uint64_t)count * lc.hkv * lc.dk;
+    const uint64_t vn = (uint64_t)count * lc.hkv * lc.dv;
+    const uint64_t on = (uint64_t)count * lc.num_heads * lc.dv;
     check_elems(q_elements, qn, "q");
     check_elems(k_elements, kn, "k");
     check_elems(v_elements, vn, "v");
@@ -1235,8 +1267,8 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
     }
     if (can_fuse_decode(ctx, lc)) {
       // One launch per chunk of rows: RoPE, append, attention and the split reduction.
-      const uint64_t qdim = (uint64_t)lc.num_heads * kv->dk, kdim = (uint64_t)kv->hkv * kv->dk;
-      const uint64_t vdim = (uint64_t)kv->hkv * kv->dv, odim = (uint64_t)lc.num_heads * kv->dv;
+      const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk, kdim = (uint64_t)lc.hkv * lc.dk;
+      const uint64_t vdim = (uint64_t)lc.hkv * lc.dv, odim = (uint64_t)lc.num_heads * lc.dv;
       for (uint32_t base = 0; base < count; base += jma::kMaxRows) {
         const uint32_t n = std::min<uint32_t>(jma::kMaxRows, count - base);
         jma::RowList rows = make_rows(n, sequences + base, positions + base);
@@ -1284,10 +1316,10 @@ static int32_t prefill_entry(bool device, jmodels_attn_context* ctx, jmodels_att
       require((uint64_t)start + n <= lc.rope->max_positions, JMODELS_ATTN_OUT_OF_RANGE,
               "positions beyond the rope table");
     require(q && k && v && out, JMODELS_ATTN_NULL_POINTER, "q/k/v/out are null");
-    const uint64_t qn = (uint64_t)n * lc.num_heads * kv->dk;
-    const uint64_t kn = (uint64_t)n * kv->hkv * kv->dk;
-    const uint64_t vn = (uint64_t)n * kv->hkv * kv->dv;
-    const uint64_t on = (uint64_t)n * lc.num_heads * kv->dv;
+    const uint64_t qn = (uint64_t)n * lc.num_heads * lc.dk;
+    const uint64_t kn = (uint64_t)n * lc.hkv * lc.dk;
+    const uint64_t vn = (uint64_t)n * lc.hkv * lc.dv;
+    const uint64_t on = (uint64_t)n * lc.num_heads * lc.dv;
     check_elems(q_elements, qn, "q");
     check_elems(k_elements, kn, "k");
     check_elems(v_elements, vn, "v");
@@ -1320,11 +1352,11 @@ static int32_t attend_causal_entry(bool device, jmodels_attn_context* ctx,
     require((uint64_t)start + n <= kv->max_seq_len, JMODELS_ATTN_OUT_OF_RANGE,
             "position out of range: " + std::to_string((uint64_t)start + n - 1));
     require(q && out, JMODELS_ATTN_NULL_POINTER, "q/out are null");
-    const uint64_t qn = (uint64_t)n * lc.num_heads * kv->dk;
-    const uint64_t on = (uint64_t)n * lc.num_heads * kv->dv;
+    const uint64_t qn = (uint64_t)n * lc.num_heads * lc.dk;
+    const uint64_t on = (uint64_t)n * lc.num_heads * lc.dv;
     check_elems(q_elements, qn, "q");
     check_elems(out_elements, on, "out");
-    if (!(kv->f16() && jma::prefill_supported((int)kv->dk, (int)kv->dv))) check_decode_shape(kv);
+    if (!(kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv))) check_decode_shape(kv, lc);
     validate_causal(kv, lc, sequence, start, n, true);
     set_device(ctx);
     if (device) {

@@ -158,6 +158,11 @@ int main() {
   cases.push_back({"128 rows, target 100000", ragged(128, 544, 544, 1), 0, 8, 4, 256, 256, true, 100000, 1, false, 0});
   cases.push_back({"single position 0", {0}, 0, 1, 1, 16, 16, false, 512, 1, false, 0});
   cases.push_back({"1M context MQA d128", {1048575}, 0, 1, 8, 128, 128, true, 512, 1, false, 0});
+  // Gemma-4 layer shapes: full layers d 512 (2 kv heads, LINEAR), sliding d 256 on a ring of
+  // window + chunk that is not a multiple of 32 (stored in round_up(356, 32) = 384 slots).
+  cases.push_back({"Gemma-4 full d512 2 sessions", {602, 252}, 0, 2, 4, 512, 512, true, 512, 1, false, 0});
+  cases.push_back({"Gemma-4 full d512 f32 8k", {8191}, 0, 2, 16, 512, 512, false, 512, 1, false, 0});
+  cases.push_back({"Gemma-4 sliding ring 356 w256", {602, 252}, 256, 4, 2, 256, 256, true, 512, 1, false, 384});
   for (const Case& c : cases) check(c);
   printf("ok\n");
   return 0;
