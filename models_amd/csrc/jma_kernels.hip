@@ -1145,10 +1145,10 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 
 // One workgroup of 16 waves per (row, query head, 64-element chunk of the head's output): out =
 // sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to kMaxWideSplits.
-// Thread t loads split t's (m, l): one round trip for all of them; the workgroup agrees on M and
-// on the weights 2^(m_s - M) (kept in LDS) and sums l in a fixed tree. Wave w then sums its
-// splits w, w + 16, ... in order, with all of their loads issued before the first is used, and
-// the sixteen sums are added in wave order: the result is the same on every run for a plan.
+// Thread t loads split t's (m, l) and wave w the chunk of its splits w, w + 16, ..., all in one
+// round trip; the workgroup agrees on M and on the weights 2^(m_s - M) (kept in LDS) and sums l
+// in a fixed tree. Wave w then sums its splits in order, and the sixteen sums are added in wave
+// order: the result is the same on every run for a plan.
 template <int DV>
 __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
   constexpr uint32_t kChunks = (DV + 63) / 64;
@@ -1169,9 +1169,20 @@ __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
                                     kvh * a.hgroups + hg, ns);
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  // Weights: thread t takes split t.
+  // Every load is issued before any is used: thread t's split-t (m, l), and the chunk elements
+  // of wave w's splits w, w + 16, ...; the two sets need one memory round trip together.
   float2 ml = {-INFINITY, 0.0f};
   if (tid < ns) ml = *(const float2*)(a.part_ml + sep_ml_float(base + tid, c16));
+  const uint32_t d = chunk * 64 + lane;
+  const uint32_t dl = d < DV ? d : DV - 1;  // lanes past the head load a valid element
+  float xv[kAhead];
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i) {
+    const uint32_t sp = wave + kWaves * i;
+    xv[i] = sp < ns ? a.part_acc[sep_acc_float(base + sp, c16, DV, dl)] : 0.0f;
+  }
+
+  // Weights: thread t takes split t.
   float mw = ml.x;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
@@ -1189,15 +1200,7 @@ __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
   if (lane == 0) s_l[wave] = lw;
   __syncthreads();
 
-  // Weighted sums of this chunk: wave w takes splits w, w + 16, ...
-  const uint32_t d = chunk * 64 + lane;
-  const uint32_t dl = d < DV ? d : DV - 1;  // lanes past the head load a valid element
-  float xv[kAhead];
-#pragma unroll
-  for (int i = 0; i < kAhead; ++i) {
-    const uint32_t sp = wave + kWaves * i;
-    xv[i] = sp < ns ? a.part_acc[sep_acc_float(base + sp, c16, DV, dl)] : 0.0f;
-  }
+  // Weighted sums of this chunk: wave w takes splits w, w + 16, ... in order.
   float X = 0.0f;
 #pragma unroll
   for (int i = 0; i < kAhead; ++i) {
