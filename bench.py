@@ -486,6 +486,65 @@ def run_c5(hip, A, rt, synth, steps: int = 64, warmup: int = 4):
                 us_per_token=elapsed / steps * 1e6, gbs=nbytes / elapsed / 1e9)
 
 
+def _gguf_weights(synth, fmt: int, rows: int, cols: int, key: str) -> np.ndarray:
+    """Synthetic GGUF blocks: uniform bytes with an f16 N(0, 0.02) scale per block."""
+    nbytes = 18 if fmt == 0 else 34
+    blocks = cols // 32
+    raw = synth.uniform_int(9, key, rows * blocks * nbytes, 0, 255).astype(np.uint8)
+    raw = raw.reshape(rows, blocks, nbytes)
+    scales = (synth.normal(9, key + "/s", (rows, blocks)) * 0.02).astype(np.float16)
+    raw[:, :, :2] = scales.view(np.uint8).reshape(rows, blocks, 2)
+    return raw.reshape(-1)
+
+
+def run_proj(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
+    """The projections around one C2 layer at decode (batch 1): Llama-3.2-1B's Q (2048 rows), K
+    and V (512 rows each) over 2048 inputs as one grouped launch writing q|k|v for the decode,
+    and the output projection (2048 x 2048) with the residual added in place; Q4_0 and Q8_0
+    weights. Each launch is repeated `per_graph` times in a graph; HIP events around the replays
+    give us per launch; GB/s counts the weight bytes (the activations are 8 KB)."""
+    cols, rows = 2048, [2048, 512, 512]
+    stream = hip.stream()
+    result = {}
+    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0)):
+        ws = [_gguf_weights(synth, fmt, r, cols, f"bench/proj/{name}/{i}") for i, r in enumerate(rows)]
+        wo = _gguf_weights(synth, fmt, cols, cols, f"bench/proj/{name}/wo")
+        dws = [rt.DeviceArray.from_host(w) for w in ws]
+        dwo = rt.DeviceArray.from_host(wo)
+        dx = rt.DeviceArray.from_host(synth.normal(9, "bench/proj/x", (cols,)))
+        dqkv = rt.DeviceArray(sum(rows))
+        dres = rt.DeviceArray.from_host(synth.normal(9, "bench/proj/res", (cols,)))
+
+        def qkv():
+            for _ in range(per_graph):
+                hip.quantized_grouped_matmul_device([fmt] * 3, [d.ptr for d in dws],
+                                                    [w.size for w in ws], rows, dx.ptr, cols,
+                                                    dqkv.ptr, sum(rows), 1, cols)
+
+        def out_proj():
+            for _ in range(per_graph):
+                hip.quantized_matmul_device(fmt, dwo.ptr, wo.size, dqkv.ptr, cols, dres.ptr, cols,
+                                            1, cols, cols, dres.ptr, A.ADDEND_RESIDUAL)
+
+        for label, fn, nbytes in (("qkv", qkv, sum(w.size for w in ws)), ("wo_residual", out_proj, wo.size)):
+            graph = rt.Graph(stream, fn)
+            graph.launch()
+            hip.synchronize()
+            e0, e1 = rt.Event(), rt.Event()
+            e0.record(stream)
+            for _ in range(reps):
+                graph.launch()
+            e1.record(stream)
+            hip.synchronize()
+            ms = e0.elapsed_ms(e1) / (reps * per_graph)
+            graph.destroy()
+            result[f"{label}_{name}"] = dict(us=round(ms * 1e3, 3), weight_bytes=int(nbytes),
+                                              gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+        for d in dws + [dwo, dx, dqkv, dres]:
+            d.free()
+    return result
+
+
 def cpu_baseline_c2(material, budget_s: float):
     """backend-java's decode attention restated in C (oracle/), one thread, on repeated C2
     layer-steps at the last decoded position until about budget_s seconds of CPU work ran."""
@@ -541,6 +600,10 @@ def main() -> int:
     ap.add_argument("--no-c1", action="store_true", help="skip the C1 f32 decode-step figure")
     ap.add_argument("--no-c4", action="store_true", help="skip the C4 ragged decode figure")
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 long-context decode figure")
+    ap.add_argument("--no-proj", action="store_true",
+                    help="skip the Q4_0 / Q8_0 projection figures")
+    ap.add_argument("--proj-only", action="store_true",
+                    help="profiling aid: run only the projection measurements, print their figures")
     ap.add_argument("--c5-only", action="store_true",
                     help="profiling aid: run only the C5 long-context decode measurement")
     ap.add_argument("--c4-only", action="store_true",
@@ -594,6 +657,9 @@ def main() -> int:
         print(json.dumps({"prefill_us": round(c3["ms"] * 1e3, 2), "tflops": round(c3["tflops"], 2),
                           "flops": c3["flops"]}), flush=True)
         return 0
+    if args.proj_only:
+        print(json.dumps(run_proj(hip, A, rt, synth)), flush=True)
+        return 0
     if args.c5_only:
         c5 = run_c5(hip, A, rt, synth)
         print(json.dumps({"c5_us_per_token": round(c5["us_per_token"], 2), "gbs": round(c5["gbs"], 1),
@@ -624,6 +690,11 @@ def main() -> int:
     if not args.no_c5:
         c5 = run_c5(hip, A, rt, synth)
         log(f"C5 long-context decode: {c5['us_per_token']:.1f} us/token, {c5['gbs']:.0f} GB/s")
+    proj = None
+    if not args.no_proj:
+        proj = run_proj(hip, A, rt, synth)
+        log("projections (us, GB/s of weights): " + ", ".join(
+            f"{k} {v['us']:.2f} {v['gbs']:.0f}" for k, v in proj.items()))
     hip.close()
 
     value = c2["algo_bytes"] / c2["elapsed"] / 1e9
@@ -713,6 +784,13 @@ def main() -> int:
             "us_per_token": round(c5["us_per_token"], 2),
             "frac_of_hbm_peak": round(c5["gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_token": c5["bytes"] // c5["steps"],
+        }
+    if proj is not None:
+        result["projections"] = {
+            "workload": "Llama-3.2-1B layer at decode (batch 1): grouped Q/K/V projection (2048 -> "
+                        "2048 + 512 + 512) and output projection 2048 x 2048 plus residual, GGUF "
+                        "Q4_0 / Q8_0 weights, activations quantized to Q8_0 in the launch",
+            **proj,
         }
     if not args.no_cpu:
         cpu = cpu_baseline_c2(c2["cpu_material"], args.cpu_seconds)

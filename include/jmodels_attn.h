@@ -74,6 +74,7 @@ extern "C" {
 #define JMODELS_ATTN_CAP_DEVICE_POINTERS (1ull << 6) /* *_device entry points */
 #define JMODELS_ATTN_CAP_QK_NORM (1ull << 7)         /* per-head RMS norm of q and k before RoPE */
 #define JMODELS_ATTN_CAP_VALUE_NORM (1ull << 8)      /* unweighted per-head RMS norm of v (Gemma 4) */
+#define JMODELS_ATTN_CAP_QUANT_MATMUL (1ull << 9)    /* Q4_0 / Q8_0 projections on device memory */
 
 /* KV storage element types. F16 stores IEEE binary16 (round to nearest even), which widens to
  * exactly Float.float16ToFloat(Float.floatToFloat16(x)) — the reference's half-precision KV
@@ -329,6 +330,47 @@ JMODELS_ATTN_API int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, 
                                     uint64_t q_elements, const float* k, uint64_t k_elements,
                                     const float* v, uint64_t v_elements, float* out,
                                     uint64_t out_elements);
+
+/* ---------------------------------------------------------------- quantized projections
+ *
+ * The projections on either side of attention: Q/K/V before the append
+ * (BJ/llama/LlamaForwardPass.java:1043-1067, with addOptionalBias :1065-1067) and the output
+ * projection plus residual after it (:1131-1138). GGUF weight formats use backend-native's codes
+ * (RS:150-161): 0 = Q4_0 (18-byte blocks), 1 = Q8_0 (34-byte blocks) run here; its other codes
+ * (Q4_K, Q6_K, Q5_K, Q5_0) return INVALID_SHAPE. Activations are quantized to Q8_0 per 32-element
+ * block and every output is the in-order chain of per-block fma(weightScale * activationScale,
+ * integer dot, sum), the arithmetic backend-native's tests require of its Q4_0 kernel exactly
+ * (backend-native/src/test/java/.../NativeKernelLibraryTest.java:67-84, 909-1023).
+ *
+ * Device pointers, asynchronous on the context stream (capturable: no scratch memory). weights:
+ * [rows][cols / 32] blocks, 2-byte aligned; input [batch][cols] f32, 16-byte aligned, cols a
+ * multiple of 32; output [batch][rows] per matrix, matrix after matrix (a grouped Q/K/V call
+ * leaves q, k and v contiguous, the layout jmodels_attn_decode_device reads). addend_mode: 0 none,
+ * 1 a bias [rows] added to every batch row (addOptionalBias), 2 a residual [batch][rows] added
+ * (x[i] += attnProjected[i]; the residual may be the output itself, updated in place). output must
+ * not alias input. */
+#define JMODELS_ATTN_WEIGHTS_Q4_0 0u
+#define JMODELS_ATTN_WEIGHTS_Q8_0 1u
+#define JMODELS_ATTN_ADDEND_NONE 0u
+#define JMODELS_ATTN_ADDEND_BIAS 1u
+#define JMODELS_ATTN_ADDEND_RESIDUAL 2u
+
+/* jmodels_quantized_f32_batched_matmul_with_context (RS:535-580) on device memory, plus the
+ * addend. */
+JMODELS_ATTN_API int32_t jmodels_attn_quantized_matmul_device(jmodels_attn_context* ctx, uint32_t format,
+                                             const void* weights, uint64_t weight_bytes,
+                                             const float* input, uint64_t input_elements,
+                                             float* output, uint64_t output_elements,
+                                             uint32_t batch_size, uint32_t rows, uint32_t cols,
+                                             const float* addend, uint32_t addend_mode);
+/* jmodels_quantized_f32_grouped_batched_matmul_with_context (RS:582-637) on device memory: up to
+ * 16 matrices (1 allowed here) sharing one activation batch; addends (NULL with addend_mode 0)
+ * holds one pointer per matrix. */
+JMODELS_ATTN_API int32_t jmodels_attn_quantized_grouped_matmul_device(
+    jmodels_attn_context* ctx, const uint32_t* formats, const void* const* weights,
+    const uint64_t* weight_bytes, const uint32_t* rows, uint32_t matrix_count, const float* input,
+    uint64_t input_elements, float* output, uint64_t output_elements, uint32_t batch_size,
+    uint32_t cols, const float* const* addends, uint32_t addend_mode);
 
 #ifdef __cplusplus
 }

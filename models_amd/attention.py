@@ -58,6 +58,11 @@ NORM_VALUE_RMS = 1
 
 KV_F32 = 0
 KV_F16 = 1
+WEIGHTS_Q4_0 = 0
+WEIGHTS_Q8_0 = 1
+ADDEND_NONE = 0
+ADDEND_BIAS = 1
+ADDEND_RESIDUAL = 2
 
 EXPORTS = (
     "jmodels_attn_abi_version", "jmodels_attn_capabilities", "jmodels_attn_status_name",
@@ -71,7 +76,8 @@ EXPORTS = (
     "jmodels_attn_prefill_device", "jmodels_attn_attend_causal",
     "jmodels_attn_attend_causal_device", "jmodels_attn_norm_create", "jmodels_attn_norm_create_ex",
     "jmodels_attn_norm_destroy", "jmodels_attn_decode_device_noalloc",
-    "jmodels_attn_kv_create_layered",
+    "jmodels_attn_kv_create_layered", "jmodels_attn_quantized_matmul_device",
+    "jmodels_attn_quantized_grouped_matmul_device",
 )
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -128,6 +134,11 @@ def _declare(lib: ctypes.CDLL) -> None:
                                           ctypes.POINTER(_vp)]),
         "jmodels_attn_kv_create_layered": (_i32, [_vp, _u32, _u32, _u32, _vp, _u32, ctypes.POINTER(_vp)]),
         "jmodels_attn_kv_destroy": (_i32, [_vp]),
+        "jmodels_attn_quantized_matmul_device": (_i32, [_vp, _u32, _vp, _u64, _vp, _u64, _vp, _u64,
+                                                        _u32, _u32, _u32, _vp, _u32]),
+        "jmodels_attn_quantized_grouped_matmul_device": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _vp,
+                                                                _u64, _vp, _u64, _u32, _u32, _vp,
+                                                                _u32]),
         "jmodels_attn_kv_clear": (_i32, [_vp, _i32]),
         "jmodels_attn_kv_discard_from": (_i32, [_vp, _u32, _u32]),
         "jmodels_attn_kv_contains": (_i32, [_vp, _u32, _u32, _u32, ctypes.POINTER(_i32)]),
@@ -273,6 +284,56 @@ class HipAttentionLibrary:
         heads, head lengths and retention, as Gemma4KvCache builds them
         (gemma4/Gemma4KvCache.java:39-47)."""
         return HipKvCache(self, list(specs), max_seq_len, half_precision, sequences, uniform=False)
+
+
+    # ---- quantized projections (device pointers, asynchronous on the context stream)
+
+    def quantized_matmul_device(self, fmt: int, weights_ptr: int, weight_bytes: int, x_ptr: int,
+                                x_elems: int, out_ptr: int, out_elems: int, batch: int, rows: int,
+                                cols: int, addend_ptr: Optional[int] = None,
+                                addend_mode: int = ADDEND_NONE) -> None:
+        """jmodels_quantized_f32_batched_matmul_with_context on device memory (Q4_0 / Q8_0)."""
+        self.check(self.lib.jmodels_attn_quantized_matmul_device(
+            self.ctx, fmt, weights_ptr, weight_bytes, x_ptr, x_elems, out_ptr, out_elems, batch,
+            rows, cols, addend_ptr, addend_mode), "quantized_matmul_device")
+
+    def quantized_grouped_matmul_device(self, formats, weight_ptrs, weight_bytes, rows, x_ptr: int,
+                                        x_elems: int, out_ptr: int, out_elems: int, batch: int,
+                                        cols: int, addend_ptrs=None,
+                                        addend_mode: int = ADDEND_NONE) -> None:
+        """Q/K/V (or any up to 16 matrices) over one activation batch; outputs matrix after
+        matrix, each [batch][rows]."""
+        n = len(formats)
+        fm = (ctypes.c_uint32 * n)(*formats)
+        wp = (ctypes.c_void_p * n)(*weight_ptrs)
+        wb = (ctypes.c_uint64 * n)(*weight_bytes)
+        rw = (ctypes.c_uint32 * n)(*rows)
+        ad = (ctypes.c_void_p * n)(*addend_ptrs) if addend_ptrs is not None else None
+        self.check(self.lib.jmodels_attn_quantized_grouped_matmul_device(
+            self.ctx, fm, wp, wb, rw, n, x_ptr, x_elems, out_ptr, out_elems, batch, cols, ad,
+            addend_mode), "quantized_grouped_matmul_device")
+
+    def quantized_matmul(self, fmt: int, weights, x, batch: int, rows: int, cols: int,
+                         addend=None, addend_mode: int = ADDEND_NONE) -> np.ndarray:
+        """Host-buffer convenience over quantized_matmul_device: uploads the GGUF weight bytes,
+        the activations [batch][cols] and the addend, runs, returns out [batch, rows]."""
+        from models_amd import hip_runtime as rt
+        wb = np.frombuffer(bytes(weights), np.uint8) if isinstance(weights, (bytes, bytearray)) \
+            else np.ascontiguousarray(weights, np.uint8).reshape(-1)
+        xs = _f32(x)
+        dw, dx = rt.DeviceArray.from_host(wb), rt.DeviceArray.from_host(xs)
+        dout = rt.DeviceArray(batch * rows)
+        dadd = rt.DeviceArray.from_host(_f32(addend)) if addend is not None else None
+        try:
+            self.quantized_matmul_device(fmt, dw.ptr, wb.size, dx.ptr, xs.size, dout.ptr,
+                                         batch * rows, batch, rows, cols,
+                                         dadd.ptr if dadd is not None else None, addend_mode)
+            self.synchronize()
+            return dout.download().reshape(batch, rows)
+        finally:
+            for d in (dw, dx, dout, dadd):
+                if d is not None:
+                    d.free()
 
 
 class HipRotaryTable:

@@ -1,7 +1,7 @@
 """Builds libjmodels_attn.so (gfx950) in-tree with hipcc.
 
 Run ``python -m models_amd.build`` or call :func:`build`. The library is the product: the HIP
-kernels (csrc/jma_kernels.hip) and the C-ABI runtime (csrc/jma_runtime.cpp) declared in
+kernels (csrc/jma_kernels.hip, csrc/jma_quant.hip) and the C-ABI runtime (csrc/jma_runtime.cpp) declared in
 include/jmodels_attn.h.
 """
 
@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB_NAME = "libjmodels_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = [os.path.join(HERE, "csrc", "jma_kernels.hip"), os.path.join(HERE, "csrc", "jma_runtime.cpp")]
+SOURCES = [os.path.join(HERE, "csrc", "jma_kernels.hip"), os.path.join(HERE, "csrc", "jma_quant.hip"),
+           os.path.join(HERE, "csrc", "jma_runtime.cpp")]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

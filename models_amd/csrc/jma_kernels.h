@@ -152,4 +152,28 @@ hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStrea
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stream);
 
+// ---------------------------------------------------------------- block-quantized projections
+
+// Matrices one quantized-projection launch may serve (the reference's grouped calls take up to 16,
+// backend-native/src/main/rust/model-kernels/src/lib.rs:96).
+constexpr uint32_t kQMaxMatrices = 16;
+
+struct QMatrix {
+  const uint8_t* w;      // GGUF blocks, [rows][cols / 32] blocks of 18 (Q4_0) or 34 (Q8_0) bytes
+  float* out;            // [batch][rows]
+  const float* addend;   // bias [rows] (addend_mode 1) or residual [batch][rows] (2); may be out
+  uint32_t rows, tile0;  // tile0: this matrix's first workgroup
+};
+
+struct QMatArgs {
+  const float* x;  // activations [batch][cols], 16-byte aligned
+  uint32_t batch, cols, blocks, rows_per_tile, count, addend_mode;
+  QMatrix m[kQMaxMatrices];
+};
+
+// Dynamic LDS of one workgroup: Q8_0 activations, their scales and sums, and the tile's terms.
+size_t qmatvec_lds_bytes(uint32_t batch, uint32_t cols, uint32_t rows_per_tile);
+// fmt: 0 = Q4_0, 1 = Q8_0 (every matrix of the launch). tiles = sum of ceil(rows / rows_per_tile).
+hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream);
+
 }  // namespace jma

@@ -1,0 +1,212 @@
+// GGUF block-quantized matrix-vector products for the projections around attention (the Q/K/V
+// projection before the append, llama/LlamaForwardPass.java:1043-1067, and the output projection
+// plus residual after it, :1131-1138), on gfx950.
+//
+// Arithmetic (the definition backend-native's tests hold its Q4_0 kernel to exactly,
+// backend-native/src/test/java/com/integrallis/models/backend/nativekernel/
+// NativeKernelLibraryTest.java:909-1023): each 32-element block of an activation row is quantized
+// to Q8_0 (absmax, inverse 127 / absmax, element = nearest integer of x * inverse by the 1.5 * 2^23
+// trick, scale = f16-rounded absmax / 127); each output is the in-order chain over the row's
+// blocks of fma(weightScale * activationScale, integer block dot, sum). Integer dots are exact and
+// every float operation is the reference's, in its order, so the outputs are the oracle's bit for
+// bit.
+//
+// Work: one 256-thread workgroup per tile of R rows of one matrix. It quantizes the activation
+// rows itself into LDS (a few KB at decode sizes: no separate launch), forms every (row, block)
+// term of its tile in parallel (coalesced 16-bit weight loads: 18- and 34-byte blocks are only
+// 2-byte aligned; 4-element integer dots with v_dot4_i32_i8), then one thread per (activation row,
+// output row) runs the block chain from LDS. The bytes are the weights (HBM-bound at large
+// shapes); at decode shapes a launch is latency-bound.
+#include <hip/hip_runtime.h>
+
+#include "jma_kernels.h"
+
+namespace jma {
+namespace {
+
+constexpr uint32_t kQThreads = 256;
+
+template <int kCtrl>
+__device__ __forceinline__ int dpp_int(int x) {
+  return __builtin_amdgcn_mov_dpp(x, kCtrl, 0xF, 0xF, false);
+}
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+
+// ggmlNearestInt (NativeKernelLibraryTest.java:1019-1022): x + 1.5 * 2^23 rounds x to an integer
+// (nearest, ties to even) in the low mantissa bits.
+__device__ __forceinline__ int nearest_int(float v) {
+#pragma clang fp contract(off)
+  const float s = v + 12582912.0f;
+  return (int)(__float_as_uint(s) & 0x007FFFFFu) - 0x00400000;
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Weight block of a format: a 16-bit scale, then 16 (Q4_0) or 32 (Q8_0) bytes, read as 16-bit
+// halves (the blocks are 2-byte aligned only).
+template <int FMT>
+struct QBlock {
+  static constexpr uint32_t kHalves = FMT == 0 ? 9u : 17u;
+  uint32_t h[kHalves];
+  __device__ __forceinline__ void load(const uint16_t* rec) {
+#pragma unroll
+    for (uint32_t i = 0; i < kHalves; ++i) h[i] = rec[i];
+  }
+  __device__ __forceinline__ uint32_t word(uint32_t j) const { return h[1 + 2 * j] | (h[2 + 2 * j] << 16); }
+  // Integer dot of the block with Q8_0 activations aq (8 words of 4 int8) whose element sum is
+  // asum. Q4_0: byte i holds element i in its low nibble and element i + 16 in its high one, each
+  // offset by 8; the offset is applied as -8 * asum.
+  __device__ __forceinline__ int dot(const int* aq, int asum) const {
+    int d = 0;
+    if constexpr (FMT == 0) {
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t w = word(j);
+        d = __builtin_amdgcn_sdot4((int)(w & 0x0F0F0F0Fu), aq[j], d, false);
+        d = __builtin_amdgcn_sdot4((int)((w >> 4) & 0x0F0F0F0Fu), aq[4 + j], d, false);
+      }
+      d -= 8 * asum;
+    } else {
+#pragma unroll
+      for (uint32_t j = 0; j < 8; ++j) d = __builtin_amdgcn_sdot4((int)word(j), aq[j], d, false);
+    }
+    return d;
+  }
+};
+
+}  // namespace
+
+template <int FMT>
+__global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char q_lds[];
+  const uint32_t nb = a.batch, cols = a.cols, K = a.blocks, R = a.rows_per_tile, Kp = K + 1;
+  int8_t* act_q = (int8_t*)q_lds;                                   // [nb][cols]
+  float* act_scale = (float*)(q_lds + ((nb * cols + 15u) & ~15u));  // [nb][K]
+  int* act_sum = (int*)(act_scale + nb * K);                        // [nb][K]
+  float* t_scale = (float*)(act_sum + nb * K);                      // [nb][R][Kp]
+  float* t_dot = t_scale + nb * R * Kp;                             // [nb][R][Kp]
+
+  uint32_t mi = 0;
+  for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
+  const uint8_t* w = a.m[mi].w;
+  float* out = a.m[mi].out;
+  const float* addend = a.m[mi].addend;
+  const uint32_t rows = a.m[mi].rows;
+  const uint32_t r0 = (blockIdx.x - a.m[mi].tile0) * R;
+  const uint32_t nrows = min(R, rows - r0);
+  const uint32_t nunits = nrows * K;
+  constexpr uint32_t kRecHalves = FMT == 0 ? 9u : 17u;  // block bytes / 2
+  const uint16_t* wrec = (const uint16_t*)(w + (uint64_t)r0 * K * (2u * kRecHalves));
+  const uint32_t tid = threadIdx.x;
+
+  // A thread's first kU units (every unit of a tile of up to 1024 terms) are in flight while the
+  // activations are quantized.
+  constexpr uint32_t kU = 4;
+  QBlock<FMT> unit[kU];
+#pragma unroll
+  for (uint32_t i = 0; i < kU; ++i)
+    if (tid + i * kQThreads < nunits) unit[i].load(wrec + (uint64_t)(tid + i * kQThreads) * kRecHalves);
+
+  // Q8_0 activations: four threads per 32-element block, eight elements each.
+  for (uint32_t t = tid; t < nb * K * 4u; t += kQThreads) {
+    const uint32_t b = t / (K * 4u), rem = t % (K * 4u), blk = rem >> 2, qtr = rem & 3u;
+    const float* xs = a.x + (uint64_t)b * cols + blk * 32u + qtr * 8u;
+    const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(xv[i]));  // a NaN element is skipped
+    am = fmaxf(am, __int_as_float(dpp_int<kQuadXor1>(__float_as_int(am))));
+    am = fmaxf(am, __int_as_float(dpp_int<kQuadXor2>(__float_as_int(am))));
+    const float inverse = am == 0.0f ? 0.0f : 127.0f / am;
+    uint32_t packed[2] = {0u, 0u};
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float scaled;
+      {
+#pragma clang fp contract(off)
+        scaled = xv[i] * inverse;
+      }
+      const int q = nearest_int(scaled);
+      s += (int)(int8_t)q;
+      packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+    }
+    *(uint2*)(act_q + (uint64_t)b * cols + blk * 32u + qtr * 8u) = make_uint2(packed[0], packed[1]);
+    s += dpp_int<kQuadXor1>(s);
+    s += dpp_int<kQuadXor2>(s);
+    if (qtr == 0) {
+      act_scale[b * K + blk] = (float)(_Float16)(am / 127.0f);
+      act_sum[b * K + blk] = s;
+    }
+  }
+  __syncthreads();
+
+  // Every (row, block) term of the tile: the scale product and the integer dot, per activation
+  // row. Tiles of more than kU * 256 terms (rows over 32768 inputs) load further units in turn.
+  auto terms = [&](const QBlock<FMT>& wb, uint32_t u) {
+    const uint32_t row = u / K, blk = u % K;
+    const float wscale = f16_bits_to_float(wb.h[0]);
+    for (uint32_t b = 0; b < nb; ++b) {
+      const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 32u);
+      const int d = wb.dot(aq, act_sum[b * K + blk]);
+      const uint32_t at = (b * R + row) * Kp + blk;
+      t_scale[at] = wscale * act_scale[b * K + blk];
+      t_dot[at] = (float)d;
+    }
+  };
+#pragma unroll
+  for (uint32_t i = 0; i < kU; ++i)
+    if (tid + i * kQThreads < nunits) terms(unit[i], tid + i * kQThreads);
+  for (uint32_t u = tid + kU * kQThreads; u < nunits; u += kQThreads) {
+    QBlock<FMT> wb;
+    wb.load(wrec + (uint64_t)u * kRecHalves);
+    terms(wb, u);
+  }
+  __syncthreads();
+
+  // One thread per (activation row, output row): sum = fma(scale, dot, sum) over the blocks in
+  // order, then the optional bias or residual (one float add, as addOptionalBias and the
+  // residual loop do).
+  for (uint32_t t = tid; t < nb * nrows; t += kQThreads) {
+    const uint32_t b = t / nrows, row = t % nrows;
+    const float* ps = t_scale + (b * R + row) * Kp;
+    const float* pd = t_dot + (b * R + row) * Kp;
+    float sum = 0.0f;
+    uint32_t blk = 0;
+    for (; blk + 8 <= K; blk += 8) {  // the LDS reads of eight steps ahead of their fma chain
+      float sc[8], dt[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sc[i] = ps[blk + i], dt[i] = pd[blk + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sum = __builtin_fmaf(sc[i], dt[i], sum);
+    }
+    for (; blk < K; ++blk) sum = __builtin_fmaf(ps[blk], pd[blk], sum);
+    const uint32_t r = r0 + row;
+    if (a.addend_mode == 1) sum = sum + addend[r];
+    else if (a.addend_mode == 2) sum = sum + addend[(uint64_t)b * rows + r];
+    out[(uint64_t)b * rows + r] = sum;
+  }
+}
+
+size_t qmatvec_lds_bytes(uint32_t batch, uint32_t cols, uint32_t rows_per_tile) {
+  const uint32_t K = cols / 32u;
+  return ((size_t)batch * cols + 15u) / 16u * 16u + (size_t)batch * K * 8u +
+         (size_t)2u * batch * rows_per_tile * (K + 1u) * 4u;
+}
+
+hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream) {
+  const size_t lds = qmatvec_lds_bytes(a.batch, a.cols, a.rows_per_tile);
+  if (fmt == 0)
+    hipLaunchKernelGGL(qmatvec_kernel<0>, dim3(tiles), dim3(kQThreads), lds, stream, a);
+  else if (fmt == 1)
+    hipLaunchKernelGGL(qmatvec_kernel<1>, dim3(tiles), dim3(kQThreads), lds, stream, a);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace jma

@@ -649,6 +649,95 @@ T* stage(DeviceBuffer& buf, const T* host, uint64_t elems, hipStream_t stream) {
   return (T*)buf.ptr;
 }
 
+// One matrix of a quantized projection call.
+struct QuantMatrix {
+  uint32_t format;
+  const void* weights;
+  uint64_t bytes;
+  uint32_t rows;
+  const float* addend;
+};
+
+// Checks a quantized projection call the way backend-native checks its batched matmuls
+// (RS:1017-1060: null pointers, shape, buffer sizes), then launches it: activation rows in chunks
+// that fit one workgroup's LDS, one launch per chunk and weight format.
+void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMatrix>& mats,
+                           const float* input, uint64_t input_elements, float* output,
+                           uint64_t output_elements, uint32_t batch, uint32_t cols,
+                           uint32_t addend_mode) {
+  check_ctx(ctx);
+  require(input != nullptr && output != nullptr, JMODELS_ATTN_NULL_POINTER, "null input or output");
+  require(batch > 0 && cols > 0 && cols % 32 == 0, JMODELS_ATTN_INVALID_SHAPE,
+          "batch_size and cols must be > 0 and cols a multiple of 32");
+  require(addend_mode <= JMODELS_ATTN_ADDEND_RESIDUAL, JMODELS_ATTN_INVALID_SHAPE,
+          "unknown addend_mode " + std::to_string(addend_mode));
+  require(((uintptr_t)input & 15u) == 0, JMODELS_ATTN_INVALID_SHAPE,
+          "input must be 16-byte aligned");
+  const uint32_t K = cols / 32;
+  uint64_t total_rows = 0;
+  for (size_t i = 0; i < mats.size(); ++i) {
+    const QuantMatrix& m = mats[i];
+    const std::string at = " (matrix " + std::to_string(i) + ")";
+    require(m.format == JMODELS_ATTN_WEIGHTS_Q4_0 || m.format == JMODELS_ATTN_WEIGHTS_Q8_0,
+            JMODELS_ATTN_INVALID_SHAPE,
+            "weight format " + std::to_string(m.format) + " has no device kernel" + at);
+    require(m.weights != nullptr, JMODELS_ATTN_NULL_POINTER, "null weights" + at);
+    require(m.rows > 0, JMODELS_ATTN_INVALID_SHAPE, "rows must be > 0" + at);
+    require(((uintptr_t)m.weights & 1u) == 0, JMODELS_ATTN_INVALID_SHAPE,
+            "weights must be 2-byte aligned" + at);
+    require(addend_mode == 0 || m.addend != nullptr, JMODELS_ATTN_NULL_POINTER, "null addend" + at);
+    const uint64_t need = (uint64_t)m.rows * K * (m.format == JMODELS_ATTN_WEIGHTS_Q4_0 ? 18u : 34u);
+    require(m.bytes >= need, JMODELS_ATTN_BUFFER_TOO_SMALL,
+            "weights hold " + std::to_string(m.bytes) + " bytes, need " + std::to_string(need) + at);
+    total_rows += m.rows;
+  }
+  require(input_elements >= (uint64_t)batch * cols, JMODELS_ATTN_BUFFER_TOO_SMALL,
+          "input holds " + std::to_string(input_elements) + " elements, needs " +
+              std::to_string((uint64_t)batch * cols));
+  require(output_elements >= (uint64_t)batch * total_rows, JMODELS_ATTN_BUFFER_TOO_SMALL,
+          "output holds " + std::to_string(output_elements) + " elements, needs " +
+              std::to_string((uint64_t)batch * total_rows));
+  // Up to 512 (row, block) terms per workgroup (two per thread, all loaded at once); activation
+  // rows per launch as LDS allows (at most 8, within 64 KB).
+  constexpr size_t kLds = 64u * 1024u;
+  uint32_t tile = std::max<uint32_t>(1u, std::min<uint32_t>(64u, 512u / K));
+  while (tile > 1 && jma::qmatvec_lds_bytes(1, cols, tile) > kLds) tile /= 2;
+  require(jma::qmatvec_lds_bytes(1, cols, tile) <= kLds, JMODELS_ATTN_INVALID_SHAPE,
+          "cols too large for the device projection: " + std::to_string(cols));
+  uint32_t chunk = 8;
+  while (chunk > 1 && jma::qmatvec_lds_bytes(chunk, cols, tile) > kLds) --chunk;
+  set_device(ctx);
+  for (uint32_t b0 = 0; b0 < batch; b0 += chunk) {
+    const uint32_t nb = std::min(chunk, batch - b0);
+    for (uint32_t fmt = 0; fmt < 2; ++fmt) {
+      jma::QMatArgs a{};
+      a.x = input + (uint64_t)b0 * cols;
+      a.batch = nb;
+      a.cols = cols;
+      a.blocks = K;
+      a.rows_per_tile = tile;
+      a.addend_mode = addend_mode;
+      uint32_t tiles = 0;
+      uint64_t out_off = 0;
+      for (const QuantMatrix& m : mats) {
+        if (m.format == fmt) {
+          jma::QMatrix& q = a.m[a.count++];
+          q.w = (const uint8_t*)m.weights;
+          q.out = output + out_off + (uint64_t)b0 * m.rows;
+          q.addend = addend_mode == JMODELS_ATTN_ADDEND_RESIDUAL ? m.addend + (uint64_t)b0 * m.rows
+                                                                 : m.addend;
+          q.rows = m.rows;
+          q.tile0 = tiles;
+          tiles += (m.rows + tile - 1) / tile;
+        }
+        out_off += (uint64_t)batch * m.rows;
+      }
+      if (a.count == 0) continue;
+      hip_check(jma::launch_qmatvec(a, fmt, tiles, ctx->stream), "quantized matmul launch");
+    }
+  }
+}
+
 }  // namespace
 
 // ================================================================ exports
@@ -661,7 +750,7 @@ uint64_t jmodels_attn_capabilities(void) {
   return JMODELS_ATTN_CAP_DECODE_F32 | JMODELS_ATTN_CAP_DECODE_F16 | JMODELS_ATTN_CAP_PREFILL_MFMA |
          JMODELS_ATTN_CAP_RAGGED_DECODE | JMODELS_ATTN_CAP_SLIDING_WINDOW |
          JMODELS_ATTN_CAP_RING_LAYERS | JMODELS_ATTN_CAP_DEVICE_POINTERS | JMODELS_ATTN_CAP_QK_NORM |
-         JMODELS_ATTN_CAP_VALUE_NORM;
+         JMODELS_ATTN_CAP_VALUE_NORM | JMODELS_ATTN_CAP_QUANT_MATMUL;
 }
 
 const char* jmodels_attn_status_name(int32_t status) {
@@ -1475,6 +1564,38 @@ int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, jmodels_attn_kv* 
                                     uint64_t out_elements) {
   return prefill_entry(true, ctx, kv, layer, sequence, start, n, q, q_elements, k, k_elements, v,
                        v_elements, out, out_elements);
+}
+
+int32_t jmodels_attn_quantized_matmul_device(jmodels_attn_context* ctx, uint32_t format,
+                                             const void* weights, uint64_t weight_bytes,
+                                             const float* input, uint64_t input_elements,
+                                             float* output, uint64_t output_elements,
+                                             uint32_t batch_size, uint32_t rows, uint32_t cols,
+                                             const float* addend, uint32_t addend_mode) {
+  return guard([&] {
+    quantized_matmul_impl(ctx, {QuantMatrix{format, weights, weight_bytes, rows, addend}}, input,
+                          input_elements, output, output_elements, batch_size, cols, addend_mode);
+  });
+}
+
+int32_t jmodels_attn_quantized_grouped_matmul_device(
+    jmodels_attn_context* ctx, const uint32_t* formats, const void* const* weights,
+    const uint64_t* weight_bytes, const uint32_t* rows, uint32_t matrix_count, const float* input,
+    uint64_t input_elements, float* output, uint64_t output_elements, uint32_t batch_size,
+    uint32_t cols, const float* const* addends, uint32_t addend_mode) {
+  return guard([&] {
+    require(formats != nullptr && weights != nullptr && weight_bytes != nullptr && rows != nullptr,
+            JMODELS_ATTN_NULL_POINTER, "null matrix table");
+    require(addend_mode == 0 || addends != nullptr, JMODELS_ATTN_NULL_POINTER, "null addends");
+    require(matrix_count >= 1 && matrix_count <= jma::kQMaxMatrices, JMODELS_ATTN_INVALID_SHAPE,
+            "matrix_count must be in [1, 16]");
+    std::vector<QuantMatrix> mats(matrix_count);
+    for (uint32_t i = 0; i < matrix_count; ++i)
+      mats[i] = QuantMatrix{formats[i], weights[i], weight_bytes[i], rows[i],
+                            addend_mode ? addends[i] : nullptr};
+    quantized_matmul_impl(ctx, mats, input, input_elements, output, output_elements, batch_size,
+                          cols, addend_mode);
+  });
 }
 
 }  // extern "C"

@@ -938,3 +938,79 @@ int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* ke
   return gqa_rows_batch(count, q, keys, values, rows, key_row_stride, value_row_stride, num_heads,
                         num_kv_heads, key_length, value_length, scale, out, threads, 1);
 }
+
+/* ================================================================ GGUF block-quantized projection */
+
+/* ggmlNearestInt (NativeKernelLibraryTest.java:1019-1022; RS:4072-4075): adding 1.5 * 2^23 puts
+ * the value's integer part in the low mantissa bits, rounded to nearest even. */
+static int ggml_nearest_int(float value) {
+  const float shifted = value + 12582912.0f;
+  uint32_t bits;
+  memcpy(&bits, &shifted, 4);
+  return (int)(bits & 0x007fffffu) - 0x00400000;
+}
+
+void jmo_q8_0_quantize(const float* x, int batch, int cols, int8_t* q, float* scales) {
+  const int blocks = cols / 32;
+  for (int b = 0; b < batch; b++) {
+    for (int blk = 0; blk < blocks; blk++) {
+      const float* v = x + (size_t)b * cols + (size_t)blk * 32;
+      float absmax = 0.0f;
+      for (int i = 0; i < 32; i++) {
+        const float a = fabsf(v[i]);
+        if (a > absmax) absmax = a; /* a NaN compares false and is skipped */
+      }
+      const float inverse = absmax == 0.0f ? 0.0f : 127.0f / absmax;
+      scales[(size_t)b * blocks + blk] = jmo_f16_to_float(jmo_float_to_f16(absmax / 127.0f));
+      for (int i = 0; i < 32; i++) {
+        const float scaled = v[i] * inverse;
+        q[(size_t)b * cols + (size_t)blk * 32 + i] = (int8_t)ggml_nearest_int(scaled);
+      }
+    }
+  }
+}
+
+int jmo_quantized_matmul(int format, const uint8_t* weights, const float* input, int batch,
+                         int rows, int cols, float* out) {
+  if ((format != JMO_FMT_Q4_0 && format != JMO_FMT_Q8_0) || cols <= 0 || cols % 32 != 0 ||
+      rows <= 0 || batch <= 0)
+    return JMO_ILLEGAL_ARGUMENT;
+  const int blocks = cols / 32;
+  const int block_bytes = format == JMO_FMT_Q4_0 ? 18 : 34;
+  int8_t* q = (int8_t*)malloc((size_t)batch * cols);
+  float* scales = (float*)malloc((size_t)batch * blocks * sizeof(float));
+  if (!q || !scales) {
+    free(q);
+    free(scales);
+    return JMO_ILLEGAL_STATE;
+  }
+  jmo_q8_0_quantize(input, batch, cols, q, scales);
+  for (int b = 0; b < batch; b++) {
+    for (int r = 0; r < rows; r++) {
+      float sum = 0.0f;
+      for (int blk = 0; blk < blocks; blk++) {
+        const uint8_t* w = weights + ((size_t)r * blocks + blk) * block_bytes;
+        const float weight_scale = jmo_f16_to_float((uint16_t)(w[0] | (w[1] << 8)));
+        const int8_t* a = q + (size_t)b * cols + (size_t)blk * 32;
+        int dot = 0;
+        if (format == JMO_FMT_Q4_0) {
+          /* byte i holds element i in its low nibble and element i + 16 in its high one, each
+           * offset by 8 (:921-926) */
+          for (int i = 0; i < 16; i++) {
+            const int packed = w[2 + i];
+            dot += ((packed & 0xf) - 8) * a[i];
+            dot += ((packed >> 4) - 8) * a[i + 16];
+          }
+        } else {
+          for (int i = 0; i < 32; i++) dot += (int8_t)w[2 + i] * a[i];
+        }
+        const float scale = weight_scale * scales[(size_t)b * blocks + blk];
+        sum = fmaf(scale, (float)dot, sum); /* Math.fma (:929-930) */
+      }
+      out[(size_t)b * rows + r] = sum;
+    }
+  }
+  free(q);
+  free(scales);
+  return JMO_OK;
+}

@@ -183,6 +183,32 @@ int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* ke
                        int value_row_stride, int num_heads, int num_kv_heads, int key_length,
                        int value_length, float scale, float* const* out, int threads);
 
+/* ---------------------------------------------------------------- GGUF block-quantized projection
+ *
+ * The Q/K/V and output projections around attention (llama/LlamaForwardPass.java:1043-1067,
+ * 1131-1138) multiply a GGUF block-quantized weight matrix [rows][cols] by f32 activations. For
+ * Q4_0 and Q8_0 weights both backend-native (backend-native/src/main/rust/model-kernels/src/
+ * lib.rs, the batched matmul exports at RS:540-700) and vectors-core quantize each 32-element
+ * activation block to Q8_0 and take integer dot products per block. Restated here from the
+ * reference implementation in backend-native's tests, which the native Q4_0 kernel must match
+ * exactly (backend-native/src/test/java/com/integrallis/models/backend/nativekernel/
+ * NativeKernelLibraryTest.java:67-84 with :909-1023). */
+#define JMO_FMT_Q4_0 0 /* 18-byte blocks: f16 scale, 16 bytes of nibbles (RS:87) */
+#define JMO_FMT_Q8_0 1 /* 34-byte blocks: f16 scale, 32 int8 (RS:89) */
+
+/* quantizeInputs (NativeKernelLibraryTest.java:998-1017; RS quantize_q8_0_batch_scalar): per
+ * 32-element block, absmax (a NaN element is skipped, as Rust's f32::max does), inverse scale
+ * 127 / absmax (0 for an all-zero block), scale = f16-rounded absmax / 127, element =
+ * ggmlNearestInt(x * inverse) (:1019-1022). q [batch*cols], scales [batch*cols/32]. */
+void jmo_q8_0_quantize(const float* x, int batch, int cols, int8_t* q, float* scales);
+
+/* referenceQ4_0F32BatchedMatmul / referenceQ8_0F32BatchedMatmul (NativeKernelLibraryTest.java:
+ * 909-936, 938-965): out[b*rows + r] = sum over blocks in order of
+ * fma(weightScale * activationScale, integerDot, sum). JMO_ILLEGAL_ARGUMENT for an unknown format
+ * or cols not a multiple of 32. */
+int jmo_quantized_matmul(int format, const uint8_t* weights, const float* input, int batch,
+                         int rows, int cols, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,14 @@ KvCache                     KvCacheTest offsets/buffers/growth/discard/clear/bou
 LayeredKvCache              LayeredKvCacheTest spans (2,2,4,2),(4,2,0,0), buffers, bytes (:28-160)
 rms_norm / qk_norm_heads    TensorOpsTest.RmsNorm known answers (:42-67); float64 rms on random
                             heads; in place == out of place; zero head -> 0 (rms = sqrt(eps))
+q8_0 activation quantize    ggmlNearestInt == IEEE round-half-even (numpy rint) over the int8
+                            range and ties; scales == numpy float16 of absmax/127; zero and NaN
+                            blocks; every |q| <= 127 and q * scale within half a step of x
+quantized matmul Q4_0/Q8_0  float64 dot of the dequantized weights with the dequantized Q8_0
+                            activations (rounding of the per-block fma chain only); hand-computed
+                            one-block cases (nibble order, the -8 offset, scale product); the
+                            fixtures of NativeKernelLibraryTest (inputs / fillWeights /
+                            fillQ8_0Weights, :660-702) regenerated as data
 attention start (window)    EncoderAttentionWindowTest causal bounds (:76-145); brute force
 gqa / decode / prefill      float64 dense softmax(QK^T s)V on small shapes (brute force); L=1 -> V;
                             uniform scores -> mean of V rows; one-hot key; equal Q within a GQA
@@ -140,6 +148,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "jmo_gqa_rows_batch8": (c_int, [c_int, ctypes.POINTER(_f32p), ctypes.POINTER(_f32p),
                                        ctypes.POINTER(_f32p), _i32p, c_int, c_int, c_int, c_int,
                                        c_int, c_int, c_float, ctypes.POINTER(_f32p), c_int]),
+        "jmo_q8_0_quantize": (None, [_f32p, c_int, c_int, c_void, _f32p]),
+        "jmo_quantized_matmul": (c_int, [c_int, c_void, _f32p, c_int, c_int, c_int, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -514,3 +524,37 @@ def gqa_rows_batch(qs, keys_list, values_list, num_heads, num_kv_heads, key_leng
                                     key_length, value_length, scale,
                                     P(*[_ptr(a) for a in outs]), threads), "gqa_rows_batch")
     return outs
+
+
+# ------------------------------------------------------------------ GGUF block-quantized projection
+
+FMT_Q4_0 = 0
+FMT_Q8_0 = 1
+BLOCK_BYTES = {FMT_Q4_0: 18, FMT_Q8_0: 34}
+
+
+def q8_0_quantize(x, batch: int, cols: int):
+    """quantizeInputs (NativeKernelLibraryTest.java:998-1017): (int8 [batch*cols], scales)."""
+    x = _f32(x)
+    if x.size != batch * cols or cols % 32:
+        raise OracleError(ILLEGAL_ARGUMENT, "q8_0_quantize shape")
+    q = np.empty(batch * cols, np.int8)
+    scales = np.empty(batch * cols // 32, np.float32)
+    lib().jmo_q8_0_quantize(_ptr(x), batch, cols, q.ctypes.data, _ptr(scales))
+    return q, scales
+
+
+def quantized_matmul(fmt: int, weights, x, batch: int, rows: int, cols: int) -> np.ndarray:
+    """referenceQ4_0F32BatchedMatmul / referenceQ8_0F32BatchedMatmul
+    (NativeKernelLibraryTest.java:909-965): out [batch, rows]."""
+    if isinstance(weights, (bytes, bytearray)):
+        weights = np.frombuffer(bytes(weights), np.uint8)
+    w = np.ascontiguousarray(weights, dtype=np.uint8).reshape(-1)
+    x = _f32(x)
+    if fmt not in BLOCK_BYTES or cols % 32 or w.size < rows * cols // 32 * BLOCK_BYTES[fmt] \
+            or x.size != batch * cols:
+        raise OracleError(ILLEGAL_ARGUMENT, "quantized_matmul shape")
+    out = np.empty(batch * rows, np.float32)
+    _check(lib().jmo_quantized_matmul(fmt, w.ctypes.data, _ptr(x), batch, rows, cols, _ptr(out)),
+           "quantized_matmul")
+    return out.reshape(batch, rows)

@@ -343,6 +343,56 @@ def sliding_layers():
             "sliding": [l % 6 != 5 for l in range(24)]}
 
 
+def _f16_bits(x):
+    import numpy as np
+    return int(np.array([x], np.float32).astype(np.float16).view(np.uint16)[0])
+
+
+def quantized_matmul_cases():
+    # backend-native/src/test/java/com/integrallis/models/backend/nativekernel/
+    # NativeKernelLibraryTest.java: the synthetic activations and weights its quantized-matmul
+    # tests build (inputs :660-668, fillWeights :670-684, fillQ8_0Weights :686-702), written out
+    # as data. The relation each test asserts between the native kernel and the test's own
+    # reference (:909-1023) is kept with the case: "exact" (containsExactly) or an absolute
+    # tolerance (BLOCK_QUANT_REDUCTION_TOLERANCE 2e-5, :35).
+    def activations(batch, cols):
+        return [((col * 17 + b * 11) % 29 - 14) * 0.125 for b in range(batch) for col in range(cols)]
+
+    def q4_0_weights(rows, cols):
+        out = bytearray()
+        for row in range(rows):
+            for block in range(cols // 32):
+                out += _f16_bits((row + block + 1) * 0.125).to_bytes(2, "little")
+                for lane in range(16):
+                    low = (row * 3 + block * 5 + lane) & 0xF
+                    high = (row * 7 + block * 2 + lane * 3) & 0xF
+                    out.append(low | high << 4)
+        return out.hex()
+
+    def q8_0_weights(rows, cols):
+        out = bytearray()
+        for row in range(rows):
+            for block in range(cols // 32):
+                out += _f16_bits((row + block + 1) * 0.03125).to_bytes(2, "little")
+                for lane in range(32):
+                    out.append(((row * 37 + block * 19 + lane * 11) & 0xFF) - 128 & 0xFF)
+        return out.hex()
+
+    cases = []
+    for name, src, batch, rows in (
+            ("computesQ4_0BatchedMatrixMultiplication", ":67-84", 2, 3),
+            ("reusableGgufKernelComputesAcrossWorkspaceGrowth[1x2]", ":101-126", 1, 2),
+            ("reusableGgufKernelComputesAcrossWorkspaceGrowth[3x128]", ":101-126", 3, 128)):
+        cases.append({"name": name, "src": "NativeKernelLibraryTest.java" + src, "format": 0,
+                      "batch": batch, "rows": rows, "cols": 64, "relation": "exact",
+                      "input": activations(batch, 64), "weights_hex": q4_0_weights(rows, 64)})
+    cases.append({"name": "reusableGgufKernelComputesQ8_0BatchedMatrixMultiplicationWithinReductionTolerance",
+                  "src": "NativeKernelLibraryTest.java:176-196", "format": 1, "batch": 3, "rows": 5,
+                  "cols": 64, "relation": 2e-5, "input": activations(3, 64),
+                  "weights_hex": q8_0_weights(5, 64)})
+    return cases
+
+
 def main():
     data = {
         "about": "Known answers transcribed from backend-java unit tests (see each 'src').",
@@ -354,6 +404,7 @@ def main():
         "value_norm": value_norm_cases(),
         "attention_start": window_cases(),
         "sliding_layers": sliding_layers(),
+        "quantized_matmul": quantized_matmul_cases(),
     }
     path = os.path.join(HERE, "reference_known_answers.json")
     with open(path, "w") as f:
