@@ -487,26 +487,34 @@ def run_c5(hip, A, rt, synth, steps: int = 64, warmup: int = 4):
 
 
 def _gguf_weights(synth, fmt: int, rows: int, cols: int, key: str) -> np.ndarray:
-    """Synthetic GGUF blocks: uniform bytes with an f16 N(0, 0.02) scale per block."""
-    nbytes = 18 if fmt == 0 else 34
-    blocks = cols // 32
+    """Synthetic GGUF blocks: uniform bytes with f16 N(0, 0.02) scales where the format keeps
+    them (Q4_0 / Q8_0 bytes 0-1, Q4_K bytes 0-3, Q6_K bytes 208-209)."""
+    nbytes, elems = {0: (18, 32), 1: (34, 32), 2: (144, 256), 3: (210, 256)}[fmt]
+    blocks = cols // elems
     raw = synth.uniform_int(9, key, rows * blocks * nbytes, 0, 255).astype(np.uint8)
     raw = raw.reshape(rows, blocks, nbytes)
-    scales = (synth.normal(9, key + "/s", (rows, blocks)) * 0.02).astype(np.float16)
-    raw[:, :, :2] = scales.view(np.uint8).reshape(rows, blocks, 2)
+    scales = (synth.normal(9, key + "/s", (rows, blocks, 2)) * 0.02).astype(np.float16)
+    scales = scales.view(np.uint8).reshape(rows, blocks, 4)
+    if fmt == 2:
+        raw[:, :, 0:4] = scales
+    elif fmt == 3:
+        raw[:, :, 208:210] = scales[..., :2]
+    else:
+        raw[:, :, 0:2] = scales[..., :2]
     return raw.reshape(-1)
 
 
 def run_proj(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
     """The projections around one C2 layer at decode (batch 1): Llama-3.2-1B's Q (2048 rows), K
     and V (512 rows each) over 2048 inputs as one grouped launch writing q|k|v for the decode,
-    and the output projection (2048 x 2048) with the residual added in place; Q4_0 and Q8_0
-    weights. Each launch is repeated `per_graph` times in a graph; HIP events around the replays
+    and the output projection (2048 x 2048) with the residual added in place; Q4_0, Q8_0, Q4_K
+    and Q6_K weights. Each launch is repeated `per_graph` times in a graph; HIP events around the replays
     give us per launch; GB/s counts the weight bytes (the activations are 8 KB)."""
     cols, rows = 2048, [2048, 512, 512]
     stream = hip.stream()
     result = {}
-    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0)):
+    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0), ("q4_k", A.WEIGHTS_Q4_K),
+                      ("q6_k", A.WEIGHTS_Q6_K)):
         ws = [_gguf_weights(synth, fmt, r, cols, f"bench/proj/{name}/{i}") for i, r in enumerate(rows)]
         wo = _gguf_weights(synth, fmt, cols, cols, f"bench/proj/{name}/wo")
         dws = [rt.DeviceArray.from_host(w) for w in ws]
@@ -789,7 +797,8 @@ def main() -> int:
         result["projections"] = {
             "workload": "Llama-3.2-1B layer at decode (batch 1): grouped Q/K/V projection (2048 -> "
                         "2048 + 512 + 512) and output projection 2048 x 2048 plus residual, GGUF "
-                        "Q4_0 / Q8_0 weights, activations quantized to Q8_0 in the launch",
+                        "Q4_0 / Q8_0 / Q4_K / Q6_K weights, activations quantized (Q8_0 or Q8_K) "
+                        "in the launch",
             **proj,
         }
     if not args.no_cpu:

@@ -336,21 +336,27 @@ JMODELS_ATTN_API int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, 
  * The projections on either side of attention: Q/K/V before the append
  * (BJ/llama/LlamaForwardPass.java:1043-1067, with addOptionalBias :1065-1067) and the output
  * projection plus residual after it (:1131-1138). GGUF weight formats use backend-native's codes
- * (RS:150-161): 0 = Q4_0 (18-byte blocks), 1 = Q8_0 (34-byte blocks) run here; its other codes
- * (Q4_K, Q6_K, Q5_K, Q5_0) return INVALID_SHAPE. Activations are quantized to Q8_0 per 32-element
- * block and every output is the in-order chain of per-block fma(weightScale * activationScale,
- * integer dot, sum), the arithmetic backend-native's tests require of its Q4_0 kernel exactly
- * (backend-native/src/test/java/.../NativeKernelLibraryTest.java:67-84, 909-1023).
+ * (RS:150-161): 0 = Q4_0 (18-byte blocks of 32), 1 = Q8_0 (34 bytes), 2 = Q4_K (144-byte blocks
+ * of 256), 3 = Q6_K (210 bytes) run here; its other codes (Q5_K, Q5_0) return INVALID_SHAPE.
+ * Q4_0 / Q8_0: activations quantized to Q8_0 per 32-element block, every output the in-order chain
+ * of per-block fma(weightScale * activationScale, integer dot, sum), the arithmetic
+ * backend-native's tests require of its Q4_0 kernel exactly (backend-native/src/test/java/.../
+ * NativeKernelLibraryTest.java:67-84, 909-1023). Q4_K / Q6_K: Q8_K activations and the float
+ * order of backend-native's scalar row kernels (RS:3410-3459, 3519-3577; its tests hold the
+ * K-quant kernels to 2e-3 of the Java path). One call takes either Q4_0 / Q8_0 or K-quant
+ * matrices, not both (their activation formats differ).
  *
  * Device pointers, asynchronous on the context stream (capturable: no scratch memory). weights:
- * [rows][cols / 32] blocks, 2-byte aligned; input [batch][cols] f32, 16-byte aligned, cols a
- * multiple of 32; output [batch][rows] per matrix, matrix after matrix (a grouped Q/K/V call
+ * [rows][cols / 32 or cols / 256] blocks, 2-byte aligned; input [batch][cols] f32, 16-byte
+ * aligned, cols a multiple of the block size; output [batch][rows] per matrix, matrix after matrix (a grouped Q/K/V call
  * leaves q, k and v contiguous, the layout jmodels_attn_decode_device reads). addend_mode: 0 none,
  * 1 a bias [rows] added to every batch row (addOptionalBias), 2 a residual [batch][rows] added
  * (x[i] += attnProjected[i]; the residual may be the output itself, updated in place). output must
  * not alias input. */
 #define JMODELS_ATTN_WEIGHTS_Q4_0 0u
 #define JMODELS_ATTN_WEIGHTS_Q8_0 1u
+#define JMODELS_ATTN_WEIGHTS_Q4_K 2u
+#define JMODELS_ATTN_WEIGHTS_Q6_K 3u
 #define JMODELS_ATTN_ADDEND_NONE 0u
 #define JMODELS_ATTN_ADDEND_BIAS 1u
 #define JMODELS_ATTN_ADDEND_RESIDUAL 2u

@@ -159,7 +159,8 @@ hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stre
 constexpr uint32_t kQMaxMatrices = 16;
 
 struct QMatrix {
-  const uint8_t* w;      // GGUF blocks, [rows][cols / 32] blocks of 18 (Q4_0) or 34 (Q8_0) bytes
+  const uint8_t* w;      // GGUF blocks: [rows][cols / 32] of 18 (Q4_0) or 34 (Q8_0) bytes, or
+                         // [rows][cols / 256] of 144 (Q4_K) or 210 (Q6_K) bytes
   float* out;            // [batch][rows]
   const float* addend;   // bias [rows] (addend_mode 1) or residual [batch][rows] (2); may be out
   uint32_t rows, tile0;  // tile0: this matrix's first workgroup
@@ -173,7 +174,9 @@ struct QMatArgs {
 
 // Dynamic LDS of one workgroup: Q8_0 activations, their scales and sums, and the tile's terms.
 size_t qmatvec_lds_bytes(uint32_t batch, uint32_t cols, uint32_t rows_per_tile);
-// fmt: 0 = Q4_0, 1 = Q8_0 (every matrix of the launch). tiles = sum of ceil(rows / rows_per_tile).
+size_t qkmatvec_lds_bytes(uint32_t fmt, uint32_t batch, uint32_t cols, uint32_t rows_per_tile);
+// fmt: 0 = Q4_0, 1 = Q8_0 (blocks = cols / 32), 2 = Q4_K, 3 = Q6_K (blocks = cols / 256), every
+// matrix of the launch. tiles = sum of ceil(rows / rows_per_tile).
 hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream);
 
 }  // namespace jma

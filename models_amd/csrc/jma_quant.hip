@@ -192,6 +192,208 @@ __global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- K-quants (Q4_K, Q6_K)
+//
+// Q8_K activations (quantize_q8_k_batch, backend-native/src/main/rust/model-kernels/src/lib.rs:
+// 3906-3952): per 256-element block, the element of largest magnitude (the first on ties, NaN
+// skipped) sets inverse = -127 / max, element = min(nearest(inverse * x), 127), sums of 16
+// elements, scale = 1 / inverse. Rows as backend-native's scalar row kernels form them
+// (dot_q4_k_q8_k_row_scalar :3410-3459, dot_q6_k_q8_k_row_scalar :3519-3577); the integer parts
+// are exact in any order, so eight threads share each (row, block) and only the float chains
+// keep the reference's order.
+template <int FMT>
+__global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
+  constexpr uint32_t kNT = FMT == 2 ? 4u : 9u;         // floats per (row, block) term
+  constexpr uint32_t kBlockBytes = FMT == 2 ? 144u : 210u;
+  extern __shared__ __attribute__((aligned(16))) unsigned char q_lds[];
+  const uint32_t nb = a.batch, cols = a.cols, KB = a.blocks, R = a.rows_per_tile;
+  const uint32_t rs = KB * kNT + 1;  // floats per (activation row, output row) of terms
+  int8_t* act_q = (int8_t*)q_lds;                                   // [nb][cols]
+  float* act_scale = (float*)(q_lds + ((nb * cols + 15u) & ~15u));  // [nb][KB]
+  int* act_sum = (int*)(act_scale + nb * KB);                       // [nb][cols / 16]
+  float* terms = (float*)(act_sum + nb * (cols / 16u));             // [nb][R][rs]
+
+  uint32_t mi = 0;
+  for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
+  const uint8_t* w = a.m[mi].w;
+  float* out = a.m[mi].out;
+  const float* addend = a.m[mi].addend;
+  const uint32_t rows = a.m[mi].rows;
+  const uint32_t r0 = (blockIdx.x - a.m[mi].tile0) * R;
+  const uint32_t nrows = min(R, rows - r0);
+  const uint32_t nunits = nrows * KB;
+  const uint8_t* wtile = w + (uint64_t)r0 * KB * kBlockBytes;
+  const uint32_t tid = threadIdx.x, sub = tid & 7u;
+
+  // Q8_K activations: 32 threads per block, eight consecutive elements each.
+  for (uint32_t t = tid; t < nb * KB * 32u; t += kQThreads) {
+    const uint32_t b = t / (KB * 32u), blk = (t / 32u) % KB, part = t & 31u;
+    const float* xs = a.x + (uint64_t)b * cols + blk * 256u + part * 8u;
+    const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    float best = 0.0f, bval = 0.0f;
+    uint32_t bidx = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float m = fabsf(xv[i]);
+      if (m > best) {  // strict: the first of equal magnitudes; a NaN compares false
+        best = m;
+        bval = xv[i];
+        bidx = part * 8u + i;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const float ob = __shfl_xor(best, o, 32), ov = __shfl_xor(bval, o, 32);
+      const uint32_t oi = __shfl_xor(bidx, o, 32);
+      if (ob > best || (ob == best && oi < bidx)) {
+        best = ob;
+        bval = ov;
+        bidx = oi;
+      }
+    }
+    int8_t* qd = act_q + (uint64_t)b * cols + blk * 256u + part * 8u;
+    int s = 0;
+    if (best == 0.0f) {
+      *(uint2*)qd = make_uint2(0u, 0u);
+    } else {
+      const float inverse = -127.0f / bval;
+      uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float scaled;
+        {
+#pragma clang fp contract(off)
+          scaled = inverse * xv[i];
+        }
+        const int q = min(nearest_int(scaled), 127);
+        s += (int)(int8_t)q;
+        packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+      }
+      *(uint2*)qd = make_uint2(packed[0], packed[1]);
+    }
+    s += __shfl_xor(s, 1, 32);  // two threads make one 16-element sum
+    if ((part & 1u) == 0) act_sum[b * (cols / 16u) + blk * 16u + part / 2u] = s;
+    if (part == 0) act_scale[b * KB + blk] = best == 0.0f ? 0.0f : 1.0f / (-127.0f / bval);
+  }
+  __syncthreads();
+
+  // Terms: eight threads per (row, block); every thread of a unit runs the same batch loop.
+  for (uint32_t t = tid; t < ((nunits * 8u + 63u) & ~63u); t += kQThreads) {
+    const uint32_t u = min(t / 8u, nunits - 1u);  // the last wave's spare lanes repeat a unit
+    const bool real = t / 8u < nunits;
+    const uint32_t row = u / KB, blk = u % KB;
+    const uint8_t* wb = wtile + (uint64_t)u * kBlockBytes;
+    if constexpr (FMT == 2) {
+      const uint16_t* h = (const uint16_t*)wb;
+      const float wd = f16_bits_to_float(h[0]), wdmin = f16_bits_to_float(h[1]);
+      uint32_t scb[12];
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        const uint32_t x = h[2 + i];
+        scb[2 * i] = x & 0xFFu;
+        scb[2 * i + 1] = x >> 8;
+      }
+      const uint32_t g = sub;
+      const int sc = g < 4 ? (int)(scb[g] & 63u) : (int)((scb[g + 4] & 15u) | ((scb[g - 4] >> 6) << 4));
+      const int mn = g < 4 ? (int)(scb[g + 4] & 63u) : (int)((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4));
+      uint32_t nib[8];
+      const uint16_t* qh16 = h + 8 + (g >> 1) * 16;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nib[i] = (uint32_t)qh16[2 * i] | ((uint32_t)qh16[2 * i + 1] << 16);
+      const uint32_t shift = (g & 1u) * 4u;
+      for (uint32_t b = 0; b < nb; ++b) {
+        const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 256u + g * 32u);
+        int dot = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          dot = __builtin_amdgcn_sdot4((int)((nib[i] >> shift) & 0x0F0F0F0Fu), aq[i], dot, false);
+        const int* s16 = act_sum + b * (cols / 16u) + blk * 16u;
+        int qs = sc * dot, ms = mn * (s16[2 * g] + s16[2 * g + 1]);
+        qs += __shfl_xor(qs, 1, 8);
+        qs += __shfl_xor(qs, 2, 8);
+        qs += __shfl_xor(qs, 4, 8);
+        ms += __shfl_xor(ms, 1, 8);
+        ms += __shfl_xor(ms, 2, 8);
+        ms += __shfl_xor(ms, 4, 8);
+        if (real && sub == 0) {
+          const float as = act_scale[b * KB + blk];
+          float* tt = terms + (b * R + row) * rs + blk * kNT;
+          tt[0] = wd * as;
+          tt[1] = (float)qs;
+          tt[2] = -(wdmin * as);
+          tt[3] = (float)ms;
+        }
+      }
+    } else {
+      // Lane class l = sub: elements i, i + 8, i + 16, i + 24 of each 32-run, both halves, all
+      // four quarters (ql low / high nibble, qh bit pairs), each times its int8 group scale.
+      const int8_t* sc = (const int8_t*)(wb + 192);
+      const float wd = (float)__builtin_bit_cast(_Float16, (uint16_t)(wb[208] | (wb[209] << 8)));
+      int ql1[8], ql2[8], qhh[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t hf = k >> 2, i = sub + 8u * (k & 3);
+        ql1[k] = wb[hf * 64u + i];
+        ql2[k] = wb[hf * 64u + 32u + i];
+        qhh[k] = wb[128u + hf * 32u + i];
+      }
+      for (uint32_t b = 0; b < nb; ++b) {
+        const int8_t* aq = act_q + (uint64_t)b * cols + blk * 256u;
+        int acc = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t hf = k >> 2, i = sub + 8u * (k & 3), si = i / 16u;
+          const int q1 = ((ql1[k] & 15) | ((qhh[k] & 3) << 4)) - 32;
+          const int q2 = ((ql2[k] & 15) | (((qhh[k] >> 2) & 3) << 4)) - 32;
+          const int q3 = ((ql1[k] >> 4) | (((qhh[k] >> 4) & 3) << 4)) - 32;
+          const int q4 = ((ql2[k] >> 4) | (((qhh[k] >> 6) & 3) << 4)) - 32;
+          const int8_t* aa = aq + hf * 128u;
+          acc += sc[hf * 8u + si] * q1 * aa[i];
+          acc += sc[hf * 8u + si + 2u] * q2 * aa[i + 32u];
+          acc += sc[hf * 8u + si + 4u] * q3 * aa[i + 64u];
+          acc += sc[hf * 8u + si + 6u] * q4 * aa[i + 96u];
+        }
+        if (real) {
+          float* tt = terms + (b * R + row) * rs + blk * kNT;
+          if (sub == 0) tt[0] = wd * act_scale[b * KB + blk];
+          tt[1 + sub] = (float)acc;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  for (uint32_t t = tid; t < nb * nrows; t += kQThreads) {
+    const uint32_t b = t / nrows, row = t % nrows;
+    const float* tt = terms + (b * R + row) * rs;
+    float sum = 0.0f;
+    if constexpr (FMT == 2) {
+      for (uint32_t blk = 0; blk < KB; ++blk) {
+        sum = __builtin_fmaf(tt[blk * 4], tt[blk * 4 + 1], sum);
+        sum = __builtin_fmaf(tt[blk * 4 + 2], tt[blk * 4 + 3], sum);
+      }
+    } else {
+      float ls[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (uint32_t blk = 0; blk < KB; ++blk)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) ls[l] = __builtin_fmaf(tt[blk * 9], tt[blk * 9 + 1 + l], ls[l]);
+#pragma unroll
+      for (int l = 0; l < 8; ++l) sum = sum + ls[l];
+    }
+    const uint32_t r = r0 + row;
+    if (a.addend_mode == 1) sum = sum + addend[r];
+    else if (a.addend_mode == 2) sum = sum + addend[(uint64_t)b * rows + r];
+    out[(uint64_t)b * rows + r] = sum;
+  }
+}
+
+size_t qkmatvec_lds_bytes(uint32_t fmt, uint32_t batch, uint32_t cols, uint32_t rows_per_tile) {
+  const uint32_t KB = cols / 256u, nt = fmt == 2 ? 4u : 9u;
+  return ((size_t)batch * cols + 15u) / 16u * 16u + (size_t)batch * KB * 4u +
+         (size_t)batch * (cols / 16u) * 4u + (size_t)batch * rows_per_tile * (KB * nt + 1u) * 4u;
+}
+
 size_t qmatvec_lds_bytes(uint32_t batch, uint32_t cols, uint32_t rows_per_tile) {
   const uint32_t K = cols / 32u;
   return ((size_t)batch * cols + 15u) / 16u * 16u + (size_t)batch * K * 8u +
@@ -204,6 +406,12 @@ hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipSt
     hipLaunchKernelGGL(qmatvec_kernel<0>, dim3(tiles), dim3(kQThreads), lds, stream, a);
   else if (fmt == 1)
     hipLaunchKernelGGL(qmatvec_kernel<1>, dim3(tiles), dim3(kQThreads), lds, stream, a);
+  else if (fmt == 2)
+    hipLaunchKernelGGL(qkmatvec_kernel<2>, dim3(tiles), dim3(kQThreads),
+                       qkmatvec_lds_bytes(2, a.batch, a.cols, a.rows_per_tile), stream, a);
+  else if (fmt == 3)
+    hipLaunchKernelGGL(qkmatvec_kernel<3>, dim3(tiles), dim3(kQThreads),
+                       qkmatvec_lds_bytes(3, a.batch, a.cols, a.rows_per_tile), stream, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

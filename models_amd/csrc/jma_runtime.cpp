@@ -667,26 +667,39 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
                            uint32_t addend_mode) {
   check_ctx(ctx);
   require(input != nullptr && output != nullptr, JMODELS_ATTN_NULL_POINTER, "null input or output");
-  require(batch > 0 && cols > 0 && cols % 32 == 0, JMODELS_ATTN_INVALID_SHAPE,
-          "batch_size and cols must be > 0 and cols a multiple of 32");
+  require(!mats.empty(), JMODELS_ATTN_INVALID_SHAPE, "no matrices");
+  // Q4_0 / Q8_0 take Q8_0 activations (32-element blocks), the K-quants Q8_K (256): one call
+  // shares one activation format, as backend-native's grouped calls require (RS:1196-1204).
+  const bool kq = mats[0].format == JMODELS_ATTN_WEIGHTS_Q4_K || mats[0].format == JMODELS_ATTN_WEIGHTS_Q6_K;
+  const uint32_t elems = kq ? 256u : 32u;
+  require(batch > 0 && cols > 0 && cols % elems == 0, JMODELS_ATTN_INVALID_SHAPE,
+          "batch_size and cols must be > 0 and cols a multiple of " + std::to_string(elems));
   require(addend_mode <= JMODELS_ATTN_ADDEND_RESIDUAL, JMODELS_ATTN_INVALID_SHAPE,
           "unknown addend_mode " + std::to_string(addend_mode));
   require(((uintptr_t)input & 15u) == 0, JMODELS_ATTN_INVALID_SHAPE,
           "input must be 16-byte aligned");
-  const uint32_t K = cols / 32;
+  const uint32_t K = cols / elems;
+  auto block_bytes = [](uint32_t f) -> uint64_t {
+    return f == JMODELS_ATTN_WEIGHTS_Q4_0 ? 18u : f == JMODELS_ATTN_WEIGHTS_Q8_0 ? 34u
+           : f == JMODELS_ATTN_WEIGHTS_Q4_K ? 144u : 210u;
+  };
   uint64_t total_rows = 0;
   for (size_t i = 0; i < mats.size(); ++i) {
     const QuantMatrix& m = mats[i];
     const std::string at = " (matrix " + std::to_string(i) + ")";
-    require(m.format == JMODELS_ATTN_WEIGHTS_Q4_0 || m.format == JMODELS_ATTN_WEIGHTS_Q8_0,
+    require(m.format == JMODELS_ATTN_WEIGHTS_Q4_0 || m.format == JMODELS_ATTN_WEIGHTS_Q8_0 ||
+                m.format == JMODELS_ATTN_WEIGHTS_Q4_K || m.format == JMODELS_ATTN_WEIGHTS_Q6_K,
             JMODELS_ATTN_INVALID_SHAPE,
             "weight format " + std::to_string(m.format) + " has no device kernel" + at);
+    const bool mkq = m.format == JMODELS_ATTN_WEIGHTS_Q4_K || m.format == JMODELS_ATTN_WEIGHTS_Q6_K;
+    require(mkq == kq, JMODELS_ATTN_INVALID_SHAPE,
+            "one call mixes block formats (Q4_0/Q8_0) with K-quants (Q4_K/Q6_K)" + at);
     require(m.weights != nullptr, JMODELS_ATTN_NULL_POINTER, "null weights" + at);
     require(m.rows > 0, JMODELS_ATTN_INVALID_SHAPE, "rows must be > 0" + at);
     require(((uintptr_t)m.weights & 1u) == 0, JMODELS_ATTN_INVALID_SHAPE,
             "weights must be 2-byte aligned" + at);
     require(addend_mode == 0 || m.addend != nullptr, JMODELS_ATTN_NULL_POINTER, "null addend" + at);
-    const uint64_t need = (uint64_t)m.rows * K * (m.format == JMODELS_ATTN_WEIGHTS_Q4_0 ? 18u : 34u);
+    const uint64_t need = (uint64_t)m.rows * K * block_bytes(m.format);
     require(m.bytes >= need, JMODELS_ATTN_BUFFER_TOO_SMALL,
             "weights hold " + std::to_string(m.bytes) + " bytes, need " + std::to_string(need) + at);
     total_rows += m.rows;
@@ -697,19 +710,27 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(output_elements >= (uint64_t)batch * total_rows, JMODELS_ATTN_BUFFER_TOO_SMALL,
           "output holds " + std::to_string(output_elements) + " elements, needs " +
               std::to_string((uint64_t)batch * total_rows));
-  // Up to 512 (row, block) terms per workgroup (two per thread, all loaded at once); activation
-  // rows per launch as LDS allows (at most 8, within 64 KB).
+  // Up to 512 (row, block) terms per workgroup for the 32-element formats (two per thread, all
+  // loaded at once), 64 for the K-quants (eight threads each); activation rows per launch as LDS
+  // allows (at most 8, within 64 KB).
   constexpr size_t kLds = 64u * 1024u;
-  uint32_t tile = std::max<uint32_t>(1u, std::min<uint32_t>(64u, 512u / K));
-  while (tile > 1 && jma::qmatvec_lds_bytes(1, cols, tile) > kLds) tile /= 2;
-  require(jma::qmatvec_lds_bytes(1, cols, tile) <= kLds, JMODELS_ATTN_INVALID_SHAPE,
+  auto lds = [&](uint32_t nb, uint32_t t) {
+    size_t m = 0;
+    for (const QuantMatrix& q : mats)
+      m = std::max(m, kq ? jma::qkmatvec_lds_bytes(q.format, nb, cols, t)
+                         : jma::qmatvec_lds_bytes(nb, cols, t));
+    return m;
+  };
+  uint32_t tile = std::max<uint32_t>(1u, std::min<uint32_t>(64u, (kq ? 64u : 512u) / K));
+  while (tile > 1 && lds(1, tile) > kLds) tile /= 2;
+  require(lds(1, tile) <= kLds, JMODELS_ATTN_INVALID_SHAPE,
           "cols too large for the device projection: " + std::to_string(cols));
   uint32_t chunk = 8;
-  while (chunk > 1 && jma::qmatvec_lds_bytes(chunk, cols, tile) > kLds) --chunk;
+  while (chunk > 1 && lds(chunk, tile) > kLds) --chunk;
   set_device(ctx);
   for (uint32_t b0 = 0; b0 < batch; b0 += chunk) {
     const uint32_t nb = std::min(chunk, batch - b0);
-    for (uint32_t fmt = 0; fmt < 2; ++fmt) {
+    for (uint32_t fmt = 0; fmt < 4; ++fmt) {
       jma::QMatArgs a{};
       a.x = input + (uint64_t)b0 * cols;
       a.batch = nb;

@@ -970,10 +970,148 @@ void jmo_q8_0_quantize(const float* x, int batch, int cols, int8_t* q, float* sc
   }
 }
 
+void jmo_q8_k_quantize(const float* x, int batch, int cols, int8_t* q, float* scales,
+                       int16_t* sums) {
+  const int blocks = cols / 256;
+  for (int b = 0; b < batch; b++) {
+    for (int blk = 0; blk < blocks; blk++) {
+      const size_t off = (size_t)b * cols + (size_t)blk * 256;
+      const float* v = x + off;
+      float max = 0.0f, absmax = 0.0f;
+      for (int i = 0; i < 256; i++) {
+        const float a = fabsf(v[i]);
+        if (a > absmax) { /* strict: the first of equal magnitudes wins; NaN compares false */
+          absmax = a;
+          max = v[i];
+        }
+      }
+      int16_t* s16 = sums + (size_t)b * (cols / 16) + (size_t)blk * 16;
+      if (absmax == 0.0f) {
+        memset(q + off, 0, 256);
+        memset(s16, 0, 16 * sizeof(int16_t));
+        scales[(size_t)b * blocks + blk] = 0.0f;
+        continue;
+      }
+      const float inverse = -127.0f / max;
+      int block_sum = 0;
+      for (int i = 0; i < 256; i++) {
+        const float scaled = inverse * v[i];
+        int quant = ggml_nearest_int(scaled);
+        if (quant > 127) quant = 127;
+        q[off + i] = (int8_t)quant;
+        block_sum += (int8_t)quant;
+        if ((i + 1) % 16 == 0) {
+          s16[i / 16] = (int16_t)block_sum;
+          block_sum = 0;
+        }
+      }
+      scales[(size_t)b * blocks + blk] = 1.0f / inverse;
+    }
+  }
+}
+
+/* qk_scale / qk_min (RS:3861-3878): 6-bit scale and min of 32-element group g of a Q4_K block. */
+static int qk_scale(const uint8_t* sc, int g) {
+  if (g < 4) return sc[g] & 0x3f;
+  return (sc[g + 4] & 0x0f) | ((sc[g - 4] >> 6) << 4);
+}
+static int qk_min(const uint8_t* sc, int g) {
+  if (g < 4) return sc[g + 4] & 0x3f;
+  return (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+}
+
+static float kquant_row(int format, const uint8_t* w_row, const int8_t* aq, const float* ascale,
+                        const int16_t* asum, int blocks) {
+  if (format == JMO_FMT_Q4_K) {
+    float sum = 0.0f;
+    for (int blk = 0; blk < blocks; blk++) {
+      const uint8_t* w = w_row + (size_t)blk * 144;
+      const float d = jmo_f16_to_float((uint16_t)(w[0] | (w[1] << 8))) * ascale[blk];
+      const float dmin = jmo_f16_to_float((uint16_t)(w[2] | (w[3] << 8))) * ascale[blk];
+      const uint8_t* sc = w + 4;
+      const uint8_t* qs = w + 16;
+      const int8_t* a = aq + (size_t)blk * 256;
+      const int16_t* s16 = asum + (size_t)blk * 16;
+      int qsum = 0, msum = 0;
+      for (int g = 0; g < 8; g++) {
+        const uint8_t* packed = qs + (g >> 1) * 32;
+        const int shift = (g & 1) * 4;
+        int dot = 0;
+        for (int i = 0; i < 32; i++) dot += ((packed[i] >> shift) & 0x0f) * a[g * 32 + i];
+        qsum += qk_scale(sc, g) * dot;
+        msum += qk_min(sc, g) * (s16[2 * g] + s16[2 * g + 1]);
+      }
+      sum = fmaf(d, (float)qsum, sum);
+      sum = fmaf(-dmin, (float)msum, sum);
+    }
+    return sum;
+  }
+  /* Q6_K */
+  float lane_sums[8] = {0};
+  for (int blk = 0; blk < blocks; blk++) {
+    const uint8_t* w = w_row + (size_t)blk * 210;
+    const float d = jmo_f16_to_float((uint16_t)(w[208] | (w[209] << 8))) * ascale[blk];
+    const uint8_t* ql = w;
+    const uint8_t* qh = w + 128;
+    const int8_t* sc = (const int8_t*)(w + 192);
+    const int8_t* a = aq + (size_t)blk * 256;
+    int isum[8] = {0};
+    for (int sb = 0; sb < 2; sb++) {
+      for (int i = 0; i < 32; i++) {
+        const int si = i / 16;
+        const int l1 = ql[sb * 64 + i], l2 = ql[sb * 64 + 32 + i], hi = qh[sb * 32 + i];
+        const int q1 = ((l1 & 0x0f) | ((hi & 3) << 4)) - 32;
+        const int q2 = ((l2 & 0x0f) | (((hi >> 2) & 3) << 4)) - 32;
+        const int q3 = ((l1 >> 4) | (((hi >> 4) & 3) << 4)) - 32;
+        const int q4 = ((l2 >> 4) | (((hi >> 6) & 3) << 4)) - 32;
+        const int8_t* aa = a + sb * 128;
+        int* acc = &isum[i & 7];
+        *acc += sc[sb * 8 + si] * q1 * aa[i];
+        *acc += sc[sb * 8 + si + 2] * q2 * aa[i + 32];
+        *acc += sc[sb * 8 + si + 4] * q3 * aa[i + 64];
+        *acc += sc[sb * 8 + si + 6] * q4 * aa[i + 96];
+      }
+    }
+    for (int l = 0; l < 8; l++) lane_sums[l] = fmaf(d, (float)isum[l], lane_sums[l]);
+  }
+  float sum = 0.0f;
+  for (int l = 0; l < 8; l++) sum += lane_sums[l];
+  return sum;
+}
+
+static int kquant_matmul(int format, const uint8_t* weights, const float* input, int batch,
+                         int rows, int cols, float* out) {
+  const int blocks = cols / 256;
+  const int block_bytes = format == JMO_FMT_Q4_K ? 144 : 210;
+  int8_t* q = (int8_t*)malloc((size_t)batch * cols);
+  float* scales = (float*)malloc((size_t)batch * blocks * sizeof(float));
+  int16_t* sums = (int16_t*)malloc((size_t)batch * (cols / 16) * sizeof(int16_t));
+  if (!q || !scales || !sums) {
+    free(q);
+    free(scales);
+    free(sums);
+    return JMO_ILLEGAL_STATE;
+  }
+  jmo_q8_k_quantize(input, batch, cols, q, scales, sums);
+  for (int b = 0; b < batch; b++)
+    for (int r = 0; r < rows; r++)
+      out[(size_t)b * rows + r] =
+          kquant_row(format, weights + (size_t)r * blocks * block_bytes, q + (size_t)b * cols,
+                     scales + (size_t)b * blocks, sums + (size_t)b * (cols / 16), blocks);
+  free(q);
+  free(scales);
+  free(sums);
+  return JMO_OK;
+}
+
 int jmo_quantized_matmul(int format, const uint8_t* weights, const float* input, int batch,
                          int rows, int cols, float* out) {
-  if ((format != JMO_FMT_Q4_0 && format != JMO_FMT_Q8_0) || cols <= 0 || cols % 32 != 0 ||
-      rows <= 0 || batch <= 0)
+  if (rows <= 0 || batch <= 0 || cols <= 0) return JMO_ILLEGAL_ARGUMENT;
+  if (format == JMO_FMT_Q4_K || format == JMO_FMT_Q6_K) {
+    if (cols % 256 != 0) return JMO_ILLEGAL_ARGUMENT;
+    return kquant_matmul(format, weights, input, batch, rows, cols, out);
+  }
+  if ((format != JMO_FMT_Q4_0 && format != JMO_FMT_Q8_0) || cols % 32 != 0)
     return JMO_ILLEGAL_ARGUMENT;
   const int blocks = cols / 32;
   const int block_bytes = format == JMO_FMT_Q4_0 ? 18 : 34;

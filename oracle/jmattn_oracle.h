@@ -195,6 +195,8 @@ int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* ke
  * NativeKernelLibraryTest.java:67-84 with :909-1023). */
 #define JMO_FMT_Q4_0 0 /* 18-byte blocks: f16 scale, 16 bytes of nibbles (RS:87) */
 #define JMO_FMT_Q8_0 1 /* 34-byte blocks: f16 scale, 32 int8 (RS:89) */
+#define JMO_FMT_Q4_K 2 /* 144-byte blocks of 256: d, dmin, 12 bytes of 6-bit scales/mins, nibbles (RS:90) */
+#define JMO_FMT_Q6_K 3 /* 210-byte blocks of 256: ql[128], qh[64], int8 scales[16], d (RS:92) */
 
 /* quantizeInputs (NativeKernelLibraryTest.java:998-1017; RS quantize_q8_0_batch_scalar): per
  * 32-element block, absmax (a NaN element is skipped, as Rust's f32::max does), inverse scale
@@ -202,10 +204,23 @@ int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* ke
  * ggmlNearestInt(x * inverse) (:1019-1022). q [batch*cols], scales [batch*cols/32]. */
 void jmo_q8_0_quantize(const float* x, int batch, int cols, int8_t* q, float* scales);
 
+/* quantize_q8_k_batch (RS:3906-3952), the activations of the K-quant formats: per 256-element
+ * block, the element of largest magnitude (the first on ties; NaN skipped) sets
+ * inverse = -127 / max; element = min(nearest(inverse * x), 127); sums of 16 consecutive
+ * elements; scale = 1 / inverse; an all-zero block has scale 0, elements 0, sums 0.
+ * q [batch*cols], scales [batch*cols/256], sums [batch*cols/16]. */
+void jmo_q8_k_quantize(const float* x, int batch, int cols, int8_t* q, float* scales,
+                       int16_t* sums);
+
 /* referenceQ4_0F32BatchedMatmul / referenceQ8_0F32BatchedMatmul (NativeKernelLibraryTest.java:
  * 909-936, 938-965): out[b*rows + r] = sum over blocks in order of
- * fma(weightScale * activationScale, integerDot, sum). JMO_ILLEGAL_ARGUMENT for an unknown format
- * or cols not a multiple of 32. */
+ * fma(weightScale * activationScale, integerDot, sum). Q4_K and Q6_K with Q8_K activations as
+ * backend-native's scalar row kernels compute them (dot_q4_k_q8_k_row_scalar, RS:3410-3459:
+ * per block sum = fma(d, sum_g scale_g * dot_g, sum) then fma(-dmin, sum_g min_g * sums_g, sum),
+ * d and dmin the weight's f16 factors times the activation scale; dot_q6_k_q8_k_row_scalar,
+ * RS:3519-3577: eight integer lane sums per block (lane = element index within its 32-run mod 8),
+ * eight fma chains over the blocks, the lanes added in order at the end). JMO_ILLEGAL_ARGUMENT for
+ * an unknown format or cols not a multiple of the block size (32, or 256 for K-quants). */
 int jmo_quantized_matmul(int format, const uint8_t* weights, const float* input, int batch,
                          int rows, int cols, float* out);
 

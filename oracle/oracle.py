@@ -25,6 +25,12 @@ rms_norm / qk_norm_heads    TensorOpsTest.RmsNorm known answers (:42-67); float6
 q8_0 activation quantize    ggmlNearestInt == IEEE round-half-even (numpy rint) over the int8
                             range and ties; scales == numpy float16 of absmax/127; zero and NaN
                             blocks; every |q| <= 127 and q * scale within half a step of x
+q8_k activation quantize    numpy: sign-aware block maximum (first index on ties), rint,
+                            clamp at 127, 16-element sums, scale 1 / inverse
+quantized matmul Q4_K/Q6_K  NativeKernelLibraryTest's block builders (q4KBlock, q6KBlock) whose
+                            logical scales, mins and quants numpy's dequantization must recover;
+                            float64 product of the dequantized blocks (one rounding per term of the
+                            fma chains)
 quantized matmul Q4_0/Q8_0  float64 dot of the dequantized weights with the dequantized Q8_0
                             activations (rounding of the per-block fma chain only); hand-computed
                             one-block cases (nibble order, the -8 offset, scale product); the
@@ -149,6 +155,7 @@ def _declare(L: ctypes.CDLL) -> None:
                                        ctypes.POINTER(_f32p), _i32p, c_int, c_int, c_int, c_int,
                                        c_int, c_int, c_float, ctypes.POINTER(_f32p), c_int]),
         "jmo_q8_0_quantize": (None, [_f32p, c_int, c_int, c_void, _f32p]),
+        "jmo_q8_k_quantize": (None, [_f32p, c_int, c_int, c_void, _f32p, c_void]),
         "jmo_quantized_matmul": (c_int, [c_int, c_void, _f32p, c_int, c_int, c_int, _f32p]),
     }
     for name, (res, args) in sig.items():
@@ -530,7 +537,23 @@ def gqa_rows_batch(qs, keys_list, values_list, num_heads, num_kv_heads, key_leng
 
 FMT_Q4_0 = 0
 FMT_Q8_0 = 1
-BLOCK_BYTES = {FMT_Q4_0: 18, FMT_Q8_0: 34}
+FMT_Q4_K = 2
+FMT_Q6_K = 3
+BLOCK_BYTES = {FMT_Q4_0: 18, FMT_Q8_0: 34, FMT_Q4_K: 144, FMT_Q6_K: 210}
+BLOCK_ELEMS = {FMT_Q4_0: 32, FMT_Q8_0: 32, FMT_Q4_K: 256, FMT_Q6_K: 256}
+
+
+def q8_k_quantize(x, batch: int, cols: int):
+    """quantize_q8_k_batch (RS:3906-3952): (int8 [batch*cols], scales [batch*cols/256],
+    int16 sums [batch*cols/16])."""
+    x = _f32(x)
+    if x.size != batch * cols or cols % 256:
+        raise OracleError(ILLEGAL_ARGUMENT, "q8_k_quantize shape")
+    q = np.empty(batch * cols, np.int8)
+    scales = np.empty(batch * cols // 256, np.float32)
+    sums = np.empty(batch * cols // 16, np.int16)
+    lib().jmo_q8_k_quantize(_ptr(x), batch, cols, q.ctypes.data, _ptr(scales), sums.ctypes.data)
+    return q, scales, sums
 
 
 def q8_0_quantize(x, batch: int, cols: int):
@@ -551,8 +574,8 @@ def quantized_matmul(fmt: int, weights, x, batch: int, rows: int, cols: int) -> 
         weights = np.frombuffer(bytes(weights), np.uint8)
     w = np.ascontiguousarray(weights, dtype=np.uint8).reshape(-1)
     x = _f32(x)
-    if fmt not in BLOCK_BYTES or cols % 32 or w.size < rows * cols // 32 * BLOCK_BYTES[fmt] \
-            or x.size != batch * cols:
+    if fmt not in BLOCK_BYTES or cols % BLOCK_ELEMS[fmt] \
+            or w.size < rows * cols // BLOCK_ELEMS[fmt] * BLOCK_BYTES[fmt] or x.size != batch * cols:
         raise OracleError(ILLEGAL_ARGUMENT, "quantized_matmul shape")
     out = np.empty(batch * rows, np.float32)
     _check(lib().jmo_quantized_matmul(fmt, w.ctypes.data, _ptr(x), batch, rows, cols, _ptr(out)),

@@ -386,6 +386,70 @@ def quantized_matmul_cases():
         cases.append({"name": name, "src": "NativeKernelLibraryTest.java" + src, "format": 0,
                       "batch": batch, "rows": rows, "cols": 64, "relation": "exact",
                       "input": activations(batch, 64), "weights_hex": q4_0_weights(rows, 64)})
+    # K-quant blocks (q4KBlock :740-764, q6KBlock :830-858, q6Quant :860-862), each with the
+    # logical values its builder encodes (what a correct dequantization must recover), under the
+    # reference's K-quant relation (K_QUANT_REDUCTION_TOLERANCE 2e-3, :36).
+    q4_scales = [5, 12, 30, 60, 7, 15, 31, 63]
+    q4_mins = [3, 8, 20, 45, 1, 10, 25, 50]
+
+    def q4_k(rows, cols):
+        out, quants = bytearray(), []
+        for row in range(rows):
+            for block in range(cols // 256):
+                b = bytearray(144)
+                b[0:2] = _f16_bits((row + 1) * 0.03125).to_bytes(2, "little")
+                b[2:4] = _f16_bits((block + 1) * 0.015625).to_bytes(2, "little")
+                for g in range(4):
+                    b[4 + g] = q4_scales[g]
+                    b[8 + g] = q4_mins[g]
+                for g in range(4, 8):
+                    b[8 + g] = (q4_scales[g] & 0x0F) | ((q4_mins[g] & 0x0F) << 4)
+                    b[g] |= (q4_scales[g] >> 4) << 6
+                    b[4 + g] |= (q4_mins[g] >> 4) << 6
+                qv = []
+                for g in range(8):
+                    off, shift = 16 + (g >> 1) * 32, (g & 1) * 4
+                    for i in range(32):
+                        quant = (row * 13 + block * 7 + g * 5 + i * 3) & 0x0F
+                        b[off + i] |= quant << shift
+                        qv.append(quant)
+                quants.append(qv)
+                out += b
+        return out.hex(), quants
+
+    def q6_k(rows, cols):
+        out, quants, scales = bytearray(), [], []
+        for row in range(rows):
+            for block in range(cols // 256):
+                b = bytearray(210)
+                sc = [(row * 5 + block * 3 + i * 7) % 17 - 8 for i in range(16)]
+                for i in range(16):
+                    b[192 + i] = sc[i] & 0xFF
+                b[208:210] = _f16_bits((row + block + 1) * 0.015625).to_bytes(2, "little")
+                qv = [(row * 19 + block * 11 + i * 7) % 64 - 32 for i in range(256)]
+                for sb in range(2):
+                    pb, lb, hb = sb * 128, sb * 64, 128 + sb * 32
+                    for i in range(32):
+                        q1, q2, q3, q4 = (qv[pb + i + 32 * t] + 32 for t in range(4))
+                        b[lb + i] = (q1 & 0x0F) | ((q3 & 0x0F) << 4)
+                        b[lb + 32 + i] = (q2 & 0x0F) | ((q4 & 0x0F) << 4)
+                        b[hb + i] = (((q1 >> 4) & 3) | (((q2 >> 4) & 3) << 2) | (((q3 >> 4) & 3) << 4)
+                                     | (((q4 >> 4) & 3) << 6))
+                quants.append(qv)
+                scales.append(sc)
+                out += b
+        return out.hex(), quants, scales
+
+    hx, quants = q4_k(5, 512)
+    cases.append({"name": "reusableGgufKernelMatchesVectorSemanticsForKQuantizedBatchedMultiplication[Q4_K]",
+                  "src": "NativeKernelLibraryTest.java:246-271", "format": 2, "batch": 3, "rows": 5,
+                  "cols": 512, "relation": 2e-3, "input": activations(3, 512), "weights_hex": hx,
+                  "logical": {"scales": q4_scales, "mins": q4_mins, "quants": quants}})
+    hx, quants, scales = q6_k(5, 512)
+    cases.append({"name": "reusableGgufKernelMatchesVectorSemanticsForKQuantizedBatchedMultiplication[Q6_K]",
+                  "src": "NativeKernelLibraryTest.java:246-271", "format": 3, "batch": 3, "rows": 5,
+                  "cols": 512, "relation": 2e-3, "input": activations(3, 512), "weights_hex": hx,
+                  "logical": {"quants": quants, "scales": scales}})
     cases.append({"name": "reusableGgufKernelComputesQ8_0BatchedMatrixMultiplicationWithinReductionTolerance",
                   "src": "NativeKernelLibraryTest.java:176-196", "format": 1, "batch": 3, "rows": 5,
                   "cols": 64, "relation": 2e-5, "input": activations(3, 64),

@@ -54,6 +54,19 @@ def _exact(got, want, what):
                              f"at {i}: {got.reshape(-1)[i]!r} vs {want.reshape(-1)[i]!r}")
 
 
+def _kquant_weights(fmt, rows, cols, key):
+    nbytes = 144 if fmt == A.WEIGHTS_Q4_K else 210
+    raw = synth.uniform_int(11, key, rows * cols // 256 * nbytes, 0, 255).astype(np.uint8)
+    raw = raw.reshape(rows, cols // 256, nbytes)
+    d = (synth.normal(11, key + "/d", (rows, cols // 256, 2)) * 0.002).astype(np.float16)
+    d = d.view(np.uint8).reshape(rows, cols // 256, 4)
+    if fmt == A.WEIGHTS_Q4_K:
+        raw[:, :, 0:4] = d
+    else:
+        raw[:, :, 208:210] = d[..., :2]
+    return raw.reshape(-1)
+
+
 def test_reference_fixtures_bit_exact(hip, known_answers):
     """NativeKernelLibraryTest's own cases (fixtures regenerated as data): the device result is the
     oracle's bit for bit, which is the relation the reference asserts for Q4_0 (containsExactly)
@@ -82,6 +95,57 @@ def test_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
     got = hip.quantized_matmul(fmt, w, x, batch, rows, cols)
     want = oracle.quantized_matmul(fmt, w, x, batch, rows, cols)
     _exact(got, want, f"fmt {fmt} {batch}x{rows}x{cols}")
+
+
+@pytest.mark.parametrize("fmt", [A.WEIGHTS_Q4_K, A.WEIGHTS_Q6_K])
+@pytest.mark.parametrize("batch,rows,cols", [(1, 1, 256), (1, 3072, 2048), (3, 17, 4096),
+                                             (9, 100, 512), (1, 64, 14336)])
+def test_kquant_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
+    """Q4_K and Q6_K with Q8_K activations: the device repeats backend-native's scalar row
+    kernels' float order (the integer parts are exact in any order), so the outputs are the
+    oracle's bits; batches over 8 run in chunks."""
+    w = _kquant_weights(fmt, rows, cols, f"kq/{fmt}/{rows}/{cols}")
+    x = synth.normal(11, f"kq/x/{batch}/{cols}", (batch, cols)) * 1.5
+    got = hip.quantized_matmul(fmt, w, x, batch, rows, cols)
+    want = oracle.quantized_matmul(fmt, w, x, batch, rows, cols)
+    _exact(got, want, f"fmt {fmt} {batch}x{rows}x{cols}")
+
+
+def test_kquant_activation_edge_cases_and_grouped_q4_k_m(hip):
+    """Q8_K edge cases (an all-zero block, equal magnitudes of opposite sign where the first sets
+    the sign, a NaN skipped by the maximum) through a Q4_K_M-style grouped call: Q and K in Q4_K,
+    V in Q6_K, one launch per format; and a call mixing Q4_0 with a K-quant is refused."""
+    cols, rows = 1024, [1024, 256, 256]
+    fmts = [A.WEIGHTS_Q4_K, A.WEIGHTS_Q4_K, A.WEIGHTS_Q6_K]
+    ws = [_kquant_weights(f, r, cols, f"km/{i}") for i, (f, r) in enumerate(zip(fmts, rows))]
+    x = synth.normal(11, "km/x", (3, cols))
+    x[0, :256] = 0.0
+    x[1, 256:512] *= 0.1
+    x[1, 300], x[1, 310] = -4.0, 4.0
+    x[2, 600] = np.nan
+    dws = [rt.DeviceArray.from_host(w) for w in ws]
+    dx = rt.DeviceArray.from_host(x)
+    dout = rt.DeviceArray(3 * sum(rows))
+    try:
+        hip.quantized_grouped_matmul_device(fmts, [d.ptr for d in dws], [w.size for w in ws], rows,
+                                            dx.ptr, x.size, dout.ptr, 3 * sum(rows), 3, cols)
+        hip.synchronize()
+        got, off = dout.download(), 0
+        for i, (f, r) in enumerate(zip(fmts, rows)):
+            _exact(got[off:off + 3 * r].reshape(3, r), oracle.quantized_matmul(f, ws[i], x, 3, r, cols),
+                   f"Q4_K_M matrix {i}")
+            off += 3 * r
+        q40 = _weights(A.WEIGHTS_Q4_0, 8, cols, "km/q40")
+        d40 = rt.DeviceArray.from_host(q40)
+        with pytest.raises(A.AttentionStatusError) as info:
+            hip.quantized_grouped_matmul_device([A.WEIGHTS_Q4_0, A.WEIGHTS_Q4_K], [d40.ptr, dws[0].ptr],
+                                                [q40.size, ws[0].size], [8, rows[0]], dx.ptr, x.size,
+                                                dout.ptr, 3 * sum(rows), 1, cols)
+        assert info.value.status == A.INVALID_SHAPE
+        d40.free()
+    finally:
+        for d in dws + [dx, dout]:
+            d.free()
 
 
 def test_non_finite_and_zero_activations_bit_exact(hip):
@@ -240,7 +304,9 @@ def test_rejections(hip):
                 xe, out.ptr, oe, batch, rows, cols, add, mode)
         assert call() == A.OK
         hip.synchronize()
-        for fmt in (2, 3, 4, 5, 99):
+        for fmt in (4, 5, 99):  # Q5_K, Q5_0: no device kernel
+            assert call(fmt=fmt) == A.INVALID_SHAPE
+        for fmt in (2, 3):  # K-quants need cols a multiple of 256
             assert call(fmt=fmt) == A.INVALID_SHAPE
         assert call(cols=48, rows=1) == A.INVALID_SHAPE
         assert call(rows=0) == A.INVALID_SHAPE

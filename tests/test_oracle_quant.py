@@ -147,6 +147,8 @@ def test_quantized_matmul_rows_and_batches_are_independent(oracle):
 
 def test_reference_fixtures_against_float64(oracle, known_answers):
     for case in known_answers["quantized_matmul"]:
+        if case["format"] not in (0, 1):
+            continue  # the K-quant cases: test_kquant_matmul_matches_float64
         w = bytes.fromhex(case["weights_hex"])
         b, r, c = case["batch"], case["rows"], case["cols"]
         x = np.float32(case["input"])
@@ -160,3 +162,145 @@ def test_quantized_matmul_rejects_bad_shapes(oracle):
         oracle.quantized_matmul(0, bytes(18), np.zeros(31, np.float32), 1, 1, 31)
     with pytest.raises(oracle.OracleError):
         oracle.quantized_matmul(7, bytes(18), np.zeros(32, np.float32), 1, 1, 32)
+
+
+# ------------------------------------------------------------------ K-quants (Q8_K activations)
+
+def _q8_k_numpy(x, cols):
+    """Q8_K from numpy's float32 ops: the block's largest-magnitude element (first on ties, NaN
+    skipped) sets inverse = -127 / max; q = min(rint(inverse * x), 127); 16-element sums;
+    scale = 1 / inverse."""
+    x = np.asarray(x, np.float32).reshape(-1, 256)
+    q = np.zeros(x.shape, np.int32)
+    scales = np.zeros(x.shape[0], np.float32)
+    for i, v in enumerate(x):
+        a = np.where(np.isnan(v), np.float32(-1), np.abs(v))
+        k = int(np.argmax(a))  # first index of the largest magnitude
+        if a[k] <= 0:
+            continue
+        inverse = np.float32(-127) / v[k]
+        with np.errstate(invalid="ignore"):
+            scaled = (inverse * v).astype(np.float32)
+        q[i] = np.minimum(np.where(np.isnan(scaled), 0, np.rint(scaled)), 127)
+        scales[i] = np.float32(1) / inverse
+    sums = q.reshape(-1, 16).sum(axis=1)
+    return q.reshape(-1).astype(np.int8), scales, sums.astype(np.int16)
+
+
+def _dequant_q4_k(w, rows, cols):
+    """GGML Q4_K (144-byte blocks of 256): d, dmin, 6-bit scales and mins of 8 groups packed in 12
+    bytes, group g's 32 nibbles in bytes 32(g/2) .. +31 (low nibble for even g)."""
+    b = np.frombuffer(bytes(w), np.uint8).reshape(rows, cols // 256, 144)
+    d = b[:, :, 0:2].copy().view(np.float16).astype(np.float32)[..., 0]
+    dmin = b[:, :, 2:4].copy().view(np.float16).astype(np.float32)[..., 0]
+    sc = b[:, :, 4:16].astype(np.int32)
+    scales = np.zeros((rows, cols // 256, 8), np.int32)
+    mins = np.zeros_like(scales)
+    scales[..., :4] = sc[..., 0:4] & 63
+    mins[..., :4] = sc[..., 4:8] & 63
+    scales[..., 4:] = (sc[..., 8:12] & 15) | ((sc[..., 0:4] >> 6) << 4)
+    mins[..., 4:] = (sc[..., 8:12] >> 4) | ((sc[..., 4:8] >> 6) << 4)
+    qs = b[:, :, 16:144].astype(np.int32).reshape(rows, cols // 256, 4, 32)
+    quants = np.stack([qs & 15, qs >> 4], axis=3).reshape(rows, cols // 256, 8, 32)
+    return d, dmin, scales, mins, quants
+
+
+def _dequant_q6_k(w, rows, cols):
+    """GGML Q6_K (210-byte blocks of 256): element 128h + 32t + i of half h takes the low nibble
+    of ql[64h + i (+32 for t odd)] (high nibble for t >= 2) and bits 2t..2t+1 of qh[32h + i] as
+    its top two bits, minus 32; int8 scale per 16 elements; f16 d at byte 208."""
+    b = np.frombuffer(bytes(w), np.uint8).reshape(rows, cols // 256, 210).astype(np.int32)
+    q = np.zeros((rows, cols // 256, 256), np.int32)
+    for h in range(2):
+        ql = b[..., 64 * h:64 * h + 64]
+        qh = b[..., 128 + 32 * h:128 + 32 * h + 32]
+        for t in range(4):
+            low = (ql[..., 32 * (t & 1):32 * (t & 1) + 32] >> (4 * (t >> 1))) & 15
+            q[..., 128 * h + 32 * t:128 * h + 32 * t + 32] = (low | (((qh >> (2 * t)) & 3) << 4)) - 32
+    scales = b[..., 192:208].astype(np.int8).astype(np.int32)
+    d = np.frombuffer(bytes(w), np.uint8).reshape(rows, cols // 256, 210)[..., 208:210].copy()
+    d = d.view(np.float16).astype(np.float32)[..., 0]
+    return d, scales, q
+
+
+def _float64_kquant(fmt, w, x, batch, rows, cols):
+    q, ascale, asum = _q8_k_numpy(x, cols)
+    nb = cols // 256
+    q = q.reshape(batch, nb, 256).astype(np.int64)
+    ascale = ascale.reshape(batch, nb)
+    if fmt == 2:
+        d, dmin, scales, mins, quants = _dequant_q4_k(w, rows, cols)
+        dots = np.einsum("rkgj,bkgj->brkg", quants.astype(np.int64), q.reshape(batch, nb, 8, 32))
+        qsum = (dots * scales[None]).sum(axis=3)
+        gsum = asum.reshape(batch, nb, 8, 2).sum(axis=3).astype(np.int64)
+        msum = (mins[None] * gsum[:, None]).sum(axis=3)
+        dd = (d[None] * ascale[:, None]).astype(np.float32).astype(np.float64)
+        dm = (dmin[None] * ascale[:, None]).astype(np.float32).astype(np.float64)
+        terms = np.stack([dd * qsum, -dm * msum], axis=-1)
+    else:
+        d, scales, quants = _dequant_q6_k(w, rows, cols)
+        per16 = scales.repeat(16, axis=2)  # scale of each element
+        prods = np.einsum("rke,bke->brk", (quants * per16).astype(np.int64), q)
+        dd = (d[None] * ascale[:, None]).astype(np.float32).astype(np.float64)
+        terms = (dd * prods)[..., None]
+    return terms.sum(axis=(2, 3)), np.abs(terms).sum(axis=(2, 3)), terms.shape[2] * terms.shape[3] + 8
+
+
+def test_q8_k_quantize_matches_numpy(oracle):
+    x = synth.normal(7, "q8k/x", (6 * 256,)) * 2.0
+    x[:256] = 0.0                              # zero block
+    x[256:512] *= 0.1
+    x[256 + 10] = 5.0                          # ties of magnitude: the first one sets the sign
+    x[256 + 20] = -5.0
+    x[512 + 3] = np.nan                        # NaN skipped by the maximum
+    x[768:1024] = np.linspace(-127, 127, 256)  # max 127 at the end: inverse -1
+    q, s, sums = oracle.q8_k_quantize(x, 1, 6 * 256)
+    q_ref, s_ref, sums_ref = _q8_k_numpy(x, 6 * 256)
+    np.testing.assert_array_equal(q, q_ref)
+    np.testing.assert_array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(sums, sums_ref)
+    assert s[0] == 0 and not q[:256].any()
+    assert s[1] < 0  # first of +5 / -5 is +5: inverse -127 / 5, scale -5 / 127
+    assert int(q[256 + 10]) == -127 and int(q[256 + 20]) == 127
+
+
+@pytest.mark.parametrize("fmt", [2, 3])
+def test_kquant_fixture_blocks_dequantize_to_their_logical_values(known_answers, fmt):
+    """The reference test's block builders record what each element means; numpy's GGML
+    dequantization recovers exactly that, which pins the layouts the float64 check below uses."""
+    case = next(c for c in known_answers["quantized_matmul"] if c["format"] == fmt)
+    w, rows, cols = bytes.fromhex(case["weights_hex"]), case["rows"], case["cols"]
+    lg = case["logical"]
+    if fmt == 2:
+        d, dmin, scales, mins, quants = _dequant_q4_k(w, rows, cols)
+        assert (scales == np.array(lg["scales"])).all() and (mins == np.array(lg["mins"])).all()
+        np.testing.assert_array_equal(quants.reshape(-1, 256), np.array(lg["quants"]))
+        np.testing.assert_array_equal(d[:, 0], (np.arange(rows) + 1) * 0.03125)
+    else:
+        d, scales, quants = _dequant_q6_k(w, rows, cols)
+        np.testing.assert_array_equal(quants.reshape(-1, 256), np.array(lg["quants"]))
+        np.testing.assert_array_equal(scales.reshape(-1, 16), np.array(lg["scales"]))
+
+
+@pytest.mark.parametrize("fmt", [2, 3])
+def test_kquant_matmul_matches_float64(oracle, known_answers, fmt):
+    cases = [c for c in known_answers["quantized_matmul"] if c["format"] == fmt]
+    rnd = _random_kquant(fmt, 9, 1024, f"kq/{fmt}")
+    for w, x, b, r, c in [(bytes.fromhex(k["weights_hex"]), np.float32(k["input"]), k["batch"],
+                           k["rows"], k["cols"]) for k in cases] + [
+            (rnd, synth.normal(7, f"kq/x{fmt}", (2, 1024)), 2, 9, 1024)]:
+        out = oracle.quantized_matmul(fmt, w, x, b, r, c)
+        ref, mag, n = _float64_kquant(fmt, w, x, b, r, c)
+        assert np.all(np.abs(out.astype(np.float64) - ref) <= n * 2.0 ** -24 * mag + 1e-30), fmt
+
+
+def _random_kquant(fmt, rows, cols, key):
+    nbytes = 144 if fmt == 2 else 210
+    raw = synth.uniform_int(7, key, rows * cols // 256 * nbytes, 0, 255).astype(np.uint8)
+    raw = raw.reshape(rows, cols // 256, nbytes)
+    d = (synth.normal(7, key + "/d", (rows, cols // 256, 2)) * 0.01).astype(np.float16).view(np.uint8)
+    if fmt == 2:
+        raw[:, :, 0:4] = d.reshape(rows, cols // 256, 4)
+    else:
+        raw[:, :, 208:210] = d.reshape(rows, cols // 256, 4)[..., :2]
+    return raw.reshape(-1).tobytes()
