@@ -27,6 +27,7 @@ namespace jma {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 
 // Lambdas over shared state must inline, or the captured state (accumulators included) would be
 // spilled to scratch memory.
@@ -366,6 +367,10 @@ __device__ __forceinline__ float4_t load_part(__amdgpu_buffer_rsrc_t rs, uint32_
   return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCoherent);
 }
 
+__device__ __forceinline__ float2_t load_part2(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kCoherent);
+}
+
 __device__ __forceinline__ void store_part(__amdgpu_buffer_rsrc_t rs, uint32_t off, float4_t v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kCoherent);
 }
@@ -439,7 +444,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
   constexpr uint32_t kQ4 = DV / 4;   // quads per head
   constexpr int kI = B / SUB;        // splits one thread takes
   static_assert(SUB == 1 || SUB == 2 || SUB == 4 || SUB == 8, "sub-threads per quad");
-  static_assert(kI <= 8, "splits per thread");
+  static_assert(kI <= 32, "splits per thread");
   const uint32_t tid = threadIdx.x;
   const uint32_t E4 = nreal * kQ4;
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(part);
@@ -456,12 +461,13 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
       const uint32_t g = r + SUB * i;
       return qok && g < ns && g != split;
     };
-    float4_t xv[kI], mv[kI];
+    float4_t xv[kI];
+    float2_t mv[kI];
 #pragma unroll
     for (int i = 0; i < kI; ++i) {
       const uint32_t w = base(r + SUB * i, hs);
       xv[i] = needed(i) ? load_part(rs, w + e * 4) : float4_t{0.f, 0.f, 0.f, 0.f};
-      mv[i] = needed(i) ? load_part(rs, w + DV * 4) : float4_t{0.f, 0.f, 0.f, 0.f};
+      mv[i] = needed(i) ? load_part2(rs, w + DV * 4) : float2_t{0.f, 0.f};
     }
     float mx, lw;  // this workgroup's own partial, while the loads are in flight
     float4_t own;
@@ -484,7 +490,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
         if (!needed(i)) continue;
         const uint32_t w = base(r + SUB * i, hs);
         if (!written(xv[i])) xv[i] = load_part(rs, w + e * 4);
-        if (!written(float4_t{mv[i][0], mv[i][1], mv[i][0], mv[i][1]})) mv[i] = load_part(rs, w + DV * 4);
+        if (!written(float4_t{mv[i][0], mv[i][1], mv[i][0], mv[i][1]})) mv[i] = load_part2(rs, w + DV * 4);
       }
     }
     // Per-thread maximum, then the maximum over the quad's SUB threads.
@@ -1103,14 +1109,19 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     // workgroup's threads when the head group has few quads.
     constexpr int kSubMax = kW;  // 64 * kW threads over >= 64 quads
     const bool narrow = nreal * (DV / 4) * kSubMax <= 64 * kW;
+    // One quad per thread covers every quad of the group in one poll round; only the four-wave
+    // instances (head dim >= 256, one wave per SIMD) have the registers for all its splits.
+    const bool one_round = kW == 4 && nreal * (DV / 4) <= 64 * kW;
     if (ns <= 8) {
       if (narrow) reduce_group<8, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
       else reduce_group<8, 1, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     } else if (ns <= 16) {
       if (narrow) reduce_group<16, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else if (kW == 4 && one_round) reduce_group<16, kW == 4 ? 1 : 2, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
       else reduce_group<16, 2, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     } else {
       if (narrow) reduce_group<32, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else if (kW == 4 && one_round) reduce_group<32, kW == 4 ? 1 : 4, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
       else reduce_group<32, 4, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     }
     return;

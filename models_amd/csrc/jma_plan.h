@@ -81,7 +81,8 @@ struct DecodePlan {
 
 inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_t window,
                               uint32_t hkv, uint32_t group, int dk, int dv, bool f16,
-                              int target_blocks, int tiles_per_wave, bool unfused) {
+                              int target_blocks, int tiles_per_wave, bool unfused,
+                              int min_split_tiles = 0) {
   DecodePlan p;
   const uint32_t blk = (uint32_t)v_block(f16);
   p.hgroups = (group + kHeadSlots - 1) / kHeadSlots;
@@ -96,7 +97,8 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     units += (uint64_t)ntiles[i] * hkv * p.hgroups;
   }
   const uint64_t target = (uint64_t)std::max(target_blocks, 1);
-  uint64_t tps = (uint64_t)decode_waves(dk) * (uint64_t)std::max(tiles_per_wave, 1);
+  uint64_t tps = min_split_tiles > 0 ? (uint64_t)min_split_tiles
+                                     : (uint64_t)decode_waves(dk) * (uint64_t)std::max(tiles_per_wave, 1);
   tps = std::max<uint64_t>(tps, (units + target - 1) / target);
   const uint64_t tps_fused = std::max<uint64_t>(tps, (max_tiles + kMaxSplits - 1) / kMaxSplits);
   bool wide = false;
@@ -108,6 +110,19 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
   }
   tps = wide ? std::max<uint64_t>(tps, (max_tiles + kMaxWideSplits - 1) / kMaxWideSplits)
              : tps_fused;
+  // Short rows: a launch of few workgroups (under an eighth of the target) that each stream more
+  // than 64 KB waits on the per-CU load issue rate (~64 KB per us), so it takes half the tiles
+  // per split (at least one per two waves) and twice the workgroups, as long as each extra
+  // split's partial (dv + 4 floats per query head, read back by the reducer) stays within 2 KB.
+  const uint64_t tile_bytes = (uint64_t)blk * (uint64_t)(dk + dv) * (f16 ? 2u : 4u);
+  const uint64_t part_bytes = (uint64_t)std::min<uint32_t>(group, kHeadSlots) * (dv + 4) * 4;
+  const uint64_t base_tps = (uint64_t)decode_waves(dk) * (uint64_t)std::max(tiles_per_wave, 1);
+  if (min_split_tiles == 0 && !wide && tps == base_tps && tps >= 2 && tps * tile_bytes > 65536 &&
+      part_bytes <= 2048 && (max_tiles + tps / 2 - 1) / (tps / 2) <= (uint64_t)kMaxSplits) {
+    uint64_t few = 0;
+    for (uint32_t i = 0; i < count; ++i) few += (ntiles[i] + tps - 1) / tps * hkv * p.hgroups;
+    if (few * 8 < target) tps /= 2;
+  }
   p.tiles_per_split = (uint32_t)tps;
   uint32_t items = 0;
   bool uniform = true;

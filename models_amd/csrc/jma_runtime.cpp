@@ -128,6 +128,7 @@ struct jmodels_attn_context {
   DeviceBuffer part_acc, part_ml, part_f, counters, pf_part, pf_tickets, qrot, stage_q, stage_k, stage_v, stage_out;
   int decode_target_blocks = 512;   // workgroups a decode launch aims for (two per CU)
   int tiles_per_wave = 1;           // minimum tiles each decode wave streams
+  int min_split_tiles = 0;          // minimum tiles per decode split; 0: waves x tiles_per_wave
   int prefill_split_tiles = -1;     // split prefill row blocks of this many kv tiles; -1: automatic
   uint32_t cus = 256;               // compute units of the device
   bool unfused = false;             // JMA_UNFUSED=1: separate append and reduce kernels
@@ -410,7 +411,8 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   }
   const jma::DecodePlan plan =
       jma::plan_decode(rows.count, rows.pos, lc.window, lc.hkv, lc.group, (int)lc.dk, (int)lc.dv,
-                       kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave, ctx->unfused);
+                       kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave, ctx->unfused,
+                       ctx->min_split_tiles);
   a.tiles_per_split = plan.tiles_per_split;
   for (uint32_t i = 0; i <= rows.count; ++i) a.item_start[i] = plan.item_start[i];
   for (uint32_t i = 0; i < rows.count; ++i) a.nsplit[i] = plan.nsplit[i];
@@ -807,6 +809,7 @@ jmodels_attn_context* jmodels_attn_context_create(int32_t device) {
     ctx->device = device;
     ctx->decode_target_blocks = std::max(1, env_int("JMA_DECODE_TARGET_BLOCKS", 512));
     ctx->tiles_per_wave = std::max(1, env_int("JMA_DECODE_TILES_PER_WAVE", 1));
+    ctx->min_split_tiles = std::max(0, env_int("JMA_DECODE_MIN_SPLIT_TILES", 0));
     ctx->prefill_split_tiles = std::max(-1, env_int("JMA_PREFILL_SPLIT_TILES", -1));
     ctx->cus = (uint32_t)std::max(1, prop.multiProcessorCount);
     ctx->unfused = env_int("JMA_UNFUSED", 0) != 0;

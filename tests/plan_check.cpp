@@ -33,6 +33,7 @@ struct Case {
   int target, tiles_per_wave;
   bool unfused;
   uint32_t ring;  // ring capacity of the layer, 0 = linear
+  int min_split = 0;  // JMA_DECODE_MIN_SPLIT_TILES (0: the planner's own choice)
 };
 
 [[noreturn]] void die(const Case& c, const std::string& what) {
@@ -44,7 +45,7 @@ void check(const Case& c) {
   const uint32_t count = (uint32_t)c.pos.size();
   if (count == 0 || count > (uint32_t)kMaxRows) die(c, "row count");
   const DecodePlan p = plan_decode(count, c.pos.data(), c.window, c.hkv, c.group, c.dk, c.dv, c.f16,
-                                   c.target, c.tiles_per_wave, c.unfused);
+                                   c.target, c.tiles_per_wave, c.unfused, c.min_split);
   const uint32_t blk = (uint32_t)v_block(c.f16);
   const uint32_t hgroups = p.hgroups;
   if (hgroups != (c.group + kHeadSlots - 1) / kHeadSlots) die(c, "head groups");
@@ -156,6 +157,10 @@ int main() {
   cases.push_back({"two head groups (20 q heads / kv head)", ragged(7, 1, 9000, 3), 0, 2, 20, 128, 128, true, 512, 1, false, 0});
   cases.push_back({"128 rows x 8 kv x 4 head groups, long", ragged(128, 60000, 65535, 9), 0, 8, 64, 128, 128, true, 512, 1, false, 0});
   cases.push_back({"128 rows, target 100000", ragged(128, 544, 544, 1), 0, 8, 4, 256, 256, true, 100000, 1, false, 0});
+  cases.push_back({"short rows d128 f16 24/8 @1024 (halved)", {1024}, 0, 8, 3, 128, 128, true, 512, 1, false, 0});
+  cases.push_back({"min split tiles 1, ragged d256", ragged(5, 40, 2048, 13), 0, 2, 4, 256, 256, true, 512, 1, false, 0, 1});
+  cases.push_back({"min split tiles 2, C5 sliding ring", {32767}, 512, 1, 4, 256, 256, true, 512, 1, false, 544, 2});
+  cases.push_back({"min split tiles 1, C5 global (wide)", {32767}, 0, 1, 4, 256, 256, true, 512, 1, false, 0, 1});
   cases.push_back({"single position 0", {0}, 0, 1, 1, 16, 16, false, 512, 1, false, 0});
   cases.push_back({"1M context MQA d128", {1048575}, 0, 1, 8, 128, 128, true, 512, 1, false, 0});
   // Gemma-4 layer shapes: full layers d 512 (2 kv heads, LINEAR), sliding d 256 on a ring of
