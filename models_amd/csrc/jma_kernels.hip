@@ -144,10 +144,9 @@ __global__ __launch_bounds__(256) void rope_append_kernel(const AppendArgs a) {
         o[e1] = y1;
       }
     } else {
-      KV* kr = (KV*)a.kv.k + seq * a.kv.seq_stride_k + a.kv.layer_off_k +
-               ((uint64_t)h * a.kv.cap + slot) * a.dk;
-      kr[e0] = (KV)y0;
-      kr[e1] = (KV)y1;
+      KV* kr = (KV*)a.kv.k + seq * a.kv.seq_stride_k + a.kv.layer_off_k + (uint64_t)h * a.kv.cap * a.dk;
+      kr[k_index(slot, e0, a.dk, kF16)] = (KV)y0;
+      kr[k_index(slot, e1, a.dk, kF16)] = (KV)y1;
     }
     return;
   }
@@ -222,6 +221,8 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141; // row_half_mirror
 
 // Fragments of one tile (kBlk positions) of K and V for one lane, in matrix-core operand order.
+// K tiles are stored in 64-byte column panels (k_index), so each operand load below reads 1 KB of
+// contiguous memory across the wave, like the V loads.
 template <typename KV, int DK, int DV>
 struct Tile;
 
@@ -231,11 +232,12 @@ struct Tile<_Float16, DK, DV> {
   half8_t k[2][DK / 32];
   half8_t v[DV / 16];
   __device__ __forceinline__ void load_k(const _Float16* kb, uint32_t slot0, int c16, int g) {
+    const _Float16* kt = kb + (uint64_t)slot0 * DK;  // slot0 starts a tile
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int c = 0; c < DK / 32; ++c)
-        k[b][c] = *(const half8_t*)(kb + (uint64_t)(slot0 + 16 * b + c16) * DK + 32 * c + 8 * g);
+        k[b][c] = *(const half8_t*)(kt + c * (32 * 32) + (16 * b + c16) * 32 + 8 * g);
   }
   __device__ __forceinline__ void load_v(const _Float16* vb, uint32_t slot0, int c16, int g) {
     const _Float16* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
@@ -255,9 +257,10 @@ struct Tile<float, DK, DV> {
   float4_t k[DK / 16];
   float4_t v[DV / 16];
   __device__ __forceinline__ void load_k(const float* kb, uint32_t slot0, int c16, int g) {
+    const float* kt = kb + (uint64_t)slot0 * DK;  // slot0 starts a tile
 #pragma unroll
     for (int c = 0; c < DK / 16; ++c)
-      k[c] = *(const float4_t*)(kb + (uint64_t)(slot0 + c16) * DK + 16 * c + 4 * g);
+      k[c] = *(const float4_t*)(kt + c * (16 * 16) + c16 * 16 + 4 * g);
   }
   __device__ __forceinline__ void load_v(const float* vb, uint32_t slot0, int c16, int g) {
     const float* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
@@ -747,52 +750,104 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   const float* cs = cos_t ? cos_t + (uint64_t)pos * pairs : nullptr;
   const float* sn = cos_t ? sin_t + (uint64_t)pos * pairs : nullptr;
 
-  // Fused append. The new row's tile is the last of the row's last split: the row is rotated
-  // into LDS, from where the wave owning that tile patches it into its registers, and the head
-  // group 0 workgroup stores it to the cache (the next launches read it there).
+  // Fused append and q staging. The loads of both (the new K / V row elements with their RoPE
+  // factors, then the q elements with theirs) are all issued before any of them is used: a
+  // vector-memory wait also waits for every earlier load of the wave, the tile loads included, so
+  // using the append's loads before issuing the q loads would put a second memory round trip on
+  // the path of the workgroup that appends (and the reducer waits for that workgroup).
+  //
+  // Append: the new row's tile is the last of the row's last split. One thread per K pair (rotated
+  // as rope_append_kernel rotates it) or V element pair, the workgroup's threads taking
+  // DK / 2 + DV / 2 pairs in turn (two turns at head dimension 512); the row goes to LDS, from
+  // where the wave owning that tile patches it into its registers, and the head group 0
+  // workgroup stores it to the cache (the next launches read it there).
   const bool append = k_new != nullptr && split == ns - 1;
+  constexpr uint32_t kPairs = DK / 2 + DV / 2;
+  constexpr uint32_t kTurns = (kPairs + 64 * kW - 1) / (64 * kW);
+  const float* kx = append ? k_new + ((uint64_t)row * hkv + kvh) * DK : nullptr;
+  const float* vx = append ? v_new + ((uint64_t)row * hkv + kvh) * DV : nullptr;
+  float ax0[kTurns], ax1[kTurns], afc[kTurns], afs[kTurns];
   if (append) {
-    // One thread per K pair (rotated as rope_append_kernel rotates it) or V element pair, the
-    // workgroup's threads taking DK / 2 + DV / 2 pairs in turn (two turns at head dimension 512).
-    const uint32_t slot = ring ? pos % cap : pos;
-    const float* kx = k_new + ((uint64_t)row * hkv + kvh) * DK;
-    const float* vx = v_new + ((uint64_t)row * hkv + kvh) * DV;
-    constexpr uint32_t kPairs = DK / 2 + DV / 2;
-    constexpr uint32_t kTurns = (kPairs + 64 * kW - 1) / (64 * kW);
 #pragma unroll
     for (uint32_t turn = 0; turn < kTurns; ++turn) {
-    const uint32_t tid = threadIdx.x + turn * 64 * kW;
-    if (tid < DK / 2) {
-      const uint32_t j = tid;
-      const bool rot = cs != nullptr && j < pairs;
-      const uint32_t e0 = rot && neox ? j : 2 * j, e1 = rot && neox ? j + pairs : 2 * j + 1;
-      float y0 = kx[e0], y1 = kx[e1], fc = 1.0f, fs = 0.0f;
-      // QK-norm of the head before RoPE, as the append kernel applies it.
-      if (a.k_norm_w != nullptr) head_rms_norm(kx, DK, a.k_norm_w, a.norm_eps, e0, e1, y0, y1);
-      if (cs != nullptr) {
-        fc = cs[rot ? j : 0u];
-        fs = sn[rot ? j : 0u];
-      }
-      if (rot) rotate_pair(y0, y1, fc, fs);
-      s_new_k[e0] = (KV)y0;
-      s_new_k[e1] = (KV)y1;
-      if (hg == 0) {
-        kb[(uint64_t)slot * DK + e0] = (KV)y0;
-        kb[(uint64_t)slot * DK + e1] = (KV)y1;
-      }
-    } else if (tid < DK / 2 + DV / 2) {
-      const uint32_t d = 2 * (tid - DK / 2);
-      float v0 = vx[d], v1 = vx[d + 1];
-      if (a.v_norm != 0u) value_rms_norm(vx, DV, a.norm_eps, v0, v1);
-      s_new_v[d] = (KV)v0;
-      s_new_v[d + 1] = (KV)v1;
-      if (hg == 0) {
-        const uint32_t r = kF16 ? perm32(slot % kBlk) : slot % kBlk;
-        KV* vp = vb + (uint64_t)(slot / kBlk) * DV * kBlk + (uint64_t)d * kBlk + r;
-        vp[0] = (KV)v0;
-        vp[kBlk] = (KV)v1;
+      const uint32_t tid = threadIdx.x + turn * 64 * kW;
+      afc[turn] = 1.0f;
+      afs[turn] = 0.0f;
+      if (tid < DK / 2) {
+        const uint32_t j = tid;
+        const bool rot = cs != nullptr && j < pairs;
+        ax0[turn] = kx[rot && neox ? j : 2 * j];
+        ax1[turn] = kx[rot && neox ? j + pairs : 2 * j + 1];
+        if (cs != nullptr) {
+          afc[turn] = cs[rot ? j : 0u];
+          afs[turn] = sn[rot ? j : 0u];
+        }
+      } else if (tid < kPairs) {
+        const uint32_t d = 2 * (tid - DK / 2);
+        ax0[turn] = vx[d];
+        ax1[turn] = vx[d + 1];
       }
     }
+  }
+
+  // q of this head group, rotated here when the caller passed raw q, times the score scale,
+  // staged in LDS by the whole workgroup: thread k takes RoPE pair k (head k / (DK/2)).
+  const uint32_t nreal = min(16u, group - hg * 16);  // query heads of this head group
+  constexpr uint32_t kHalf = DK / 2;
+  constexpr int kIt = (16 * kHalf + 64 * kW - 1) / (64 * kW);
+  const uint32_t nq = nreal * kHalf;
+  const bool rope_on = rope_q != 0 && cs != nullptr;
+  const float* qg = q_in + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DK;
+  float qy0[kIt], qy1[kIt], qfc[kIt], qfs[kIt];
+  uint32_t qe0[kIt], qe1[kIt];
+  bool qrot[kIt];
+#pragma unroll
+  for (int it = 0; it < kIt; ++it) {
+    const uint32_t k = min(threadIdx.x + 64 * kW * it, nq - 1);  // indices clamped: every load valid
+    const uint32_t hs = k / kHalf, j = k % kHalf;
+    qrot[it] = rope_on && j < pairs;
+    qe0[it] = hs * DK + (qrot[it] && neox ? j : 2 * j);
+    qe1[it] = hs * DK + (qrot[it] && neox ? j + pairs : 2 * j + 1);
+    qy0[it] = qg[qe0[it]];
+    qy1[it] = qg[qe1[it]];
+    if (rope_on) {
+      qfc[it] = cs[qrot[it] ? j : 0u];
+      qfs[it] = sn[qrot[it] ? j : 0u];
+    }
+  }
+
+  if (append) {
+    const uint32_t slot = ring ? pos % cap : pos;
+#pragma unroll
+    for (uint32_t turn = 0; turn < kTurns; ++turn) {
+      const uint32_t tid = threadIdx.x + turn * 64 * kW;
+      if (tid < DK / 2) {
+        const uint32_t j = tid;
+        const bool rot = cs != nullptr && j < pairs;
+        const uint32_t e0 = rot && neox ? j : 2 * j, e1 = rot && neox ? j + pairs : 2 * j + 1;
+        float y0 = ax0[turn], y1 = ax1[turn];
+        // QK-norm of the head before RoPE, as the append kernel applies it.
+        if (a.k_norm_w != nullptr) head_rms_norm(kx, DK, a.k_norm_w, a.norm_eps, e0, e1, y0, y1);
+        if (rot) rotate_pair(y0, y1, afc[turn], afs[turn]);
+        s_new_k[e0] = (KV)y0;
+        s_new_k[e1] = (KV)y1;
+        if (hg == 0) {
+          kb[k_index(slot, e0, DK, kF16)] = (KV)y0;
+          kb[k_index(slot, e1, DK, kF16)] = (KV)y1;
+        }
+      } else if (tid < kPairs) {
+        const uint32_t d = 2 * (tid - DK / 2);
+        float v0 = ax0[turn], v1 = ax1[turn];
+        if (a.v_norm != 0u) value_rms_norm(vx, DV, a.norm_eps, v0, v1);
+        s_new_v[d] = (KV)v0;
+        s_new_v[d + 1] = (KV)v1;
+        if (hg == 0) {
+          const uint32_t r = kF16 ? perm32(slot % kBlk) : slot % kBlk;
+          KV* vp = vb + (uint64_t)(slot / kBlk) * DV * kBlk + (uint64_t)d * kBlk + r;
+          vp[0] = (KV)v0;
+          vp[kBlk] = (KV)v1;
+        }
+      }
     }
   }
   // Lanes of the wave owning the new row's tile that hold that row: K lanes hold tile rows
@@ -803,33 +858,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   const bool k_lane = patch_wave && (uint32_t)c16 == (r_new & 15u);
   const bool v_lane = patch_wave && (uint32_t)g == v_at / (kF16 ? 8u : 4u);
 
-  // q of this head group, rotated here when the caller passed raw q, times the score scale,
-  // staged in LDS by the whole workgroup: thread k takes RoPE pair k (head k / (DK/2)). Every
-  // load is issued (indices clamped) before any is used, so this costs one memory round trip.
-  const uint32_t nreal = min(16u, group - hg * 16);  // query heads of this head group
   {
-    constexpr uint32_t kHalf = DK / 2;
-    constexpr int kIt = (16 * kHalf + 64 * kW - 1) / (64 * kW);
-    const uint32_t nq = nreal * kHalf;
-    const bool rope_on = rope_q != 0 && cs != nullptr;
-    const float* qg = q_in + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DK;
-    float y0[kIt], y1[kIt], fc[kIt], fs[kIt];
-    uint32_t e0[kIt], e1[kIt];
-    bool rot[kIt];
-#pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const uint32_t k = min(threadIdx.x + 64 * kW * it, nq - 1);
-      const uint32_t hs = k / kHalf, j = k % kHalf;
-      rot[it] = rope_on && j < pairs;
-      e0[it] = hs * DK + (rot[it] && neox ? j : 2 * j);
-      e1[it] = hs * DK + (rot[it] && neox ? j + pairs : 2 * j + 1);
-      y0[it] = qg[e0[it]];
-      y1[it] = qg[e1[it]];
-      if (rope_on) {
-        fc[it] = cs[rot[it] ? j : 0u];
-        fs[it] = sn[rot[it] ? j : 0u];
-      }
-    }
     // Raw q of a QK-norm layer: each head's scale (one thread per head, the append kernel's
     // arithmetic), then every element times that scale and its weight, before RoPE.
     const float* qw = rope_q != 0 ? (const float*)a.q_norm_w : nullptr;
@@ -840,17 +869,17 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
       if (threadIdx.x + 64 * kW * it >= nq) continue;
-      float u0 = y0[it], u1 = y1[it];
-      const uint32_t hs = e0[it] / DK;
+      float u0 = qy0[it], u1 = qy1[it];
+      const uint32_t hs = qe0[it] / DK;
       if (qw != nullptr) {
 #pragma clang fp contract(off)
         const float sc = s_qn[hs];
-        u0 = u0 * sc * qw[e0[it] - hs * DK];
-        u1 = u1 * sc * qw[e1[it] - hs * DK];
+        u0 = u0 * sc * qw[qe0[it] - hs * DK];
+        u1 = u1 * sc * qw[qe1[it] - hs * DK];
       }
-      if (rot[it]) rotate_pair(u0, u1, fc[it], fs[it]);
-      s_q[hs][e0[it] - hs * DK] = u0 * qscale;
-      s_q[hs][e1[it] - hs * DK] = u1 * qscale;
+      if (qrot[it]) rotate_pair(u0, u1, qfc[it], qfs[it]);
+      s_q[hs][qe0[it] - hs * DK] = u0 * qscale;
+      s_q[hs][qe1[it] - hs * DK] = u1 * qscale;
     }
   }
   if constexpr (!kOne)
@@ -919,13 +948,20 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         }
       }
     }
+    // The new row's V elements: every LDS read is issued before any is used, then each lands in
+    // operand element v_at % kQ (the same for the whole workgroup, so one uniform branch picks the
+    // element and the selects inside it are branch-free).
     auto patch_v = [&]() JMA_INL {
-      if (v_lane) {
+      KV nv[kNv];
 #pragma unroll
-        for (int n = 0; n < kNv; ++n)
+      for (int n = 0; n < kNv; ++n) nv[n] = s_new_v[16 * n + c16];
+      const uint32_t ev = v_at % (uint32_t)kQ;
 #pragma unroll
-          for (int e = 0; e < kQ; ++e)
-            if ((uint32_t)e == v_at % (uint32_t)kQ) cur.v[n][e] = s_new_v[16 * n + c16];
+      for (int e = 0; e < kQ; ++e) {
+        if ((uint32_t)e == ev) {
+#pragma unroll
+          for (int n = 0; n < kNv; ++n) cur.v[n][e] = v_lane ? nv[n] : cur.v[n][e];
+        }
       }
     };
     if constexpr (decltype(patch)::value && !kSplitKV) patch_v();
@@ -1639,7 +1675,9 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   for (int i = 0; i < kCPW; ++i) {
     const uint32_t c = s + S * i;
     const uint32_t rk = c * (512 / D) + lane / kNC;
-    koff[i] = 2 * (rk * D + 8 * ((lane % kNC) ^ swz_k<D>(rk)));
+    // 16-byte chunk cc of tile row rk sits in column panel cc / 4 of the tile (k_index).
+    const uint32_t cc = (lane % kNC) ^ swz_k<D>(rk);
+    koff[i] = 2 * ((cc / 4) * (32 * 32) + rk * 32 + 8 * (cc % 4));
     const uint32_t rv = c * 16 + lane / 4;
     voff[i] = 2 * (rv * 32 + 8 * ((lane % 4) ^ swz_v(rv)));
   }

@@ -31,8 +31,25 @@ constexpr int kMaxWideSplits = 1024;
 // many head slots per work item.
 constexpr int kHeadSlots = 16;
 
-// Storage block (slots) of the transposed V layout.
+// Storage block (slots) of the transposed V layout, and of the K tiles.
 JMA_HD int v_block(bool f16) { return f16 ? 32 : 16; }
+
+// K layout inside one (sequence, layer, kv head) region of cap * key_length elements: blocks of
+// B = v_block slots, each stored as key_length / W column panels of B rows x W elements, where a
+// panel row is 64 bytes (W = 32 f16 or 16 f32 elements). One matrix-core operand load of a tile
+// (16 or 32 rows x 64 bytes across a wave) is then 1 KB of contiguous memory; row-major rows
+// would spread it over 16 separate 64-byte pieces, which a compute unit issues 2-3x slower. A
+// key length that is not a multiple of W keeps the rows whole (W = key_length).
+JMA_HD uint32_t k_panel(uint32_t key_length, bool f16) {
+  const uint32_t w = f16 ? 32u : 16u;
+  return key_length % w == 0 ? w : key_length;
+}
+// Element offset of K element e of slot `slot` in its region.
+JMA_HD uint64_t k_index(uint32_t slot, uint32_t e, uint32_t key_length, bool f16) {
+  const uint32_t b = (uint32_t)v_block(f16), w = k_panel(key_length, f16);
+  return (uint64_t)(slot - slot % b) * key_length + (uint64_t)(e / w) * (b * w) +
+         (uint64_t)(slot % b) * w + e % w;
+}
 
 JMA_HD uint32_t first_visible(uint32_t position, uint32_t window) {
   // LlamaConfig.attentionStartPosition, causal branch (llama/LlamaConfig.java:184-195).

@@ -1244,7 +1244,7 @@ int32_t jmodels_attn_kv_read(jmodels_attn_context* ctx, const jmodels_attn_kv* k
         if (keys)
           for (uint32_t d = 0; d < key_len; ++d)
             keys[(uint64_t)(p - from) * kdim + h * key_len + d] =
-                widen(hk.data(), ((uint64_t)h * cap + slot) * key_len + d);
+                widen(hk.data(), (uint64_t)h * cap * key_len + jma::k_index(slot, d, key_len, kv->f16()));
         if (values)
           for (uint32_t d = 0; d < value_len; ++d)
             values[(uint64_t)(p - from) * vdim + h * value_len + d] =

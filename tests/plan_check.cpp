@@ -10,6 +10,10 @@
 //   - arrival-ticket counters lie inside the planned counter buffer;
 //   - split counts stay within the fused (32) or separate (1024) caps;
 //   - the separate reduction (reduce_kernel) reads only items its row's groups own.
+// It also checks the K tile layout (k_index): a bijection of every (slot, element) of a region,
+// and the addresses the kernels form for their K loads (decode operand loads, prefill
+// direct-to-LDS chunks) name the elements k_index places there, each decode operand load reading
+// one contiguous 1 KB run.
 // Prints one line per case and "ok" at the end; exits non-zero on the first failed check.
 #include <stdint.h>
 #include <stdio.h>
@@ -134,6 +138,61 @@ std::vector<uint32_t> run(uint32_t start, uint32_t n) {
   return v;
 }
 
+void k_fail(const std::string& what) {
+  fprintf(stderr, "FAILED K layout: %s\n", what.c_str());
+  exit(1);
+}
+
+// The prefill kernel's XOR swizzle of 16-byte chunks inside a K tile row (swz_k in
+// jma_kernels.hip).
+uint32_t swz_k(int d, uint32_t r) {
+  if (d >= 128) return (r & 7u) | ((r >> 1) & 8u);
+  if (d == 64) return r & 7u;
+  return (r >> 1) & 3u;
+}
+
+void check_k_layout(uint32_t dk, bool f16, uint32_t cap) {
+  const std::string tag = std::string(f16 ? "f16" : "f32") + " dk " + std::to_string(dk);
+  std::vector<uint8_t> seen((size_t)cap * dk, 0);
+  for (uint32_t slot = 0; slot < cap; ++slot)
+    for (uint32_t e = 0; e < dk; ++e) {
+      const uint64_t i = k_index(slot, e, dk, f16);
+      if (i >= (uint64_t)cap * dk || seen[i]++) k_fail(tag + ": not a bijection");
+    }
+  const uint32_t blk = (uint32_t)v_block(f16);
+  if (dk % (f16 ? 32u : 16u) != 0) return;  // decode and prefill take these widths only
+  // Decode operand loads (Tile::load_k): lane (g, c16) of the load (b, c) of the tile at slot0.
+  for (uint32_t slot0 = 0; slot0 < cap; slot0 += blk)
+    for (uint32_t b = 0; b < (f16 ? 2u : 1u); ++b)
+      for (uint32_t c = 0; c < dk / (f16 ? 32u : 16u); ++c) {
+        uint64_t lo = ~0ull, hi = 0;
+        for (uint32_t lane = 0; lane < 64; ++lane) {
+          const uint32_t g = lane >> 4, c16 = lane & 15;
+          const uint32_t n = f16 ? 8u : 4u;  // elements per 16-byte load
+          const uint64_t a = f16 ? (uint64_t)slot0 * dk + c * 1024 + (16 * b + c16) * 32 + 8 * g
+                                 : (uint64_t)slot0 * dk + c * 256 + c16 * 16 + 4 * g;
+          for (uint32_t j = 0; j < n; ++j) {
+            const uint32_t row = slot0 + 16 * b + c16, e = (f16 ? 32 : 16) * c + n * g + j;
+            if (a + j != k_index(row, e, dk, f16)) k_fail(tag + ": decode operand load");
+          }
+          lo = std::min(lo, a);
+          hi = std::max(hi, a + n);
+        }
+        if ((hi - lo) * (f16 ? 2 : 4) != 1024) k_fail(tag + ": decode operand load not contiguous");
+      }
+  if (!f16 || dk > 256) return;
+  // Prefill direct-to-LDS chunks: chunk c, lane l stages 16 bytes of tile row rk.
+  const uint32_t nc = dk / 8;
+  for (uint32_t c = 0; c < dk / 16; ++c)
+    for (uint32_t lane = 0; lane < 64; ++lane) {
+      const uint32_t rk = c * (512 / dk) + lane / nc;
+      const uint32_t cc = (lane % nc) ^ swz_k((int)dk, rk);
+      const uint64_t off = (cc / 4) * (32 * 32) + rk * 32 + 8 * (cc % 4);
+      for (uint32_t j = 0; j < 8; ++j)
+        if (off + j != k_index(rk, 8 * cc + j, dk, true)) k_fail(tag + ": prefill chunk");
+    }
+}
+
 }  // namespace
 
 int main() {
@@ -169,6 +228,10 @@ int main() {
   cases.push_back({"Gemma-4 full d512 f32 8k", {8191}, 0, 2, 16, 512, 512, false, 512, 1, false, 0});
   cases.push_back({"Gemma-4 sliding ring 356 w256", {602, 252}, 256, 4, 2, 256, 256, true, 512, 1, false, 384});
   for (const Case& c : cases) check(c);
+  for (bool f16 : {true, false})
+    for (uint32_t dk : {16u, 32u, 48u, 64u, 80u, 128u, 256u, 512u})
+      check_k_layout(dk, f16, 96);
+  printf("K layout: bijective, kernel K loads match k_index\n");
   printf("ok\n");
   return 0;
 }

@@ -2,7 +2,9 @@
 address and undefined-behaviour sanitizers, plans every BASELINE decode shape (C1-C5 at their
 configured sizes, including C5's global layers with the wide split plan and its sliding-window
 ring layers) and extreme tuning settings with the runtime's own planner, then walks every
-workgroup's partial-buffer, counter and tile indexing with the kernels' own index functions."""
+workgroup's partial-buffer, counter and tile indexing with the kernels' own index functions. It
+also checks the K tile layout (k_index is a bijection, and the decode and prefill K loads address
+the elements it places there, each decode operand load one contiguous 1 KB run)."""
 
 import os
 import shutil
@@ -25,3 +27,4 @@ def test_decode_plans_stay_in_bounds(tmp_path):
     assert run.returncode == 0, run.stdout + run.stderr
     assert run.stdout.strip().endswith("ok"), run.stdout
     assert "C5 global d256 4/1 @32767" in run.stdout and "separate" in run.stdout
+    assert "K layout: bijective" in run.stdout
