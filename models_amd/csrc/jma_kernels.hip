@@ -211,7 +211,7 @@ __device__ __forceinline__ float wave_sum_groups(float x) {
 
 // DPP lane exchanges inside groups of 8 consecutive lanes: partner lane i ^ 1, i ^ 2, and
 // 7 - i within each half row (which, once the quads hold equal values, pairs quad 0 with quad 1
-// as i ^ 4 would).
+// as i ^ 4 would); row_mirror pairs the two halves of a row of 16 the same way.
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xF, 0xF, false));
@@ -219,6 +219,7 @@ __device__ __forceinline__ float dpp(float x) {
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141; // row_half_mirror
+constexpr int kDppRowMirror = 0x140;  // row_mirror: lane 15 - i within each row of 16
 
 // Fragments of one tile (kBlk positions) of K and V for one lane, in matrix-core operand order.
 // K tiles are stored in 64-byte column panels (k_index), so each operand load below reads 1 KB of
@@ -1190,19 +1191,39 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 
 // ================================================================ kernel 4: cross-split reduce
 
+// Maximum and sum over the 64 lanes of a wave in VALU lane exchanges (DPP inside rows of 16, then
+// the row swaps); every lane ends with the result, formed in the same fixed tree.
+__device__ __forceinline__ float wave_max64(float x) {
+  x = fmaxf(x, dpp<kDppXor1>(x));
+  x = fmaxf(x, dpp<kDppXor2>(x));
+  x = fmaxf(x, dpp<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppRowMirror>(x));
+  return wave_max_groups(x);
+}
+__device__ __forceinline__ float wave_sum64(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  x += dpp<kDppHalfMirror>(x);
+  x += dpp<kDppRowMirror>(x);
+  return wave_sum_groups(x);
+}
+
 // One workgroup of 16 waves per (row, query head, 64-element chunk of the head's output): out =
 // sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to kMaxWideSplits.
-// Thread t loads split t's (m, l) and wave w the chunk of its splits w, w + 16, ..., all in one
-// round trip; the workgroup agrees on M and on the weights 2^(m_s - M) (kept in LDS) and sums l
-// in a fixed tree. Wave w then sums its splits in order, and the sixteen sums are added in wave
-// order: the result is the same on every run for a plan.
+// Lane (s4, q) of wave w takes output quad q of the chunk for splits (16 i + w) * 4 + s4,
+// i = 0, 1, ...: each load instruction moves 16 bytes per lane, four splits' 256-byte rows. Thread
+// t also loads split t's (m, l) for the maximum M and the weights, which go through LDS; every
+// load is issued before any is used (one memory round trip). Sums run in a fixed order (per lane
+// over i, then the four split lanes in a tree, then the waves in order), so the result is the
+// same on every run for a plan.
 template <int DV>
 __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
   constexpr uint32_t kChunks = (DV + 63) / 64;
   constexpr int kWaves = 16;
-  constexpr int kAhead = kMaxWideSplits / kWaves;  // splits one wave sums at most
-  __shared__ float s_w[kMaxWideSplits];
-  __shared__ float s_m[kWaves], s_l[kWaves], s_x[kWaves][64];
+  constexpr int kPer = kMaxWideSplits / (kWaves * 4);  // splits one lane sums at most
+  __shared__ float2 s_ml[kMaxWideSplits];
+  __shared__ float s_m[kWaves], s_l[kWaves];
+  __shared__ float4_t s_x[kWaves][16];
   const uint32_t chunk = blockIdx.x % kChunks;
   const uint32_t row = blockIdx.x / kChunks / a.num_heads;
   const uint32_t head = blockIdx.x / kChunks % a.num_heads;
@@ -1215,56 +1236,55 @@ __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
   const uint64_t base = group_item0(a.ns_uniform, a.item_start[row], row, hkv, a.hgroups,
                                     kvh * a.hgroups + hg, ns);
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const uint32_t s4 = lane >> 4, q = lane & 15;
+  const uint32_t e = chunk * 64 + 4 * q;
+  const uint32_t el = e < DV ? e : DV - 4;  // lanes past the head load a valid quad
 
-  // Every load is issued before any is used: thread t's split-t (m, l), and the chunk elements
-  // of wave w's splits w, w + 16, ...; the two sets need one memory round trip together.
   float2 ml = {-INFINITY, 0.0f};
   if (tid < ns) ml = *(const float2*)(a.part_ml + sep_ml_float(base + tid, c16));
-  const uint32_t d = chunk * 64 + lane;
-  const uint32_t dl = d < DV ? d : DV - 1;  // lanes past the head load a valid element
-  float xv[kAhead];
+  float4_t xv[kPer];
 #pragma unroll
-  for (int i = 0; i < kAhead; ++i) {
-    const uint32_t sp = wave + kWaves * i;
-    xv[i] = sp < ns ? a.part_acc[sep_acc_float(base + sp, c16, DV, dl)] : 0.0f;
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t sp = (i * kWaves + wave) * 4 + s4;
+    xv[i] = sp < ns ? *(const float4_t*)(a.part_acc + sep_acc_float(base + sp, c16, DV, el))
+                    : float4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Weights: thread t takes split t.
-  float mw = ml.x;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
+  if (tid < ns) s_ml[tid] = ml;
+  const float mw = wave_max64(ml.x);
   if (lane == 0) s_m[wave] = mw;
   __syncthreads();
   float M = s_m[0];
 #pragma unroll
   for (int i = 1; i < kWaves; ++i) M = fmaxf(M, s_m[i]);
   const float mu = M == -INFINITY ? 0.0f : M;
-  const float wt = tid < ns ? __builtin_amdgcn_exp2f(ml.x - mu) : 0.0f;
-  if (tid < ns) s_w[tid] = wt;
-  float lw = tid < ns ? ml.y * wt : 0.0f;
+  const float lw = wave_sum64(tid < ns ? ml.y * __builtin_amdgcn_exp2f(ml.x - mu) : 0.0f);
+
+  float4_t X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) lw += __shfl_xor(lw, o);
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t sp = (i * kWaves + wave) * 4 + s4;
+    if (sp < ns) {
+      const float w = __builtin_amdgcn_exp2f(s_ml[sp].x - mu);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) X[c] = fmaf(xv[i][c], w, X[c]);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) X[c] = wave_sum_groups(X[c]);  // the four split lanes of quad q
+  if (s4 == 0) s_x[wave][q] = X;
   if (lane == 0) s_l[wave] = lw;
   __syncthreads();
-
-  // Weighted sums of this chunk: wave w takes splits w, w + 16, ... in order.
-  float X = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kAhead; ++i) {
-    const uint32_t sp = wave + kWaves * i;
-    if (sp < ns) X = fmaf(xv[i], s_w[sp], X);
-  }
-  s_x[wave][lane] = X;
-  __syncthreads();
-  if (wave != 0) return;
-  float lt = 0.0f, xt = 0.0f;
+  if (wave != 0 || s4 != 0) return;
+  float lt = 0.0f;
+  float4_t xt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) {
     lt += s_l[i];
-    xt += s_x[i][lane];
+    xt += s_x[i][q];
   }
-  if (!(lt > 0.0f) && lane == 0 && chunk == 0) atomicOr(a.err, 1);  // all -inf, NaN or +inf
-  if (d < DV) a.out[((uint64_t)row * a.num_heads + head) * DV + d] = xt * (1.0f / lt);
+  if (!(lt > 0.0f) && q == 0 && chunk == 0) atomicOr(a.err, 1);  // all -inf, NaN or +inf
+  if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * a.num_heads + head) * DV + e) = xt * (1.0f / lt);
 }
 
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream) {
