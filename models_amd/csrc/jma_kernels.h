@@ -9,7 +9,8 @@
 
 namespace jma {
 
-// Where one layer's K and V live. K: [sequence][layer][kv head][slot][key_length] row-major.
+// Where one layer's K and V live. K: [sequence][layer][kv head][slot / B][key_length / W][B][W]
+// (64-byte column panels per tile of B slots, k_index in jma_plan.h).
 // V: [sequence][layer][kv head][slot / B][value_length][B] (B = 32 for f16, 16 for f32), the
 // transposed block layout the PV matrix cores read directly; f16 blocks store slot r at
 // index 8*((r%16)/4) + 4*(r/16) + r%4 (see perm32 in jma_kernels.hip).
