@@ -71,7 +71,11 @@ struct DecodeArgs {
   void* v_base;         // has the same split count, one head group; the layer's K / V base for
                         // that sequence (the kernel then skips the general indexing)
   float qscale;         // score scale * log2(e), folded into q
+  // hgroups: virtual head groups per kv head = head groups of <= 16 query heads x slices, where
+  // `slices` (1 or 4) cuts the value columns among that many workgroups (short rows at head dim
+  // 256 or 512); each virtual group has its own work items, partials and arrival ticket.
   uint32_t num_heads, group, hgroups, window;
+  uint32_t slices;
   uint32_t num_kv_heads;
   uint32_t pairs, neox, rope_q;  // rope_q: q is raw and the kernel rotates it
   // QK-norm of a fused decode: per-head RMS-norm weights for raw q (used when rope_q) and the new

@@ -224,14 +224,16 @@ constexpr int kDppRowMirror = 0x140;  // row_mirror: lane 15 - i within each row
 // Fragments of one tile (kBlk positions) of K and V for one lane, in matrix-core operand order.
 // K tiles are stored in 64-byte column panels (k_index), so each operand load below reads 1 KB of
 // contiguous memory across the wave, like the V loads.
-template <typename KV, int DK, int DV>
+// V: the DVS value columns of one column slice of a DV-wide head (vb points at the slice's first
+// column; the block stride is the whole head's).
+template <typename KV, int DK, int DV, int DVS>
 struct Tile;
 
-template <int DK, int DV>
-struct Tile<_Float16, DK, DV> {
+template <int DK, int DV, int DVS>
+struct Tile<_Float16, DK, DV, DVS> {
   static constexpr uint32_t kBlk = 32;
   half8_t k[2][DK / 32];
-  half8_t v[DV / 16];
+  half8_t v[DVS / 16];
   __device__ __forceinline__ void load_k(const _Float16* kb, uint32_t slot0, int c16, int g) {
     const _Float16* kt = kb + (uint64_t)slot0 * DK;  // slot0 starts a tile
 #pragma unroll
@@ -243,7 +245,7 @@ struct Tile<_Float16, DK, DV> {
   __device__ __forceinline__ void load_v(const _Float16* vb, uint32_t slot0, int c16, int g) {
     const _Float16* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
 #pragma unroll
-    for (int n = 0; n < DV / 16; ++n) v[n] = *(const half8_t*)(vblk + (16 * n + c16) * kBlk + 8 * g);
+    for (int n = 0; n < DVS / 16; ++n) v[n] = *(const half8_t*)(vblk + (16 * n + c16) * kBlk + 8 * g);
   }
   __device__ __forceinline__ void load(const _Float16* kb, const _Float16* vb, uint32_t slot0,
                                        int c16, int g) {
@@ -252,11 +254,11 @@ struct Tile<_Float16, DK, DV> {
   }
 };
 
-template <int DK, int DV>
-struct Tile<float, DK, DV> {
+template <int DK, int DV, int DVS>
+struct Tile<float, DK, DV, DVS> {
   static constexpr uint32_t kBlk = 16;
   float4_t k[DK / 16];
-  float4_t v[DV / 16];
+  float4_t v[DVS / 16];
   __device__ __forceinline__ void load_k(const float* kb, uint32_t slot0, int c16, int g) {
     const float* kt = kb + (uint64_t)slot0 * DK;  // slot0 starts a tile
 #pragma unroll
@@ -266,7 +268,7 @@ struct Tile<float, DK, DV> {
   __device__ __forceinline__ void load_v(const float* vb, uint32_t slot0, int c16, int g) {
     const float* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
 #pragma unroll
-    for (int n = 0; n < DV / 16; ++n) v[n] = *(const float4_t*)(vblk + (16 * n + c16) * kBlk + 4 * g);
+    for (int n = 0; n < DVS / 16; ++n) v[n] = *(const float4_t*)(vblk + (16 * n + c16) * kBlk + 4 * g);
   }
   __device__ __forceinline__ void load(const float* kb, const float* vb, uint32_t slot0, int c16,
                                        int g) {
@@ -439,7 +441,7 @@ __device__ __forceinline__ void wave_partial(const float (*s_acc)[16][DV], const
 // split order and meet across the SUB threads in a fixed shuffle tree, so the result does not
 // depend on which workgroup reduces. Every word read is set back to kClear; the (m, l) words,
 // read by all quads of a head, after a barrier.
-template <int B, int SUB, int DV, int W>
+template <int B, int SUB, int DV, int W, int OS>
 __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32_t ns,
                                              uint32_t split, uint32_t nreal,
                                              const float (*s_acc)[16][DV],
@@ -541,7 +543,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
     }
     if (qok && r == 0) {
       if (!(L > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
-      *(float4_t*)(out + hs * DV + e) = X * (1.0f / L);
+      *(float4_t*)(out + hs * OS + e) = X * (1.0f / L);
     }
   }
   __syncthreads();  // every quad of every head has read its (m, l) words
@@ -585,15 +587,20 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 // and the slot capacity). The library is built with kernel-argument preloading, so they arrive in
 // scalar registers at wave start and the first tile loads do not wait for a kernel-argument
 // load; the other instances pass zeros there and read everything from `a`.
-template <typename KV, int DK, int DV, bool kSimple, bool kOne>
+template <typename KV, int DK, int DV, int DVS, bool kSimple, bool kOne>
 __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     const void* p_kb, const void* p_vb, uint32_t p_start, uint32_t p_window, uint32_t p_tps,
     uint32_t p_cap, uint32_t p_ring, const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
-  using TileT = Tile<KV, DK, DV>;
+  using TileT = Tile<KV, DK, DV, DVS>;
   constexpr uint32_t kBlk = TileT::kBlk;
   constexpr int kNs = kF16 ? 8 : 4;   // scores per lane per tile
-  constexpr int kNv = DV / 16;        // output fragments per lane
+  constexpr int kNv = DVS / 16;       // output fragments per lane
+  // Column slices: a workgroup computes DVS of the DV value columns (the whole of q.K, the V
+  // columns and output of its slice only). The slices are virtual head groups: `hgroups` counts
+  // head groups x kSlices, and a virtual group hgv is head group hgv / kSlices, slice
+  // hgv % kSlices, with its own work items, partials and arrival tickets.
+  constexpr uint32_t kSlices = DV / DVS;
   constexpr int kC = kF16 ? DK / 32 : DK / 16;
   constexpr int kQ = kF16 ? 8 : 4;    // q elements per lane per k-chunk
   constexpr uint32_t kW = decode_waves(DK);
@@ -602,10 +609,10 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   // q rows share their LDS with the waves' combine area, which is written only after every wave
   // has left its tile loop.
   constexpr bool kQLds = DK >= 512;
-  constexpr int kAccFloats = kW * 16 * DV, kQFloats = 16 * (DK + 4);
+  constexpr int kAccFloats = kW * 16 * DVS, kQFloats = 16 * (DK + 4);
   __shared__ __attribute__((aligned(16))) float s_acc_mem[kQLds && kQFloats > kAccFloats ? kQFloats : kAccFloats];
   __shared__ __attribute__((aligned(16))) float s_q_mem[kQLds ? 4 : kQFloats];
-  float (*s_acc)[16][DV] = (float (*)[16][DV])s_acc_mem;
+  float (*s_acc)[16][DVS] = (float (*)[16][DVS])s_acc_mem;
   float (*s_q)[DK + 4] = (float (*)[DK + 4])(kQLds ? s_acc_mem : s_q_mem);  // q rows, padded against bank conflicts
   __shared__ float s_ml[kW][16][2];
   __shared__ uint32_t s_ticket;
@@ -639,7 +646,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   JMA_GLOBAL float* g_pacc = (JMA_GLOBAL float*)a.part_acc;
   JMA_GLOBAL float* g_pml = (JMA_GLOBAL float*)a.part_ml;
   JMA_GLOBAL int* g_err = (JMA_GLOBAL int*)a.err;
-  uint32_t ns, item, hg, kvh, seq, pos;
+  uint32_t ns, item, hg, hgv, slice, kvh, seq, pos;
   KV *kb, *vb;
   if constexpr (kSimple) {
     // Only the preloaded arguments here: the rest are fetched after the first tile loads issue.
@@ -654,13 +661,15 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     ns = 0;
     item = 0;
     hg = 0;
-    kvh = rest;
+    hgv = rest % kSlices;
+    slice = hgv;
+    kvh = rest / kSlices;
     seq = 0;
     pos = rows_start + row;
     ring = p_ring;
-    hgroups = 1;
+    hgroups = kSlices;
     kb = (KV*)g_kb + (uint64_t)kvh * cap * DK;
-    vb = (KV*)g_vb + (uint64_t)kvh * cap * DV;
+    vb = (KV*)g_vb + (uint64_t)kvh * cap * DV + slice * DVS * TileT::kBlk;
   } else {
     uint32_t r_seq = a.rows.seq[row], r_pos = a.rows.pos[row], r_ns = a.nsplit[row],
              r_item0 = a.item_start[row];
@@ -678,12 +687,14 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     ns = ns_uniform ? ns_uniform : r_ns;
     if (split >= ns) return;  // a listed row with fewer splits than the grid's widest row
     item = group_item0(ns_uniform, r_item0, row, hkv, hgroups, rest, ns) + split;
-    hg = hgroups == 1 ? 0u : rest % hgroups;
+    hgv = hgroups == 1 ? 0u : rest % hgroups;
+    hg = hgv / kSlices;
+    slice = hgv % kSlices;
     kvh = hgroups == 1 ? rest : rest / hgroups;
     seq = rows_contig ? rows_seq0 : r_seq;
     pos = rows_contig ? rows_start + row : r_pos;
     kb = (KV*)g_k + seq * seq_stride_k + layer_off_k + (uint64_t)kvh * cap * DK;
-    vb = (KV*)g_v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV;
+    vb = (KV*)g_v + seq * seq_stride_v + layer_off_v + (uint64_t)kvh * cap * DV + slice * DVS * TileT::kBlk;
   }
   const uint32_t first = first_visible(pos, window);
   const uint32_t t_begin = first / kBlk, t_end = pos / kBlk + 1;
@@ -728,7 +739,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     asm volatile("" : "+s"(g_q), "+s"(g_cos), "+s"(g_sin), "+s"(g_kn), "+s"(g_vn), "+s"(g_ctr),
                  "+s"(g_out), "+s"(g_tag), "+s"(g_pacc), "+s"(g_pml), "+s"(g_err));
     ns = ns_uniform;
-    item = group_item0(ns, 0, row, hkv, 1, kvh, ns) + split;
+    item = group_item0(ns, 0, row, hkv, kSlices, rest, ns) + split;
   }
   const float *q_in = (const float*)g_q, *cos_t = (const float*)g_cos, *sin_t = (const float*)g_sin;
   const float *k_new = (const float*)g_kn, *v_new = (const float*)g_vn;
@@ -740,7 +751,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   int* err = (int*)g_err;
 
   const bool fused = ns > 1 && counters != nullptr;
-  const uint64_t gid = group_counter(row, hkv, kvh, hgroups, hg);
+  const uint64_t gid = group_counter(row, hkv, kvh, hgroups, hgv);
   // Arrival ticket: its round trip overlaps the tile loads.
   uint32_t ticket = 0;
   if (fused && threadIdx.x == 0)
@@ -832,7 +843,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         if (rot) rotate_pair(y0, y1, afc[turn], afs[turn]);
         s_new_k[e0] = (KV)y0;
         s_new_k[e1] = (KV)y1;
-        if (hg == 0) {
+        if (hg == 0 && slice == 0) {
           kb[k_index(slot, e0, DK, kF16)] = (KV)y0;
           kb[k_index(slot, e1, DK, kF16)] = (KV)y1;
         }
@@ -842,7 +853,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         if (a.v_norm != 0u) value_rms_norm(vx, DV, a.norm_eps, v0, v1);
         s_new_v[d] = (KV)v0;
         s_new_v[d + 1] = (KV)v1;
-        if (hg == 0) {
+        if (hg == 0 && slice == 0) {  // vb is the unsliced base here
           const uint32_t r = kF16 ? perm32(slot % kBlk) : slot % kBlk;
           KV* vp = vb + (uint64_t)(slot / kBlk) * DV * kBlk + (uint64_t)d * kBlk + r;
           vp[0] = (KV)v0;
@@ -955,7 +966,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     auto patch_v = [&]() JMA_INL {
       KV nv[kNv];
 #pragma unroll
-      for (int n = 0; n < kNv; ++n) nv[n] = s_new_v[16 * n + c16];
+      for (int n = 0; n < kNv; ++n) nv[n] = s_new_v[slice * DVS + 16 * n + c16];
       const uint32_t ev = v_at % (uint32_t)kQ;
 #pragma unroll
       for (int e = 0; e < kQ; ++e) {
@@ -1140,50 +1151,50 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   if (reducer && threadIdx.x == 0)  // every ticket of this launch is taken: reset for the next
     __hip_atomic_store(&counters[gid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint64_t item0 = item - split;
-  float* o_grp = out + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DV;
+  float* o_grp = out + ((uint64_t)row * num_heads + kvh * group + hg * 16) * DV + slice * DVS;
   if (reducer) {
     // Sub-threads per quad: at least B / 8 (so a thread takes at most 8 splits), all of the
     // workgroup's threads when the head group has few quads.
     constexpr int kSubMax = kW;  // 64 * kW threads over >= 64 quads
-    const bool narrow = nreal * (DV / 4) * kSubMax <= 64 * kW;
+    const bool narrow = nreal * (DVS / 4) * kSubMax <= 64 * kW;
     // One quad per thread covers every quad of the group in one poll round; only the four-wave
     // instances (head dim >= 256, one wave per SIMD) have the registers for all its splits.
-    const bool one_round = kW == 4 && nreal * (DV / 4) <= 64 * kW;
+    const bool one_round = kW == 4 && nreal * (DVS / 4) <= 64 * kW;
     if (ns <= 8) {
-      if (narrow) reduce_group<8, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-      else reduce_group<8, 1, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      if (narrow) reduce_group<8, kSubMax, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<8, 1, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     } else if (ns <= 16) {
-      if (narrow) reduce_group<16, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-      else if (kW == 4 && one_round) reduce_group<16, kW == 4 ? 1 : 2, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-      else reduce_group<16, 2, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      if (narrow) reduce_group<16, kSubMax, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else if (kW == 4 && one_round) reduce_group<16, kW == 4 ? 1 : 2, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<16, 2, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     } else {
-      if (narrow) reduce_group<32, kSubMax, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-      else if (kW == 4 && one_round) reduce_group<32, kW == 4 ? 1 : 4, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
-      else reduce_group<32, 4, DV, kW>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      if (narrow) reduce_group<32, kSubMax, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else if (kW == 4 && one_round) reduce_group<32, kW == 4 ? 1 : 4, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<32, 4, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     }
     return;
   }
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(part_f);
-  for (uint32_t j = threadIdx.x; j < nreal * (DV / 4); j += 64 * kW) {
-    const uint32_t hs = j / (DV / 4), e = (j % (DV / 4)) * 4;
+  for (uint32_t j = threadIdx.x; j < nreal * (DVS / 4); j += 64 * kW) {
+    const uint32_t hs = j / (DVS / 4), e = (j % (DVS / 4)) * 4;
     float mx, lw;
     float4_t aw;
-    wave_partial<DV, kW>(s_acc, s_ml, hs, e, mx, lw, aw);
+    wave_partial<DVS, kW>(s_acc, s_ml, hs, e, mx, lw, aw);
     if (ns == 1) {
       if (!(lw > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
       *(float4_t*)(o_grp + hs * DV + e) = aw * (1.0f / lw);
     } else if (!fused) {  // reduce_kernel combines the splits after this launch
-      *(float4_t*)(part_acc + sep_acc_float(item, hs, DV, e)) = aw;
+      *(float4_t*)(part_acc + sep_acc_float(item, hs, DVS, e)) = aw;
       if (e == 0) {
         part_ml[sep_ml_float(item, hs)] = mx;
         part_ml[sep_ml_float(item, hs) + 1] = lw;
       }
     } else {
-      const uint32_t off = (uint32_t)(fused_part_float(item, hs, DV, 0) * 4);
+      const uint32_t off = (uint32_t)(fused_part_float(item, hs, DVS, 0) * 4);
       store_part(rs, off + e * 4, float4_t{canon(aw[0]), canon(aw[1]), canon(aw[2]), canon(aw[3])});
       if (e == 0) {
         const float c = __uint_as_float(kClear);
-        store_part(rs, off + DV * 4, float4_t{canon(mx), canon(lw), c, c});
+        store_part(rs, off + DVS * 4, float4_t{canon(mx), canon(lw), c, c});
       }
     }
   }
@@ -1386,23 +1397,31 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, 16, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, 32, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, 64, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, 128, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
     case 256:
+      if (a.slices == 4) {  // short rows: four 64-column slices, at most one tile per wave
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 64, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        break;
+      }
       // One tile per wave (the long-context plans cut this fine) needs one tile buffer only.
       if (a.tiles_per_split <= (uint32_t)decode_waves(256))
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       else
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     case 512:
+      if (a.slices == 4) {  // short rows: four 128-column slices
+        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 128, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        break;
+      }
       // One tile buffer always: a tile is the whole register budget of a wave at this width.
-      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 512, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     default: return hipErrorInvalidValue;
   }

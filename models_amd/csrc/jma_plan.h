@@ -88,8 +88,14 @@ JMA_HD uint64_t sep_ml_float(uint64_t item, uint32_t hs) { return (item * kHeadS
 // the target workgroups (few long rows: one sequence at a long context with few KV heads), rows
 // are cut wider, up to kMaxWideSplits splits, and reduce_kernel combines them (`separate`); a
 // context running separate kernels (`unfused`) always does.
+//
+// Column slices: at head dim 256 or 512 a launch of few workgroups (short rows: a sliding-window
+// layer) cuts each head's value columns among `slices` = 4 workgroups, each computing q.K over its
+// tiles and V and the output for a quarter of the columns. That gives four times the workgroups,
+// each streaming K and a quarter of V (instead of all of V), with a quarter of the partials to
+// exchange per split. The slices are virtual head groups: `hgroups` is head groups x slices.
 struct DecodePlan {
-  uint32_t hgroups = 0, tiles_per_split = 0, total_items = 0, max_splits = 0, ns_uniform = 0;
+  uint32_t hgroups = 0, slices = 1, tiles_per_split = 0, total_items = 0, max_splits = 0, ns_uniform = 0;
   bool any_split = false, separate = false;
   uint32_t nsplit[kMaxRows] = {};
   uint32_t item_start[kMaxRows + 1] = {};
@@ -140,6 +146,16 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     for (uint32_t i = 0; i < count; ++i) few += (ntiles[i] + tps - 1) / tps * hkv * p.hgroups;
     if (few * 8 < target) tps /= 2;
   }
+  // Column slices (above): fused plans of at most one tile per wave at head dim 256 (the sliced
+  // instance keeps one tile buffer), any at 512, whose sliced launch stays within half the target.
+  if (!unfused && !wide && dk == dv && (dk == 512 || (dk == 256 && tps <= (uint64_t)decode_waves(dk)))) {
+    uint64_t n = 0;
+    for (uint32_t i = 0; i < count; ++i) n += (ntiles[i] + tps - 1) / tps * hkv * p.hgroups;
+    if (n * 4 * 2 <= target) {
+      p.slices = 4;
+      p.hgroups *= 4;
+    }
+  }
   p.tiles_per_split = (uint32_t)tps;
   uint32_t items = 0;
   bool uniform = true;
@@ -159,7 +175,7 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     p.acc_bytes = (uint64_t)items * kHeadSlots * dv * 4;
     p.ml_bytes = (uint64_t)items * kHeadSlots * 2 * 4;
   } else if (p.any_split) {
-    p.part_f_bytes = (uint64_t)items * kHeadSlots * (dv + 4) * 4;
+    p.part_f_bytes = (uint64_t)items * kHeadSlots * (dv / p.slices + 4) * 4;
     p.counter_bytes = (uint64_t)count * hkv * p.hgroups * 4;
   }
   return p;

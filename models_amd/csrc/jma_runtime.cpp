@@ -414,13 +414,15 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
                        kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave, ctx->unfused,
                        ctx->min_split_tiles);
   a.tiles_per_split = plan.tiles_per_split;
+  a.hgroups = plan.hgroups;  // virtual head groups (head groups x column slices)
+  a.slices = plan.slices;
   for (uint32_t i = 0; i <= rows.count; ++i) a.item_start[i] = plan.item_start[i];
   for (uint32_t i = 0; i < rows.count; ++i) a.nsplit[i] = plan.nsplit[i];
   a.max_splits = plan.max_splits;
   a.total_items = plan.total_items;
   a.ns_uniform = plan.ns_uniform;
   const bool uniform = plan.ns_uniform != 0;
-  if (uniform && rows.contiguous && a.hgroups == 1) {
+  if (uniform && rows.contiguous && a.hgroups == a.slices) {
     const size_t es = kv->f16() ? 2 : 4;
     a.k_base = (char*)a.kv.k + (a.kv.seq_stride_k * rows.seq0 + a.kv.layer_off_k) * es;
     a.v_base = (char*)a.kv.v + (a.kv.seq_stride_v * rows.seq0 + a.kv.layer_off_v) * es;

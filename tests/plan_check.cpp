@@ -51,8 +51,11 @@ void check(const Case& c) {
   const DecodePlan p = plan_decode(count, c.pos.data(), c.window, c.hkv, c.group, c.dk, c.dv, c.f16,
                                    c.target, c.tiles_per_wave, c.unfused, c.min_split);
   const uint32_t blk = (uint32_t)v_block(c.f16);
-  const uint32_t hgroups = p.hgroups;
-  if (hgroups != (c.group + kHeadSlots - 1) / kHeadSlots) die(c, "head groups");
+  const uint32_t hgroups = p.hgroups;  // virtual head groups: head groups x column slices
+  if (p.slices != 1 && p.slices != 4) die(c, "column slices");
+  if (hgroups != (c.group + kHeadSlots - 1) / kHeadSlots * p.slices) die(c, "head groups");
+  if (p.slices > 1 && (p.separate || c.dk < 256 || (c.dk == 256 && p.tiles_per_split > 4)))
+    die(c, "column slices outside the sliced instances (fused, d 256 one tile per wave, d 512)");
   if (p.part_f_bytes > 0x7FFFFFF0ull) die(c, "fused partials exceed 32-bit buffer offsets");
   std::vector<int> owner(p.total_items, 0);
   const uint64_t part_f_floats = p.part_f_bytes / 4, acc_floats = p.acc_bytes / 4;
@@ -68,12 +71,13 @@ void check(const Case& c) {
     const uint32_t t_begin = first / blk, t_end = pos / blk + 1;
     std::vector<int> seen(t_end - t_begin, 0);
     for (uint32_t rest = 0; rest < c.hkv * hgroups; ++rest) {
-      const uint32_t kvh = rest / hgroups, hg = rest % hgroups;
+      const uint32_t kvh = rest / hgroups, hgv = rest % hgroups, hg = hgv / p.slices;
       const uint32_t nreal = std::min<uint32_t>(kHeadSlots, c.group - hg * kHeadSlots);
+      const uint32_t dvs = c.dv / p.slices;  // value columns of the slice
       const uint64_t item0 = group_item0(p.ns_uniform, p.item_start[row], row, c.hkv, hgroups, rest, ns);
       if (item0 + ns > p.total_items) die(c, "group items past total_items");
       if (ns > 1 && !p.separate) {
-        const uint64_t gid = group_counter(row, c.hkv, kvh, hgroups, hg);
+        const uint64_t gid = group_counter(row, c.hkv, kvh, hgroups, hgv);
         if (gid >= counters) die(c, "arrival ticket outside the counter buffer");
       }
       for (uint32_t split = 0; split < p.max_splits; ++split) {
@@ -85,6 +89,7 @@ void check(const Case& c) {
         if (s_t0 >= s_t1) die(c, "a split without tiles");
         if (rest == 0)
           for (uint32_t t = s_t0; t < s_t1; ++t) seen[t - t_begin]++;
+        if (p.slices > 1 && c.dk == 256 && s_t1 - s_t0 > 4) die(c, "sliced d256 split with more than one tile per wave");
         if (ns == 1) continue;
         for (uint32_t hs = 0; hs < nreal; ++hs) {
           if (p.separate) {
@@ -93,8 +98,8 @@ void check(const Case& c) {
           } else {
             // producer stores acc quads and the (m, l, pad, pad) word group; the reducer reads
             // the same words of every split of the group
-            if (fused_part_float(item, hs, c.dv, c.dv + 3) >= part_f_floats) die(c, "part_f index");
-            if (fused_part_float(item, hs, c.dv, c.dv + 3) * 4 + 16 > 0x7FFFFFF0ull)
+            if (fused_part_float(item, hs, dvs, dvs + 3) >= part_f_floats) die(c, "part_f index");
+            if (fused_part_float(item, hs, dvs, dvs + 3) * 4 + 16 > 0x7FFFFFF0ull)
               die(c, "part_f byte offset beyond the buffer descriptor");
           }
         }
@@ -103,7 +108,7 @@ void check(const Case& c) {
         // reduce_kernel: one workgroup per (row, query head, 64-element chunk) reads the row's
         // group base + split for split < ns
         const uint64_t base = group_item0(p.ns_uniform, p.item_start[row], row, c.hkv, hgroups,
-                                          kvh * hgroups + hg, ns);
+                                          kvh * hgroups + hgv, ns);
         if (base != item0) die(c, "reduce_kernel group base differs from the producers'");
         for (uint32_t hs = 0; hs < nreal; ++hs)
           if (sep_acc_float(base + ns - 1, hs, c.dv, c.dv - 1) >= acc_floats) die(c, "reduce read");
@@ -115,8 +120,8 @@ void check(const Case& c) {
   }
   for (uint64_t i = 0; i < p.total_items; ++i)
     if (owner[i] != 1) die(c, "work item " + std::to_string(i) + " not written exactly once");
-  printf("%-44s rows %3u tiles/split %5u splits <= %4u items %7u %s %8.1f KiB\n", c.name.c_str(),
-         count, p.tiles_per_split, p.max_splits, p.total_items,
+  printf("%-44s rows %3u tiles/split %5u splits <= %4u items %7u slices %u %s %8.1f KiB\n", c.name.c_str(),
+         count, p.tiles_per_split, p.max_splits, p.total_items, p.slices,
          p.separate ? "separate" : (p.any_split ? "fused   " : "single  "),
          (double)(p.separate ? p.acc_bytes + p.ml_bytes : p.part_f_bytes) / 1024.0);
 }
