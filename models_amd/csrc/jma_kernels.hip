@@ -815,16 +815,21 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   bool qrot[kIt];
 #pragma unroll
   for (int it = 0; it < kIt; ++it) {
-    const uint32_t k = min(threadIdx.x + 64 * kW * it, nq - 1);  // indices clamped: every load valid
+    // Turns past the head group's pairs (fewer than 16 heads) load nothing; within a turn the
+    // indices are clamped, so every load is valid.
+    const uint32_t k = min(threadIdx.x + 64 * kW * it, nq - 1);
     const uint32_t hs = k / kHalf, j = k % kHalf;
     qrot[it] = rope_on && j < pairs;
     qe0[it] = hs * DK + (qrot[it] && neox ? j : 2 * j);
     qe1[it] = hs * DK + (qrot[it] && neox ? j + pairs : 2 * j + 1);
-    qy0[it] = qg[qe0[it]];
-    qy1[it] = qg[qe1[it]];
-    if (rope_on) {
-      qfc[it] = cs[qrot[it] ? j : 0u];
-      qfs[it] = sn[qrot[it] ? j : 0u];
+    qy0[it] = qy1[it] = qfc[it] = qfs[it] = 0.0f;
+    if (64 * kW * it < nq) {
+      qy0[it] = qg[qe0[it]];
+      qy1[it] = qg[qe1[it]];
+      if (rope_on) {
+        qfc[it] = cs[qrot[it] ? j : 0u];
+        qfs[it] = sn[qrot[it] ? j : 0u];
+      }
     }
   }
 
@@ -998,19 +1003,35 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[4 * b + e] = sc[b][e];
     } else if constexpr (kF16) {
+      // The k-chunks accumulate into kNa independent chains per 16-row half (a dependent matrix
+      // op waits for its predecessor's result), added at the end.
+      constexpr int kNa = kC >= 8 ? 4 : (kC >= 4 ? 2 : 1);
+      float4_t sc[2][kNa];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        float4_t sc = {0.f, 0.f, 0.f, 0.f};
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int c = 0; c < kC; ++c) {
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qhi[c], sc, 0, 0, 0);
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qlo[c], sc, 0, 0, 0);
+        for (int i = 0; i < kNa; ++i) sc[b][i] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kC; ++c)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          sc[b][c % kNa] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qhi[c], sc[b][c % kNa], 0, 0, 0);
+          sc[b][c % kNa] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qlo[c], sc[b][c % kNa], 0, 0, 0);
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s[4 * b + e] = sc[e];
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int w = kNa / 2; w >= 1; w /= 2)
+#pragma unroll
+          for (int i = 0; i < w; ++i) sc[b][i] += sc[b][i + w];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[4 * b + e] = sc[b][0][e];
       }
     } else {
-      float4_t sc = {0.f, 0.f, 0.f, 0.f};
+      constexpr int kNa = kC >= 4 ? 4 : kC;  // independent chains, as above
+      float4_t sc[kNa];
+#pragma unroll
+      for (int i = 0; i < kNa; ++i) sc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < kC; ++c) {
         half8_t unused_h, unused_l;
@@ -1019,10 +1040,14 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         else qc = qf[c];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          sc = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[c][e], qc[e], sc, 0, 0, 0);
+          sc[c % kNa] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[c][e], qc[e], sc[c % kNa], 0, 0, 0);
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[e] = sc[e];
+      for (int w = kNa / 2; w >= 1; w /= 2)
+#pragma unroll
+        for (int i = 0; i < w; ++i) sc[i] += sc[i + w];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = sc[0][e];
     }
     if constexpr (kSplitKV) {  // V of this tile, now that K's registers are free
       cur.load_v(vb, slot0_of(tt), c16, g);
