@@ -609,11 +609,17 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   // q rows share their LDS with the waves' combine area, which is written only after every wave
   // has left its tile loop.
   constexpr bool kQLds = DK >= 512;
-  constexpr int kAccFloats = kW * 16 * DVS, kQFloats = 16 * (DK + 4);
+  // q rows in LDS, padded against bank conflicts: f32 KV keeps them as floats (kQRowF per row);
+  // f16 KV keeps the f16 hi and lo halves of each element (x = hi + lo to ~2^-22), formed once
+  // while staging, in two arrays of kQRowH halves per row.
+  constexpr int kQRowF = DK + 4, kQRowH = DK + 8;
+  constexpr int kAccFloats = kW * 16 * DVS, kQFloats = kF16 ? 16 * kQRowH : 16 * kQRowF;
   __shared__ __attribute__((aligned(16))) float s_acc_mem[kQLds && kQFloats > kAccFloats ? kQFloats : kAccFloats];
   __shared__ __attribute__((aligned(16))) float s_q_mem[kQLds ? 4 : kQFloats];
   float (*s_acc)[16][DVS] = (float (*)[16][DVS])s_acc_mem;
-  float (*s_q)[DK + 4] = (float (*)[DK + 4])(kQLds ? s_acc_mem : s_q_mem);  // q rows, padded against bank conflicts
+  float (*s_q)[kQRowF] = (float (*)[kQRowF])(kQLds ? s_acc_mem : s_q_mem);
+  _Float16 (*s_qh)[kQRowH] = (_Float16 (*)[kQRowH])(kQLds ? s_acc_mem : s_q_mem);
+  _Float16 (*s_ql)[kQRowH] = s_qh + 16;
   __shared__ float s_ml[kW][16][2];
   __shared__ uint32_t s_ticket;
   __shared__ __attribute__((aligned(16))) KV s_new_k[DK];  // the appended row, rotated
@@ -895,8 +901,18 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         u1 = u1 * sc * qw[qe1[it] - hs * DK];
       }
       if (qrot[it]) rotate_pair(u0, u1, qfc[it], qfs[it]);
-      s_q[hs][qe0[it] - hs * DK] = u0 * qscale;
-      s_q[hs][qe1[it] - hs * DK] = u1 * qscale;
+      const float x0 = u0 * qscale, x1 = u1 * qscale;
+      const uint32_t f0 = qe0[it] - hs * DK, f1 = qe1[it] - hs * DK;
+      if constexpr (kF16) {
+        const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+        s_qh[hs][f0] = h0;
+        s_ql[hs][f0] = (_Float16)(x0 - (float)h0);
+        s_qh[hs][f1] = h1;
+        s_ql[hs][f1] = (_Float16)(x1 - (float)h1);
+      } else {
+        s_q[hs][f0] = x0;
+        s_q[hs][f1] = x1;
+      }
     }
   }
   if constexpr (!kOne)
@@ -909,22 +925,11 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   half8_t qhi[kF16 ? kCR : 1], qlo[kF16 ? kCR : 1];
   float4_t qf[kF16 ? 1 : kCR];
   auto q_chunk = [&](int c, half8_t& hi, half8_t& lo, float4_t& f) JMA_INL {
-    float x[kQ];
-#pragma unroll
-    for (int i = 0; i < kQ; i += 4) {
-      const float4_t v4 = head_ok ? *(const float4_t*)&s_q[c16][(kF16 ? 32 : 16) * c + kQ * g + i]
-                                  : float4_t{0.f, 0.f, 0.f, 0.f};
-      x[i] = v4[0], x[i + 1] = v4[1], x[i + 2] = v4[2], x[i + 3] = v4[3];
-    }
-#pragma unroll
-    for (int e = 0; e < kQ; ++e) {
-      if constexpr (kF16) {
-        const _Float16 h = (_Float16)x[e];
-        hi[e] = h;
-        lo[e] = (_Float16)(x[e] - (float)h);
-      } else {
-        f[e] = x[e];
-      }
+    if constexpr (kF16) {
+      hi = head_ok ? *(const half8_t*)&s_qh[c16][32 * c + 8 * g] : half8_t{};
+      lo = head_ok ? *(const half8_t*)&s_ql[c16][32 * c + 8 * g] : half8_t{};
+    } else {
+      f = head_ok ? *(const float4_t*)&s_q[c16][16 * c + 4 * g] : float4_t{0.f, 0.f, 0.f, 0.f};
     }
   };
   if constexpr (!kQLds) {
