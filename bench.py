@@ -43,11 +43,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix
 # HBM bytes per decode launch on C2 measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# (bench.py --no-cpu --no-prefill --no-c1 --no-c4 --no-c5 --steps 8 --warmup 2), each scaled by
-# what the counter reads for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4406.3 KiB x 2.0 +
-# 316.6 KiB. Recorded with its commands in profiles/decode_c2.md; counters cannot be read from
-# inside this process.
-DECODE_TRAFFIC_BYTES = round((4406.3 * 2.0 + 316.6) * 1024)
+# (bench.py --no-cpu --no-prefill --no-c1 --no-c4 --no-c5 --no-proj --steps 8 --warmup 2), each
+# scaled by what the counter reads for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4388.3 KiB
+# x 2.0 + 316.6 KiB. The counter passes are kept with the decode profile summary under profiles/;
+# counters cannot be read from inside this process.
+DECODE_TRAFFIC_BYTES = round((4388.3 * 2.0 + 316.6) * 1024)
 
 
 def log(msg: str) -> None:
@@ -351,6 +351,59 @@ def run_c4(hip, A, rt, synth, reps: int = 10):
     return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, rows=sum(lens) + B)
 
 
+def run_c5_layer(hip, A, rt, synth, sliding: bool, per_graph: int = 32, reps: int = 5):
+    """One C5 layer on its own (profiling aid): a sliding-window layer (window 512 on a RING of
+    576 slots, theta 1e4) or a global layer (32704 positions, theta 1e6) of the C5 shape (4 Q / 1
+    KV heads, d 256, NeoX, f16 KV), filled with its prior positions; the decode step at position
+    32704 (RoPE, append, attention and the cross-split reduction) is replayed from a graph of
+    `per_graph` launches, and HIP events around the replays give the per-layer-step time. The
+    step rewrites the same row each time, so every launch sees the same cache."""
+    hq, hkv, d, prior, w = 4, 1, 256, 32704, 512
+    window, ring, theta = (w, w + 64, 1e4) if sliding else (0, 0, 1e6)
+    rope = hip.rotary_table(d, theta, 1.0, max_positions=prior + 8)
+    kv = hip.kv_cache(1, prior + 8, hkv, d, d, half_precision=True,
+                      ring_capacity=[ring] if ring else None)
+    layer = A.AttentionLayer(0, hq, sliding_window=window, neox=True, rope=rope)
+    first = prior - w if sliding else 0
+    rows, qd, kd = prior - first, hq * d, hkv * d
+    zq = rt.DeviceArray(rows * qd)
+    zq.zero()
+    dk = rt.DeviceArray.from_host(synth.normal(5, "bench/c5l/k", (rows, kd)))
+    dv = rt.DeviceArray.from_host(synth.normal(5, "bench/c5l/v", (rows, kd)))
+    kv.append_device(layer, np.zeros(rows, np.uint32), np.arange(first, prior), zq.ptr, rows * qd,
+                     dk.ptr, rows * kd, dv.ptr, rows * kd)
+    dq = rt.DeviceArray.from_host(synth.normal(5, "bench/c5l/q", (qd,)))
+    dkn = rt.DeviceArray.from_host(synth.normal(5, "bench/c5l/kn", (kd,)))
+    dvn = rt.DeviceArray.from_host(synth.normal(5, "bench/c5l/vn", (kd,)))
+    dout = rt.DeviceArray(qd)
+    stream = hip.stream()
+
+    def one():
+        kv.decode_device(layer, [0], [prior], dq.ptr, qd, dkn.ptr, kd, dvn.ptr, kd, dout.ptr, qd)
+
+    one()
+    hip.synchronize()
+    graph = rt.Graph(stream, lambda: [one() for _ in range(per_graph)])
+    for _ in range(2):
+        graph.launch()
+    rt.device_synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    best = float("inf")
+    for _ in range(reps):
+        e0.record(stream)
+        graph.launch()
+        e1.record(stream)
+        rt.device_synchronize()
+        best = min(best, e0.elapsed_ms(e1) / per_graph)
+    graph.destroy()
+    for buf in (zq, dk, dv, dq, dkn, dvn, dout):
+        buf.free()
+    kv.close()
+    rope.close()
+    nbytes = 2 * (min(prior + 1, w) if sliding else prior + 1) * hkv * d * 2
+    return dict(us=best * 1e3, bytes=nbytes, gbs=nbytes / (best * 1e-3) / 1e9)
+
+
 def run_c1(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
     """C1 Qwen3-0.6B-shaped decode step: 16 Q / 8 KV heads, d 128, NeoX theta 1e6,
     f32 KV, 512 cached positions, the new token at position 512 (RoPE, append, split-K attention
@@ -614,6 +667,9 @@ def main() -> int:
                     help="profiling aid: run only the projection measurements, print their figures")
     ap.add_argument("--c5-only", action="store_true",
                     help="profiling aid: run only the C5 long-context decode measurement")
+    ap.add_argument("--c5-layers", action="store_true",
+                    help="profiling aid: one C5 sliding-window layer and one C5 global layer, each "
+                         "replayed on its own from graphs, print their per-layer-step figures")
     ap.add_argument("--c4-only", action="store_true",
                     help="profiling aid: run only the C4 ragged decode measurement, print its figures")
     ap.add_argument("--c2-cold-only", action="store_true",
@@ -672,6 +728,13 @@ def main() -> int:
         c5 = run_c5(hip, A, rt, synth)
         print(json.dumps({"c5_us_per_token": round(c5["us_per_token"], 2), "gbs": round(c5["gbs"], 1),
                           "bytes_per_token": c5["bytes"] // c5["steps"]}), flush=True)
+        return 0
+    if args.c5_layers:
+        out = {}
+        for name, sl in (("sliding", True), ("global", False)):
+            r = run_c5_layer(hip, A, rt, synth, sl)
+            out[name] = {"us": round(r["us"], 3), "gbs": round(r["gbs"], 1), "bytes": r["bytes"]}
+        print(json.dumps({"c5_layers": out}), flush=True)
         return 0
     if args.c4_only:
         c4 = run_c4(hip, A, rt, synth)
