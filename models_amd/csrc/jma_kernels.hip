@@ -1249,57 +1249,84 @@ __device__ __forceinline__ float wave_sum64(float x) {
   return wave_sum_groups(x);
 }
 
-// One workgroup of 16 waves per (row, query head, 64-element chunk of the head's output): out =
-// sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to kMaxWideSplits.
-// Lane (s4, q) of wave w takes output quad q of the chunk for splits (16 i + w) * 4 + s4,
-// i = 0, 1, ...: each load instruction moves 16 bytes per lane, four splits' 256-byte rows. Thread
-// t also loads split t's (m, l) for the maximum M and the weights, which go through LDS; every
-// load is issued before any is used (one memory round trip). Sums run in a fixed order (per lane
-// over i, then the four split lanes in a tree, then the waves in order), so the result is the
-// same on every run for a plan.
-template <int DV>
-__global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
+// One workgroup of kWaves = 16 waves per (row, query head, 64-element chunk of the head's
+// output): out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to
+// kMaxWideSplits. (Four waves, each taking 16 splits per lane, measured slower on a 256-split C5
+// global layer: 14.1 against 12.2 us per layer-step; sixteen waves issue the loads in parallel.)
+// Lane (s, q) of wave w takes output quad q of the chunk for splits
+// (kWaves i + w) * 4 + s, so every load instruction moves 16 bytes per lane (four splits'
+// 256-byte rows, 1 KB), and thread t loads split t's (m, l) (and t + 64 kWaves, ... at 4 waves);
+// all loads are issued before any is used (one memory round trip). The workgroup agrees on M
+// through DPP and row-swap exchanges and LDS, takes the weights 2^(m_s - M) from the (m, l) staged
+// in LDS, sums each lane's splits in order, then the four split lanes in a fixed tree and the
+// waves in wave order: the same result on every run for a plan. The leading scalar arguments
+// (the partial buffers, the uniform split count, the head counts) arrive preloaded in SGPRs, so
+// the loads need no kernel-argument load first; the row tables are read only for listed rows.
+template <int DV, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc, const float* p_ml,
+                                                             uint32_t p_ns, uint32_t p_heads,
+                                                             uint32_t p_group, const DecodeArgs a) {
   constexpr uint32_t kChunks = (DV + 63) / 64;
-  constexpr int kWaves = 16;
   constexpr int kPer = kMaxWideSplits / (kWaves * 4);  // splits one lane sums at most
+  constexpr uint32_t kMl = kMaxWideSplits / (64 * kWaves);  // (m, l) words one thread loads
   __shared__ float2 s_ml[kMaxWideSplits];
   __shared__ float s_m[kWaves], s_l[kWaves];
   __shared__ float4_t s_x[kWaves][16];
+  JMA_GLOBAL const float* g_acc = (JMA_GLOBAL const float*)p_acc;
+  JMA_GLOBAL const float* g_ml = (JMA_GLOBAL const float*)p_ml;
+  asm volatile("" : "+s"(g_acc), "+s"(g_ml), "+s"(p_ns), "+s"(p_heads), "+s"(p_group));
   const uint32_t chunk = blockIdx.x % kChunks;
-  const uint32_t row = blockIdx.x / kChunks / a.num_heads;
-  const uint32_t head = blockIdx.x / kChunks % a.num_heads;
-  const uint32_t hkv = a.num_heads / a.group;
-  const uint32_t ns = a.ns_uniform ? a.ns_uniform : a.nsplit[row];
+  const uint32_t row = blockIdx.x / kChunks / p_heads;
+  const uint32_t head = blockIdx.x / kChunks % p_heads;
+  const uint32_t hkv = p_heads / p_group;
+  const uint32_t hgroups = (p_group + kHeadSlots - 1) / kHeadSlots;
+  const uint32_t ns = p_ns ? p_ns : a.nsplit[row];
   if (ns == 1) return;
-  const uint32_t kvh = head / a.group;
-  const uint32_t hl = head % a.group;
+  const uint32_t kvh = head / p_group;
+  const uint32_t hl = head % p_group;
   const uint32_t hg = hl / 16, c16 = hl % 16;
-  const uint64_t base = group_item0(a.ns_uniform, a.item_start[row], row, hkv, a.hgroups,
-                                    kvh * a.hgroups + hg, ns);
+  const uint64_t base = group_item0(p_ns, p_ns ? 0u : a.item_start[row], row, hkv, hgroups,
+                                    kvh * hgroups + hg, ns);
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t s4 = lane >> 4, q = lane & 15;
   const uint32_t e = chunk * 64 + 4 * q;
   const uint32_t el = e < DV ? e : DV - 4;  // lanes past the head load a valid quad
+  const float* acc = (const float*)g_acc;
+  const float* mlp = (const float*)g_ml;
 
-  float2 ml = {-INFINITY, 0.0f};
-  if (tid < ns) ml = *(const float2*)(a.part_ml + sep_ml_float(base + tid, c16));
+  float2 ml[kMl];
+#pragma unroll
+  for (uint32_t i = 0; i < kMl; ++i) {
+    const uint32_t sp = tid + 64 * kWaves * i;
+    ml[i] = sp < ns ? *(const float2*)(mlp + sep_ml_float(base + sp, c16)) : float2{-INFINITY, 0.0f};
+  }
   float4_t xv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const uint32_t sp = (i * kWaves + wave) * 4 + s4;
-    xv[i] = sp < ns ? *(const float4_t*)(a.part_acc + sep_acc_float(base + sp, c16, DV, el))
+    xv[i] = sp < ns ? *(const float4_t*)(acc + sep_acc_float(base + sp, c16, DV, el))
                     : float4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  if (tid < ns) s_ml[tid] = ml;
-  const float mw = wave_max64(ml.x);
+  float mt = -INFINITY;
+#pragma unroll
+  for (uint32_t i = 0; i < kMl; ++i) {
+    const uint32_t sp = tid + 64 * kWaves * i;
+    if (sp < ns) s_ml[sp] = ml[i];
+    mt = fmaxf(mt, ml[i].x);
+  }
+  const float mw = wave_max64(mt);
   if (lane == 0) s_m[wave] = mw;
   __syncthreads();
   float M = s_m[0];
 #pragma unroll
   for (int i = 1; i < kWaves; ++i) M = fmaxf(M, s_m[i]);
   const float mu = M == -INFINITY ? 0.0f : M;
-  const float lw = wave_sum64(tid < ns ? ml.y * __builtin_amdgcn_exp2f(ml.x - mu) : 0.0f);
+  float lsum = 0.0f;
+#pragma unroll
+  for (uint32_t i = 0; i < kMl; ++i)
+    if (tid + 64 * kWaves * i < ns) lsum = fmaf(ml[i].y, __builtin_amdgcn_exp2f(ml[i].x - mu), lsum);
+  const float lw = wave_sum64(lsum);
 
   float4_t X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1325,19 +1352,25 @@ __global__ __launch_bounds__(1024) void reduce_kernel(const DecodeArgs a) {
     xt += s_x[i][q];
   }
   if (!(lt > 0.0f) && q == 0 && chunk == 0) atomicOr(a.err, 1);  // all -inf, NaN or +inf
-  if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * a.num_heads + head) * DV + e) = xt * (1.0f / lt);
+  if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * p_heads + head) * DV + e) = xt * (1.0f / lt);
+}
+
+template <int DV>
+static void launch_reduce_t(const DecodeArgs& a, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((reduce_kernel<DV, 16>), grid, dim3(1024), 0, stream, a.part_acc, a.part_ml,
+                     a.ns_uniform, a.num_heads, a.group, a);
 }
 
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream) {
   const uint32_t chunks = (uint32_t)((dv + 63) / 64);
-  const dim3 grid(a.rows.count * a.num_heads * chunks), block(1024);
+  const dim3 grid(a.rows.count * a.num_heads * chunks);
   switch (dv) {
-    case 16: hipLaunchKernelGGL(reduce_kernel<16>, grid, block, 0, stream, a); break;
-    case 32: hipLaunchKernelGGL(reduce_kernel<32>, grid, block, 0, stream, a); break;
-    case 64: hipLaunchKernelGGL(reduce_kernel<64>, grid, block, 0, stream, a); break;
-    case 128: hipLaunchKernelGGL(reduce_kernel<128>, grid, block, 0, stream, a); break;
-    case 256: hipLaunchKernelGGL(reduce_kernel<256>, grid, block, 0, stream, a); break;
-    case 512: hipLaunchKernelGGL(reduce_kernel<512>, grid, block, 0, stream, a); break;
+    case 16: launch_reduce_t<16>(a, grid, stream); break;
+    case 32: launch_reduce_t<32>(a, grid, stream); break;
+    case 64: launch_reduce_t<64>(a, grid, stream); break;
+    case 128: launch_reduce_t<128>(a, grid, stream); break;
+    case 256: launch_reduce_t<256>(a, grid, stream); break;
+    case 512: launch_reduce_t<512>(a, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
