@@ -90,6 +90,8 @@ struct DecodeArgs {
   uint32_t max_splits;  // splits of the row with the most; the grid is (max_splits, kv heads *
                         // head groups, rows)
   uint32_t ns_uniform;  // > 0: every row has this many splits
+  uint32_t stream_nt;   // 1: tile loads non-temporal (a listed-rows launch streaming more K/V than
+                        // the Infinity Cache could keep)
   RowList rows;
   uint32_t item_start[kMaxRows + 1];
   uint32_t nsplit[kMaxRows];

@@ -225,12 +225,19 @@ constexpr int kDppRowMirror = 0x140;  // row_mirror: lane 15 - i within each row
 // K tiles are stored in 64-byte column panels (k_index), so each operand load below reads 1 KB of
 // contiguous memory across the wave, like the V loads.
 // V: the DVS value columns of one column slice of a DV-wide head (vb points at the slice's first
-// column; the block stride is the whole head's).
-template <typename KV, int DK, int DV, int DVS>
+// column; the block stride is the whole head's). NT: the loads are non-temporal (streamed past the
+// caches), for launches that read more K/V than the Infinity Cache could keep anyway.
+template <bool NT, typename T>
+__device__ __forceinline__ T ld16(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <typename KV, int DK, int DV, int DVS, bool NT>
 struct Tile;
 
-template <int DK, int DV, int DVS>
-struct Tile<_Float16, DK, DV, DVS> {
+template <int DK, int DV, int DVS, bool NT>
+struct Tile<_Float16, DK, DV, DVS, NT> {
   static constexpr uint32_t kBlk = 32;
   half8_t k[2][DK / 32];
   half8_t v[DVS / 16];
@@ -240,12 +247,12 @@ struct Tile<_Float16, DK, DV, DVS> {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int c = 0; c < DK / 32; ++c)
-        k[b][c] = *(const half8_t*)(kt + c * (32 * 32) + (16 * b + c16) * 32 + 8 * g);
+        k[b][c] = ld16<NT>((const half8_t*)(kt + c * (32 * 32) + (16 * b + c16) * 32 + 8 * g));
   }
   __device__ __forceinline__ void load_v(const _Float16* vb, uint32_t slot0, int c16, int g) {
     const _Float16* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
 #pragma unroll
-    for (int n = 0; n < DVS / 16; ++n) v[n] = *(const half8_t*)(vblk + (16 * n + c16) * kBlk + 8 * g);
+    for (int n = 0; n < DVS / 16; ++n) v[n] = ld16<NT>((const half8_t*)(vblk + (16 * n + c16) * kBlk + 8 * g));
   }
   __device__ __forceinline__ void load(const _Float16* kb, const _Float16* vb, uint32_t slot0,
                                        int c16, int g) {
@@ -254,8 +261,8 @@ struct Tile<_Float16, DK, DV, DVS> {
   }
 };
 
-template <int DK, int DV, int DVS>
-struct Tile<float, DK, DV, DVS> {
+template <int DK, int DV, int DVS, bool NT>
+struct Tile<float, DK, DV, DVS, NT> {
   static constexpr uint32_t kBlk = 16;
   float4_t k[DK / 16];
   float4_t v[DVS / 16];
@@ -263,12 +270,12 @@ struct Tile<float, DK, DV, DVS> {
     const float* kt = kb + (uint64_t)slot0 * DK;  // slot0 starts a tile
 #pragma unroll
     for (int c = 0; c < DK / 16; ++c)
-      k[c] = *(const float4_t*)(kt + c * (16 * 16) + c16 * 16 + 4 * g);
+      k[c] = ld16<NT>((const float4_t*)(kt + c * (16 * 16) + c16 * 16 + 4 * g));
   }
   __device__ __forceinline__ void load_v(const float* vb, uint32_t slot0, int c16, int g) {
     const float* vblk = vb + (uint64_t)(slot0 / kBlk) * DV * kBlk;
 #pragma unroll
-    for (int n = 0; n < DVS / 16; ++n) v[n] = *(const float4_t*)(vblk + (16 * n + c16) * kBlk + 4 * g);
+    for (int n = 0; n < DVS / 16; ++n) v[n] = ld16<NT>((const float4_t*)(vblk + (16 * n + c16) * kBlk + 4 * g));
   }
   __device__ __forceinline__ void load(const float* kb, const float* vb, uint32_t slot0, int c16,
                                        int g) {
@@ -587,12 +594,12 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 // and the slot capacity). The library is built with kernel-argument preloading, so they arrive in
 // scalar registers at wave start and the first tile loads do not wait for a kernel-argument
 // load; the other instances pass zeros there and read everything from `a`.
-template <typename KV, int DK, int DV, int DVS, bool kSimple, bool kOne>
+template <typename KV, int DK, int DV, int DVS, bool kSimple, bool kOne, bool kNT>
 __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     const void* p_kb, const void* p_vb, uint32_t p_start, uint32_t p_window, uint32_t p_tps,
     uint32_t p_cap, uint32_t p_ring, const DecodeArgs a) {
   constexpr bool kF16 = std::is_same<KV, _Float16>::value;
-  using TileT = Tile<KV, DK, DV, DVS>;
+  using TileT = Tile<KV, DK, DV, DVS, kNT>;
   constexpr uint32_t kBlk = TileT::kBlk;
   constexpr int kNs = kF16 ? 8 : 4;   // scores per lane per tile
   constexpr int kNv = DVS / 16;       // output fragments per lane
@@ -1448,7 +1455,7 @@ bool decode_supported(bool f16, int dk, int dv) {
   return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
 }
 
-template <typename KV, bool kSimple>
+template <typename KV, bool kSimple, bool kNT>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
   const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * decode_waves(d));
   // Preloaded leading arguments of the kSimple instance (zeros for the general one).
@@ -1460,31 +1467,31 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, 16, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, 16, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, 32, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, 64, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, 128, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, 32, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, 64, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, 128, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
     case 256:
       if (a.slices == 4) {  // short rows: four 64-column slices, at most one tile per wave
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 64, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 64, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       // One tile per wave (the long-context plans cut this fine) needs one tile buffer only.
       if (a.tiles_per_split <= (uint32_t)decode_waves(256))
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       else
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     case 512:
       if (a.slices == 4) {  // short rows: four 128-column slices
-        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 128, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 128, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       // One tile buffer always: a tile is the whole register budget of a wave at this width.
-      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 512, kSimple, true>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 512, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -1495,8 +1502,12 @@ hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStrea
   if (!decode_supported(f16, dk, dv)) return hipErrorInvalidValue;
   if (a.total_items == 0) return hipSuccess;
   const bool simple = a.k_base != nullptr;
-  if (f16) return simple ? launch_decode_t<_Float16, true>(a, dk, stream) : launch_decode_t<_Float16, false>(a, dk, stream);
-  return simple ? launch_decode_t<float, true>(a, dk, stream) : launch_decode_t<float, false>(a, dk, stream);
+  if (f16) {
+    if (simple) return launch_decode_t<_Float16, true, false>(a, dk, stream);
+    return a.stream_nt ? launch_decode_t<_Float16, false, true>(a, dk, stream)
+                       : launch_decode_t<_Float16, false, false>(a, dk, stream);
+  }
+  return simple ? launch_decode_t<float, true, false>(a, dk, stream) : launch_decode_t<float, false, false>(a, dk, stream);
 }
 
 // ================================================================ kernel 3: prefill (f16 MFMA)
