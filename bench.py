@@ -42,6 +42,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix
+F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 matrix
 # HBM bytes per decode launch on C2 measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # (bench.py --no-cpu --no-prefill --no-c1 --no-c4 --no-c5 --no-proj --steps 8 --warmup 2), each
 # scaled by what the counter reads for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4388.3 KiB
@@ -267,16 +268,31 @@ def run_c2_cold(hip, A, rt, synth, steps: int = 64):
 
 def run_c3(hip, A, rt, synth, reps: int = 10):
     """C3 causal prefill: S 2048, 24 Q heads, 8 KV heads, d 128, f16, theta 5e5 interleaved."""
-    hq, hkv, d, S, theta = 24, 8, 128, 2048, 5e5
+    return run_prefill(hip, A, rt, synth, True, 24, 8, 128, 2048, 5e5, False, "bench/c3", reps)
+
+
+# Causal prefills beside C3 (no BASELINE config of their own): f32 caches run the d-sliced kernel
+# on the f32 matrix ops, f16 caches at head dim 512 (Gemma 4 full layers) the same kernel on the
+# f16 ones. Fields: name, half, Q heads, KV heads, head dim, rows, RoPE theta, NeoX.
+PREFILL_OTHERS = [
+    ("c1_shape_f32", False, 16, 8, 128, 512, 1e6, True),
+    ("c3_shape_f32", False, 24, 8, 128, 2048, 5e5, False),
+    ("gemma4_full_layer_f16_d512", True, 8, 1, 512, 2048, 1e6, True),
+]
+
+
+def run_prefill(hip, A, rt, synth, half, hq, hkv, d, S, theta, neox, tag, reps: int = 10):
+    """Causal prefill of S rows (attention over the cached, rotated rows: the kernel alone, the
+    append done beforehand); HIP events around `reps` back-to-back launches."""
     rope = hip.rotary_table(d, theta, 1.0, max_positions=S)
-    kv = hip.kv_cache(1, S, hkv, d, d, half_precision=True)
+    kv = hip.kv_cache(1, S, hkv, d, d, half_precision=half)
     stream = hip.stream()
-    dq = rt.DeviceArray.from_host(synth.normal(3, "bench/c3/q", (S, hq * d)))
-    dk = rt.DeviceArray.from_host(synth.normal(3, "bench/c3/k", (S, hkv * d)))
-    dv = rt.DeviceArray.from_host(synth.normal(3, "bench/c3/v", (S, hkv * d)))
+    dq = rt.DeviceArray.from_host(synth.normal(3, tag + "/q", (S, hq * d)))
+    dk = rt.DeviceArray.from_host(synth.normal(3, tag + "/k", (S, hkv * d)))
+    dv = rt.DeviceArray.from_host(synth.normal(3, tag + "/v", (S, hkv * d)))
     dqr = rt.DeviceArray(S * hq * d)
     dout = rt.DeviceArray(S * hq * d)
-    layer = A.AttentionLayer(0, hq, neox=False, rope=rope)
+    layer = A.AttentionLayer(0, hq, neox=neox, rope=rope)
     kv.append_device(layer, np.zeros(S, np.uint32), np.arange(S), dq.ptr, dq.count, dk.ptr,
                      dk.count, dv.ptr, dv.count, dqr.ptr, dqr.count)
     kv.attend_causal_device(layer, 0, 0, S, dqr.ptr, dqr.count, dout.ptr, dout.count)
@@ -295,6 +311,20 @@ def run_c3(hip, A, rt, synth, reps: int = 10):
     kv.close()
     rope.close()
     return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12)
+
+
+def run_prefill_others(hip, A, rt, synth):
+    out = {}
+    for name, half, hq, hkv, d, S, theta, neox in PREFILL_OTHERS:
+        r = run_prefill(hip, A, rt, synth, half, hq, hkv, d, S, theta, neox, "bench/" + name,
+                        reps=5)
+        peak = F16_MFMA_PEAK_TFLOPS if half else F32_MFMA_PEAK_TFLOPS
+        out[name] = {"workload": f"causal prefill S {S}, {hq} Q / {hkv} KV heads, d {d}, "
+                                f"{'f16' if half else 'f32'} KV",
+                     "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 2),
+                     "frac_of_mfma_peak": round(r["tflops"] / peak, 4),
+                     "mfma_peak_tflops": peak, "flops": r["flops"]}
+    return out
 
 
 def run_c4(hip, A, rt, synth, reps: int = 10):
@@ -679,6 +709,10 @@ def main() -> int:
                     help="profiling aid: run only the C1 f32 decode-step measurement")
     ap.add_argument("--prefill-only", action="store_true",
                     help="profiling aid: run only the C3 prefill measurement, print its figures")
+    ap.add_argument("--prefill-others-only", action="store_true",
+                    help="profiling aid: run only the f32 and head-dim-512 prefill measurements")
+    ap.add_argument("--no-prefill-others", action="store_true",
+                    help="skip the f32 and head-dim-512 prefill figures")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="profiling aid: one device-to-device copy of MIB MiB (the runtime's copy "
                          "kernel), to calibrate the FETCH_SIZE / WRITE_SIZE counters")
@@ -721,6 +755,9 @@ def main() -> int:
         print(json.dumps({"prefill_us": round(c3["ms"] * 1e3, 2), "tflops": round(c3["tflops"], 2),
                           "flops": c3["flops"]}), flush=True)
         return 0
+    if args.prefill_others_only:
+        print(json.dumps({"prefill_others": run_prefill_others(hip, A, rt, synth)}), flush=True)
+        return 0
     if args.proj_only:
         print(json.dumps(run_proj(hip, A, rt, synth)), flush=True)
         return 0
@@ -753,6 +790,11 @@ def main() -> int:
     if not args.no_prefill:
         c3 = run_c3(hip, A, rt, synth)
         log(f"C3 prefill: {c3['ms'] * 1e3:.1f} us, {c3['tflops']:.1f} TFLOP/s")
+    others = None
+    if not args.no_prefill_others:
+        others = run_prefill_others(hip, A, rt, synth)
+        log("other prefills: " + ", ".join(f"{k} {v['us']:.1f} us {v['tflops']:.1f} TFLOP/s"
+                                           for k, v in others.items()))
     c4 = None
     if not args.no_c4:
         c4 = run_c4(hip, A, rt, synth)
@@ -836,6 +878,8 @@ def main() -> int:
             "frac_of_f16_mfma_peak": round(c3["tflops"] / F16_MFMA_PEAK_TFLOPS, 4),
             "flops": c3["flops"],
         }
+    if others is not None:
+        result["prefill_others"] = others
     if c4 is not None:
         result["ragged_decode"] = {
             "workload": "C4 Qwen2.5-1.5B-shaped ragged decode: 64 sessions, KV lengths "

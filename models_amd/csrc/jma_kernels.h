@@ -153,11 +153,15 @@ hipError_t fixed_scratch_reset(const FixedScratch& s, hipStream_t stream);
 
 bool decode_supported(bool f16, int dk, int dv);
 bool prefill_supported(int dk, int dv);
+// Shapes of the d-sliced prefill kernel: f32 caches at head dims 32-512, f16 caches at 512.
+bool prefill_slice_supported(bool f16, int dk, int dv);
 
 hipError_t launch_append(const AppendArgs& a, bool f16, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStream_t stream);
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stream);
+// rows_per_stripe x heads_per_stripe columns per workgroup, row_blocks = stripes; no split.
+hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, hipStream_t stream);
 
 // ---------------------------------------------------------------- block-quantized projections
 

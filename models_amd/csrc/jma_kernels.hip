@@ -3,6 +3,7 @@
 //   kernel 1  rope_append_kernel   RoPE on q and k, K/V store into the HBM-resident cache
 //   kernel 2  decode_kernel        split-K flash-decoding on MFMA, GQA heads share K/V loads
 //   kernel 3  prefill_kernel       causal / sliding-window prefill, f16 MFMA, LDS K/V tiles
+//   kernel 3b prefill_slice_kernel the same for f32 caches and head dim 512, head-dim slices
 //   kernel 4  reduce_kernel        cross-split log-sum-exp reduction
 //
 // Reference semantics (paths under backend-java/src/main/java/com/integrallis/models/backend/
@@ -2236,6 +2237,287 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   }
 }
 
+// ================================================================ kernel 3b: d-sliced prefill
+
+// Causal / sliding-window prefill for the shapes the f16 kernel above cannot hold in registers:
+// f32 caches (head dims 32..512, on the f32 matrix ops, so scores and weighted sums keep f32
+// products as the reference's do) and f16 caches at head dim 512 (Gemma 4 full layers). A
+// workgroup is one stripe of 32 (query row, query head) columns of one kv head, as in the f16
+// kernel, and its W waves cut the head dimension into W slices of DS = D / W: wave w forms the
+// partial scores of each kv tile over its DS dims of q and K, the waves add their partial tiles
+// through LDS in wave order (so every wave holds the same scores, bit for bit), each runs the
+// same online softmax, and wave w accumulates output dims w*DS .. (w+1)*DS - 1 from the same
+// dims of V. Registers scale with DS instead of D, and no wave repeats another's matrix work.
+// Tiles are read from the cache (L2-resident after the first stripe of a kv head) straight into
+// registers, one tile ahead of the one being computed.
+//
+// Operands (32x32 results: lane (j, h) holds column j, rows 8(e/4) + 4h + e%4 of element e):
+//  f32, v_mfma_f32_32x32x2_f32 (A[i][k]: i = j, k = h; B[k][c]: c = j, k = h): S^T = K Q^T with
+//    result row i = tile slot i. Lane (j, h) loads K[slot j][8m + 4h .. +3] and q[col j][8m + 4h
+//    .. +3] as float4s and gives element t of both to op (m, t), which so adds dims 8m + t and
+//    8m + 4 + t. PV: op u (u < 16) takes the lane's own probability u (slot 8(u/4) + 4h + u%4)
+//    as its B operand and V^T at the same slots as A, four consecutive slots per float4 load of
+//    an f32 V block.
+//  f16, v_mfma_f32_32x32x16_f16: as in the f16 kernel (K rows in swap34 order, so the rounded
+//    probabilities are ready PV operands against perm32-ordered V blocks); q and p are rounded
+//    to f16 there too.
+template <typename KV, int D, int W>
+__global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs a) {
+  using namespace pf;
+  constexpr bool kF16 = std::is_same<KV, _Float16>::value;
+  constexpr int DS = D / W;                      // dims of this wave's slice
+  constexpr int kNb = DS / 32;                   // 32-row blocks of its O^T slice
+  static_assert(D % W == 0 && DS % 32 == 0, "head-dim slices of 32-row blocks");
+  constexpr int kKq = kF16 ? DS / 16 : DS / 8;   // K (and q) operand registers per tile
+  constexpr int kVq = kF16 ? 2 * kNb : 4 * kNb;  // V operand registers per tile
+  using Op = typename std::conditional<kF16, half8_t, float4_t>::type;
+  struct Ops {
+    Op k[kKq];
+    Op v[kVq];
+  };
+  // Partial score tiles: [tile parity][wave][4 float4 chunks][lane]. Two buffers let one barrier
+  // per tile order both the writes before the reads and the reads before the next overwrite.
+  __shared__ float4_t s_x[2][W][4][64];
+
+  const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Kv heads vary fastest (consecutive workgroups on different XCDs, each XCD's L2 keeping few
+  // kv heads); stripes run last-first (longest causal ranges first).
+  const uint32_t kvh = blockIdx.x % a.num_kv_heads;
+  const uint32_t rest = blockIdx.x / a.num_kv_heads;
+  const uint32_t hz = rest % a.head_groups;
+  const uint32_t stripe = a.row_blocks - 1 - rest / a.head_groups;
+  const uint32_t R = a.rows_per_stripe, Gz = a.heads_per_stripe;
+  const uint32_t row0 = stripe * R;
+  const uint32_t row_last = min(row0 + R - 1, a.n - 1);
+  // This lane's column; padding columns alias a valid row and head and are never stored.
+  const uint32_t cr = min((uint32_t)j / Gz, R - 1);
+  const uint32_t hz_head = hz * Gz + (uint32_t)j % Gz;
+  const bool col_ok = (uint32_t)j < R * Gz && row0 + cr < a.n && hz_head < a.group;
+  const uint32_t crow = min(row0 + cr, a.n - 1);
+  const uint32_t head = kvh * a.group + min(hz_head, a.group - 1);
+  const uint32_t cpos = a.start + crow;
+  const uint32_t cfirst = first_visible(cpos, a.window);
+  // Positions some column of the stripe sees, [s_first, s_last], and those every column sees,
+  // [all_first, all_last] (first_visible does not decrease with the position).
+  const uint32_t s_first = first_visible(a.start + row0, a.window);
+  const uint32_t s_last = a.start + row_last;
+  const uint32_t all_first = first_visible(s_last, a.window);
+  const uint32_t all_last = a.start + row0;
+  const uint32_t t0 = s_first / 32, t1 = s_last / 32 + 1;
+
+  const KV* const kb = (const KV*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
+                       (uint64_t)kvh * a.kv.cap * D;
+  const KV* const vb = (const KV*)a.kv.v + a.seq * a.kv.seq_stride_v + a.kv.layer_off_v +
+                       (uint64_t)kvh * a.kv.cap * D;
+  // Operands of kv tile t (positions 32t .. 32t+31; a ring's physical capacity is a multiple of
+  // 32 and holds the stripe's whole visible range, so the tile is 32 consecutive slots).
+  auto load = [&](uint32_t t, Ops& op) JMA_INL {
+    const uint64_t slot0 = a.kv.ring ? (32u * t) % a.kv.cap : 32u * t;
+    const KV* const kt = kb + slot0 * D;
+    const KV* const vt = vb + slot0 * D;
+    if constexpr (kF16) {
+      // K panels of 32 slots x 32 dims (k_index); row swap34(j).
+      const uint32_t kr = swap34(j);
+#pragma unroll
+      for (int i = 0; i < kKq; ++i) {
+        const uint32_t e = 16 * (w * kKq + i) + 8 * h;
+        op.k[i] = *(const half8_t*)(kt + (e / 32) * 1024 + kr * 32 + e % 32);
+      }
+      // V blocks [32 slots, perm32][D]: row dv, halves 8(2b + h) .. +7.
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          op.v[2 * nb + b] = *(const half8_t*)(vt + (uint64_t)(32 * (w * kNb + nb) + j) * 32 + 8 * (2 * b + h));
+    } else {
+      // K panels of 16 slots x 16 dims (k_index): slot j, dims 8m + 4h .. +3.
+#pragma unroll
+      for (int i = 0; i < kKq; ++i) {
+        const uint32_t m = w * kKq + i;
+        op.k[i] = *(const float4_t*)(kt + (uint64_t)(16 * (j / 16)) * D + (m / 2) * 256 +
+                                     (j % 16) * 16 + 8 * (m % 2) + 4 * h);
+      }
+      // V blocks [16 slots][D]: row dv, slots 8c + 4h .. +3 (block c / 2).
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          op.v[4 * nb + c] = *(const float4_t*)(vt + (uint64_t)(c / 2) * 16 * D +
+                                                (uint64_t)(32 * (w * kNb + nb) + j) * 16 +
+                                                8 * (c % 2) + 4 * h);
+    }
+  };
+  // Tile slot of result element e in lane half h.
+  auto slot_of_e = [&](int e) JMA_INL -> uint32_t {
+    return kF16 ? score_slot(e, h) : (uint32_t)(8 * (e >> 2) + 4 * h + (e & 3));
+  };
+
+  Ops cur, nxt;
+  if (t0 < t1) load(t0, cur);
+
+  // q operands of this wave's slice, scaled by scale * log2(e). f16: a scaled element beyond the
+  // f16 range (where the reference's f32 scores stay finite) is reported like a non-finite score.
+  Op qf[kKq];
+  {
+    const float* const qrow = a.q + ((uint64_t)crow * a.num_heads + head) * D;
+    const float qs = col_ok ? a.qscale : 0.0f;
+    if constexpr (kF16) {
+      float qmax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kKq; ++i) {
+        const uint32_t e = 16 * (w * kKq + i) + 8 * h;
+        const float4_t x0 = *(const float4_t*)(qrow + e);
+        const float4_t x1 = *(const float4_t*)(qrow + e + 4);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          qmax = fmaxf(qmax, fmaxf(fabsf(x0[t] * qs), fabsf(x1[t] * qs)));
+          qf[i][t] = (_Float16)(x0[t] * qs);
+          qf[i][4 + t] = (_Float16)(x1[t] * qs);
+        }
+      }
+      if (__ballot(col_ok && !(qmax < 65520.0f)) != 0 && lane == 0) atomicOr(a.err, 1);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kKq; ++i) {
+        const float4_t x = *(const float4_t*)(qrow + 8 * (w * kKq + i) + 4 * h);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) qf[i][t] = x[t] * qs;
+      }
+    }
+  }
+
+  float16_t o[kNb];
+#pragma unroll
+  for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[nb][e] = 0.0f;
+  float m = -INFINITY, l = 0.0f, lb = 0.0f;
+
+  auto tile = [&](uint32_t t, const Ops& op) JMA_INL {
+    // This wave's partial scores over its dims.
+    float16_t s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.0f;
+    if constexpr (kF16) {
+#pragma unroll
+      for (int i = 0; i < kKq; ++i) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(op.k[i], qf[i], s, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kKq; ++i)
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) s = __builtin_amdgcn_mfma_f32_32x32x2f32(op.k[i][t4], qf[i][t4], s, 0, 0, 0);
+    }
+    // Every wave adds the W partial tiles in wave order.
+    if constexpr (W > 1) {
+      float4_t(*const xb)[4][64] = s_x[t & 1];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xb[w][c][lane] = float4_t{s[4 * c], s[4 * c + 1], s[4 * c + 2], s[4 * c + 3]};
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float4_t x = xb[0][c][lane];
+#pragma unroll
+        for (int r = 1; r < W; ++r) x += xb[r][c][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[4 * c + i] = x[i];
+      }
+    }
+    // Masks: positions outside [first, position] of a column are -inf (after the products, so a
+    // non-finite key there never reaches a result).
+    const uint32_t p0 = 32 * t;
+    if (!(p0 >= all_first && p0 + 31 <= all_last)) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t p = p0 + slot_of_e(e);
+        s[e] = p >= cfirst && p <= cpos ? s[e] : -INFINITY;
+      }
+    }
+    // Online softmax: the reference maximum m moves only when a tile's maximum exceeds it by
+    // more than 8 (log2 units), so exponentials stay <= 256 and most tiles skip the rescale.
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[e]);
+    tmax = half_max(tmax);
+    const bool up = tmax > m + 8.0f;
+    if (__ballot(up) != 0) {
+      const float alpha = !up ? 1.0f : (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - tmax));
+      m = up ? tmax : m;
+      l *= alpha;
+      lb *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb) o[nb] *= alpha;
+    }
+    const float mu = m == -INFINITY ? 0.0f : m;
+    // V rows at positions no column of the stripe sees may hold anything (a discarded tail, an
+    // old ring slot); their probabilities are 0, and 0 * inf would be NaN, so they are zeroed.
+    Ops v = op;
+    if (p0 < s_first || p0 + 31 > s_last) {
+#pragma unroll
+      for (int i = 0; i < kVq; ++i)
+#pragma unroll
+        for (int x = 0; x < (kF16 ? 8 : 4); ++x) {
+          const uint32_t sl = kF16 ? score_slot(8 * (i & 1) + x, h) : (uint32_t)(8 * (i & 3) + 4 * h + x);
+          const uint32_t p = p0 + sl;
+          if (p < s_first || p > s_last) v.v[i][x] = 0;
+        }
+    }
+    if constexpr (kF16) {
+      half8_t pf[2];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(s[e] - mu);
+      const half2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const half2_t pr = {pf[i >> 2][2 * (i & 3)], pf[i >> 2][2 * (i & 3) + 1]};
+        if (i & 1) lb = __builtin_amdgcn_fdot2(pr, one, lb, false);
+        else l = __builtin_amdgcn_fdot2(pr, one, l, false);
+      }
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v.v[2 * nb + b], pf[b], o[nb], 0, 0, 0);
+    } else {
+      float p[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(s[e] - mu);
+        if (e & 1) lb += p[e];
+        else l += p[e];
+      }
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.v[4 * nb + (u >> 2)][u & 3], p[u], o[nb], 0, 0, 0);
+    }
+  };
+
+  // Two tiles per iteration, so the two operand sets stay distinct registers.
+  for (uint32_t t = t0; t < t1; t += 2) {
+    if (t + 1 < t1) load(t + 1, nxt);
+    tile(t, cur);
+    if (t + 1 >= t1) break;
+    if (t + 2 < t1) load(t + 2, cur);
+    tile(t + 1, nxt);
+  }
+
+  const float L = half_sum(l + lb);
+  const bool bad = col_ok && !(L > 0.0f && L < INFINITY);
+  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  if (col_ok) {
+    float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *(float4_t*)(orow + 32 * (w * kNb + nb) + 8 * c) =
+            float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]} * inv;
+  }
+}
+
 bool prefill_supported(int dk, int dv) {
   return dk == dv && (dk == 32 || dk == 64 || dk == 128 || dk == 256);
 }
@@ -2306,6 +2588,40 @@ hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stre
     case 64: return launch_prefill_t<64>(a, stream);
     case 128: return launch_prefill_t<128>(a, stream);
     case 256: return launch_prefill_t<256>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool prefill_slice_supported(bool f16, int dk, int dv) {
+  if (dk != dv) return false;
+  return f16 ? dk == 512 : (dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512);
+}
+
+template <typename KV, int D, int W>
+hipError_t launch_prefill_slice_t(const PrefillArgs& a, hipStream_t stream) {
+  const uint64_t blocks = (uint64_t)a.row_blocks * a.head_groups * a.num_kv_heads;
+  if (blocks == 0) return hipSuccess;
+  if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prefill_slice_kernel<KV, D, W>), dim3((uint32_t)blocks), dim3(64 * W), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, hipStream_t stream) {
+  if (!prefill_slice_supported(f16, dk, dv)) return hipErrorInvalidValue;
+  if (a.heads_per_stripe == 0 || a.heads_per_stripe > 32 || a.rows_per_stripe == 0 ||
+      a.rows_per_stripe * a.heads_per_stripe > 32 || a.num_kv_heads == 0 ||
+      a.num_heads != a.num_kv_heads * a.group ||
+      a.row_blocks != (a.n + a.rows_per_stripe - 1) / a.rows_per_stripe ||
+      a.head_groups != (a.group + a.heads_per_stripe - 1) / a.heads_per_stripe)
+    return hipErrorInvalidValue;
+  if (f16) return launch_prefill_slice_t<_Float16, 512, 4>(a, stream);
+  switch (dk) {
+    case 32: return launch_prefill_slice_t<float, 32, 1>(a, stream);
+    case 64: return launch_prefill_slice_t<float, 64, 2>(a, stream);
+    case 128: return launch_prefill_slice_t<float, 128, 4>(a, stream);
+    case 256: return launch_prefill_slice_t<float, 256, 4>(a, stream);
+    case 512: return launch_prefill_slice_t<float, 512, 8>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }

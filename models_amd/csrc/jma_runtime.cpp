@@ -549,15 +549,52 @@ void check_decode_shape(const jmodels_attn_kv* kv, const LayerCall& lc) {
               ", value_length " + std::to_string(lc.dv));
 }
 
+// Which kernel runs a causal block of rows: the f16 MFMA prefill (f16 caches, head dims 32-256),
+// the d-sliced prefill (f32 caches at 32-512, f16 at 512), else the split-K decode kernel over
+// chunks of listed rows.
+enum class PrefillPath { kF16, kSlice, kDecodeRows };
+
+PrefillPath prefill_path(const jmodels_attn_kv* kv, const LayerCall& lc) {
+  if (kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv)) return PrefillPath::kF16;
+  if (jma::prefill_slice_supported(kv->f16(), (int)lc.dk, (int)lc.dv)) return PrefillPath::kSlice;
+  return PrefillPath::kDecodeRows;
+}
+
+void check_prefill_shape(const jmodels_attn_kv* kv, const LayerCall& lc) {
+  if (prefill_path(kv, lc) == PrefillPath::kDecodeRows) check_decode_shape(kv, lc);
+}
+
 // Causal attention of rows start .. start+n-1 whose K/V are cached and whose rotated queries are
 // q (computeBatchedAttention, llama/LlamaForwardPass.java:1515-1541): row b attends
-// [first(start+b), start+b]. f16 caches run the MFMA prefill kernel; f32 caches run the split-K
-// decode kernel over chunks of listed rows.
+// [first(start+b), start+b], on the kernel prefill_path picks.
 void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
                         uint32_t sequence, uint32_t start, uint32_t n, const float* q, float* out) {
   const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk;
   const uint64_t odim = (uint64_t)lc.num_heads * lc.dv;
-  if (kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv)) {
+  const PrefillPath path = prefill_path(kv, lc);
+  if (path == PrefillPath::kSlice) {
+    jma::PrefillArgs a{};
+    a.kv = kv->view(lc.layer);
+    a.q = q;
+    a.qscale = lc.scale * 1.4426950408889634f;
+    a.out = out;
+    a.err = ctx->d_err;
+    a.n = n;
+    a.start = start;
+    a.seq = sequence;
+    a.window = lc.window;
+    a.num_heads = lc.num_heads;
+    a.num_kv_heads = lc.hkv;
+    a.group = lc.group;
+    a.heads_per_stripe = std::min<uint32_t>(lc.group, 32);
+    a.rows_per_stripe = 32 / a.heads_per_stripe;
+    a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
+    a.row_blocks = (n + a.rows_per_stripe - 1) / a.rows_per_stripe;
+    hip_check(jma::launch_prefill_slice(a, kv->f16(), (int)lc.dk, (int)lc.dv, ctx->stream),
+              "prefill launch");
+    return;
+  }
+  if (path == PrefillPath::kF16) {
     jma::PrefillArgs a{};
     a.kv = kv->view(lc.layer);
     a.q = q;
@@ -620,7 +657,7 @@ void prefill_impl(jmodels_attn_context* ctx, jmodels_attn_kv* kv, const LayerCal
                   uint32_t sequence, uint32_t start, uint32_t n, const float* q, const float* k,
                   const float* v, float* out) {
   const uint64_t qdim = (uint64_t)lc.num_heads * lc.dk;
-  if (!(kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv))) check_decode_shape(kv, lc);
+  check_prefill_shape(kv, lc);
   validate_causal(kv, lc, sequence, start, n, false);
   ctx->qrot.reserve((size_t)n * qdim * sizeof(float), ctx->stream, "prefill rotated queries");
   // One launch appends every row: consecutive positions of one sequence need no row table.
@@ -1484,7 +1521,7 @@ static int32_t attend_causal_entry(bool device, jmodels_attn_context* ctx,
     const uint64_t on = (uint64_t)n * lc.num_heads * lc.dv;
     check_elems(q_elements, qn, "q");
     check_elems(out_elements, on, "out");
-    if (!(kv->f16() && jma::prefill_supported((int)lc.dk, (int)lc.dv))) check_decode_shape(kv, lc);
+    check_prefill_shape(kv, lc);
     validate_causal(kv, lc, sequence, start, n, true);
     set_device(ctx);
     if (device) {

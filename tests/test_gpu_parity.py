@@ -321,7 +321,8 @@ def test_rope_gemma4_proportional_golden_on_device(hip, known_answers):
 
 def test_c1_qwen3_decode_f32(hip):
     """16 Q heads, 8 KV heads, d 128, NeoX theta 1e6, f32 KV: 512 prior positions (causal prefill
-    through the split-K kernel) then the decode step at position 512. Full size."""
+    through the d-sliced prefill kernel on f32 matrix ops) then the decode step at position 512.
+    Full size."""
     hq, hkv, d, prior, theta = 16, 8, 128, 512, 1e6
     scale = A.default_scale(d)
     q = normal(1, "c1/q", (prior + 1, hq * d))
