@@ -384,11 +384,39 @@ def run_c4(hip, A, rt, synth, reps: int = 10):
 def run_c5_layer(hip, A, rt, synth, sliding: bool, per_graph: int = 32, reps: int = 5):
     """One C5 layer on its own (profiling aid): a sliding-window layer (window 512 on a RING of
     576 slots, theta 1e4) or a global layer (32704 positions, theta 1e6) of the C5 shape (4 Q / 1
-    KV heads, d 256, NeoX, f16 KV), filled with its prior positions; the decode step at position
-    32704 (RoPE, append, attention and the cross-split reduction) is replayed from a graph of
-    `per_graph` launches, and HIP events around the replays give the per-layer-step time. The
-    step rewrites the same row each time, so every launch sees the same cache."""
-    hq, hkv, d, prior, w = 4, 1, 256, 32704, 512
+    KV heads, d 256, NeoX, f16 KV)."""
+    return run_decode_layer(hip, A, rt, synth, 4, 1, 256, 32704, 512 if sliding else 0,
+                            per_graph, reps)
+
+
+# Decode layer-steps beside C1-C5 (no BASELINE config of their own): Gemma 4 full layers (head
+# dim 512, 8 Q / 1 KV heads, f16 KV) at a C5-length and a C2-length context. Fields: name, Q
+# heads, KV heads, head dim, prior positions.
+DECODE_OTHERS = [
+    ("gemma4_full_layer_d512_32k", 8, 1, 512, 32704),
+    ("gemma4_full_layer_d512_4k", 8, 1, 512, 4096),
+]
+
+
+def run_decode_others(hip, A, rt, synth):
+    out = {}
+    for name, hq, hkv, d, prior in DECODE_OTHERS:
+        r = run_decode_layer(hip, A, rt, synth, hq, hkv, d, prior, 0)
+        out[name] = {"workload": f"decode layer-step at position {prior}, {hq} Q / {hkv} KV heads, "
+                                 f"d {d}, f16 KV (RoPE, append, attention, reduction)",
+                     "us": round(r["us"], 3), "gbs": round(r["gbs"], 1), "bytes": r["bytes"],
+                     "frac_of_hbm_peak": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def run_decode_layer(hip, A, rt, synth, hq, hkv, d, prior, w, per_graph: int = 32, reps: int = 5):
+    """One decode layer on its own: filled with its prior positions (the last w of them on a
+    RING of w + 64 slots for a sliding-window layer, theta 1e4; all of them, theta 1e6, when w is
+    0), the decode step at position `prior` (RoPE, append, attention and the cross-split
+    reduction) is replayed from a graph of `per_graph` launches, and HIP events around the
+    replays give the per-layer-step time. The step rewrites the same row each time, so every
+    launch sees the same cache."""
+    sliding = w > 0
     window, ring, theta = (w, w + 64, 1e4) if sliding else (0, 0, 1e6)
     rope = hip.rotary_table(d, theta, 1.0, max_positions=prior + 8)
     kv = hip.kv_cache(1, prior + 8, hkv, d, d, half_precision=True,
@@ -713,6 +741,10 @@ def main() -> int:
                     help="profiling aid: run only the f32 and head-dim-512 prefill measurements")
     ap.add_argument("--no-prefill-others", action="store_true",
                     help="skip the f32 and head-dim-512 prefill figures")
+    ap.add_argument("--decode-others-only", action="store_true",
+                    help="profiling aid: run only the head-dim-512 decode layer measurements")
+    ap.add_argument("--no-decode-others", action="store_true",
+                    help="skip the head-dim-512 decode layer figures")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="profiling aid: one device-to-device copy of MIB MiB (the runtime's copy "
                          "kernel), to calibrate the FETCH_SIZE / WRITE_SIZE counters")
@@ -755,6 +787,9 @@ def main() -> int:
         print(json.dumps({"prefill_us": round(c3["ms"] * 1e3, 2), "tflops": round(c3["tflops"], 2),
                           "flops": c3["flops"]}), flush=True)
         return 0
+    if args.decode_others_only:
+        print(json.dumps({"decode_others": run_decode_others(hip, A, rt, synth)}), flush=True)
+        return 0
     if args.prefill_others_only:
         print(json.dumps({"prefill_others": run_prefill_others(hip, A, rt, synth)}), flush=True)
         return 0
@@ -795,6 +830,11 @@ def main() -> int:
         others = run_prefill_others(hip, A, rt, synth)
         log("other prefills: " + ", ".join(f"{k} {v['us']:.1f} us {v['tflops']:.1f} TFLOP/s"
                                            for k, v in others.items()))
+    dothers = None
+    if not args.no_decode_others:
+        dothers = run_decode_others(hip, A, rt, synth)
+        log("other decode layers: " + ", ".join(f"{k} {v['us']:.2f} us {v['gbs']:.0f} GB/s"
+                                                for k, v in dothers.items()))
     c4 = None
     if not args.no_c4:
         c4 = run_c4(hip, A, rt, synth)
@@ -880,6 +920,8 @@ def main() -> int:
         }
     if others is not None:
         result["prefill_others"] = others
+    if dothers is not None:
+        result["decode_others"] = dothers
     if c4 is not None:
         result["ragged_decode"] = {
             "workload": "C4 Qwen2.5-1.5B-shaped ragged decode: 64 sessions, KV lengths "

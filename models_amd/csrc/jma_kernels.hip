@@ -660,7 +660,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   JMA_GLOBAL float* g_pacc = (JMA_GLOBAL float*)a.part_acc;
   JMA_GLOBAL float* g_pml = (JMA_GLOBAL float*)a.part_ml;
   JMA_GLOBAL int* g_err = (JMA_GLOBAL int*)a.err;
-  uint32_t ns, item, hg, hgv, slice, kvh, seq, pos;
+  uint32_t ns, item, hg, hgv, slice, kvh, seq, pos, item_row0 = 0;
   KV *kb, *vb;
   if constexpr (kSimple) {
     // Only the preloaded arguments here: the rest are fetched after the first tile loads issue.
@@ -701,6 +701,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     ns = ns_uniform ? ns_uniform : r_ns;
     if (split >= ns) return;  // a listed row with fewer splits than the grid's widest row
     item = group_item0(ns_uniform, r_item0, row, hkv, hgroups, rest, ns) + split;
+    item_row0 = r_item0;
     hgv = hgroups == 1 ? 0u : rest % hgroups;
     hg = hgv / kSlices;
     slice = hgv % kSlices;
@@ -1222,10 +1223,15 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
       if (!(lw > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
       *(float4_t*)(o_grp + hs * DV + e) = aw * (1.0f / lw);
     } else if (!fused) {  // reduce_kernel combines the splits after this launch
-      *(float4_t*)(part_acc + sep_acc_float(item, hs, DVS, e)) = aw;
-      if (e == 0) {
-        part_ml[sep_ml_float(item, hs)] = mx;
-        part_ml[sep_ml_float(item, hs) + 1] = lw;
+      // Column slices write their columns into the head group's item; (m, l) are the same in
+      // every slice (each forms all of q.K), so slice 0 writes them.
+      const uint64_t it = kSlices == 1 ? (uint64_t)item
+                                       : sep_item(ns_uniform, item_row0, row, hkv, hgroups, kSlices,
+                                                  kvh, hg, ns, split);
+      *(float4_t*)(part_acc + sep_acc_float(it, hs, DV, slice * DVS + e)) = aw;
+      if (e == 0 && slice == 0) {
+        part_ml[sep_ml_float(it, hs)] = mx;
+        part_ml[sep_ml_float(it, hs) + 1] = lw;
       }
     } else {
       const uint32_t off = (uint32_t)(fused_part_float(item, hs, DVS, 0) * 4);
@@ -1293,8 +1299,9 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   const uint32_t kvh = head / p_group;
   const uint32_t hl = head % p_group;
   const uint32_t hg = hl / 16, c16 = hl % 16;
-  const uint64_t base = group_item0(p_ns, p_ns ? 0u : a.item_start[row], row, hkv, hgroups,
-                                    kvh * hgroups + hg, ns);
+  // (A sliced plan's row starts count its slices' virtual items: see sep_item.)
+  const uint64_t base = group_item0(p_ns, p_ns ? 0u : a.item_start[row] / a.slices, row, hkv,
+                                    hgroups, kvh * hgroups + hg, ns);
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const uint32_t s4 = lane >> 4, q = lane & 15;
   const uint32_t e = chunk * 64 + 4 * q;

@@ -76,6 +76,17 @@ JMA_HD uint64_t fused_part_float(uint64_t item, uint32_t hs, uint32_t dv, uint32
   return (item * kHeadSlots + hs) * (dv + 4) + e;
 }
 // Separate reduction: element e of head slot hs of item in part_acc, and its (m, l) in part_ml.
+// With column slices, the slices of one head group write their columns into a single DV-wide
+// item: the item of (row, kv head, head group, split) in the plan without slices, which is the
+// group's virtual item numbering with `hgroups` / slices groups and the row's first item / slices
+// (every row holds slices times the items it would hold unsliced). reduce_kernel reads it as an
+// unsliced plan's.
+JMA_HD uint64_t sep_item(uint32_t ns_uniform, uint32_t item_start_row, uint32_t row, uint32_t hkv,
+                         uint32_t hgroups, uint32_t slices, uint32_t kvh, uint32_t hg, uint32_t ns,
+                         uint32_t split) {
+  const uint32_t hgr = hgroups / slices;
+  return group_item0(ns_uniform, item_start_row / slices, row, hkv, hgr, kvh * hgr + hg, ns) + split;
+}
 JMA_HD uint64_t sep_acc_float(uint64_t item, uint32_t hs, uint32_t dv, uint32_t e) {
   return (item * kHeadSlots + hs) * dv + e;
 }
@@ -93,7 +104,9 @@ JMA_HD uint64_t sep_ml_float(uint64_t item, uint32_t hs) { return (item * kHeadS
 // layer) cuts each head's value columns among `slices` = 4 workgroups, each computing q.K over its
 // tiles and V and the output for a quarter of the columns. That gives four times the workgroups,
 // each streaming K and a quarter of V (instead of all of V), with a quarter of the partials to
-// exchange per split. The slices are virtual head groups: `hgroups` is head groups x slices.
+// exchange per split. The slices are virtual head groups: `hgroups` is head groups x slices. At
+// head dim 512 wide plans slice too (the unsliced instance spills registers there); their slices
+// share the separate reduction's items (sep_item).
 struct DecodePlan {
   uint32_t hgroups = 0, slices = 1, tiles_per_split = 0, total_items = 0, max_splits = 0, ns_uniform = 0;
   bool any_split = false, separate = false;
@@ -147,8 +160,10 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     if (few * 8 < target) tps /= 2;
   }
   // Column slices (above): fused plans of at most one tile per wave at head dim 256 (the sliced
-  // instance keeps one tile buffer), any at 512, whose sliced launch stays within half the target.
-  if (!unfused && !wide && dk == dv && (dk == 512 || (dk == 256 && tps <= (uint64_t)decode_waves(dk)))) {
+  // instance keeps one tile buffer), fused or wide plans at 512, whose sliced launch stays within
+  // half the target.
+  if (!unfused && dk == dv &&
+      (dk == 512 || (!wide && dk == 256 && tps <= (uint64_t)decode_waves(dk)))) {
     uint64_t n = 0;
     for (uint32_t i = 0; i < count; ++i) n += (ntiles[i] + tps - 1) / tps * hkv * p.hgroups;
     if (n * 4 * 2 <= target) {
@@ -172,8 +187,8 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
   p.ns_uniform = uniform ? p.nsplit[0] : 0u;
   p.separate = p.any_split && (unfused || wide);
   if (p.separate) {
-    p.acc_bytes = (uint64_t)items * kHeadSlots * dv * 4;
-    p.ml_bytes = (uint64_t)items * kHeadSlots * 2 * 4;
+    p.acc_bytes = (uint64_t)items / p.slices * kHeadSlots * dv * 4;
+    p.ml_bytes = (uint64_t)items / p.slices * kHeadSlots * 2 * 4;
   } else if (p.any_split) {
     p.part_f_bytes = (uint64_t)items * kHeadSlots * (dv / p.slices + 4) * 4;
     p.counter_bytes = (uint64_t)count * hkv * p.hgroups * 4;

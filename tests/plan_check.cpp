@@ -54,10 +54,12 @@ void check(const Case& c) {
   const uint32_t hgroups = p.hgroups;  // virtual head groups: head groups x column slices
   if (p.slices != 1 && p.slices != 4) die(c, "column slices");
   if (hgroups != (c.group + kHeadSlots - 1) / kHeadSlots * p.slices) die(c, "head groups");
-  if (p.slices > 1 && (p.separate || c.dk < 256 || (c.dk == 256 && p.tiles_per_split > 4)))
-    die(c, "column slices outside the sliced instances (fused, d 256 one tile per wave, d 512)");
+  if (p.slices > 1 && (c.dk < 256 || (c.dk == 256 && (p.separate || p.tiles_per_split > 4))))
+    die(c, "column slices outside the sliced instances (fused d 256 one tile per wave, d 512)");
   if (p.part_f_bytes > 0x7FFFFFF0ull) die(c, "fused partials exceed 32-bit buffer offsets");
   std::vector<int> owner(p.total_items, 0);
+  // Separate plans: (item, slice) pairs of part_acc, each written by one workgroup.
+  std::vector<int> sep_owner(p.separate ? p.total_items : 0, 0);
   const uint64_t part_f_floats = p.part_f_bytes / 4, acc_floats = p.acc_bytes / 4;
   const uint64_t ml_floats = p.ml_bytes / 4, counters = p.counter_bytes / 4;
   for (uint32_t row = 0; row < count; ++row) {
@@ -72,6 +74,7 @@ void check(const Case& c) {
     std::vector<int> seen(t_end - t_begin, 0);
     for (uint32_t rest = 0; rest < c.hkv * hgroups; ++rest) {
       const uint32_t kvh = rest / hgroups, hgv = rest % hgroups, hg = hgv / p.slices;
+      const uint32_t slice = hgv % p.slices;
       const uint32_t nreal = std::min<uint32_t>(kHeadSlots, c.group - hg * kHeadSlots);
       const uint32_t dvs = c.dv / p.slices;  // value columns of the slice
       const uint64_t item0 = group_item0(p.ns_uniform, p.item_start[row], row, c.hkv, hgroups, rest, ns);
@@ -93,8 +96,13 @@ void check(const Case& c) {
         if (ns == 1) continue;
         for (uint32_t hs = 0; hs < nreal; ++hs) {
           if (p.separate) {
-            if (sep_acc_float(item, hs, c.dv, c.dv - 1) >= acc_floats) die(c, "part_acc index");
-            if (sep_ml_float(item, hs) + 1 >= ml_floats) die(c, "part_ml index");
+            // a slice writes its columns of the head group's item (sep_item)
+            const uint64_t it = p.slices == 1 ? item
+                                              : sep_item(p.ns_uniform, p.item_start[row], row, c.hkv,
+                                                         hgroups, p.slices, kvh, hg, ns, split);
+            if (sep_acc_float(it, hs, c.dv, slice * dvs + dvs - 1) >= acc_floats) die(c, "part_acc index");
+            if (sep_ml_float(it, hs) + 1 >= ml_floats) die(c, "part_ml index");
+            if (hs == 0 && sep_owner[it * p.slices + slice]++) die(c, "part_acc columns written twice");
           } else {
             // producer stores acc quads and the (m, l, pad, pad) word group; the reducer reads
             // the same words of every split of the group
@@ -107,9 +115,13 @@ void check(const Case& c) {
       if (p.separate && ns > 1) {
         // reduce_kernel: one workgroup per (row, query head, 64-element chunk) reads the row's
         // group base + split for split < ns
-        const uint64_t base = group_item0(p.ns_uniform, p.item_start[row], row, c.hkv, hgroups,
-                                          kvh * hgroups + hgv, ns);
-        if (base != item0) die(c, "reduce_kernel group base differs from the producers'");
+        const uint32_t hgr = hgroups / p.slices;
+        const uint64_t base = group_item0(p.ns_uniform, p.item_start[row] / p.slices, row, c.hkv,
+                                          hgr, kvh * hgr + hg, ns);
+        const uint64_t prod = p.slices == 1 ? item0
+                                            : sep_item(p.ns_uniform, p.item_start[row], row, c.hkv,
+                                                       hgroups, p.slices, kvh, hg, ns, 0);
+        if (base != prod) die(c, "reduce_kernel group base differs from the producers'");
         for (uint32_t hs = 0; hs < nreal; ++hs)
           if (sep_acc_float(base + ns - 1, hs, c.dv, c.dv - 1) >= acc_floats) die(c, "reduce read");
       }
@@ -120,6 +132,18 @@ void check(const Case& c) {
   }
   for (uint64_t i = 0; i < p.total_items; ++i)
     if (owner[i] != 1) die(c, "work item " + std::to_string(i) + " not written exactly once");
+  if (p.separate) {
+    // every (item, slice) of a row with splits is written exactly once, none past the items
+    uint64_t written = 0;
+    for (uint64_t i = 0; i < sep_owner.size(); ++i) {
+      if (sep_owner[i] > 1) die(c, "part_acc columns written twice");
+      written += sep_owner[i];
+    }
+    uint64_t want = 0;
+    for (uint32_t row = 0; row < count; ++row)
+      if (p.nsplit[row] > 1) want += (uint64_t)p.nsplit[row] * c.hkv * hgroups;
+    if (written != want) die(c, "part_acc columns not covered exactly once");
+  }
   printf("%-44s rows %3u tiles/split %5u splits <= %4u items %7u slices %u %s %8.1f KiB\n", c.name.c_str(),
          count, p.tiles_per_split, p.max_splits, p.total_items, p.slices,
          p.separate ? "separate" : (p.any_split ? "fused   " : "single  "),
@@ -231,6 +255,10 @@ int main() {
   // window + chunk that is not a multiple of 32 (stored in round_up(356, 32) = 384 slots).
   cases.push_back({"Gemma-4 full d512 2 sessions", {602, 252}, 0, 2, 4, 512, 512, true, 512, 1, false, 0});
   cases.push_back({"Gemma-4 full d512 f32 8k", {8191}, 0, 2, 16, 512, 512, false, 512, 1, false, 0});
+  for (uint32_t p : {4096u, 32704u})
+    cases.push_back({"Gemma-4 full d512 8/1 @" + std::to_string(p) + " (wide)", {p}, 0, 1, 8, 512, 512, true, 512, 1, false, 0});
+  cases.push_back({"Gemma-4 full d512 ragged 3 rows x 2 groups (wide)", {20000, 5000, 12000}, 0, 1, 20, 512, 512, true, 512, 1, false, 0});
+  cases.push_back({"d512 ragged 3 rows x 2 groups, target 8192 (wide, sliced)", {9000, 5000, 7000}, 0, 1, 20, 512, 512, true, 8192, 1, false, 0});
   cases.push_back({"Gemma-4 sliding ring 356 w256", {602, 252}, 256, 4, 2, 256, 256, true, 512, 1, false, 384});
   for (const Case& c : cases) check(c);
   for (bool f16 : {true, false})

@@ -1064,6 +1064,53 @@ def test_wide_split_decode_matches_oracle(hip, half, d):
         rope.close()
 
 
+@pytest.mark.parametrize("half", [True, False])
+@pytest.mark.parametrize("case", ["one row @4096", "three ragged rows, two head groups"])
+def test_wide_sliced_d512_decode_matches_oracle(monkeypatch, half, case):
+    """Head dim 512 wide plans with column slices: four workgroups per (head group, split), each
+    forming all of q.K and a quarter of the V columns, write their columns into one part_acc item
+    that reduce_kernel combines. One row at 4096 positions (8 Q / 1 KV heads: the uniform,
+    single-group instance) and three ragged rows of 20 Q / 1 KV heads (two head groups, unequal
+    split counts, row starts in virtual items) at a workgroup target of 8192 that slices them;
+    the new token appended by the decode kernel; against the oracle over the read-back cache."""
+    d, hkv, theta = 512, 1, 1e6
+    scale = A.default_scale(d)
+    if case.startswith("one"):
+        hq, lens, target = 8, [4096], None
+    else:
+        hq, lens, target = 20, [9000, 5000, 7000], "8192"
+    if target:
+        monkeypatch.setenv("JMA_DECODE_TARGET_BLOCKS", target)
+    B = len(lens)
+    lib = A.HipAttentionLibrary(0)
+    close = assert_f16_close if half else assert_f32_close
+    try:
+        rope = lib.rotary_table(d, theta, 1.0, max_positions=max(lens) + 1)
+        kv = lib.kv_cache(1, max(lens) + 1, hkv, d, d, half_precision=half, sequences=B)
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        tag = f"wsl/{int(half)}/{case[:3]}"
+        for s_, L in enumerate(lens):
+            kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32),
+                      normal(18, f"{tag}/k{s_}", (L, hkv * d)), normal(18, f"{tag}/v{s_}", (L, hkv * d)),
+                      sequences=np.full(L, s_))
+        qn = normal(18, f"{tag}/qn", (B, hq * d))
+        kn = normal(18, f"{tag}/kn", (B, hkv * d))
+        vn = normal(18, f"{tag}/vn", (B, hkv * d))
+        got = kv.decode(layer, lens, qn, kn, vn, sequences=np.arange(B)).reshape(B, -1)
+        again = kv.decode(layer, lens, qn, kn, vn, sequences=np.arange(B)).reshape(B, -1)
+        np.testing.assert_array_equal(again, got)  # deterministic, the same row rewritten
+        for s_, L in enumerate(lens):
+            keys, values = kv.read(0, 0, L + 1, sequence=s_)
+            q_rot = rope_rows(qn[s_:s_ + 1], [L], hq, d, d, theta, True, check_against_oracle=False)
+            want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
+            err = close(got[s_], want, f"sliced wide d 512 {case} session {s_} (L={L})", head_dim=d)
+            _say(f"sliced wide d512 half={half} {case} L={L} err {err:.2e}")
+        kv.close()
+        rope.close()
+    finally:
+        lib.close()
+
+
 def test_wide_split_on_a_ring_layer_matches_oracle(hip):
     """A wide plan on a RING layer (LayeredKvCache retention, capacity 16384, window 12000) at a
     position past the first wrap (20000): the 375 visible tiles are cut into wide splits whose
