@@ -419,24 +419,32 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 // One workgroup's partial for output elements e .. e+3 of head slot hs: its waves' states
 // (s_ml, s_acc) rescaled to their common maximum and summed in wave order. Every multiply-add is
 // an explicit fmaf, so the reducer (which keeps its own partial) and a producer (which stores it)
-// compute the same bits and the result does not depend on which workgroup reduces.
+// compute the same bits and the result does not depend on which workgroup reduces. Every LDS
+// read is issued before the first use; the weights use v_exp_f32 directly (their arguments are
+// <= 0 or -inf, and a weight below 2^-126 contributes nothing).
 template <int DV, int W>
 __device__ __forceinline__ void wave_partial(const float (*s_acc)[16][DV], const float (*s_ml)[16][2],
                                              uint32_t hs, uint32_t e, float& mx, float& lw,
                                              float4_t& aw) {
+  float2 ml[W];
+  float4_t x[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    ml[w] = *(const float2*)&s_ml[w][hs][0];
+    x[w] = *(const float4_t*)&s_acc[w][hs][e];
+  }
   mx = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < W; ++w) mx = fmaxf(mx, s_ml[w][hs][0]);
+  for (int w = 0; w < W; ++w) mx = fmaxf(mx, ml[w].x);
   const float mu = mx == -INFINITY ? 0.0f : mx;
   lw = 0.0f;
   aw = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < W; ++w) {
-    const float f = exp2f(s_ml[w][hs][0] - mu);
-    lw = fmaf(s_ml[w][hs][1], f, lw);
-    const float4_t x = *(const float4_t*)&s_acc[w][hs][e];
+    const float f = __builtin_amdgcn_exp2f(ml[w].x - mu);
+    lw = fmaf(ml[w].y, f, lw);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) aw[i] = fmaf(x[i], f, aw[i]);
+    for (int i = 0; i < 4; ++i) aw[i] = fmaf(x[w][i], f, aw[i]);
   }
 }
 
@@ -1095,7 +1103,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     // final normalisation reports: no per-score check is needed.
     if (__builtin_amdgcn_ballot_w64(mt > m + 8.0f) != 0) {
       const float mn = fmaxf(m, mt);
-      const float alpha = exp2f(m - (mn == -INFINITY ? 0.0f : mn));
+      const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.0f : mn));
       m = mn;
       l *= alpha;
 #pragma unroll
