@@ -474,22 +474,30 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
     return (uint32_t)(fused_part_float(item0 + g, hs, DV, 0) * 4);
   };
   const uint32_t r = tid % SUB;
+  // Words a thread does not need (splits past ns, its own split, quads past the group) are
+  // addressed past the buffer's record count: such a load returns 0, which reads as written, and
+  // such a store is dropped, so the poll, the sums and the clear-back need no per-split branches.
+  constexpr uint32_t kSkip = 0xFFFFFF00u;
   bool timed_out = false;
   for (uint32_t q0 = 0; q0 < E4; q0 += kT / SUB) {
     const uint32_t quad = q0 + tid / SUB;
     const bool qok = quad < E4;
     const uint32_t hs = qok ? quad / kQ4 : 0u, e = qok ? (quad % kQ4) * 4 : 0u;
-    auto needed = [&](int i) JMA_INL {
+    uint32_t off_x[kI], off_m[kI];
+#pragma unroll
+    for (int i = 0; i < kI; ++i) {
       const uint32_t g = r + SUB * i;
-      return qok && g < ns && g != split;
-    };
+      const bool needed = qok && g < ns && g != split;
+      const uint32_t w = base(g, hs);
+      off_x[i] = needed ? w + e * 4 : kSkip;
+      off_m[i] = needed ? w + DV * 4 : kSkip;
+    }
     float4_t xv[kI];
     float2_t mv[kI];
 #pragma unroll
     for (int i = 0; i < kI; ++i) {
-      const uint32_t w = base(r + SUB * i, hs);
-      xv[i] = needed(i) ? load_part(rs, w + e * 4) : float4_t{0.f, 0.f, 0.f, 0.f};
-      mv[i] = needed(i) ? load_part2(rs, w + DV * 4) : float2_t{0.f, 0.f};
+      xv[i] = load_part(rs, off_x[i]);
+      mv[i] = load_part2(rs, off_m[i]);
     }
     float mx, lw;  // this workgroup's own partial, while the loads are in flight
     float4_t own;
@@ -507,15 +515,15 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
         break;
       }
       poll_barrier();
+      // Every word again (those already written read the same data).
 #pragma unroll
       for (int i = 0; i < kI; ++i) {
-        if (!needed(i)) continue;
-        const uint32_t w = base(r + SUB * i, hs);
-        if (!written(xv[i])) xv[i] = load_part(rs, w + e * 4);
-        if (!written(float4_t{mv[i][0], mv[i][1], mv[i][0], mv[i][1]})) mv[i] = load_part2(rs, w + DV * 4);
+        xv[i] = load_part(rs, off_x[i]);
+        mv[i] = load_part2(rs, off_m[i]);
       }
     }
-    // Per-thread maximum, then the maximum over the quad's SUB threads.
+    // Per-thread maximum, then the maximum over the quad's SUB threads. Splits past ns weigh
+    // 2^-inf = 0 (their words read 0), so every split takes the same code.
     float m_i[kI];
     float M = -INFINITY;
 #pragma unroll
@@ -533,14 +541,12 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 #pragma unroll
     for (int i = 0; i < kI; ++i) {
       const uint32_t g = r + SUB * i;
-      if (g >= ns) continue;
       const float wg = __builtin_amdgcn_exp2f(m_i[i] - mu);
       const float lg = g == split ? lw : mv[i][1];
       const float4_t xg = g == split ? own : xv[i];
       L = fmaf(lg, wg, L);
 #pragma unroll
       for (int c = 0; c < 4; ++c) X[c] = fmaf(xg[c], wg, X[c]);
-      if (needed(i)) clear_part(rs, base(g, hs) + e * 4);
     }
     if constexpr (SUB >= 2) {
       L += dpp<kDppXor1>(L);
@@ -561,6 +567,9 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
       if (!(L > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
       *(float4_t*)(out + hs * OS + e) = X * (1.0f / L);
     }
+    // Clear-back of the acc words, after the output store.
+#pragma unroll
+    for (int i = 0; i < kI; ++i) clear_part(rs, off_x[i]);
   }
   __syncthreads();  // every quad of every head has read its (m, l) words
   for (uint32_t k = tid; k < (ns - 1) * nreal; k += kT) {
