@@ -565,7 +565,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
     }
     if (qok && r == 0) {
       if (!(L > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
-      *(float4_t*)(out + hs * OS + e) = X * (1.0f / L);
+      *(float4_t*)(out + hs * OS + e) = X * __builtin_amdgcn_rcpf(L);  // L >= 1: no denormals
     }
     // Clear-back of the acc words, after the output store.
 #pragma unroll
@@ -1238,7 +1238,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     wave_partial<DVS, kW>(s_acc, s_ml, hs, e, mx, lw, aw);
     if (ns == 1) {
       if (!(lw > 0.0f) && e == 0) atomicOr(err, 1);  // all -inf, or a NaN / +inf score
-      *(float4_t*)(o_grp + hs * DV + e) = aw * (1.0f / lw);
+      *(float4_t*)(o_grp + hs * DV + e) = aw * __builtin_amdgcn_rcpf(lw);
     } else if (!fused) {  // reduce_kernel combines the splits after this launch
       // Column slices write their columns into the head group's item; (m, l) are the same in
       // every slice (each forms all of q.K), so slice 0 writes them.
@@ -1384,7 +1384,7 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
     xt += s_x[i][q];
   }
   if (!(lt > 0.0f) && q == 0 && chunk == 0) atomicOr(a.err, 1);  // all -inf, NaN or +inf
-  if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * p_heads + head) * DV + e) = xt * (1.0f / lt);
+  if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * p_heads + head) * DV + e) = xt * __builtin_amdgcn_rcpf(lt);
 }
 
 template <int DV>
