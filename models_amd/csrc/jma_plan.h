@@ -105,8 +105,9 @@ JMA_HD uint64_t sep_ml_float(uint64_t item, uint32_t hs) { return (item * kHeadS
 // tiles and V and the output for a quarter of the columns. That gives four times the workgroups,
 // each streaming K and a quarter of V (instead of all of V), with a quarter of the partials to
 // exchange per split. The slices are virtual head groups: `hgroups` is head groups x slices. At
-// head dim 512 wide plans slice too (the unsliced instance spills registers there); their slices
-// share the separate reduction's items (sep_item).
+// head dim 512 every plan slices (the unsliced instance spills registers there): four slices
+// when the sliced launch stays within half the target, else two (K read twice, V once); wide
+// plans' slices share the separate reduction's items (sep_item).
 struct DecodePlan {
   uint32_t hgroups = 0, slices = 1, tiles_per_split = 0, total_items = 0, max_splits = 0, ns_uniform = 0;
   bool any_split = false, separate = false;
@@ -160,8 +161,8 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     if (few * 8 < target) tps /= 2;
   }
   // Column slices (above): fused plans of at most one tile per wave at head dim 256 (the sliced
-  // instance keeps one tile buffer), fused or wide plans at 512, whose sliced launch stays within
-  // half the target.
+  // instance keeps one tile buffer) whose sliced launch stays within half the target; at 512, four
+  // slices under the same rule, else two.
   if (!unfused && dk == dv &&
       (dk == 512 || (!wide && dk == 256 && tps <= (uint64_t)decode_waves(dk)))) {
     uint64_t n = 0;
@@ -169,6 +170,9 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     if (n * 4 * 2 <= target) {
       p.slices = 4;
       p.hgroups *= 4;
+    } else if (dk == 512) {
+      p.slices = 2;
+      p.hgroups *= 2;
     }
   }
   p.tiles_per_split = (uint32_t)tps;

@@ -1064,21 +1064,30 @@ def test_wide_split_decode_matches_oracle(hip, half, d):
         rope.close()
 
 
+D512_SLICED_CASES = {
+    # name: (query heads, row lengths, workgroup target); the plan each gets (tests/plan_check.cpp
+    # prints them) follows the name
+    "one row @4096: wide, 4 slices": (8, [4096], None),
+    "one row @16000: wide, 2 slices": (8, [16000], None),
+    "three ragged rows, two head groups, target 8192: wide, 4 slices": (20, [9000, 5000, 7000], "8192"),
+    "three ragged rows, two head groups: fused, 2 slices": (20, [9000, 5000, 7000], None),
+}
+
+
 @pytest.mark.parametrize("half", [True, False])
-@pytest.mark.parametrize("case", ["one row @4096", "three ragged rows, two head groups"])
+@pytest.mark.parametrize("case", list(D512_SLICED_CASES))
 def test_wide_sliced_d512_decode_matches_oracle(monkeypatch, half, case):
-    """Head dim 512 wide plans with column slices: four workgroups per (head group, split), each
-    forming all of q.K and a quarter of the V columns, write their columns into one part_acc item
-    that reduce_kernel combines. One row at 4096 positions (8 Q / 1 KV heads: the uniform,
-    single-group instance) and three ragged rows of 20 Q / 1 KV heads (two head groups, unequal
-    split counts, row starts in virtual items) at a workgroup target of 8192 that slices them;
-    the new token appended by the decode kernel; against the oracle over the read-back cache."""
+    """Head dim 512 plans with column slices: four (short plans) or two (long ones, where four
+    would exceed the workgroup target) workgroups per (head group, split), each forming all of
+    q.K and its share of the V columns. Wide plans write the slices' columns into one part_acc
+    item that reduce_kernel combines; fused plans reduce each slice through the split exchange.
+    One row (8 Q / 1 KV heads: the uniform, single-group instance) and three ragged rows of
+    20 Q / 1 KV heads (two head groups, unequal split counts, row starts in virtual items: the
+    listed-rows instance); the new token appended by the decode kernel; against the oracle over
+    the read-back cache."""
     d, hkv, theta = 512, 1, 1e6
     scale = A.default_scale(d)
-    if case.startswith("one"):
-        hq, lens, target = 8, [4096], None
-    else:
-        hq, lens, target = 20, [9000, 5000, 7000], "8192"
+    hq, lens, target = D512_SLICED_CASES[case]
     if target:
         monkeypatch.setenv("JMA_DECODE_TARGET_BLOCKS", target)
     B = len(lens)
@@ -1088,7 +1097,7 @@ def test_wide_sliced_d512_decode_matches_oracle(monkeypatch, half, case):
         rope = lib.rotary_table(d, theta, 1.0, max_positions=max(lens) + 1)
         kv = lib.kv_cache(1, max(lens) + 1, hkv, d, d, half_precision=half, sequences=B)
         layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
-        tag = f"wsl/{int(half)}/{case[:3]}"
+        tag = f"wsl/{int(half)}/{case}"
         for s_, L in enumerate(lens):
             kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32),
                       normal(18, f"{tag}/k{s_}", (L, hkv * d)), normal(18, f"{tag}/v{s_}", (L, hkv * d)),
