@@ -1223,6 +1223,10 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
       if (narrow) reduce_group<16, kSubMax, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
       else if (kW == 4 && one_round) reduce_group<16, kW == 4 ? 1 : 2, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
       else reduce_group<16, 2, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+    } else if (ns <= 24) {  // (a thread's split slots past ns still cost poll issue slots)
+      if (narrow) reduce_group<24, kSubMax, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else if (kW == 4 && one_round) reduce_group<24, kW == 4 ? 1 : 4, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
+      else reduce_group<24, 4, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
     } else {
       if (narrow) reduce_group<32, kSubMax, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);
       else if (kW == 4 && one_round) reduce_group<32, kW == 4 ? 1 : 4, DVS, kW, DV>(part_f, item0, ns, split, nreal, s_acc, s_ml, o_grp, err);

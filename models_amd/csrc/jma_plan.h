@@ -30,6 +30,8 @@ constexpr int kMaxWideSplits = 1024;
 // Query heads one decode workgroup serves (the 16 MFMA columns); partial buffers reserve this
 // many head slots per work item.
 constexpr int kHeadSlots = 16;
+// Fewest K/V bytes a decode split streams when the planner chooses its size (plan_decode).
+constexpr uint64_t kMinSplitBytes = 96 * 1024;
 
 // Storage block (slots) of the transposed V layout, and of the K tiles.
 JMA_HD int v_block(bool f16) { return f16 ? 32 : 16; }
@@ -134,8 +136,16 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     units += (uint64_t)ntiles[i] * hkv * p.hgroups;
   }
   const uint64_t target = (uint64_t)std::max(target_blocks, 1);
+  const uint64_t tile_bytes = (uint64_t)blk * (uint64_t)(dk + dv) * (f16 ? 2u : 4u);
   uint64_t tps = min_split_tiles > 0 ? (uint64_t)min_split_tiles
                                      : (uint64_t)decode_waves(dk) * (uint64_t)std::max(tiles_per_wave, 1);
+  // Every split streams at least kMinSplitBytes: a split's exchange (its partial stored, polled and
+  // combined) costs about as much as streaming that many bytes through one compute unit, so
+  // smaller splits add exchange work without saving time. One tile per wave already streams that
+  // much at head dim 128 and above; at 64 and below the split takes more tiles (C2, d 64: 12
+  // tiles, 11 splits, 7.6 against 8.1 us per launch with 8 tiles, 17 splits).
+  if (min_split_tiles == 0) tps = std::max<uint64_t>(tps, (kMinSplitBytes + tile_bytes - 1) / tile_bytes);
+  const uint64_t base_tps = tps;
   tps = std::max<uint64_t>(tps, (units + target - 1) / target);
   const uint64_t tps_fused = std::max<uint64_t>(tps, (max_tiles + kMaxSplits - 1) / kMaxSplits);
   bool wide = false;
@@ -151,9 +161,7 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
   // than 64 KB waits on the per-CU load issue rate (~64 KB per us), so it takes half the tiles
   // per split (at least one per two waves) and twice the workgroups, as long as each extra
   // split's partial (dv + 4 floats per query head, read back by the reducer) stays within 2 KB.
-  const uint64_t tile_bytes = (uint64_t)blk * (uint64_t)(dk + dv) * (f16 ? 2u : 4u);
   const uint64_t part_bytes = (uint64_t)std::min<uint32_t>(group, kHeadSlots) * (dv + 4) * 4;
-  const uint64_t base_tps = (uint64_t)decode_waves(dk) * (uint64_t)std::max(tiles_per_wave, 1);
   if (min_split_tiles == 0 && !wide && tps == base_tps && tps >= 2 && tps * tile_bytes > 65536 &&
       part_bytes <= 2048 && (max_tiles + tps / 2 - 1) / (tps / 2) <= (uint64_t)kMaxSplits) {
     uint64_t few = 0;
