@@ -1014,6 +1014,25 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     };
     if constexpr (decltype(patch)::value && !kSplitKV) patch_v();
     const uint32_t p0 = tt * kBlk;
+    // Only the first and last tiles of the visible range hold masked rows. Their value elements
+    // (element i of each V operand is the position of score i) are cleared too, through the
+    // bit masks vkeep (one per 32-bit word of an operand): a masked slot may hold anything (a
+    // discarded tail, an old ring slot, a value that overflowed f16), and 0 * inf would reach the
+    // result. The masks depend on positions only, so they are formed ahead of the matrix ops
+    // (whose results only take the selects).
+    const bool edge = p0 < first || p0 + kBlk - 1 > pos;
+    uint32_t okbits = ~0u;
+    uint32_t vkeep[4] = {~0u, ~0u, ~0u, ~0u};
+    if (edge) {
+#pragma unroll
+      for (int i = 0; i < kNs; ++i) {
+        const uint32_t p = kF16 ? p0 + 16 * (i >> 2) + 4 * g + (i & 3) : p0 + 4 * g + i;
+        const bool ok = p >= first && p <= pos;
+        okbits &= ok ? ~0u : ~(1u << i);
+        if constexpr (kF16) vkeep[i >> 1] &= ok ? ~0u : ((i & 1) ? 0x0000FFFFu : 0xFFFF0000u);
+        else vkeep[i] = ok ? ~0u : 0u;
+      }
+    }
     float s[kNs];
     if constexpr (kF16 && kQLds) {
       // q chunk c is formed once from LDS and serves both 16-row halves of the tile.
@@ -1084,23 +1103,9 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
       cur.load_v(vb, slot0_of(tt), c16, g);
       if constexpr (decltype(patch)::value) patch_v();
     }
-    // Only the first and last tiles of the visible range hold masked rows. Their value elements
-    // (element i of each V operand is the position of score i) are cleared too, through the
-    // bit masks vkeep (one per 32-bit word of an operand): a masked slot may hold anything (a
-    // discarded tail, an old ring slot, a value that overflowed f16), and 0 * inf would reach the
-    // result.
-    uint32_t vkeep[4] = {~0u, ~0u, ~0u, ~0u};
-    if (p0 < first || p0 + kBlk - 1 > pos) {
+    if (edge) {
 #pragma unroll
-      for (int i = 0; i < kNs; ++i) {
-        const uint32_t p = kF16 ? p0 + 16 * (i >> 2) + 4 * g + (i & 3) : p0 + 4 * g + i;
-        const bool ok = p >= first && p <= pos;
-        s[i] = ok ? s[i] : -INFINITY;
-        if (!ok) {
-          if constexpr (kF16) vkeep[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-          else vkeep[i] = 0u;
-        }
-      }
+      for (int i = 0; i < kNs; ++i) s[i] = (okbits >> i) & 1u ? s[i] : -INFINITY;
     }
     float mt = s[0];
 #pragma unroll
