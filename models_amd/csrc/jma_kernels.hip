@@ -221,6 +221,8 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141; // row_half_mirror
 constexpr int kDppRowMirror = 0x140;  // row_mirror: lane 15 - i within each row of 16
+constexpr int kDppRowRor4 = 0x124;    // row_ror:4 (lane i of a row of 16 reads lane (i + 4) % 16)
+constexpr int kDppRowRor8 = 0x128;    // row_ror:8
 
 // Fragments of one tile (kBlk positions) of K and V for one lane, in matrix-core operand order.
 // K tiles are stored in 64-byte column panels (k_index), so each operand load below reads 1 KB of
@@ -1302,16 +1304,19 @@ __device__ __forceinline__ float wave_sum64(float x) {
 // waves in wave order: the same result on every run for a plan. The leading scalar arguments
 // (the partial buffers, the uniform split count, the head counts) arrive preloaded in SGPRs, so
 // the loads need no kernel-argument load first; the row tables are read only for listed rows.
-template <int DV, int kWaves>
+template <int DV, int kWaves, int kQ>
 __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc, const float* p_ml,
                                                              uint32_t p_ns, uint32_t p_heads,
                                                              uint32_t p_group, const DecodeArgs a) {
-  constexpr uint32_t kChunks = (DV + 63) / 64;
-  constexpr int kPer = kMaxWideSplits / (kWaves * 4);  // splits one lane sums at most
+  static_assert(kQ == 4 || kQ == 16, "quads per workgroup");
+  constexpr uint32_t kOut = 4 * kQ;                          // outputs per workgroup
+  constexpr uint32_t kChunks = (DV + kOut - 1) / kOut;
+  constexpr uint32_t kSL = 64 / kQ;                          // split lanes of a quad per wave
+  constexpr int kPer = kMaxWideSplits / (kWaves * kSL);      // splits one lane sums at most
   constexpr uint32_t kMl = kMaxWideSplits / (64 * kWaves);  // (m, l) words one thread loads
   __shared__ float2 s_ml[kMaxWideSplits];
   __shared__ float s_m[kWaves], s_l[kWaves];
-  __shared__ float4_t s_x[kWaves][16];
+  __shared__ float4_t s_x[kWaves][kQ];
   JMA_GLOBAL const float* g_acc = (JMA_GLOBAL const float*)p_acc;
   JMA_GLOBAL const float* g_ml = (JMA_GLOBAL const float*)p_ml;
   asm volatile("" : "+s"(g_acc), "+s"(g_ml), "+s"(p_ns), "+s"(p_heads), "+s"(p_group));
@@ -1329,8 +1334,8 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   const uint64_t base = group_item0(p_ns, p_ns ? 0u : a.item_start[row] / a.slices, row, hkv,
                                     hgroups, kvh * hgroups + hg, ns);
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const uint32_t s4 = lane >> 4, q = lane & 15;
-  const uint32_t e = chunk * 64 + 4 * q;
+  const uint32_t sl = lane / kQ, q = lane % kQ;
+  const uint32_t e = chunk * kOut + 4 * q;
   const uint32_t el = e < DV ? e : DV - 4;  // lanes past the head load a valid quad
   const float* acc = (const float*)g_acc;
   const float* mlp = (const float*)g_ml;
@@ -1344,7 +1349,7 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   float4_t xv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const uint32_t sp = (i * kWaves + wave) * 4 + s4;
+    const uint32_t sp = (i * kWaves + wave) * kSL + sl;
     xv[i] = sp < ns ? *(const float4_t*)(acc + sep_acc_float(base + sp, c16, DV, el))
                     : float4_t{0.f, 0.f, 0.f, 0.f};
   }
@@ -1372,19 +1377,27 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   float4_t X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const uint32_t sp = (i * kWaves + wave) * 4 + s4;
+    const uint32_t sp = (i * kWaves + wave) * kSL + sl;
     if (sp < ns) {
       const float w = __builtin_amdgcn_exp2f(s_ml[sp].x - mu);
 #pragma unroll
       for (int c = 0; c < 4; ++c) X[c] = fmaf(xv[i][c], w, X[c]);
     }
   }
+  // The split lanes of quad q: with 16 quads one lane in each row of 16; with 4 quads four lanes
+  // 4 apart in every row, summed by row rotations first.
 #pragma unroll
-  for (int c = 0; c < 4; ++c) X[c] = wave_sum_groups(X[c]);  // the four split lanes of quad q
-  if (s4 == 0) s_x[wave][q] = X;
+  for (int c = 0; c < 4; ++c) {
+    if constexpr (kQ == 4) {
+      X[c] += dpp<kDppRowRor4>(X[c]);
+      X[c] += dpp<kDppRowRor8>(X[c]);
+    }
+    X[c] = wave_sum_groups(X[c]);
+  }
+  if (sl == 0) s_x[wave][q] = X;
   if (lane == 0) s_l[wave] = lw;
   __syncthreads();
-  if (wave != 0 || s4 != 0) return;
+  if (wave != 0 || sl != 0) return;
   float lt = 0.0f;
   float4_t xt = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1396,22 +1409,29 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * p_heads + head) * DV + e) = xt * __builtin_amdgcn_rcpf(lt);
 }
 
+// Workgroups of 16 outputs when 64-output ones would leave most compute units idle (few rows
+// and heads: a long-context layer), else 64.
 template <int DV>
-static void launch_reduce_t(const DecodeArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((reduce_kernel<DV, 16>), grid, dim3(1024), 0, stream, a.part_acc, a.part_ml,
-                     a.ns_uniform, a.num_heads, a.group, a);
+static void launch_reduce_t(const DecodeArgs& a, hipStream_t stream) {
+  const uint32_t wide_groups = a.rows.count * a.num_heads * ((DV + 63) / 64);
+  if (wide_groups < 128 && DV >= 16) {
+    const dim3 grid(a.rows.count * a.num_heads * ((DV + 15) / 16));
+    hipLaunchKernelGGL((reduce_kernel<DV, 16, 4>), grid, dim3(1024), 0, stream, a.part_acc, a.part_ml,
+                       a.ns_uniform, a.num_heads, a.group, a);
+  } else {
+    hipLaunchKernelGGL((reduce_kernel<DV, 16, 16>), dim3(wide_groups), dim3(1024), 0, stream, a.part_acc,
+                       a.part_ml, a.ns_uniform, a.num_heads, a.group, a);
+  }
 }
 
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream) {
-  const uint32_t chunks = (uint32_t)((dv + 63) / 64);
-  const dim3 grid(a.rows.count * a.num_heads * chunks);
   switch (dv) {
-    case 16: launch_reduce_t<16>(a, grid, stream); break;
-    case 32: launch_reduce_t<32>(a, grid, stream); break;
-    case 64: launch_reduce_t<64>(a, grid, stream); break;
-    case 128: launch_reduce_t<128>(a, grid, stream); break;
-    case 256: launch_reduce_t<256>(a, grid, stream); break;
-    case 512: launch_reduce_t<512>(a, grid, stream); break;
+    case 16: launch_reduce_t<16>(a, stream); break;
+    case 32: launch_reduce_t<32>(a, stream); break;
+    case 64: launch_reduce_t<64>(a, stream); break;
+    case 128: launch_reduce_t<128>(a, stream); break;
+    case 256: launch_reduce_t<256>(a, stream); break;
+    case 512: launch_reduce_t<512>(a, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
