@@ -44,11 +44,12 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix
 F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 matrix
 # HBM bytes per decode launch on C2 measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# (bench.py --no-cpu --no-prefill --no-c1 --no-c4 --no-c5 --no-proj --steps 8 --warmup 2), each
-# scaled by what the counter reads for a 64 MiB device copy (FETCH x2.0, WRITE x1.0): 4388.3 KiB
-# x 2.0 + 316.6 KiB. The counter passes are kept with the decode profile summary under profiles/;
-# counters cannot be read from inside this process.
-DECODE_TRAFFIC_BYTES = round((4388.3 * 2.0 + 316.6) * 1024)
+# (bench.py --no-cpu --no-prefill --no-c1 --no-c4 --no-c5 --no-proj --no-prefill-others
+# --no-decode-others --steps 8 --warmup 2), each scaled by what the counter reads for a 64 MiB
+# device copy (FETCH x2.0, WRITE x1.0): 4364.5 KiB x 2.0 + 207.1 KiB. The counter passes are kept
+# with the decode profile summary under profiles/; counters cannot be read from inside this
+# process.
+DECODE_TRAFFIC_BYTES = round((4364.5 * 2.0 + 207.1) * 1024)
 
 
 def log(msg: str) -> None:
