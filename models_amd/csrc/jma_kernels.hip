@@ -614,7 +614,7 @@ __device__ __forceinline__ void reduce_group(float* part, uint64_t item0, uint32
 // and the slot capacity). The library is built with kernel-argument preloading, so they arrive in
 // scalar registers at wave start and the first tile loads do not wait for a kernel-argument
 // load; the other instances pass zeros there and read everything from `a`.
-template <typename KV, int DK, int DV, int DVS, bool kSimple, bool kOne, bool kNT>
+template <typename KV, int DK, int DV, int DVS, bool kSimple, bool kOne, bool kNT, bool kPack>
 __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     const void* p_kb, const void* p_vb, uint32_t p_start, uint32_t p_window, uint32_t p_tps,
     uint32_t p_cap, uint32_t p_ring, const DecodeArgs a) {
@@ -623,6 +623,12 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   constexpr uint32_t kBlk = TileT::kBlk;
   constexpr int kNs = kF16 ? 8 : 4;   // scores per lane per tile
   constexpr int kNv = DVS / 16;       // output fragments per lane
+  // kP (f16 KV, head dim 512, kv groups of at most 8 query heads): the hi and lo halves of q, and
+  // of p, share one matrix op as columns j and 8 + j of head j, instead of taking one op each.
+  // Each lane pair (j, 8 + j) adds its two partial scores with one row rotation, so both lanes
+  // hold the whole score and the same softmax state; column 8 + j of the PV product accumulates
+  // the lo halves, added to column j once the tile loop is done. Half the matrix ops per tile.
+  constexpr bool kP = kPack && kF16 && DK == 512;
   // Column slices: a workgroup computes DVS of the DV value columns (the whole of q.K, the V
   // columns and output of its slice only). The slices are virtual head groups: `hgroups` counts
   // head groups x kSlices, and a virtual group hgv is head group hgv / kSlices, slice
@@ -793,6 +799,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 
   const uint32_t hl = hg * 16 + c16;
   const bool head_ok = hl < group;
+  // The q operand column of this lane holds a real head (kP: head c16 % 8, hi or lo half).
+  const bool qcol_ok = kP ? ((uint32_t)c16 & 7u) + hg * 16 < group : head_ok;
   const float* cs = cos_t ? cos_t + (uint64_t)pos * pairs : nullptr;
   const float* sn = cos_t ? sin_t + (uint64_t)pos * pairs : nullptr;
 
@@ -953,7 +961,12 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   half8_t qhi[kF16 ? kCR : 1], qlo[kF16 ? kCR : 1];
   float4_t qf[kF16 ? 1 : kCR];
   auto q_chunk = [&](int c, half8_t& hi, half8_t& lo, float4_t& f) JMA_INL {
-    if constexpr (kF16) {
+    if constexpr (kP) {  // hi: the packed operand (column j: hi of head j, 8 + j: its lo)
+      const uint32_t hq = (uint32_t)c16 & 7u;
+      const _Float16* row = c16 < 8 ? &s_qh[hq][0] : &s_ql[hq][0];
+      hi = qcol_ok ? *(const half8_t*)(row + 32 * c + 8 * g) : half8_t{};
+      lo = half8_t{};
+    } else if constexpr (kF16) {
       hi = head_ok ? *(const half8_t*)&s_qh[c16][32 * c + 8 * g] : half8_t{};
       lo = head_ok ? *(const half8_t*)&s_ql[c16][32 * c + 8 * g] : half8_t{};
     } else {
@@ -1047,7 +1060,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
           sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qh, sc[b], 0, 0, 0);
-          sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], ql, sc[b], 0, 0, 0);
+          if constexpr (!kP) sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], ql, sc[b], 0, 0, 0);
         }
       }
 #pragma unroll
@@ -1068,7 +1081,8 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
           sc[b][c % kNa] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qhi[c], sc[b][c % kNa], 0, 0, 0);
-          sc[b][c % kNa] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qlo[c], sc[b][c % kNa], 0, 0, 0);
+          if constexpr (!kP)
+            sc[b][c % kNa] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[b][c], qlo[c], sc[b][c % kNa], 0, 0, 0);
         }
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
@@ -1100,6 +1114,10 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         for (int i = 0; i < w; ++i) sc[i] += sc[i + w];
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[e] = sc[0][e];
+    }
+    if constexpr (kP) {  // the hi and lo partial scores of each head meet in lanes j and 8 + j
+#pragma unroll
+      for (int i = 0; i < kNs; ++i) s[i] += dpp<kDppRowRor8>(s[i]);
     }
     if constexpr (kSplitKV) {  // V of this tile, now that K's registers are free
       cur.load_v(vb, slot0_of(tt), c16, g);
@@ -1142,11 +1160,18 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         phi[i] = h;
         plo[i] = (_Float16)(p[i] - (float)h);
       }
+      if constexpr (kP) {
+        const half8_t pp = c16 < 8 ? phi : plo;  // column j: hi of head j, 8 + j: its lo
 #pragma unroll
-      for (int n = 0; n < kNv; ++n) {
-        const half8_t vn = keep_bits(cur.v[n], vkeep);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vn, phi, acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vn, plo, acc[n], 0, 0, 0);
+        for (int n = 0; n < kNv; ++n)
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(keep_bits(cur.v[n], vkeep), pp, acc[n], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int n = 0; n < kNv; ++n) {
+          const half8_t vn = keep_bits(cur.v[n], vkeep);
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vn, phi, acc[n], 0, 0, 0);
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vn, plo, acc[n], 0, 0, 0);
+        }
       }
     } else {
 #pragma unroll
@@ -1196,6 +1221,12 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
   }
 
   l = wave_sum_groups(l);
+  if constexpr (kP) {  // column 8 + j holds the lo halves' share of head j's output
+#pragma unroll
+    for (int n = 0; n < kNv; ++n)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[n][e] += dpp<kDppRowRor8>(acc[n][e]);
+  }
   if constexpr (kQLds) __syncthreads();  // every wave is done with the q rows the combine area overlays
 
   // Every wave publishes its state; then one thread per (head, element) combines the waves.
@@ -1509,7 +1540,7 @@ bool decode_supported(bool f16, int dk, int dv) {
   return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
 }
 
-template <typename KV, bool kSimple, bool kNT>
+template <typename KV, bool kSimple, bool kNT, bool kPack>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
   const dim3 grid(a.max_splits, a.num_kv_heads * a.hgroups, a.rows.count), block(64 * decode_waves(d));
   // Preloaded leading arguments of the kSimple instance (zeros for the general one).
@@ -1521,35 +1552,35 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
   switch (d) {
     case 16:
       if constexpr (!std::is_same<KV, _Float16>::value) {
-        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, 16, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 16, 16, 16, kSimple, false, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       return hipErrorInvalidValue;
-    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, 32, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
-    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, 64, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
-    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, 128, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<KV, 32, 32, 32, kSimple, false, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 64: hipLaunchKernelGGL((decode_kernel<KV, 64, 64, 64, kSimple, false, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
+    case 128: hipLaunchKernelGGL((decode_kernel<KV, 128, 128, 128, kSimple, false, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a); break;
     case 256:
       if (a.slices == 4) {  // short rows: four 64-column slices, at most one tile per wave
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 64, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 64, kSimple, true, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       // One tile per wave (the long-context plans cut this fine) needs one tile buffer only.
       if (a.tiles_per_split <= (uint32_t)decode_waves(256))
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, true, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       else
-        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, false, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 256, 256, 256, kSimple, false, kNT, false>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     case 512:
       if (a.slices == 4) {  // short rows: four 128-column slices
-        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 128, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 128, kSimple, true, kNT, kPack>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       if (a.slices == 2) {
-        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 256, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 256, kSimple, true, kNT, kPack>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
       // One tile buffer always: a tile is the whole register budget of a wave at this width.
-      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 512, kSimple, true, kNT>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
+      hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 512, kSimple, true, kNT, kPack>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -1561,11 +1592,20 @@ hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStrea
   if (a.total_items == 0) return hipSuccess;
   const bool simple = a.k_base != nullptr;
   if (f16) {
-    if (simple) return launch_decode_t<_Float16, true, false>(a, dk, stream);
-    return a.stream_nt ? launch_decode_t<_Float16, false, true>(a, dk, stream)
-                       : launch_decode_t<_Float16, false, false>(a, dk, stream);
+    // Head dim 512 with groups of at most 8 query heads per kv head takes the packed hi / lo
+    // columns (measured: 4k context 12.8 -> 12.0 us, 32k 28.6 -> 28.2; at head dims 64 and 256 the
+    // extra row rotations cost more than the halved matrix ops save).
+    if (a.group <= 8 && dk == 512) {
+      if (simple) return launch_decode_t<_Float16, true, false, true>(a, dk, stream);
+      return a.stream_nt ? launch_decode_t<_Float16, false, true, true>(a, dk, stream)
+                         : launch_decode_t<_Float16, false, false, true>(a, dk, stream);
+    }
+    if (simple) return launch_decode_t<_Float16, true, false, false>(a, dk, stream);
+    return a.stream_nt ? launch_decode_t<_Float16, false, true, false>(a, dk, stream)
+                       : launch_decode_t<_Float16, false, false, false>(a, dk, stream);
   }
-  return simple ? launch_decode_t<float, true, false>(a, dk, stream) : launch_decode_t<float, false, false>(a, dk, stream);
+  return simple ? launch_decode_t<float, true, false, false>(a, dk, stream)
+                : launch_decode_t<float, false, false, false>(a, dk, stream);
 }
 
 // ================================================================ kernel 3: prefill (f16 MFMA)
