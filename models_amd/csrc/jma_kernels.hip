@@ -80,6 +80,27 @@ __device__ __forceinline__ float head_rms_scale(const float* x, uint32_t d, floa
   return 1.0f / rms;
 }
 
+// head_rms_scale for a head dim known at compile time: the head's loads are issued in batches of
+// eight 16-byte loads ahead of the in-order sum (the loop above waits for each load in turn).
+template <uint32_t D>
+__device__ __forceinline__ float head_rms_scale_d(const float* x, float eps) {
+#pragma clang fp contract(off)
+  constexpr uint32_t kB = D >= 32 ? 8u : D / 4;  // 16-byte loads per batch
+  float ss = 0.0f;
+#pragma unroll
+  for (uint32_t b = 0; b < D / 4; b += kB) {
+    float4_t v[kB];
+#pragma unroll
+    for (uint32_t i = 0; i < kB; ++i) v[i] = *(const float4_t*)(x + 4 * (b + i));
+#pragma unroll
+    for (uint32_t i = 0; i < kB; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = ss + v[i][e] * v[i][e];
+  }
+  const float rms = (float)sqrt((double)(ss / (float)D + eps));
+  return 1.0f / rms;
+}
+
 __device__ __forceinline__ void head_rms_norm(const float* x, uint32_t d, const float* w, float eps,
                                               uint32_t e0, uint32_t e1, float& y0, float& y1) {
 #pragma clang fp contract(off)
@@ -886,7 +907,12 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
         const uint32_t e0 = rot && neox ? j : 2 * j, e1 = rot && neox ? j + pairs : 2 * j + 1;
         float y0 = ax0[turn], y1 = ax1[turn];
         // QK-norm of the head before RoPE, as the append kernel applies it.
-        if (a.k_norm_w != nullptr) head_rms_norm(kx, DK, a.k_norm_w, a.norm_eps, e0, e1, y0, y1);
+        if (a.k_norm_w != nullptr) {
+#pragma clang fp contract(off)
+          const float sc = head_rms_scale_d<DK>(kx, a.norm_eps);
+          y0 = y0 * sc * a.k_norm_w[e0];
+          y1 = y1 * sc * a.k_norm_w[e1];
+        }
         if (rot) rotate_pair(y0, y1, afc[turn], afs[turn]);
         s_new_k[e0] = (KV)y0;
         s_new_k[e1] = (KV)y1;
@@ -922,7 +948,7 @@ __global__ __launch_bounds__(64 * decode_waves(DK)) void decode_kernel(
     // arithmetic), then every element times that scale and its weight, before RoPE.
     const float* qw = rope_q != 0 ? (const float*)a.q_norm_w : nullptr;
     if (qw != nullptr) {
-      if (threadIdx.x < nreal) s_qn[threadIdx.x] = head_rms_scale(qg + threadIdx.x * DK, DK, a.norm_eps);
+      if (threadIdx.x < nreal) s_qn[threadIdx.x] = head_rms_scale_d<DK>(qg + threadIdx.x * DK, a.norm_eps);
       __syncthreads();
     }
 #pragma unroll
