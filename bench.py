@@ -869,10 +869,14 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) Q/K/V, counter-based SplitMix64 + Box-Muller)",
         "config": {
             "workload": "C2 Llama-3.2-1B-shaped decode: 32 Q heads, 8 KV heads, head_dim 64, "
-                        "f16 KV, context 4096, 16 layers, 128 consecutive decode steps, "
-                        "RoPE theta 5e5",
+                        "f16 KV, context 4096, 16 layers, RoPE theta 5e5; the eager pass and the "
+                        "graph captures cover the configured 128 consecutive decode steps, the "
+                        f"timed region replays the first {args.steps} of them",
             "batch": 1, "layers": 16, "context": 4096, "kv_dtype": "f16",
             "accumulate": "f32", "step": "one token through 16 layers (append + attention)",
+            "timed_steps": args.steps,
+            "timed_positions": [4096, 4096 + args.steps - 1],
+            "configured_steps": 128,
         },
         "us_per_token": round(c2["elapsed"] / args.steps * 1e6, 3),
         "us_per_token_eager_python": round(c2["eager_us_per_token"], 3),

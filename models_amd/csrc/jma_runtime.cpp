@@ -374,8 +374,32 @@ struct FusedAppend {
   bool rope_q = false;  // q is raw: the kernel applies the layer's QK-norm and RoPE
 };
 
-// fixed: null = the context's grow-only scratch; else the device's fixed scratch, and a plan
-// that needs more than it holds is refused (BUFFER_TOO_SMALL) before anything is enqueued.
+jma::DecodePlan decode_plan(const jmodels_attn_context* ctx, const jmodels_attn_kv* kv,
+                           const LayerCall& lc, const jma::RowList& rows) {
+  return jma::plan_decode(rows.count, rows.pos, lc.window, lc.hkv, lc.group, (int)lc.dk,
+                          (int)lc.dv, kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave,
+                          ctx->unfused, ctx->min_split_tiles);
+}
+
+// Refuses (BUFFER_TOO_SMALL) a launch plan whose scratch exceeds the device's fixed array.
+void check_fixed_fit(const jma::DecodePlan& plan, const jma::FixedScratch& fixed) {
+  auto fits = [&](size_t need, size_t have, const char* what) {
+    require(need <= have, JMODELS_ATTN_BUFFER_TOO_SMALL,
+            std::string("the launch plan needs ") + std::to_string(need) + " bytes of " + what +
+                ", the fixed scratch holds " + std::to_string(have));
+  };
+  if (plan.separate) {
+    fits(plan.acc_bytes, fixed.part_acc_bytes, "split partials");
+    fits(plan.ml_bytes, fixed.part_ml_bytes, "split maxima and sums");
+  } else if (plan.any_split) {
+    fits(plan.part_f_bytes, fixed.part_f_bytes, "split exchange partials");
+    fits(plan.counter_bytes, fixed.counters_bytes, "arrival tickets");
+  }
+}
+
+// fixed: null = the context's grow-only scratch; else the device's fixed scratch. The callers
+// check every chunk's plan against it (check_fixed_fit) before they enqueue anything, so a
+// refusal leaves the cache and the stream untouched; the check here repeats that.
 void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const LayerCall& lc,
                      const jma::RowList& rows, const float* q, float* out,
                      const FusedAppend& fa = FusedAppend(),
@@ -409,10 +433,7 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     }
     a.norm_eps = lc.norm->eps;
   }
-  const jma::DecodePlan plan =
-      jma::plan_decode(rows.count, rows.pos, lc.window, lc.hkv, lc.group, (int)lc.dk, (int)lc.dv,
-                       kv->f16(), ctx->decode_target_blocks, ctx->tiles_per_wave, ctx->unfused,
-                       ctx->min_split_tiles);
+  const jma::DecodePlan plan = decode_plan(ctx, kv, lc, rows);
   a.tiles_per_split = plan.tiles_per_split;
   a.hgroups = plan.hgroups;  // virtual head groups (head groups x column slices)
   a.slices = plan.slices;
@@ -440,16 +461,10 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     }
     a.stream_nt = bytes > (uint64_t(128) << 20) ? 1u : 0u;
   }
-  auto fits = [&](size_t need, size_t have, const char* what) {
-    require(need <= have, JMODELS_ATTN_BUFFER_TOO_SMALL,
-            std::string("the launch plan needs ") + std::to_string(need) + " bytes of " + what +
-                ", the fixed scratch holds " + std::to_string(have));
-  };
+  if (fixed) check_fixed_fit(plan, *fixed);
   if (plan.separate) {
     const size_t acc_b = plan.acc_bytes, ml_b = plan.ml_bytes;
     if (fixed) {
-      fits(acc_b, fixed->part_acc_bytes, "split partials");
-      fits(ml_b, fixed->part_ml_bytes, "split maxima and sums");
       a.part_acc = fixed->part_acc;
       a.part_ml = fixed->part_ml;
     } else {
@@ -462,13 +477,11 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
     // Arrival tickets start at zero and every partial word starts not-written; the reducing
     // workgroups restore both, so they are zeroed only when (re)allocated, never inside a launch
     // sequence a caller may capture.
-    const size_t part_b = plan.part_f_bytes, ctr_b = plan.counter_bytes;
+    const size_t part_b = plan.part_f_bytes;
     // The exchange addresses its partials with 32-bit byte offsets (a buffer descriptor).
     require(part_b <= 0x7FFFFFF0u, JMODELS_ATTN_INVALID_SHAPE,
             "decode plan needs more than 2 GiB of split partials (lower JMA_DECODE_TARGET_BLOCKS)");
     if (fixed) {
-      fits(part_b, fixed->part_f_bytes, "split exchange partials");
-      fits(ctr_b, fixed->counters_bytes, "arrival tickets");
       a.part_f = fixed->part_f;
       a.counters = fixed->counters;
     } else {
@@ -1419,6 +1432,20 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
                                             std::to_string(kv->ring[lc.layer]));
       if (first < p) kv->require_range(sequences[i], lc.layer, first, p - 1);
     }
+    if (fixed) {
+      // Every launch's plan and the rotated-query buffer are checked against the fixed scratch
+      // before anything is enqueued: a refusal appends nothing and marks nothing. Both paths
+      // below cut the rows into the same chunks of kMaxRows.
+      for (uint32_t base = 0; base < count; base += jma::kMaxRows) {
+        const uint32_t n = std::min<uint32_t>(jma::kMaxRows, count - base);
+        check_fixed_fit(decode_plan(ctx, kv, lc, make_rows(n, sequences + base, positions + base)),
+                        *fixed);
+      }
+      if (!can_fuse_decode(ctx, lc))
+        require(qn * sizeof(float) <= fixed->qrot_bytes, JMODELS_ATTN_BUFFER_TOO_SMALL,
+                "the rotated queries need " + std::to_string(qn * sizeof(float)) +
+                    " bytes, the fixed scratch holds " + std::to_string(fixed->qrot_bytes));
+    }
     set_device(ctx);
     const float* dq = q;
     const float* dk = k;
@@ -1447,10 +1474,7 @@ static int32_t decode_entry(bool device, jmodels_attn_context* ctx, jmodels_attn
     } else {
       float* qrot = nullptr;
       if (fixed) {
-        require(qn * sizeof(float) <= fixed->qrot_bytes, JMODELS_ATTN_BUFFER_TOO_SMALL,
-                "the rotated queries need " + std::to_string(qn * sizeof(float)) +
-                    " bytes, the fixed scratch holds " + std::to_string(fixed->qrot_bytes));
-        qrot = fixed->qrot;
+        qrot = fixed->qrot;  // its size was checked above, before anything was enqueued
       } else {
         ctx->qrot.reserve(qn * sizeof(float), ctx->stream, "decode rotated queries");
         qrot = (float*)ctx->qrot.ptr;

@@ -747,13 +747,16 @@ def test_c5_gemma3_long_context_full_size(hip):
     """BASELINE configs[4] at its configured size: 4 Q / 1 KV heads (MQA), d 256, NeoX RoPE
     (theta 1e4 on sliding layers, 1e6 on the global layers 5, 11, 17, 23), f16 KV, 26 layers in
     the 5 sliding (window 512) : 1 global pattern (LlamaConfig.usesSlidingWindow and
-    attentionStartPosition, llama/LlamaConfig.java:157-162, 184-195), 32704 prior positions and 3
-    decode steps. Sliding layers keep LayeredKvCache RING retention of 544 slots (window + one
-    32-row chunk) holding their last 512 prior positions; the global layers hold all 32704 and
-    run the wide split plans. Every layer and step against the oracle's GQA over the window read
-    back from the device, with the appended rows bit-exact."""
+    attentionStartPosition, llama/LlamaConfig.java:157-162, 184-195), 32704 prior positions and
+    the configured 64 decode steps (to position 32767, the cache's last). Sliding layers keep
+    LayeredKvCache RING retention of 544 slots (window + one 32-row chunk) holding their last 512
+    prior positions; the global layers hold all 32704 and run the wide split plans. Eight steps
+    spread over the run (0, 9, ..., 63) check every layer against the oracle's GQA over the window
+    read back from the device, with the appended rows bit-exact."""
     from models_amd.hip_runtime import DeviceArray
-    hq, hkv, d, prior, steps, layers, w, ring = 4, 1, 256, 32704, 3, 26, 512, 544
+    hq, hkv, d, prior, steps, layers, w, ring = 4, 1, 256, 32704, 64, 26, 512, 544
+    checked = list(range(0, steps, 9))
+    assert len(checked) == 8 and checked[-1] == steps - 1
     scale = A.default_scale(d)
     n = prior + steps
     qd, kd = hq * d, hkv * d
@@ -785,6 +788,8 @@ def test_c5_gemma3_long_context_full_size(hip):
         for st in range(steps):
             p = prior + st
             outs = [kv.decode(lp[l], [p], q[l, st], kn[l, st], vn[l, st]) for l in range(layers)]
+            if st not in checked:
+                continue
             qs, ks, vs = [], [], []
             for l in range(layers):
                 theta = 1e4 if sliding[l] else 1e6
@@ -803,8 +808,11 @@ def test_c5_gemma3_long_context_full_size(hip):
             for l in range(layers):
                 rel = assert_f16_close(outs[l], want[l], f"C5 full layer {l} step {st}", head_dim=d)
                 worst[sliding[l]] = max(worst[sliding[l]], rel)
-            # the ring holds what was stored and nothing older
-            assert kv.contains(0, prior - w) and not kv.contains(0, prior - w - 1)
+            # the ring holds the last 544 positions stored (the 512 prior ones appended first,
+            # then the decoded rows) and nothing older
+            oldest = max(prior - w, p + 1 - ring)
+            assert kv.contains(0, oldest) and not kv.contains(0, oldest - 1)
+            _say(f"C5 full step {st}: 26 layers against the oracle")
         _say(f"C5 full worst normwise rel err: sliding {worst[True]:.2e}, global {worst[False]:.2e}")
     finally:
         for buf in (zq, dk, dv):
@@ -885,12 +893,14 @@ def test_error_paths_match_reference_exceptions(hip):
 
 # ------------------------------------------------------------------ properties at full size
 
-def test_c2_full_size_spot_checks_and_properties(hip):
+def test_c2_full_size_every_layer_step_and_properties(hip):
     """C2 at its full size (16 layers, 4096 prior positions, 128 steps) through the device-pointer
-    entry points, as the benchmark runs it. Checks: oracle spot checks at the first and last step
-    of the first and last layer; a second replay after discard_from(4096) reproduces the outputs
-    exactly (idempotence of the resident cache); the rows the run appended equal the oracle's
-    rotated, f16-rounded K."""
+    entry points, as the benchmark runs it. Checks: every one of the 16 x 128 layer-steps against
+    the oracle's GQA (groupedQueryAttention, llama/LlamaForwardPass.java:1543-1593) over the
+    cache read back from the device, the 128 rows of a layer in one threaded oracle batch; a
+    second replay after discard_from(4096) reproduces the outputs exactly (idempotence of the
+    resident cache); every row the run appended, in every layer, equals the oracle's rotated,
+    f16-rounded K and f16-rounded V."""
     from models_amd.hip_runtime import DeviceArray
     hq, hkv, d, prior, steps, layers, theta = 32, 8, 64, 4096, 128, 16, 5e5
     scale = A.default_scale(d)
@@ -937,21 +947,26 @@ def test_c2_full_size_spot_checks_and_properties(hip):
         second = run_steps()
         np.testing.assert_array_equal(first, second)
         _say("C2 full: replay identical")
-        for l in (0, layers - 1):
+        worst = 0.0
+        for l in range(layers):
             keys, values = kv.read(l, 0, n)
-            keys = keys.reshape(n, -1)
-            values = values.reshape(n, -1)
+            keys = np.ascontiguousarray(keys.reshape(n, -1))
+            values = np.ascontiguousarray(values.reshape(n, -1))
             k_rot = oracle.f16_round(rope_rows(k_host[l][prior:], range(prior, n), hkv, d, d,
-                                               theta, False))
+                                               theta, False, check_against_oracle=(l == 0)))
             np.testing.assert_array_equal(keys[prior:], k_rot)
             np.testing.assert_array_equal(values, oracle.f16_round(v_host[l]))
-            for s in (0, steps - 1):
-                p = prior + s
-                q_rot = rope_rows(q_host[l, s:s + 1], [p], hq, d, d, theta, False)
-                want = oracle.gqa_rows(q_rot[0], keys[:p + 1], values[:p + 1], hq, hkv, d, d,
-                                       scale)
-                rel = assert_f16_close(first[l, s], want, f"C2 full layer {l} step {s}", head_dim=d)
-                _say(f"C2 full layer {l} step {s} rel {rel:.2e}")
+            q_rot = rope_rows(q_host[l], range(prior, n), hq, d, d, theta, False,
+                              check_against_oracle=(l == 0))
+            want = oracle.gqa_rows_batch([q_rot[s] for s in range(steps)],
+                                         [keys[:prior + s + 1] for s in range(steps)],
+                                         [values[:prior + s + 1] for s in range(steps)],
+                                         hq, hkv, d, d, scale, threads=16)
+            for s in range(steps):
+                rel = assert_f16_close(first[l, s], want[s], f"C2 full layer {l} step {s}",
+                                       head_dim=d)
+                worst = max(worst, rel)
+            _say(f"C2 full layer {l}: 128 steps against the oracle, worst rel {worst:.2e}")
     finally:
         for buf in (zeros_q, dq, dk, dv, dout):
             buf.free()

@@ -162,3 +162,55 @@ def test_noalloc_refuses_plans_beyond_the_fixed_scratch(monkeypatch):
             rope.close()
     finally:
         lib.close()
+
+
+def test_noalloc_refusal_enqueues_nothing_on_any_path(monkeypatch):
+    """The fixed-scratch check covers every launch of a call before the first one is enqueued:
+    (a) on the separate-kernel path (10 rotary pairs, not a multiple of 8), whose append would
+    otherwise run before the attention launch is planned; (b) on the fused path with 256
+    sessions, two launches of 128 rows, where only the second launch (long rows) exceeds the
+    fixed scratch. Either call is refused with BUFFER_TOO_SMALL and no new row is appended or
+    marked; decode_device then runs the same call."""
+    monkeypatch.setenv("JMA_DECODE_TARGET_BLOCKS", "100000")
+    lib = A.HipAttentionLibrary(0)
+    hq, hkv, d, n = 32, 8, 256, 544
+    try:
+        for case, pairs, B in (("separate kernels", 10, 128), ("second launch", d // 2, 256)):
+            rope = lib.rotary_table(2 * pairs, 1e4, 1.0, max_positions=n + 1)
+            kv = lib.kv_cache(1, n + 1, hkv, d, d, half_precision=True, sequences=B)
+            layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+            # case (b): sessions 0..127 hold 10 rows (one tile, no split), 128..255 hold n - 1
+            lens = [n - 1] * B if B == 128 else [10] * 128 + [n - 1] * 128
+            zq = rt.DeviceArray(n * hq * d)
+            zq.zero()
+            dk = rt.DeviceArray.from_host(normal(45, "ref/k", (n, hkv * d)))
+            dv = rt.DeviceArray.from_host(normal(45, "ref/v", (n, hkv * d)))
+            dq = rt.DeviceArray.from_host(normal(45, "ref/q", (B, hq * d)))
+            dkn = rt.DeviceArray.from_host(normal(45, "ref/kn", (B, hkv * d)))
+            dvn = rt.DeviceArray.from_host(normal(45, "ref/vn", (B, hkv * d)))
+            dout = rt.DeviceArray(B * hq * d)
+            try:
+                for s, L in enumerate(lens):
+                    kv.append_device(layer, np.full(L, s, np.uint32), np.arange(L), zq.ptr,
+                                     L * hq * d, dk.ptr, L * hkv * d, dv.ptr, L * hkv * d)
+                lib.synchronize()
+                args = ([*range(B)], lens, dq.ptr, B * hq * d, dkn.ptr, B * hkv * d, dvn.ptr,
+                        B * hkv * d, dout.ptr, B * hq * d)
+                with pytest.raises(A.AttentionStatusError) as e:
+                    kv.decode_device_noalloc(layer, *args)
+                assert e.value.status == A.BUFFER_TOO_SMALL, (case, e.value)
+                lib.synchronize()
+                for s in (0, B // 2, B - 1):
+                    assert not kv.contains(0, lens[s], sequence=s), (case, s)
+                kv.decode_device(layer, *args)
+                lib.synchronize()
+                assert all(kv.contains(0, lens[s], sequence=s) for s in (0, B // 2, B - 1))
+                assert np.all(np.isfinite(dout.download()))
+                _say(f"{case}: refused before anything ran")
+            finally:
+                for b in (zq, dk, dv, dq, dkn, dvn, dout):
+                    b.free()
+                kv.close()
+                rope.close()
+    finally:
+        lib.close()
