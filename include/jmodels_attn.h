@@ -74,7 +74,8 @@ extern "C" {
 #define JMODELS_ATTN_CAP_DEVICE_POINTERS (1ull << 6) /* *_device entry points */
 #define JMODELS_ATTN_CAP_QK_NORM (1ull << 7)         /* per-head RMS norm of q and k before RoPE */
 #define JMODELS_ATTN_CAP_VALUE_NORM (1ull << 8)      /* unweighted per-head RMS norm of v (Gemma 4) */
-#define JMODELS_ATTN_CAP_QUANT_MATMUL (1ull << 9)    /* Q4_0 / Q8_0 projections on device memory */
+#define JMODELS_ATTN_CAP_QUANT_MATMUL (1ull << 9)    /* Q4_0 / Q8_0 / Q5_0 / Q4_K / Q5_K / Q6_K
+                                                        projections on device memory */
 
 /* KV storage element types. F16 stores IEEE binary16 (round to nearest even), which widens to
  * exactly Float.float16ToFloat(Float.floatToFloat16(x)) — the reference's half-precision KV
@@ -340,15 +341,15 @@ JMODELS_ATTN_API int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, 
  * The projections on either side of attention: Q/K/V before the append
  * (BJ/llama/LlamaForwardPass.java:1043-1067, with addOptionalBias :1065-1067) and the output
  * projection plus residual after it (:1131-1138). GGUF weight formats use backend-native's codes
- * (RS:150-161): 0 = Q4_0 (18-byte blocks of 32), 1 = Q8_0 (34 bytes), 2 = Q4_K (144-byte blocks
- * of 256), 3 = Q6_K (210 bytes) run here; its other codes (Q5_K, Q5_0) return INVALID_SHAPE.
- * Q4_0 / Q8_0: activations quantized to Q8_0 per 32-element block, every output the in-order chain
- * of per-block fma(weightScale * activationScale, integer dot, sum), the arithmetic
- * backend-native's tests require of its Q4_0 kernel exactly (backend-native/src/test/java/.../
- * NativeKernelLibraryTest.java:67-84, 909-1023). Q4_K / Q6_K: Q8_K activations and the float
- * order of backend-native's scalar row kernels (RS:3410-3459, 3519-3577; its tests hold the
- * K-quant kernels to 2e-3 of the Java path). One call takes either Q4_0 / Q8_0 or K-quant
- * matrices, not both (their activation formats differ).
+ * (RS:150-161), all six on the device: 0 = Q4_0 (18-byte blocks of 32), 1 = Q8_0 (34 bytes),
+ * 5 = Q5_0 (22 bytes), 2 = Q4_K (144-byte blocks of 256), 4 = Q5_K (176 bytes), 3 = Q6_K (210).
+ * Q4_0 / Q8_0 / Q5_0: activations quantized to Q8_0 per 32-element block, every output the
+ * in-order chain of per-block fma(weightScale * activationScale, integer dot, sum), the
+ * arithmetic backend-native's tests require of its Q4_0 kernel exactly (backend-native/src/test/
+ * java/.../NativeKernelLibraryTest.java:67-84, 909-993). Q4_K / Q5_K / Q6_K: Q8_K activations and
+ * the float order of backend-native's scalar row kernels (RS:3410-3577; its tests hold the
+ * K-quant kernels to 2e-3 of the Java path). One call takes either 32-element block formats or
+ * K-quants, not both (their activation formats differ).
  *
  * Device pointers, asynchronous on the context stream (capturable: no scratch memory). weights:
  * [rows][cols / 32 or cols / 256] blocks, 2-byte aligned; input [batch][cols] f32, 16-byte
@@ -361,6 +362,8 @@ JMODELS_ATTN_API int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, 
 #define JMODELS_ATTN_WEIGHTS_Q8_0 1u
 #define JMODELS_ATTN_WEIGHTS_Q4_K 2u
 #define JMODELS_ATTN_WEIGHTS_Q6_K 3u
+#define JMODELS_ATTN_WEIGHTS_Q5_K 4u
+#define JMODELS_ATTN_WEIGHTS_Q5_0 5u
 #define JMODELS_ATTN_ADDEND_NONE 0u
 #define JMODELS_ATTN_ADDEND_BIAS 1u
 #define JMODELS_ATTN_ADDEND_RESIDUAL 2u

@@ -62,6 +62,8 @@ WEIGHTS_Q4_0 = 0
 WEIGHTS_Q8_0 = 1
 WEIGHTS_Q4_K = 2
 WEIGHTS_Q6_K = 3
+WEIGHTS_Q5_K = 4
+WEIGHTS_Q5_0 = 5
 ADDEND_NONE = 0
 ADDEND_BIAS = 1
 ADDEND_RESIDUAL = 2
@@ -294,8 +296,8 @@ class HipAttentionLibrary:
                                 x_elems: int, out_ptr: int, out_elems: int, batch: int, rows: int,
                                 cols: int, addend_ptr: Optional[int] = None,
                                 addend_mode: int = ADDEND_NONE) -> None:
-        """jmodels_quantized_f32_batched_matmul_with_context on device memory (Q4_0, Q8_0, Q4_K,
-        Q6_K)."""
+        """jmodels_quantized_f32_batched_matmul_with_context on device memory (Q4_0, Q8_0, Q5_0,
+        Q4_K, Q5_K, Q6_K)."""
         self.check(self.lib.jmodels_attn_quantized_matmul_device(
             self.ctx, fmt, weights_ptr, weight_bytes, x_ptr, x_elems, out_ptr, out_elems, batch,
             rows, cols, addend_ptr, addend_mode), "quantized_matmul_device")

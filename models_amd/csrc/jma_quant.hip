@@ -45,11 +45,16 @@ __device__ __forceinline__ float f16_bits_to_float(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// Weight block of a format: a 16-bit scale, then 16 (Q4_0) or 32 (Q8_0) bytes, read as 16-bit
-// halves (the blocks are 2-byte aligned only).
+// Bits 0..3 of x moved to bit 4 of bytes 0..3 (the four shifted copies of x do not overlap, so
+// the product has no carries).
+__device__ __forceinline__ uint32_t fifth_bits(uint32_t x) { return ((x * 0x00204081u) & 0x01010101u) << 4; }
+
+// Weight block of a format (backend-native's codes: 0 Q4_0, 1 Q8_0, 5 Q5_0): a 16-bit scale,
+// then 16 bytes of nibbles (Q4_0), a 32-bit word of fifth bits and 16 bytes of nibbles (Q5_0) or
+// 32 int8 (Q8_0), read as 16-bit halves (the blocks are 2-byte aligned only).
 template <int FMT>
 struct QBlock {
-  static constexpr uint32_t kHalves = FMT == 0 ? 9u : 17u;
+  static constexpr uint32_t kHalves = FMT == 0 ? 9u : FMT == 5 ? 11u : 17u;
   uint32_t h[kHalves];
   __device__ __forceinline__ void load(const uint16_t* rec) {
 #pragma unroll
@@ -58,7 +63,9 @@ struct QBlock {
   __device__ __forceinline__ uint32_t word(uint32_t j) const { return h[1 + 2 * j] | (h[2 + 2 * j] << 16); }
   // Integer dot of the block with Q8_0 activations aq (8 words of 4 int8) whose element sum is
   // asum. Q4_0: byte i holds element i in its low nibble and element i + 16 in its high one, each
-  // offset by 8; the offset is applied as -8 * asum.
+  // offset by 8; the offset is applied as -8 * asum. Q5_0: the same nibbles with bit j of the
+  // word at byte 2 as element j's fifth bit, offset by 16 (dot_q5_0_q8_0_row_scalar,
+  // backend-native/src/main/rust/model-kernels/src/lib.rs:3204-3252): elements 0..31 as bytes.
   __device__ __forceinline__ int dot(const int* aq, int asum) const {
     int d = 0;
     if constexpr (FMT == 0) {
@@ -69,6 +76,17 @@ struct QBlock {
         d = __builtin_amdgcn_sdot4((int)((w >> 4) & 0x0F0F0F0Fu), aq[4 + j], d, false);
       }
       d -= 8 * asum;
+    } else if constexpr (FMT == 5) {
+      const uint32_t high = word(0);
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t w = h[3 + 2 * j] | (h[4 + 2 * j] << 16);
+        const uint32_t lo = (w & 0x0F0F0F0Fu) | fifth_bits((high >> (4 * j)) & 15u);
+        const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | fifth_bits((high >> (16 + 4 * j)) & 15u);
+        d = __builtin_amdgcn_sdot4((int)lo, aq[j], d, false);
+        d = __builtin_amdgcn_sdot4((int)hi, aq[4 + j], d, false);
+      }
+      d -= 16 * asum;
     } else {
 #pragma unroll
       for (uint32_t j = 0; j < 8; ++j) d = __builtin_amdgcn_sdot4((int)word(j), aq[j], d, false);
@@ -98,7 +116,7 @@ __global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
   const uint32_t r0 = (blockIdx.x - a.m[mi].tile0) * R;
   const uint32_t nrows = min(R, rows - r0);
   const uint32_t nunits = nrows * K;
-  constexpr uint32_t kRecHalves = FMT == 0 ? 9u : 17u;  // block bytes / 2
+  constexpr uint32_t kRecHalves = QBlock<FMT>::kHalves;  // block bytes / 2
   const uint16_t* wrec = (const uint16_t*)(w + (uint64_t)r0 * K * (2u * kRecHalves));
   const uint32_t tid = threadIdx.x;
 
@@ -192,19 +210,22 @@ __global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- K-quants (Q4_K, Q6_K)
+// ---------------------------------------------------------------- K-quants (Q4_K, Q5_K, Q6_K)
 //
 // Q8_K activations (quantize_q8_k_batch, backend-native/src/main/rust/model-kernels/src/lib.rs:
 // 3906-3952): per 256-element block, the element of largest magnitude (the first on ties, NaN
 // skipped) sets inverse = -127 / max, element = min(nearest(inverse * x), 127), sums of 16
 // elements, scale = 1 / inverse. Rows as backend-native's scalar row kernels form them
-// (dot_q4_k_q8_k_row_scalar :3410-3459, dot_q6_k_q8_k_row_scalar :3519-3577); the integer parts
-// are exact in any order, so eight threads share each (row, block) and only the float chains
-// keep the reference's order.
+// (dot_q4_k_q8_k_row_scalar :3410-3459, dot_q5_k_q8_k_row_scalar :3461-3518,
+// dot_q6_k_q8_k_row_scalar :3519-3577); the integer parts are exact in any order, so eight
+// threads share each (row, block) and only the float chains keep the reference's order. Q5_K is
+// Q4_K with a 32-byte array of fifth bits ahead of the nibbles (bit g of byte i: element i of
+// group g), so the two share their code and float chain.
 template <int FMT>
 __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
-  constexpr uint32_t kNT = FMT == 2 ? 4u : 9u;         // floats per (row, block) term
-  constexpr uint32_t kBlockBytes = FMT == 2 ? 144u : 210u;
+  constexpr bool kQ45 = FMT == 2 || FMT == 4;          // Q4_K or Q5_K
+  constexpr uint32_t kNT = kQ45 ? 4u : 9u;             // floats per (row, block) term
+  constexpr uint32_t kBlockBytes = FMT == 2 ? 144u : FMT == 4 ? 176u : 210u;
   extern __shared__ __attribute__((aligned(16))) unsigned char q_lds[];
   const uint32_t nb = a.batch, cols = a.cols, KB = a.blocks, R = a.rows_per_tile;
   const uint32_t rs = KB * kNT + 1;  // floats per (activation row, output row) of terms
@@ -284,7 +305,7 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
     const bool real = t / 8u < nunits;
     const uint32_t row = u / KB, blk = u % KB;
     const uint8_t* wb = wtile + (uint64_t)u * kBlockBytes;
-    if constexpr (FMT == 2) {
+    if constexpr (kQ45) {
       const uint16_t* h = (const uint16_t*)wb;
       const float wd = f16_bits_to_float(h[0]), wdmin = f16_bits_to_float(h[1]);
       uint32_t scb[12];
@@ -297,17 +318,26 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
       const uint32_t g = sub;
       const int sc = g < 4 ? (int)(scb[g] & 63u) : (int)((scb[g + 4] & 15u) | ((scb[g - 4] >> 6) << 4));
       const int mn = g < 4 ? (int)(scb[g + 4] & 63u) : (int)((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4));
+      // The group's 32 quants as 8 words of 4 bytes: nibbles (Q5_K: plus bit g of each qh byte
+      // as the byte's bit 4).
       uint32_t nib[8];
-      const uint16_t* qh16 = h + 8 + (g >> 1) * 16;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) nib[i] = (uint32_t)qh16[2 * i] | ((uint32_t)qh16[2 * i + 1] << 16);
+      const uint16_t* qn16 = h + (FMT == 4 ? 24 : 8) + (g >> 1) * 16;
       const uint32_t shift = (g & 1u) * 4u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        nib[i] = (((uint32_t)qn16[2 * i] | ((uint32_t)qn16[2 * i + 1] << 16)) >> shift) & 0x0F0F0F0Fu;
+      if constexpr (FMT == 4) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t qh = (uint32_t)h[8 + 2 * i] | ((uint32_t)h[9 + 2 * i] << 16);
+          nib[i] |= ((qh >> g) & 0x01010101u) << 4;
+        }
+      }
       for (uint32_t b = 0; b < nb; ++b) {
         const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 256u + g * 32u);
         int dot = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          dot = __builtin_amdgcn_sdot4((int)((nib[i] >> shift) & 0x0F0F0F0Fu), aq[i], dot, false);
+        for (int i = 0; i < 8; ++i) dot = __builtin_amdgcn_sdot4((int)nib[i], aq[i], dot, false);
         const int* s16 = act_sum + b * (cols / 16u) + blk * 16u;
         int qs = sc * dot, ms = mn * (s16[2 * g] + s16[2 * g + 1]);
         qs += __shfl_xor(qs, 1, 8);
@@ -368,7 +398,7 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
     const uint32_t b = t / nrows, row = t % nrows;
     const float* tt = terms + (b * R + row) * rs;
     float sum = 0.0f;
-    if constexpr (FMT == 2) {
+    if constexpr (kQ45) {
       for (uint32_t blk = 0; blk < KB; ++blk) {
         sum = __builtin_fmaf(tt[blk * 4], tt[blk * 4 + 1], sum);
         sum = __builtin_fmaf(tt[blk * 4 + 2], tt[blk * 4 + 3], sum);
@@ -389,7 +419,7 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
 }
 
 size_t qkmatvec_lds_bytes(uint32_t fmt, uint32_t batch, uint32_t cols, uint32_t rows_per_tile) {
-  const uint32_t KB = cols / 256u, nt = fmt == 2 ? 4u : 9u;
+  const uint32_t KB = cols / 256u, nt = fmt == 3 ? 9u : 4u;
   return ((size_t)batch * cols + 15u) / 16u * 16u + (size_t)batch * KB * 4u +
          (size_t)batch * (cols / 16u) * 4u + (size_t)batch * rows_per_tile * (KB * nt + 1u) * 4u;
 }
@@ -412,6 +442,11 @@ hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipSt
   else if (fmt == 3)
     hipLaunchKernelGGL(qkmatvec_kernel<3>, dim3(tiles), dim3(kQThreads),
                        qkmatvec_lds_bytes(3, a.batch, a.cols, a.rows_per_tile), stream, a);
+  else if (fmt == 4)
+    hipLaunchKernelGGL(qkmatvec_kernel<4>, dim3(tiles), dim3(kQThreads),
+                       qkmatvec_lds_bytes(4, a.batch, a.cols, a.rows_per_tile), stream, a);
+  else if (fmt == 5)
+    hipLaunchKernelGGL(qmatvec_kernel<5>, dim3(tiles), dim3(kQThreads), lds, stream, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -735,9 +735,12 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   check_ctx(ctx);
   require(input != nullptr && output != nullptr, JMODELS_ATTN_NULL_POINTER, "null input or output");
   require(!mats.empty(), JMODELS_ATTN_INVALID_SHAPE, "no matrices");
-  // Q4_0 / Q8_0 take Q8_0 activations (32-element blocks), the K-quants Q8_K (256): one call
-  // shares one activation format, as backend-native's grouped calls require (RS:1196-1204).
-  const bool kq = mats[0].format == JMODELS_ATTN_WEIGHTS_Q4_K || mats[0].format == JMODELS_ATTN_WEIGHTS_Q6_K;
+  // Q4_0 / Q8_0 / Q5_0 take Q8_0 activations (32-element blocks), the K-quants Q8_K (256): one
+  // call shares one activation format, as backend-native's grouped calls require (RS:1196-1204).
+  auto is_kquant = [](uint32_t f) {
+    return f == JMODELS_ATTN_WEIGHTS_Q4_K || f == JMODELS_ATTN_WEIGHTS_Q5_K || f == JMODELS_ATTN_WEIGHTS_Q6_K;
+  };
+  const bool kq = is_kquant(mats[0].format);
   const uint32_t elems = kq ? 256u : 32u;
   require(batch > 0 && cols > 0 && cols % elems == 0, JMODELS_ATTN_INVALID_SHAPE,
           "batch_size and cols must be > 0 and cols a multiple of " + std::to_string(elems));
@@ -746,21 +749,26 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(((uintptr_t)input & 15u) == 0, JMODELS_ATTN_INVALID_SHAPE,
           "input must be 16-byte aligned");
   const uint32_t K = cols / elems;
+  // GGUF block sizes (RS:87-92).
   auto block_bytes = [](uint32_t f) -> uint64_t {
-    return f == JMODELS_ATTN_WEIGHTS_Q4_0 ? 18u : f == JMODELS_ATTN_WEIGHTS_Q8_0 ? 34u
-           : f == JMODELS_ATTN_WEIGHTS_Q4_K ? 144u : 210u;
+    switch (f) {
+      case JMODELS_ATTN_WEIGHTS_Q4_0: return 18u;
+      case JMODELS_ATTN_WEIGHTS_Q8_0: return 34u;
+      case JMODELS_ATTN_WEIGHTS_Q4_K: return 144u;
+      case JMODELS_ATTN_WEIGHTS_Q6_K: return 210u;
+      case JMODELS_ATTN_WEIGHTS_Q5_K: return 176u;
+      default: return 22u;  // Q5_0
+    }
   };
   uint64_t total_rows = 0;
   for (size_t i = 0; i < mats.size(); ++i) {
     const QuantMatrix& m = mats[i];
     const std::string at = " (matrix " + std::to_string(i) + ")";
-    require(m.format == JMODELS_ATTN_WEIGHTS_Q4_0 || m.format == JMODELS_ATTN_WEIGHTS_Q8_0 ||
-                m.format == JMODELS_ATTN_WEIGHTS_Q4_K || m.format == JMODELS_ATTN_WEIGHTS_Q6_K,
-            JMODELS_ATTN_INVALID_SHAPE,
-            "weight format " + std::to_string(m.format) + " has no device kernel" + at);
-    const bool mkq = m.format == JMODELS_ATTN_WEIGHTS_Q4_K || m.format == JMODELS_ATTN_WEIGHTS_Q6_K;
-    require(mkq == kq, JMODELS_ATTN_INVALID_SHAPE,
-            "one call mixes block formats (Q4_0/Q8_0) with K-quants (Q4_K/Q6_K)" + at);
+    require(m.format <= JMODELS_ATTN_WEIGHTS_Q5_0, JMODELS_ATTN_INVALID_SHAPE,
+            "unknown weight format " + std::to_string(m.format) + at);
+    require(is_kquant(m.format) == kq, JMODELS_ATTN_INVALID_SHAPE,
+            "one call mixes 32-element block formats (Q4_0/Q8_0/Q5_0) with K-quants "
+            "(Q4_K/Q5_K/Q6_K)" + at);
     require(m.weights != nullptr, JMODELS_ATTN_NULL_POINTER, "null weights" + at);
     require(m.rows > 0, JMODELS_ATTN_INVALID_SHAPE, "rows must be > 0" + at);
     require(((uintptr_t)m.weights & 1u) == 0, JMODELS_ATTN_INVALID_SHAPE,
@@ -797,7 +805,7 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   set_device(ctx);
   for (uint32_t b0 = 0; b0 < batch; b0 += chunk) {
     const uint32_t nb = std::min(chunk, batch - b0);
-    for (uint32_t fmt = 0; fmt < 4; ++fmt) {
+    for (uint32_t fmt = 0; fmt <= JMODELS_ATTN_WEIGHTS_Q5_0; ++fmt) {
       jma::QMatArgs a{};
       a.x = input + (uint64_t)b0 * cols;
       a.batch = nb;

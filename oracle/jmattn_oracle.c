@@ -1046,6 +1046,36 @@ static float kquant_row(int format, const uint8_t* w_row, const int8_t* aq, cons
     }
     return sum;
   }
+  if (format == JMO_FMT_Q5_K) {
+    /* dot_q5_k_q8_k_row_scalar (RS:3461-3518): Q4_K's arithmetic, each quant taking bit g of
+     * qh[index] as its fifth bit (value 16). */
+    float sum = 0.0f;
+    for (int blk = 0; blk < blocks; blk++) {
+      const uint8_t* w = w_row + (size_t)blk * 176;
+      const float d = jmo_f16_to_float((uint16_t)(w[0] | (w[1] << 8))) * ascale[blk];
+      const float dmin = jmo_f16_to_float((uint16_t)(w[2] | (w[3] << 8))) * ascale[blk];
+      const uint8_t* sc = w + 4;
+      const uint8_t* qh = w + 16;
+      const uint8_t* qs = w + 48;
+      const int8_t* a = aq + (size_t)blk * 256;
+      const int16_t* s16 = asum + (size_t)blk * 16;
+      int qsum = 0, msum = 0;
+      for (int g = 0; g < 8; g++) {
+        const uint8_t* packed = qs + (g >> 1) * 32;
+        const int shift = (g & 1) * 4;
+        int dot = 0;
+        for (int i = 0; i < 32; i++) {
+          const int quant = ((packed[i] >> shift) & 0x0f) | ((qh[i] >> g) & 1 ? 16 : 0);
+          dot += quant * a[g * 32 + i];
+        }
+        qsum += qk_scale(sc, g) * dot;
+        msum += qk_min(sc, g) * (s16[2 * g] + s16[2 * g + 1]);
+      }
+      sum = fmaf(d, (float)qsum, sum);
+      sum = fmaf(-dmin, (float)msum, sum);
+    }
+    return sum;
+  }
   /* Q6_K */
   float lane_sums[8] = {0};
   for (int blk = 0; blk < blocks; blk++) {
@@ -1082,7 +1112,7 @@ static float kquant_row(int format, const uint8_t* w_row, const int8_t* aq, cons
 static int kquant_matmul(int format, const uint8_t* weights, const float* input, int batch,
                          int rows, int cols, float* out) {
   const int blocks = cols / 256;
-  const int block_bytes = format == JMO_FMT_Q4_K ? 144 : 210;
+  const int block_bytes = format == JMO_FMT_Q4_K ? 144 : format == JMO_FMT_Q5_K ? 176 : 210;
   int8_t* q = (int8_t*)malloc((size_t)batch * cols);
   float* scales = (float*)malloc((size_t)batch * blocks * sizeof(float));
   int16_t* sums = (int16_t*)malloc((size_t)batch * (cols / 16) * sizeof(int16_t));
@@ -1107,14 +1137,15 @@ static int kquant_matmul(int format, const uint8_t* weights, const float* input,
 int jmo_quantized_matmul(int format, const uint8_t* weights, const float* input, int batch,
                          int rows, int cols, float* out) {
   if (rows <= 0 || batch <= 0 || cols <= 0) return JMO_ILLEGAL_ARGUMENT;
-  if (format == JMO_FMT_Q4_K || format == JMO_FMT_Q6_K) {
+  if (format == JMO_FMT_Q4_K || format == JMO_FMT_Q5_K || format == JMO_FMT_Q6_K) {
     if (cols % 256 != 0) return JMO_ILLEGAL_ARGUMENT;
     return kquant_matmul(format, weights, input, batch, rows, cols, out);
   }
-  if ((format != JMO_FMT_Q4_0 && format != JMO_FMT_Q8_0) || cols % 32 != 0)
+  if ((format != JMO_FMT_Q4_0 && format != JMO_FMT_Q8_0 && format != JMO_FMT_Q5_0) ||
+      cols % 32 != 0)
     return JMO_ILLEGAL_ARGUMENT;
   const int blocks = cols / 32;
-  const int block_bytes = format == JMO_FMT_Q4_0 ? 18 : 34;
+  const int block_bytes = format == JMO_FMT_Q4_0 ? 18 : format == JMO_FMT_Q5_0 ? 22 : 34;
   int8_t* q = (int8_t*)malloc((size_t)batch * cols);
   float* scales = (float*)malloc((size_t)batch * blocks * sizeof(float));
   if (!q || !scales) {
@@ -1138,6 +1169,19 @@ int jmo_quantized_matmul(int format, const uint8_t* weights, const float* input,
             const int packed = w[2 + i];
             dot += ((packed & 0xf) - 8) * a[i];
             dot += ((packed >> 4) - 8) * a[i + 16];
+          }
+        } else if (format == JMO_FMT_Q5_0) {
+          /* referenceQ5_0F32BatchedMatmul (NativeKernelLibraryTest.java:966-993; RS:3204-3252):
+           * byte i holds the low nibbles of elements i and i + 16, bits i and i + 16 of the
+           * little-endian word at byte 2 their fifth bits, each element offset by 16 */
+          const uint32_t high = (uint32_t)w[2] | ((uint32_t)w[3] << 8) | ((uint32_t)w[4] << 16) |
+                                ((uint32_t)w[5] << 24);
+          for (int i = 0; i < 16; i++) {
+            const int packed = w[6 + i];
+            const int lo = ((packed & 0xf) | (int)(((high >> i) & 1u) << 4)) - 16;
+            const int hi = ((packed >> 4) | (int)(((high >> (i + 16)) & 1u) << 4)) - 16;
+            dot += lo * a[i];
+            dot += hi * a[i + 16];
           }
         } else {
           for (int i = 0; i < 32; i++) dot += (int8_t)w[2 + i] * a[i];

@@ -197,6 +197,8 @@ int jmo_gqa_rows_batch8(int count, const float* const* q, const float* const* ke
 #define JMO_FMT_Q8_0 1 /* 34-byte blocks: f16 scale, 32 int8 (RS:89) */
 #define JMO_FMT_Q4_K 2 /* 144-byte blocks of 256: d, dmin, 12 bytes of 6-bit scales/mins, nibbles (RS:90) */
 #define JMO_FMT_Q6_K 3 /* 210-byte blocks of 256: ql[128], qh[64], int8 scales[16], d (RS:92) */
+#define JMO_FMT_Q5_K 4 /* 176-byte blocks of 256: d, dmin, 12 bytes of scales/mins, qh[32], nibbles (RS:91) */
+#define JMO_FMT_Q5_0 5 /* 22-byte blocks: f16 scale, 32 high bits, 16 bytes of nibbles (RS:88) */
 
 /* quantizeInputs (NativeKernelLibraryTest.java:998-1017; RS quantize_q8_0_batch_scalar): per
  * 32-element block, absmax (a NaN element is skipped, as Rust's f32::max does), inverse scale

@@ -27,15 +27,16 @@ q8_0 activation quantize    ggmlNearestInt == IEEE round-half-even (numpy rint) 
                             blocks; every |q| <= 127 and q * scale within half a step of x
 q8_k activation quantize    numpy: sign-aware block maximum (first index on ties), rint,
                             clamp at 127, 16-element sums, scale 1 / inverse
-quantized matmul Q4_K/Q6_K  NativeKernelLibraryTest's block builders (q4KBlock, q6KBlock) whose
-                            logical scales, mins and quants numpy's dequantization must recover;
-                            float64 product of the dequantized blocks (one rounding per term of the
-                            fma chains)
-quantized matmul Q4_0/Q8_0  float64 dot of the dequantized weights with the dequantized Q8_0
-                            activations (rounding of the per-block fma chain only); hand-computed
-                            one-block cases (nibble order, the -8 offset, scale product); the
-                            fixtures of NativeKernelLibraryTest (inputs / fillWeights /
-                            fillQ8_0Weights, :660-702) regenerated as data
+quantized matmul Q4_K/Q5_K/ NativeKernelLibraryTest's block builders (q4KBlock, q5KBlock,
+  Q6_K                      q6KBlock) whose logical scales, mins and quants numpy's dequantization
+                            must recover; float64 product of the dequantized blocks (one rounding
+                            per term of the fma chains); Q5_K with its fifth bits cleared == Q4_K
+quantized matmul Q4_0/Q8_0/ float64 dot of the dequantized weights with the dequantized Q8_0
+  Q5_0                      activations (rounding of the per-block fma chain only); hand-computed
+                            one-block cases (nibble order, the -8 / -16 offsets, the fifth bits,
+                            scale product); the fixtures of NativeKernelLibraryTest (inputs /
+                            fillWeights / fillQ8_0Weights / fillQ5_0Weights, :660-722)
+                            regenerated as data, fillQ5_0Weights with its logical quants
 attention start (window)    EncoderAttentionWindowTest causal bounds (:76-145); brute force
 gqa / decode / prefill      float64 dense softmax(QK^T s)V on small shapes (brute force); L=1 -> V;
                             uniform scores -> mean of V rows; one-hot key; equal Q within a GQA
@@ -539,8 +540,12 @@ FMT_Q4_0 = 0
 FMT_Q8_0 = 1
 FMT_Q4_K = 2
 FMT_Q6_K = 3
-BLOCK_BYTES = {FMT_Q4_0: 18, FMT_Q8_0: 34, FMT_Q4_K: 144, FMT_Q6_K: 210}
-BLOCK_ELEMS = {FMT_Q4_0: 32, FMT_Q8_0: 32, FMT_Q4_K: 256, FMT_Q6_K: 256}
+FMT_Q5_K = 4
+FMT_Q5_0 = 5
+BLOCK_BYTES = {FMT_Q4_0: 18, FMT_Q8_0: 34, FMT_Q4_K: 144, FMT_Q6_K: 210, FMT_Q5_K: 176,
+               FMT_Q5_0: 22}
+BLOCK_ELEMS = {FMT_Q4_0: 32, FMT_Q8_0: 32, FMT_Q4_K: 256, FMT_Q6_K: 256, FMT_Q5_K: 256,
+               FMT_Q5_0: 32}
 
 
 def q8_k_quantize(x, batch: int, cols: int):
@@ -568,8 +573,9 @@ def q8_0_quantize(x, batch: int, cols: int):
 
 
 def quantized_matmul(fmt: int, weights, x, batch: int, rows: int, cols: int) -> np.ndarray:
-    """referenceQ4_0F32BatchedMatmul / referenceQ8_0F32BatchedMatmul
-    (NativeKernelLibraryTest.java:909-965): out [batch, rows]."""
+    """referenceQ4_0F32BatchedMatmul / referenceQ8_0F32BatchedMatmul /
+    referenceQ5_0F32BatchedMatmul (NativeKernelLibraryTest.java:909-993) and backend-native's
+    scalar K-quant row kernels (RS:3410-3577): out [batch, rows]."""
     if isinstance(weights, (bytes, bytearray)):
         weights = np.frombuffer(bytes(weights), np.uint8)
     w = np.ascontiguousarray(weights, dtype=np.uint8).reshape(-1)

@@ -440,6 +440,72 @@ def quantized_matmul_cases():
                 out += b
         return out.hex(), quants, scales
 
+    def q5_0_weights(rows, cols):
+        # fillQ5_0Weights (:701-722): per lane a 5-bit low and high value, nibbles at byte 6 +
+        # lane, fifth bits as bits lane and lane + 16 of the little-endian word at byte 2.
+        out, quants = bytearray(), []
+        for row in range(rows):
+            for block in range(cols // 32):
+                b = bytearray(22)
+                b[0:2] = _f16_bits((row + block + 1) * 0.0625).to_bytes(2, "little")
+                high_bits, lows, highs = 0, [], []
+                for lane in range(16):
+                    low = (row * 17 + block * 11 + lane * 5) & 0x1F
+                    high = (row * 13 + block * 7 + lane * 9) & 0x1F
+                    b[6 + lane] = (low & 0x0F) | ((high & 0x0F) << 4)
+                    high_bits |= ((low >> 4) & 1) << lane
+                    high_bits |= ((high >> 4) & 1) << (lane + 16)
+                    lows.append(low)
+                    highs.append(high)
+                b[2:6] = high_bits.to_bytes(4, "little")
+                quants.append(lows + highs)  # elements 0-15, then 16-31 (before the -16 offset)
+                out += b
+        return out.hex(), quants
+
+    def q5_k(rows, cols):
+        # q5KBlock (:799-828): q4KBlock's scales and mins, 5-bit quants whose fifth bit of group
+        # g sits in bit g of byte 16 + index.
+        out, quants = bytearray(), []
+        for row in range(rows):
+            for block in range(cols // 256):
+                b = bytearray(176)
+                b[0:2] = _f16_bits((row + 1) * 0.03125).to_bytes(2, "little")
+                b[2:4] = _f16_bits((block + 1) * 0.015625).to_bytes(2, "little")
+                for g in range(4):
+                    b[4 + g] = q4_scales[g]
+                    b[8 + g] = q4_mins[g]
+                for g in range(4, 8):
+                    b[8 + g] = (q4_scales[g] & 0x0F) | ((q4_mins[g] & 0x0F) << 4)
+                    b[g] |= (q4_scales[g] >> 4) << 6
+                    b[4 + g] |= (q4_mins[g] >> 4) << 6
+                qv = []
+                for g in range(8):
+                    off, shift = 48 + (g >> 1) * 32, (g & 1) * 4
+                    for i in range(32):
+                        quant = (row * 17 + block * 11 + g * 7 + i * 5) & 0x1F
+                        b[off + i] |= (quant & 0x0F) << shift
+                        if quant & 0x10:
+                            b[16 + i] |= 1 << g
+                        qv.append(quant)
+                quants.append(qv)
+                out += b
+        return out.hex(), quants
+
+    hx, quants = q5_0_weights(5, 64)
+    cases.append({"name": "reusableGgufKernelComputesQ5_0BatchedMatrixMultiplicationWithinReductionTolerance",
+                  "src": "NativeKernelLibraryTest.java:199-220", "format": 5, "batch": 3, "rows": 5,
+                  "cols": 64, "relation": 2e-5, "input": activations(3, 64), "weights_hex": hx,
+                  "logical": {"quants": quants}})
+    hx, quants = q5_0_weights(5, 256)
+    cases.append({"name": "reusableGgufKernelComputesQ5_0SingleTokenProjectionWithinQuantizedTolerance",
+                  "src": "NativeKernelLibraryTest.java:222-244", "format": 5, "batch": 1, "rows": 5,
+                  "cols": 256, "relation": 1e-3, "input": activations(1, 256), "weights_hex": hx,
+                  "logical": {"quants": quants}})
+    hx, quants = q5_k(5, 512)
+    cases.append({"name": "reusableGgufKernelMatchesVectorSemanticsForKQuantizedBatchedMultiplication[Q5_K]",
+                  "src": "NativeKernelLibraryTest.java:246-271", "format": 4, "batch": 3, "rows": 5,
+                  "cols": 512, "relation": 2e-3, "input": activations(3, 512), "weights_hex": hx,
+                  "logical": {"scales": q4_scales, "mins": q4_mins, "quants": quants}})
     hx, quants = q4_k(5, 512)
     cases.append({"name": "reusableGgufKernelMatchesVectorSemanticsForKQuantizedBatchedMultiplication[Q4_K]",
                   "src": "NativeKernelLibraryTest.java:246-271", "format": 2, "batch": 3, "rows": 5,

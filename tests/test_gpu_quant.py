@@ -36,7 +36,7 @@ def hip():
 
 def _weights(fmt, rows, cols, key, scale=0.02):
     blocks = cols // 32
-    nbytes = 18 if fmt == 0 else 34
+    nbytes = {A.WEIGHTS_Q4_0: 18, A.WEIGHTS_Q8_0: 34, A.WEIGHTS_Q5_0: 22}[fmt]
     raw = synth.uniform_int(11, key, rows * blocks * nbytes, 0, 255).astype(np.uint8)
     raw = raw.reshape(rows, blocks, nbytes)
     s = (synth.normal(11, key + "/s", (rows, blocks)) * scale).astype(np.float16)
@@ -55,12 +55,12 @@ def _exact(got, want, what):
 
 
 def _kquant_weights(fmt, rows, cols, key):
-    nbytes = 144 if fmt == A.WEIGHTS_Q4_K else 210
+    nbytes = {A.WEIGHTS_Q4_K: 144, A.WEIGHTS_Q5_K: 176, A.WEIGHTS_Q6_K: 210}[fmt]
     raw = synth.uniform_int(11, key, rows * cols // 256 * nbytes, 0, 255).astype(np.uint8)
     raw = raw.reshape(rows, cols // 256, nbytes)
     d = (synth.normal(11, key + "/d", (rows, cols // 256, 2)) * 0.002).astype(np.float16)
     d = d.view(np.uint8).reshape(rows, cols // 256, 4)
-    if fmt == A.WEIGHTS_Q4_K:
+    if fmt in (A.WEIGHTS_Q4_K, A.WEIGHTS_Q5_K):
         raw[:, :, 0:4] = d
     else:
         raw[:, :, 208:210] = d[..., :2]
@@ -83,7 +83,7 @@ def test_reference_fixtures_bit_exact(hip, known_answers):
         _say(f"{case['name']}: bit-exact")
 
 
-@pytest.mark.parametrize("fmt", [A.WEIGHTS_Q4_0, A.WEIGHTS_Q8_0])
+@pytest.mark.parametrize("fmt", [A.WEIGHTS_Q4_0, A.WEIGHTS_Q8_0, A.WEIGHTS_Q5_0])
 @pytest.mark.parametrize("batch,rows,cols", [(1, 1, 32), (1, 3072, 2048), (3, 17, 2080),
                                              (13, 100, 512), (1, 64, 14336), (8, 300, 896),
                                              (9, 1, 32), (130, 257, 2048), (64, 128, 96),
@@ -100,11 +100,11 @@ def test_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
     _exact(got, want, f"fmt {fmt} {batch}x{rows}x{cols}")
 
 
-@pytest.mark.parametrize("fmt", [A.WEIGHTS_Q4_K, A.WEIGHTS_Q6_K])
+@pytest.mark.parametrize("fmt", [A.WEIGHTS_Q4_K, A.WEIGHTS_Q5_K, A.WEIGHTS_Q6_K])
 @pytest.mark.parametrize("batch,rows,cols", [(1, 1, 256), (1, 3072, 2048), (3, 17, 4096),
                                              (9, 100, 512), (1, 64, 14336)])
 def test_kquant_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
-    """Q4_K and Q6_K with Q8_K activations: the device repeats backend-native's scalar row
+    """Q4_K, Q5_K and Q6_K with Q8_K activations: the device repeats backend-native's scalar row
     kernels' float order (the integer parts are exact in any order), so the outputs are the
     oracle's bits; batches over 8 run in chunks."""
     w = _kquant_weights(fmt, rows, cols, f"kq/{fmt}/{rows}/{cols}")
@@ -149,6 +149,45 @@ def test_kquant_activation_edge_cases_and_grouped_q4_k_m(hip):
     finally:
         for d in dws + [dx, dout]:
             d.free()
+
+
+def test_q5_formats_in_grouped_calls(hip):
+    """The Q5 formats in grouped calls as GGUF files mix them: a Q5_K_M-style layer (Q and K in
+    Q5_K, V in Q6_K, one launch per format) and a Q5_0 / Q8_0 / Q4_0 mix with biases, outputs
+    q|k|v contiguous, each matrix bit-exact against the oracle; every fifth bit set or clear
+    (0xFF / 0x00 qh bytes) in one matrix of each call."""
+    cols, rows, batch = 2048, [2048, 512, 512], 3
+    x = synth.normal(11, "q5g/x", (batch, cols))
+    dx = rt.DeviceArray.from_host(x)
+    for fmts in ([A.WEIGHTS_Q5_K, A.WEIGHTS_Q5_K, A.WEIGHTS_Q6_K],
+                 [A.WEIGHTS_Q5_0, A.WEIGHTS_Q8_0, A.WEIGHTS_Q4_0]):
+        kq = fmts[0] == A.WEIGHTS_Q5_K
+        ws = [(_kquant_weights if kq else _weights)(f, r, cols, f"q5g/{f}/{i}")
+              for i, (f, r) in enumerate(zip(fmts, rows))]
+        if kq:  # matrix 1: every qh byte 0xFF (every quant's fifth bit set)
+            ws[1].reshape(rows[1], cols // 256, 176)[:, :, 16:48] = 0xFF
+        else:   # matrix 0: every high-bit word 0 (every element offset to -16 + nibble)
+            ws[0].reshape(rows[0], cols // 32, 22)[:, :, 2:6] = 0
+        biases = [synth.normal(11, f"q5g/b{i}", (r,)) for i, r in enumerate(rows)]
+        dws = [rt.DeviceArray.from_host(w) for w in ws]
+        dbs = [rt.DeviceArray.from_host(b) for b in biases]
+        dout = rt.DeviceArray(batch * sum(rows))
+        try:
+            hip.quantized_grouped_matmul_device(fmts, [d.ptr for d in dws], [w.size for w in ws],
+                                                rows, dx.ptr, x.size, dout.ptr, dout.count, batch,
+                                                cols, [d.ptr for d in dbs], A.ADDEND_BIAS)
+            hip.synchronize()
+            got, off = dout.download(), 0
+            for i, (f, r) in enumerate(zip(fmts, rows)):
+                want = (oracle.quantized_matmul(f, ws[i], x, batch, r, cols) + biases[i][None, :])
+                _exact(got[off:off + batch * r].reshape(batch, r), want.astype(np.float32),
+                       f"formats {fmts} matrix {i}")
+                off += batch * r
+            _say(f"grouped {fmts}: bit-exact")
+        finally:
+            for d in dws + dbs + [dout]:
+                d.free()
+    dx.free()
 
 
 def test_non_finite_and_zero_activations_bit_exact(hip):
@@ -339,9 +378,10 @@ def test_graph_replays_equal_eager(hip):
 
 
 def test_rejections(hip):
-    """backend-native's checks (RS:1017-1060) and this ABI's own: unknown or host-only formats,
-    cols not a multiple of 32, short buffers, null pointers, misaligned activations."""
-    w = rt.DeviceArray(18 * 4, np.uint8)
+    """backend-native's checks (RS:1017-1060) and this ABI's own: unknown formats, cols not a
+    multiple of the format's block, short buffers (per format's block size), null pointers,
+    misaligned activations."""
+    w = rt.DeviceArray(22 * 4, np.uint8)
     x = rt.DeviceArray(64)
     out = rt.DeviceArray(64)
     try:
@@ -352,10 +392,12 @@ def test_rejections(hip):
                 xe, out.ptr, oe, batch, rows, cols, add, mode)
         assert call() == A.OK
         hip.synchronize()
-        for fmt in (4, 5, 99):  # Q5_K, Q5_0: no device kernel
+        assert call(fmt=99) == A.INVALID_SHAPE
+        for fmt in (2, 3, 4):  # K-quants need cols a multiple of 256
             assert call(fmt=fmt) == A.INVALID_SHAPE
-        for fmt in (2, 3):  # K-quants need cols a multiple of 256
-            assert call(fmt=fmt) == A.INVALID_SHAPE
+        assert call(fmt=5, wbytes=87) == A.BUFFER_TOO_SMALL  # Q5_0: 2 rows x 2 blocks x 22 bytes
+        assert call(fmt=5, wbytes=88) == A.OK
+        hip.synchronize()
         assert call(cols=48, rows=1) == A.INVALID_SHAPE
         assert call(rows=0) == A.INVALID_SHAPE
         assert call(batch=0) == A.INVALID_SHAPE

@@ -25,15 +25,24 @@ def _quantize_numpy(x, cols):
     return q.reshape(-1), scales
 
 
+_NBYTES = {0: 18, 1: 34, 5: 22}
+
+
 def _dequantize_numpy(fmt, weights, rows, cols):
-    """GGML Q4_0 / Q8_0 blocks -> (per-block f32 scales [rows, blocks], int values [rows, cols])."""
+    """GGML Q4_0 / Q8_0 / Q5_0 blocks -> (per-block f32 scales [rows, blocks], int values
+    [rows, cols])."""
     blocks = cols // 32
-    nbytes = 18 if fmt == 0 else 34
+    nbytes = _NBYTES[fmt]
     w = np.frombuffer(bytes(weights), np.uint8)[:rows * blocks * nbytes].reshape(rows, blocks, nbytes)
     scales = w[:, :, :2].copy().view(np.float16).astype(np.float32).reshape(rows, blocks)
     if fmt == 0:
         nib = w[:, :, 2:].astype(np.int32)
         vals = np.concatenate([(nib & 0xF) - 8, (nib >> 4) - 8], axis=2)  # elements 0-15, 16-31
+    elif fmt == 5:
+        high = w[:, :, 2:6].copy().view("<u4").astype(np.int64)[..., 0]  # bit j: element j's 5th bit
+        bits = (high[..., None] >> np.arange(32)) & 1
+        nib = w[:, :, 6:].astype(np.int32)
+        vals = np.concatenate([nib & 0xF, nib >> 4], axis=2) + 16 * bits - 16
     else:
         vals = w[:, :, 2:].view(np.int8).astype(np.int32)
     return scales, vals.reshape(rows, cols)
@@ -54,7 +63,7 @@ def _float64_matmul(fmt, weights, x, batch, rows, cols):
 
 def _random_weights(fmt, rows, cols, key):
     blocks = cols // 32
-    nbytes = 18 if fmt == 0 else 34
+    nbytes = _NBYTES[fmt]
     raw = synth.uniform_int(7, key, rows * blocks * nbytes, 0, 255).astype(np.uint8)
     raw = raw.reshape(rows, blocks, nbytes)
     scales = (synth.normal(7, key + "/s", (rows, blocks)) * 0.02).astype(np.float16)
@@ -121,7 +130,35 @@ def test_q8_0_one_block_by_hand(oracle):
     assert out[0, 0] == np.float32(127 * (3 - 16) + (-1) * (30 - 16))
 
 
-@pytest.mark.parametrize("fmt", [0, 1])
+def test_q5_0_one_block_by_hand(oracle):
+    # scale 1.0; every nibble 0: elements whose fifth bit is set are 16 - 16 = 0, the others -16
+    x = np.zeros(32, np.float32)
+    x[0], x[5], x[16], x[31] = 127.0, 2.0, 3.0, -4.0  # absmax 127: q == x
+    high = (1 << 5) | (1 << 16)                       # elements 5 and 16 read 0
+    w = bytes([0x00, 0x3C]) + high.to_bytes(4, "little") + bytes(16)
+    out = oracle.quantized_matmul(5, w, x, 1, 1, 32)
+    assert out[0, 0] == np.float32(-16 * (127.0 - 4.0))
+    # nibble 0xF in the low half of byte 3 (element 3) and the high half (element 19), fifth
+    # bits set on both: 31 - 16 = 15 each; every other element -16
+    x2 = np.zeros(32, np.float32)
+    x2[3], x2[19], x2[0] = 2.0, 3.0, 127.0
+    packed = bytearray(16)
+    packed[3] = 0xFF
+    w2 = bytes([0x00, 0x3C]) + ((1 << 3) | (1 << 19)).to_bytes(4, "little") + bytes(packed)
+    out2 = oracle.quantized_matmul(5, w2, x2, 1, 1, 32)
+    assert out2[0, 0] == np.float32(15 * 2.0 + 15 * 3.0 - 16 * 127.0)
+
+
+def test_q5_0_fixture_blocks_dequantize_to_their_logical_values(known_answers):
+    """fillQ5_0Weights records each lane's 5-bit low and high values; numpy's GGML Q5_0
+    dequantization recovers them (before the -16 offset)."""
+    for case in (c for c in known_answers["quantized_matmul"] if c["format"] == 5):
+        w, rows, cols = bytes.fromhex(case["weights_hex"]), case["rows"], case["cols"]
+        _, vals = _dequantize_numpy(5, w, rows, cols)
+        np.testing.assert_array_equal(vals.reshape(-1, 32) + 16, np.array(case["logical"]["quants"]))
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 5])
 def test_quantized_matmul_matches_float64_dequantized(oracle, fmt):
     batch, rows, cols = 3, 40, 512
     w = _random_weights(fmt, rows, cols, f"qm/w{fmt}")
@@ -147,7 +184,7 @@ def test_quantized_matmul_rows_and_batches_are_independent(oracle):
 
 def test_reference_fixtures_against_float64(oracle, known_answers):
     for case in known_answers["quantized_matmul"]:
-        if case["format"] not in (0, 1):
+        if case["format"] not in (0, 1, 5):
             continue  # the K-quant cases: test_kquant_matmul_matches_float64
         w = bytes.fromhex(case["weights_hex"])
         b, r, c = case["batch"], case["rows"], case["cols"]
@@ -205,6 +242,17 @@ def _dequant_q4_k(w, rows, cols):
     return d, dmin, scales, mins, quants
 
 
+def _dequant_q5_k(w, rows, cols):
+    """GGML Q5_K (176-byte blocks of 256): Q4_K's d, dmin and 6-bit scales and mins, qh[32] at
+    byte 16 (bit g of qh[i] is the fifth bit of element i of group g), the nibbles at byte 48."""
+    b = np.frombuffer(bytes(w), np.uint8).reshape(rows, cols // 256, 176)
+    q4 = np.concatenate([b[:, :, :16], b[:, :, 48:]], axis=2).reshape(-1).tobytes()
+    d, dmin, scales, mins, nib = _dequant_q4_k(q4, rows, cols)
+    qh = b[:, :, 16:48].astype(np.int32)
+    fifth = (qh[:, :, None, :] >> np.arange(8)[None, None, :, None]) & 1
+    return d, dmin, scales, mins, nib + 16 * fifth
+
+
 def _dequant_q6_k(w, rows, cols):
     """GGML Q6_K (210-byte blocks of 256): element 128h + 32t + i of half h takes the low nibble
     of ql[64h + i (+32 for t odd)] (high nibble for t >= 2) and bits 2t..2t+1 of qh[32h + i] as
@@ -228,8 +276,8 @@ def _float64_kquant(fmt, w, x, batch, rows, cols):
     nb = cols // 256
     q = q.reshape(batch, nb, 256).astype(np.int64)
     ascale = ascale.reshape(batch, nb)
-    if fmt == 2:
-        d, dmin, scales, mins, quants = _dequant_q4_k(w, rows, cols)
+    if fmt in (2, 4):
+        d, dmin, scales, mins, quants = (_dequant_q4_k if fmt == 2 else _dequant_q5_k)(w, rows, cols)
         dots = np.einsum("rkgj,bkgj->brkg", quants.astype(np.int64), q.reshape(batch, nb, 8, 32))
         qsum = (dots * scales[None]).sum(axis=3)
         gsum = asum.reshape(batch, nb, 8, 2).sum(axis=3).astype(np.int64)
@@ -264,15 +312,15 @@ def test_q8_k_quantize_matches_numpy(oracle):
     assert int(q[256 + 10]) == -127 and int(q[256 + 20]) == 127
 
 
-@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("fmt", [2, 3, 4])
 def test_kquant_fixture_blocks_dequantize_to_their_logical_values(known_answers, fmt):
     """The reference test's block builders record what each element means; numpy's GGML
     dequantization recovers exactly that, which pins the layouts the float64 check below uses."""
     case = next(c for c in known_answers["quantized_matmul"] if c["format"] == fmt)
     w, rows, cols = bytes.fromhex(case["weights_hex"]), case["rows"], case["cols"]
     lg = case["logical"]
-    if fmt == 2:
-        d, dmin, scales, mins, quants = _dequant_q4_k(w, rows, cols)
+    if fmt in (2, 4):
+        d, dmin, scales, mins, quants = (_dequant_q4_k if fmt == 2 else _dequant_q5_k)(w, rows, cols)
         assert (scales == np.array(lg["scales"])).all() and (mins == np.array(lg["mins"])).all()
         np.testing.assert_array_equal(quants.reshape(-1, 256), np.array(lg["quants"]))
         np.testing.assert_array_equal(d[:, 0], (np.arange(rows) + 1) * 0.03125)
@@ -282,7 +330,7 @@ def test_kquant_fixture_blocks_dequantize_to_their_logical_values(known_answers,
         np.testing.assert_array_equal(scales.reshape(-1, 16), np.array(lg["scales"]))
 
 
-@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("fmt", [2, 3, 4])
 def test_kquant_matmul_matches_float64(oracle, known_answers, fmt):
     cases = [c for c in known_answers["quantized_matmul"] if c["format"] == fmt]
     rnd = _random_kquant(fmt, 9, 1024, f"kq/{fmt}")
@@ -295,12 +343,32 @@ def test_kquant_matmul_matches_float64(oracle, known_answers, fmt):
 
 
 def _random_kquant(fmt, rows, cols, key):
-    nbytes = 144 if fmt == 2 else 210
+    nbytes = {2: 144, 3: 210, 4: 176}[fmt]
     raw = synth.uniform_int(7, key, rows * cols // 256 * nbytes, 0, 255).astype(np.uint8)
     raw = raw.reshape(rows, cols // 256, nbytes)
     d = (synth.normal(7, key + "/d", (rows, cols // 256, 2)) * 0.01).astype(np.float16).view(np.uint8)
-    if fmt == 2:
+    if fmt in (2, 4):
         raw[:, :, 0:4] = d.reshape(rows, cols // 256, 4)
     else:
         raw[:, :, 208:210] = d.reshape(rows, cols // 256, 4)[..., :2]
     return raw.reshape(-1).tobytes()
+
+
+def test_q5_k_without_fifth_bits_is_q4_k_and_each_fifth_bit_adds_16(oracle):
+    """A Q5_K block with qh cleared is the Q4_K block of the same d, dmin, scales, mins and
+    nibbles (the same outputs bit for bit); setting every fifth bit of group g adds
+    16 * scale_g * (sum of that group's Q8_K activations) to the block's integer sum, which the
+    float64 reference of the dequantized blocks prices exactly."""
+    rows, cols = 6, 512
+    w5 = np.frombuffer(_random_kquant(4, rows, cols, "q5k/eq"), np.uint8).reshape(rows, 2, 176).copy()
+    w5[:, :, 16:48] = 0
+    w4 = np.concatenate([w5[:, :, :16], w5[:, :, 48:]], axis=2)
+    x = synth.normal(7, "q5k/eq/x", (2, cols))
+    a = oracle.quantized_matmul(4, w5.reshape(-1).tobytes(), x, 2, rows, cols)
+    b = oracle.quantized_matmul(2, w4.reshape(-1).tobytes(), x, 2, rows, cols)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    w5[:, 1, 16:48] = 0x24  # fifth bits of groups 2 and 5 in the second block
+    out = oracle.quantized_matmul(4, w5.reshape(-1).tobytes(), x, 2, rows, cols)
+    ref, mag, n = _float64_kquant(4, w5.reshape(-1).tobytes(), x, 2, rows, cols)
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= n * 2.0 ** -24 * mag + 1e-30)
+    assert not np.array_equal(out, a)
