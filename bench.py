@@ -600,14 +600,15 @@ def run_c5(hip, A, rt, synth, steps: int = 64, warmup: int = 4):
 
 def _gguf_weights(synth, fmt: int, rows: int, cols: int, key: str) -> np.ndarray:
     """Synthetic GGUF blocks: uniform bytes with f16 N(0, 0.02) scales where the format keeps
-    them (Q4_0 / Q8_0 bytes 0-1, Q4_K bytes 0-3, Q6_K bytes 208-209)."""
-    nbytes, elems = {0: (18, 32), 1: (34, 32), 2: (144, 256), 3: (210, 256)}[fmt]
+    them (Q4_0 / Q8_0 / Q5_0 bytes 0-1, Q4_K / Q5_K bytes 0-3, Q6_K bytes 208-209)."""
+    nbytes, elems = {0: (18, 32), 1: (34, 32), 2: (144, 256), 3: (210, 256), 4: (176, 256),
+                     5: (22, 32)}[fmt]
     blocks = cols // elems
     raw = synth.uniform_int(9, key, rows * blocks * nbytes, 0, 255).astype(np.uint8)
     raw = raw.reshape(rows, blocks, nbytes)
     scales = (synth.normal(9, key + "/s", (rows, blocks, 2)) * 0.02).astype(np.float16)
     scales = scales.view(np.uint8).reshape(rows, blocks, 4)
-    if fmt == 2:
+    if fmt in (2, 4):
         raw[:, :, 0:4] = scales
     elif fmt == 3:
         raw[:, :, 208:210] = scales[..., :2]
@@ -619,14 +620,15 @@ def _gguf_weights(synth, fmt: int, rows: int, cols: int, key: str) -> np.ndarray
 def run_proj(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
     """The projections around one C2 layer at decode (batch 1): Llama-3.2-1B's Q (2048 rows), K
     and V (512 rows each) over 2048 inputs as one grouped launch writing q|k|v for the decode,
-    and the output projection (2048 x 2048) with the residual added in place; Q4_0, Q8_0, Q4_K
-    and Q6_K weights. Each launch is repeated `per_graph` times in a graph; HIP events around the replays
+    and the output projection (2048 x 2048) with the residual added in place; Q4_0, Q8_0, Q5_0,
+    Q4_K, Q5_K and Q6_K weights; then C3's grouped Q/K/V projection at its 2048-row prompt. Each
+    launch is repeated `per_graph` times in a graph; HIP events around the replays
     give us per launch; GB/s counts the weight bytes (the activations are 8 KB)."""
     cols, rows = 2048, [2048, 512, 512]
     stream = hip.stream()
     result = {}
-    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0), ("q4_k", A.WEIGHTS_Q4_K),
-                      ("q6_k", A.WEIGHTS_Q6_K)):
+    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0), ("q5_0", A.WEIGHTS_Q5_0),
+                      ("q4_k", A.WEIGHTS_Q4_K), ("q5_k", A.WEIGHTS_Q5_K), ("q6_k", A.WEIGHTS_Q6_K)):
         ws = [_gguf_weights(synth, fmt, r, cols, f"bench/proj/{name}/{i}") for i, r in enumerate(rows)]
         wo = _gguf_weights(synth, fmt, cols, cols, f"bench/proj/{name}/wo")
         dws = [rt.DeviceArray.from_host(w) for w in ws]
@@ -662,6 +664,39 @@ def run_proj(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
                                               gbs=round(nbytes / (ms * 1e-3) / 1e9, 1))
         for d in dws + [dwo, dx, dqkv, dres]:
             d.free()
+    # Prefill-sized: C3's Llama-3.2-3B Q (3072 rows), K and V (1024 each) over 3072 inputs for
+    # the 2048-row prompt, one grouped call (one launch per format), events around 3 replays.
+    cols, rows, batch = 3072, [3072, 1024, 1024], 2048
+    dx = rt.DeviceArray.from_host(synth.normal(9, "bench/proj/xp", (batch, cols)))
+    dqkv = rt.DeviceArray(batch * sum(rows))
+    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0), ("q4_k", A.WEIGHTS_Q4_K)):
+        ws = [_gguf_weights(synth, fmt, r, cols, f"bench/projp/{name}/{i}") for i, r in enumerate(rows)]
+        dws = [rt.DeviceArray.from_host(w) for w in ws]
+
+        def qkv_prefill():
+            hip.quantized_grouped_matmul_device([fmt] * 3, [d.ptr for d in dws], [w.size for w in ws],
+                                                rows, dx.ptr, batch * cols, dqkv.ptr, dqkv.count,
+                                                batch, cols)
+
+        graph = rt.Graph(stream, qkv_prefill)
+        graph.launch()
+        hip.synchronize()
+        e0, e1 = rt.Event(), rt.Event()
+        e0.record(stream)
+        for _ in range(3):
+            graph.launch()
+        e1.record(stream)
+        hip.synchronize()
+        ms = e0.elapsed_ms(e1) / 3
+        graph.destroy()
+        macs = batch * sum(rows) * cols
+        result[f"qkv_prefill2048_{name}"] = dict(
+            us=round(ms * 1e3, 1), weight_bytes=int(sum(w.size for w in ws)),
+            tops=round(2 * macs / (ms * 1e-3) / 1e12, 2))
+        for d in dws:
+            d.free()
+    dx.free()
+    dqkv.free()
     return result
 
 

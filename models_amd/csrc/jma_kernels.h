@@ -170,8 +170,8 @@ hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, 
 constexpr uint32_t kQMaxMatrices = 16;
 
 struct QMatrix {
-  const uint8_t* w;      // GGUF blocks: [rows][cols / 32] of 18 (Q4_0) or 34 (Q8_0) bytes, or
-                         // [rows][cols / 256] of 144 (Q4_K) or 210 (Q6_K) bytes
+  const uint8_t* w;      // GGUF blocks: [rows][cols / 32] of qmat_block_bytes(fmt) bytes (Q4_0,
+                         // Q8_0, Q5_0), or [rows][cols / 256] (Q4_K, Q5_K, Q6_K)
   float* out;            // [batch][rows]
   const float* addend;   // bias [rows] (addend_mode 1) or residual [batch][rows] (2); may be out
   uint32_t rows, tile0;  // tile0: this matrix's first workgroup
@@ -180,14 +180,14 @@ struct QMatrix {
 struct QMatArgs {
   const float* x;  // activations [batch][cols], 16-byte aligned
   uint32_t batch, cols, blocks, rows_per_tile, count, addend_mode;
+  uint32_t chunk;       // activation rows per pass through LDS (plan_qmat)
+  uint32_t group_rows;  // activation rows per workgroup along the grid's y (qmat_group_rows)
   QMatrix m[kQMaxMatrices];
 };
 
-// Dynamic LDS of one workgroup: Q8_0 activations, their scales and sums, and the tile's terms.
-size_t qmatvec_lds_bytes(uint32_t batch, uint32_t cols, uint32_t rows_per_tile);
-size_t qkmatvec_lds_bytes(uint32_t fmt, uint32_t batch, uint32_t cols, uint32_t rows_per_tile);
-// fmt: 0 = Q4_0, 1 = Q8_0 (blocks = cols / 32), 2 = Q4_K, 3 = Q6_K (blocks = cols / 256), every
-// matrix of the launch. tiles = sum of ceil(rows / rows_per_tile).
+// fmt: backend-native's code (qmat_kquant: blocks = cols / 256, else cols / 32), every matrix of
+// the launch. tiles = sum of ceil(rows / rows_per_tile); the grid is tiles x ceil(batch /
+// group_rows).
 hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream);
 
 }  // namespace jma

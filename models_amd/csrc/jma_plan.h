@@ -1,6 +1,7 @@
 // Decode launch planning and the index formulas of the decode split exchange, shared by the host
 // runtime (jma_runtime.cpp), the kernels (jma_kernels.hip) and a CPU bounds check
-// (tests/plan_check.cpp). Plain C++: no HIP types, so it also builds with g++ alone.
+// (tests/plan_check.cpp); and the launch planning of the quantized projections (jma_quant.hip,
+// checked by tests/qmat_check.cpp). Plain C++: no HIP types, so it also builds with g++ alone.
 #pragma once
 
 #include <stdint.h>
@@ -206,6 +207,80 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
     p.counter_bytes = (uint64_t)count * hkv * p.hgroups * 4;
   }
   return p;
+}
+
+// ---------------------------------------------------------------- quantized projections
+//
+// Launch planning of the block-quantized projections (jma_quant.hip), shared by the runtime and a
+// CPU bounds check (tests/qmat_check.cpp). A launch serves every matrix of one weight format:
+// workgroup (x, y) takes rows_per_tile rows of one matrix (tiles in matrix order) and the
+// activation rows y * group_rows .. + group_rows - 1, which pass through its LDS chunk rows at a
+// time while the tile's weight blocks stay in its registers or caches.
+
+// backend-native's weight codes (RS:150-161): 0 Q4_0, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q5_K, 5 Q5_0.
+JMA_HD bool qmat_kquant(uint32_t fmt) { return fmt == 2 || fmt == 3 || fmt == 4; }
+JMA_HD uint32_t qmat_block_elems(uint32_t fmt) { return qmat_kquant(fmt) ? 256u : 32u; }
+// GGUF block bytes (RS:87-92).
+JMA_HD uint32_t qmat_block_bytes(uint32_t fmt) {
+  return fmt == 0 ? 18u : fmt == 1 ? 34u : fmt == 2 ? 144u : fmt == 3 ? 210u : fmt == 4 ? 176u : 22u;
+}
+
+// Dynamic LDS of one workgroup for `chunk` activation rows: Q8_0 activations, their scales and
+// block sums, then the tile's (scale product, integer dot) terms per (activation row, tile row).
+JMA_HD uint64_t qmatvec_lds_bytes(uint32_t chunk, uint32_t cols, uint32_t rows_per_tile) {
+  const uint64_t K = cols / 32u;
+  return ((uint64_t)chunk * cols + 15u) / 16u * 16u + (uint64_t)chunk * K * 8u +
+         2u * (uint64_t)chunk * rows_per_tile * (K + 1u) * 4u;
+}
+// K-quants: Q8_K activations, scales and 16-element sums, then 4 (Q4_K, Q5_K) or 9 (Q6_K)
+// floats per (activation row, tile row, 256-block).
+JMA_HD uint64_t qkmatvec_lds_bytes(uint32_t fmt, uint32_t chunk, uint32_t cols, uint32_t rows_per_tile) {
+  const uint64_t KB = cols / 256u, nt = fmt == 3 ? 9u : 4u;
+  return ((uint64_t)chunk * cols + 15u) / 16u * 16u + (uint64_t)chunk * KB * 4u +
+         (uint64_t)chunk * (cols / 16u) * 4u + (uint64_t)chunk * rows_per_tile * (KB * nt + 1u) * 4u;
+}
+
+constexpr uint64_t kQMatLds = 64u * 1024u;   // dynamic LDS a projection workgroup may take
+constexpr uint32_t kQMatMaxChunk = 8;        // activation rows per pass
+constexpr uint32_t kQMatTargetBlocks = 1024;  // workgroups a projection launch aims for
+
+struct QMatPlan {
+  uint32_t rows_per_tile = 0, chunk = 0;  // 0: cols too large for one workgroup's LDS
+};
+
+// Rows per tile (up to 512 (row, block) terms for the 32-element formats, two per thread; 64 for
+// the K-quants, eight threads each) and activation rows per pass, the largest that keep every
+// format of the call within kQMatLds.
+inline QMatPlan plan_qmat(const uint32_t* formats, uint32_t count, uint32_t cols) {
+  QMatPlan p;
+  if (count == 0) return p;
+  const bool kq = qmat_kquant(formats[0]);
+  const uint32_t K = cols / qmat_block_elems(formats[0]);
+  if (K == 0) return p;
+  auto lds = [&](uint32_t chunk, uint32_t tile) {
+    uint64_t m = 0;
+    for (uint32_t i = 0; i < count; ++i)
+      m = std::max(m, kq ? qkmatvec_lds_bytes(formats[i], chunk, cols, tile)
+                         : qmatvec_lds_bytes(chunk, cols, tile));
+    return m;
+  };
+  uint32_t tile = std::max<uint32_t>(1u, std::min<uint32_t>(64u, (kq ? 64u : 512u) / K));
+  while (tile > 1 && lds(1, tile) > kQMatLds) tile /= 2;
+  if (lds(1, tile) > kQMatLds) return p;
+  uint32_t chunk = kQMatMaxChunk;
+  while (chunk > 1 && lds(chunk, tile) > kQMatLds) --chunk;
+  p.rows_per_tile = tile;
+  p.chunk = chunk;
+  return p;
+}
+
+// Activation rows per workgroup of a launch with `tiles` weight tiles: whole passes, as few as
+// keep the launch near kQMatTargetBlocks workgroups (one pass each at decode batches).
+JMA_HD uint32_t qmat_group_rows(uint32_t batch, uint32_t chunk, uint32_t tiles) {
+  const uint64_t passes = (batch + chunk - 1) / chunk;
+  uint64_t per = (passes * tiles + kQMatTargetBlocks - 1) / kQMatTargetBlocks;
+  per = per < 1 ? 1 : (per > passes ? passes : per);
+  return (uint32_t)(per * chunk);
 }
 
 }  // namespace jma

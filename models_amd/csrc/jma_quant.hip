@@ -100,12 +100,14 @@ struct QBlock {
 template <int FMT>
 __global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char q_lds[];
-  const uint32_t nb = a.batch, cols = a.cols, K = a.blocks, R = a.rows_per_tile, Kp = K + 1;
-  int8_t* act_q = (int8_t*)q_lds;                                   // [nb][cols]
-  float* act_scale = (float*)(q_lds + ((nb * cols + 15u) & ~15u));  // [nb][K]
-  int* act_sum = (int*)(act_scale + nb * K);                        // [nb][K]
-  float* t_scale = (float*)(act_sum + nb * K);                      // [nb][R][Kp]
-  float* t_dot = t_scale + nb * R * Kp;                             // [nb][R][Kp]
+  // LDS holds one pass of nc activation rows; the workgroup's rows (blockIdx.y's group) pass
+  // through it in turn while the weight tile stays in registers.
+  const uint32_t nc = a.chunk, cols = a.cols, K = a.blocks, R = a.rows_per_tile, Kp = K + 1;
+  int8_t* act_q = (int8_t*)q_lds;                                   // [nc][cols]
+  float* act_scale = (float*)(q_lds + ((nc * cols + 15u) & ~15u));  // [nc][K]
+  int* act_sum = (int*)(act_scale + nc * K);                        // [nc][K]
+  float* t_scale = (float*)(act_sum + nc * K);                      // [nc][R][Kp]
+  float* t_dot = t_scale + nc * R * Kp;                             // [nc][R][Kp]
 
   uint32_t mi = 0;
   for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
@@ -120,93 +122,99 @@ __global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
   const uint16_t* wrec = (const uint16_t*)(w + (uint64_t)r0 * K * (2u * kRecHalves));
   const uint32_t tid = threadIdx.x;
 
-  // A thread's first kU units (every unit of a tile of up to 1024 terms) are in flight while the
-  // activations are quantized.
+  // A thread's first kU units (every unit of a tile of up to 1024 terms) are loaded once, in
+  // flight while the first activations are quantized, and serve every pass.
   constexpr uint32_t kU = 4;
   QBlock<FMT> unit[kU];
 #pragma unroll
   for (uint32_t i = 0; i < kU; ++i)
     if (tid + i * kQThreads < nunits) unit[i].load(wrec + (uint64_t)(tid + i * kQThreads) * kRecHalves);
 
-  // Q8_0 activations: four threads per 32-element block, eight elements each.
-  for (uint32_t t = tid; t < nb * K * 4u; t += kQThreads) {
-    const uint32_t b = t / (K * 4u), rem = t % (K * 4u), blk = rem >> 2, qtr = rem & 3u;
-    const float* xs = a.x + (uint64_t)b * cols + blk * 32u + qtr * 8u;
-    const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
-    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    float am = 0.0f;
+  const uint32_t g0 = blockIdx.y * a.group_rows, g1 = min(a.batch, g0 + a.group_rows);
+  for (uint32_t b0 = g0; b0 < g1; b0 += nc) {
+    const uint32_t nb = min(nc, g1 - b0);
+    const float* xb = a.x + (uint64_t)b0 * cols;
+    // Q8_0 activations: four threads per 32-element block, eight elements each.
+    for (uint32_t t = tid; t < nb * K * 4u; t += kQThreads) {
+      const uint32_t b = t / (K * 4u), rem = t % (K * 4u), blk = rem >> 2, qtr = rem & 3u;
+      const float* xs = xb + (uint64_t)b * cols + blk * 32u + qtr * 8u;
+      const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      float am = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(xv[i]));  // a NaN element is skipped
-    am = fmaxf(am, __int_as_float(dpp_int<kQuadXor1>(__float_as_int(am))));
-    am = fmaxf(am, __int_as_float(dpp_int<kQuadXor2>(__float_as_int(am))));
-    const float inverse = am == 0.0f ? 0.0f : 127.0f / am;
-    uint32_t packed[2] = {0u, 0u};
-    int s = 0;
+      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(xv[i]));  // a NaN element is skipped
+      am = fmaxf(am, __int_as_float(dpp_int<kQuadXor1>(__float_as_int(am))));
+      am = fmaxf(am, __int_as_float(dpp_int<kQuadXor2>(__float_as_int(am))));
+      const float inverse = am == 0.0f ? 0.0f : 127.0f / am;
+      uint32_t packed[2] = {0u, 0u};
+      int s = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float scaled;
-      {
+      for (int i = 0; i < 8; ++i) {
+        float scaled;
+        {
 #pragma clang fp contract(off)
-        scaled = xv[i] * inverse;
+          scaled = xv[i] * inverse;
+        }
+        const int q = nearest_int(scaled);
+        s += (int)(int8_t)q;
+        packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
       }
-      const int q = nearest_int(scaled);
-      s += (int)(int8_t)q;
-      packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+      *(uint2*)(act_q + (uint64_t)b * cols + blk * 32u + qtr * 8u) = make_uint2(packed[0], packed[1]);
+      s += dpp_int<kQuadXor1>(s);
+      s += dpp_int<kQuadXor2>(s);
+      if (qtr == 0) {
+        act_scale[b * K + blk] = (float)(_Float16)(am / 127.0f);
+        act_sum[b * K + blk] = s;
+      }
     }
-    *(uint2*)(act_q + (uint64_t)b * cols + blk * 32u + qtr * 8u) = make_uint2(packed[0], packed[1]);
-    s += dpp_int<kQuadXor1>(s);
-    s += dpp_int<kQuadXor2>(s);
-    if (qtr == 0) {
-      act_scale[b * K + blk] = (float)(_Float16)(am / 127.0f);
-      act_sum[b * K + blk] = s;
-    }
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // Every (row, block) term of the tile: the scale product and the integer dot, per activation
-  // row. Tiles of more than kU * 256 terms (rows over 32768 inputs) load further units in turn.
-  auto terms = [&](const QBlock<FMT>& wb, uint32_t u) {
-    const uint32_t row = u / K, blk = u % K;
-    const float wscale = f16_bits_to_float(wb.h[0]);
-    for (uint32_t b = 0; b < nb; ++b) {
-      const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 32u);
-      const int d = wb.dot(aq, act_sum[b * K + blk]);
-      const uint32_t at = (b * R + row) * Kp + blk;
-      t_scale[at] = wscale * act_scale[b * K + blk];
-      t_dot[at] = (float)d;
-    }
-  };
+    // Every (row, block) term of the tile: the scale product and the integer dot, per activation
+    // row. Tiles of more than kU * 256 terms (rows over 32768 inputs) load further units in turn.
+    auto terms = [&](const QBlock<FMT>& wb, uint32_t u) {
+      const uint32_t row = u / K, blk = u % K;
+      const float wscale = f16_bits_to_float(wb.h[0]);
+      for (uint32_t b = 0; b < nb; ++b) {
+        const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 32u);
+        const int d = wb.dot(aq, act_sum[b * K + blk]);
+        const uint32_t at = (b * R + row) * Kp + blk;
+        t_scale[at] = wscale * act_scale[b * K + blk];
+        t_dot[at] = (float)d;
+      }
+    };
 #pragma unroll
-  for (uint32_t i = 0; i < kU; ++i)
-    if (tid + i * kQThreads < nunits) terms(unit[i], tid + i * kQThreads);
-  for (uint32_t u = tid + kU * kQThreads; u < nunits; u += kQThreads) {
-    QBlock<FMT> wb;
-    wb.load(wrec + (uint64_t)u * kRecHalves);
-    terms(wb, u);
-  }
-  __syncthreads();
+    for (uint32_t i = 0; i < kU; ++i)
+      if (tid + i * kQThreads < nunits) terms(unit[i], tid + i * kQThreads);
+    for (uint32_t u = tid + kU * kQThreads; u < nunits; u += kQThreads) {
+      QBlock<FMT> wb;
+      wb.load(wrec + (uint64_t)u * kRecHalves);
+      terms(wb, u);
+    }
+    __syncthreads();
 
-  // One thread per (activation row, output row): sum = fma(scale, dot, sum) over the blocks in
-  // order, then the optional bias or residual (one float add, as addOptionalBias and the
-  // residual loop do).
-  for (uint32_t t = tid; t < nb * nrows; t += kQThreads) {
-    const uint32_t b = t / nrows, row = t % nrows;
-    const float* ps = t_scale + (b * R + row) * Kp;
-    const float* pd = t_dot + (b * R + row) * Kp;
-    float sum = 0.0f;
-    uint32_t blk = 0;
-    for (; blk + 8 <= K; blk += 8) {  // the LDS reads of eight steps ahead of their fma chain
-      float sc[8], dt[8];
+    // One thread per (activation row, output row): sum = fma(scale, dot, sum) over the blocks in
+    // order, then the optional bias or residual (one float add, as addOptionalBias and the
+    // residual loop do).
+    for (uint32_t t = tid; t < nb * nrows; t += kQThreads) {
+      const uint32_t b = t / nrows, row = t % nrows;
+      const float* ps = t_scale + (b * R + row) * Kp;
+      const float* pd = t_dot + (b * R + row) * Kp;
+      float sum = 0.0f;
+      uint32_t blk = 0;
+      for (; blk + 8 <= K; blk += 8) {  // the LDS reads of eight steps ahead of their fma chain
+        float sc[8], dt[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sc[i] = ps[blk + i], dt[i] = pd[blk + i];
+        for (int i = 0; i < 8; ++i) sc[i] = ps[blk + i], dt[i] = pd[blk + i];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum = __builtin_fmaf(sc[i], dt[i], sum);
+        for (int i = 0; i < 8; ++i) sum = __builtin_fmaf(sc[i], dt[i], sum);
+      }
+      for (; blk < K; ++blk) sum = __builtin_fmaf(ps[blk], pd[blk], sum);
+      const uint32_t r = r0 + row;
+      const uint64_t o = (uint64_t)(b0 + b) * rows + r;
+      if (a.addend_mode == 1) sum = sum + addend[r];
+      else if (a.addend_mode == 2) sum = sum + addend[o];
+      out[o] = sum;
     }
-    for (; blk < K; ++blk) sum = __builtin_fmaf(ps[blk], pd[blk], sum);
-    const uint32_t r = r0 + row;
-    if (a.addend_mode == 1) sum = sum + addend[r];
-    else if (a.addend_mode == 2) sum = sum + addend[(uint64_t)b * rows + r];
-    out[(uint64_t)b * rows + r] = sum;
   }
 }
 
@@ -227,12 +235,14 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
   constexpr uint32_t kNT = kQ45 ? 4u : 9u;             // floats per (row, block) term
   constexpr uint32_t kBlockBytes = FMT == 2 ? 144u : FMT == 4 ? 176u : 210u;
   extern __shared__ __attribute__((aligned(16))) unsigned char q_lds[];
-  const uint32_t nb = a.batch, cols = a.cols, KB = a.blocks, R = a.rows_per_tile;
+  // One pass of nc activation rows in LDS at a time (qmatvec_kernel); the tile's weight blocks
+  // come from memory in the first pass and from the caches in later ones.
+  const uint32_t nc = a.chunk, cols = a.cols, KB = a.blocks, R = a.rows_per_tile;
   const uint32_t rs = KB * kNT + 1;  // floats per (activation row, output row) of terms
-  int8_t* act_q = (int8_t*)q_lds;                                   // [nb][cols]
-  float* act_scale = (float*)(q_lds + ((nb * cols + 15u) & ~15u));  // [nb][KB]
-  int* act_sum = (int*)(act_scale + nb * KB);                       // [nb][cols / 16]
-  float* terms = (float*)(act_sum + nb * (cols / 16u));             // [nb][R][rs]
+  int8_t* act_q = (int8_t*)q_lds;                                   // [nc][cols]
+  float* act_scale = (float*)(q_lds + ((nc * cols + 15u) & ~15u));  // [nc][KB]
+  int* act_sum = (int*)(act_scale + nc * KB);                       // [nc][cols / 16]
+  float* terms = (float*)(act_sum + nc * (cols / 16u));             // [nc][R][rs]
 
   uint32_t mi = 0;
   for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
@@ -246,207 +256,202 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
   const uint8_t* wtile = w + (uint64_t)r0 * KB * kBlockBytes;
   const uint32_t tid = threadIdx.x, sub = tid & 7u;
 
-  // Q8_K activations: 32 threads per block, eight consecutive elements each.
-  for (uint32_t t = tid; t < nb * KB * 32u; t += kQThreads) {
-    const uint32_t b = t / (KB * 32u), blk = (t / 32u) % KB, part = t & 31u;
-    const float* xs = a.x + (uint64_t)b * cols + blk * 256u + part * 8u;
-    const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
-    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    float best = 0.0f, bval = 0.0f;
-    uint32_t bidx = 0xFFFFFFFFu;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float m = fabsf(xv[i]);
-      if (m > best) {  // strict: the first of equal magnitudes; a NaN compares false
-        best = m;
-        bval = xv[i];
-        bidx = part * 8u + i;
-      }
-    }
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-      const float ob = __shfl_xor(best, o, 32), ov = __shfl_xor(bval, o, 32);
-      const uint32_t oi = __shfl_xor(bidx, o, 32);
-      if (ob > best || (ob == best && oi < bidx)) {
-        best = ob;
-        bval = ov;
-        bidx = oi;
-      }
-    }
-    int8_t* qd = act_q + (uint64_t)b * cols + blk * 256u + part * 8u;
-    int s = 0;
-    if (best == 0.0f) {
-      *(uint2*)qd = make_uint2(0u, 0u);
-    } else {
-      const float inverse = -127.0f / bval;
-      uint32_t packed[2] = {0u, 0u};
+  const uint32_t g0 = blockIdx.y * a.group_rows, g1 = min(a.batch, g0 + a.group_rows);
+  for (uint32_t b0 = g0; b0 < g1; b0 += nc) {
+    const uint32_t nb = min(nc, g1 - b0);
+    const float* xb = a.x + (uint64_t)b0 * cols;
+    // Q8_K activations: 32 threads per block, eight consecutive elements each.
+    for (uint32_t t = tid; t < nb * KB * 32u; t += kQThreads) {
+      const uint32_t b = t / (KB * 32u), blk = (t / 32u) % KB, part = t & 31u;
+      const float* xs = xb + (uint64_t)b * cols + blk * 256u + part * 8u;
+      const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      float best = 0.0f, bval = 0.0f;
+      uint32_t bidx = 0xFFFFFFFFu;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float scaled;
-        {
-#pragma clang fp contract(off)
-          scaled = inverse * xv[i];
+        const float m = fabsf(xv[i]);
+        if (m > best) {  // strict: the first of equal magnitudes; a NaN compares false
+          best = m;
+          bval = xv[i];
+          bidx = part * 8u + i;
         }
-        const int q = min(nearest_int(scaled), 127);
-        s += (int)(int8_t)q;
-        packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
       }
-      *(uint2*)qd = make_uint2(packed[0], packed[1]);
-    }
-    s += __shfl_xor(s, 1, 32);  // two threads make one 16-element sum
-    if ((part & 1u) == 0) act_sum[b * (cols / 16u) + blk * 16u + part / 2u] = s;
-    if (part == 0) act_scale[b * KB + blk] = best == 0.0f ? 0.0f : 1.0f / (-127.0f / bval);
-  }
-  __syncthreads();
-
-  // Terms: eight threads per (row, block); every thread of a unit runs the same batch loop.
-  for (uint32_t t = tid; t < ((nunits * 8u + 63u) & ~63u); t += kQThreads) {
-    const uint32_t u = min(t / 8u, nunits - 1u);  // the last wave's spare lanes repeat a unit
-    const bool real = t / 8u < nunits;
-    const uint32_t row = u / KB, blk = u % KB;
-    const uint8_t* wb = wtile + (uint64_t)u * kBlockBytes;
-    if constexpr (kQ45) {
-      const uint16_t* h = (const uint16_t*)wb;
-      const float wd = f16_bits_to_float(h[0]), wdmin = f16_bits_to_float(h[1]);
-      uint32_t scb[12];
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        const uint32_t x = h[2 + i];
-        scb[2 * i] = x & 0xFFu;
-        scb[2 * i + 1] = x >> 8;
+      for (int o = 1; o < 32; o <<= 1) {
+        const float ob = __shfl_xor(best, o, 32), ov = __shfl_xor(bval, o, 32);
+        const uint32_t oi = __shfl_xor(bidx, o, 32);
+        if (ob > best || (ob == best && oi < bidx)) {
+          best = ob;
+          bval = ov;
+          bidx = oi;
+        }
       }
-      const uint32_t g = sub;
-      const int sc = g < 4 ? (int)(scb[g] & 63u) : (int)((scb[g + 4] & 15u) | ((scb[g - 4] >> 6) << 4));
-      const int mn = g < 4 ? (int)(scb[g + 4] & 63u) : (int)((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4));
-      // The group's 32 quants as 8 words of 4 bytes: nibbles (Q5_K: plus bit g of each qh byte
-      // as the byte's bit 4).
-      uint32_t nib[8];
-      const uint16_t* qn16 = h + (FMT == 4 ? 24 : 8) + (g >> 1) * 16;
-      const uint32_t shift = (g & 1u) * 4u;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        nib[i] = (((uint32_t)qn16[2 * i] | ((uint32_t)qn16[2 * i + 1] << 16)) >> shift) & 0x0F0F0F0Fu;
-      if constexpr (FMT == 4) {
+      int8_t* qd = act_q + (uint64_t)b * cols + blk * 256u + part * 8u;
+      int s = 0;
+      if (best == 0.0f) {
+        *(uint2*)qd = make_uint2(0u, 0u);
+      } else {
+        const float inverse = -127.0f / bval;
+        uint32_t packed[2] = {0u, 0u};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const uint32_t qh = (uint32_t)h[8 + 2 * i] | ((uint32_t)h[9 + 2 * i] << 16);
-          nib[i] |= ((qh >> g) & 0x01010101u) << 4;
+          float scaled;
+          {
+#pragma clang fp contract(off)
+            scaled = inverse * xv[i];
+          }
+          const int q = min(nearest_int(scaled), 127);
+          s += (int)(int8_t)q;
+          packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
         }
+        *(uint2*)qd = make_uint2(packed[0], packed[1]);
       }
-      for (uint32_t b = 0; b < nb; ++b) {
-        const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 256u + g * 32u);
-        int dot = 0;
+      s += __shfl_xor(s, 1, 32);  // two threads make one 16-element sum
+      if ((part & 1u) == 0) act_sum[b * (cols / 16u) + blk * 16u + part / 2u] = s;
+      if (part == 0) act_scale[b * KB + blk] = best == 0.0f ? 0.0f : 1.0f / (-127.0f / bval);
+    }
+    __syncthreads();
+
+    // Terms: eight threads per (row, block); every thread of a unit runs the same batch loop.
+    for (uint32_t t = tid; t < ((nunits * 8u + 63u) & ~63u); t += kQThreads) {
+      const uint32_t u = min(t / 8u, nunits - 1u);  // the last wave's spare lanes repeat a unit
+      const bool real = t / 8u < nunits;
+      const uint32_t row = u / KB, blk = u % KB;
+      const uint8_t* wb = wtile + (uint64_t)u * kBlockBytes;
+      if constexpr (kQ45) {
+        const uint16_t* h = (const uint16_t*)wb;
+        const float wd = f16_bits_to_float(h[0]), wdmin = f16_bits_to_float(h[1]);
+        uint32_t scb[12];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dot = __builtin_amdgcn_sdot4((int)nib[i], aq[i], dot, false);
-        const int* s16 = act_sum + b * (cols / 16u) + blk * 16u;
-        int qs = sc * dot, ms = mn * (s16[2 * g] + s16[2 * g + 1]);
-        qs += __shfl_xor(qs, 1, 8);
-        qs += __shfl_xor(qs, 2, 8);
-        qs += __shfl_xor(qs, 4, 8);
-        ms += __shfl_xor(ms, 1, 8);
-        ms += __shfl_xor(ms, 2, 8);
-        ms += __shfl_xor(ms, 4, 8);
-        if (real && sub == 0) {
-          const float as = act_scale[b * KB + blk];
-          float* tt = terms + (b * R + row) * rs + blk * kNT;
-          tt[0] = wd * as;
-          tt[1] = (float)qs;
-          tt[2] = -(wdmin * as);
-          tt[3] = (float)ms;
+        for (int i = 0; i < 6; ++i) {
+          const uint32_t x = h[2 + i];
+          scb[2 * i] = x & 0xFFu;
+          scb[2 * i + 1] = x >> 8;
         }
-      }
-    } else {
-      // Lane class l = sub: elements i, i + 8, i + 16, i + 24 of each 32-run, both halves, all
-      // four quarters (ql low / high nibble, qh bit pairs), each times its int8 group scale.
-      const int8_t* sc = (const int8_t*)(wb + 192);
-      const float wd = (float)__builtin_bit_cast(_Float16, (uint16_t)(wb[208] | (wb[209] << 8)));
-      int ql1[8], ql2[8], qhh[8];
+        const uint32_t g = sub;
+        const int sc = g < 4 ? (int)(scb[g] & 63u) : (int)((scb[g + 4] & 15u) | ((scb[g - 4] >> 6) << 4));
+        const int mn = g < 4 ? (int)(scb[g + 4] & 63u) : (int)((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4));
+        // The group's 32 quants as 8 words of 4 bytes: nibbles (Q5_K: plus bit g of each qh byte
+        // as the byte's bit 4).
+        uint32_t nib[8];
+        const uint16_t* qn16 = h + (FMT == 4 ? 24 : 8) + (g >> 1) * 16;
+        const uint32_t shift = (g & 1u) * 4u;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t hf = k >> 2, i = sub + 8u * (k & 3);
-        ql1[k] = wb[hf * 64u + i];
-        ql2[k] = wb[hf * 64u + 32u + i];
-        qhh[k] = wb[128u + hf * 32u + i];
-      }
-      for (uint32_t b = 0; b < nb; ++b) {
-        const int8_t* aq = act_q + (uint64_t)b * cols + blk * 256u;
-        int acc = 0;
+        for (int i = 0; i < 8; ++i)
+          nib[i] = (((uint32_t)qn16[2 * i] | ((uint32_t)qn16[2 * i + 1] << 16)) >> shift) & 0x0F0F0F0Fu;
+        if constexpr (FMT == 4) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t qh = (uint32_t)h[8 + 2 * i] | ((uint32_t)h[9 + 2 * i] << 16);
+            nib[i] |= ((qh >> g) & 0x01010101u) << 4;
+          }
+        }
+        for (uint32_t b = 0; b < nb; ++b) {
+          const int* aq = (const int*)(act_q + (uint64_t)b * cols + blk * 256u + g * 32u);
+          int dot = 0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dot = __builtin_amdgcn_sdot4((int)nib[i], aq[i], dot, false);
+          const int* s16 = act_sum + b * (cols / 16u) + blk * 16u;
+          int qs = sc * dot, ms = mn * (s16[2 * g] + s16[2 * g + 1]);
+          qs += __shfl_xor(qs, 1, 8);
+          qs += __shfl_xor(qs, 2, 8);
+          qs += __shfl_xor(qs, 4, 8);
+          ms += __shfl_xor(ms, 1, 8);
+          ms += __shfl_xor(ms, 2, 8);
+          ms += __shfl_xor(ms, 4, 8);
+          if (real && sub == 0) {
+            const float as = act_scale[b * KB + blk];
+            float* tt = terms + (b * R + row) * rs + blk * kNT;
+            tt[0] = wd * as;
+            tt[1] = (float)qs;
+            tt[2] = -(wdmin * as);
+            tt[3] = (float)ms;
+          }
+        }
+      } else {
+        // Lane class l = sub: elements i, i + 8, i + 16, i + 24 of each 32-run, both halves, all
+        // four quarters (ql low / high nibble, qh bit pairs), each times its int8 group scale.
+        const int8_t* sc = (const int8_t*)(wb + 192);
+        const float wd = (float)__builtin_bit_cast(_Float16, (uint16_t)(wb[208] | (wb[209] << 8)));
+        int ql1[8], ql2[8], qhh[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const uint32_t hf = k >> 2, i = sub + 8u * (k & 3), si = i / 16u;
-          const int q1 = ((ql1[k] & 15) | ((qhh[k] & 3) << 4)) - 32;
-          const int q2 = ((ql2[k] & 15) | (((qhh[k] >> 2) & 3) << 4)) - 32;
-          const int q3 = ((ql1[k] >> 4) | (((qhh[k] >> 4) & 3) << 4)) - 32;
-          const int q4 = ((ql2[k] >> 4) | (((qhh[k] >> 6) & 3) << 4)) - 32;
-          const int8_t* aa = aq + hf * 128u;
-          acc += sc[hf * 8u + si] * q1 * aa[i];
-          acc += sc[hf * 8u + si + 2u] * q2 * aa[i + 32u];
-          acc += sc[hf * 8u + si + 4u] * q3 * aa[i + 64u];
-          acc += sc[hf * 8u + si + 6u] * q4 * aa[i + 96u];
+          const uint32_t hf = k >> 2, i = sub + 8u * (k & 3);
+          ql1[k] = wb[hf * 64u + i];
+          ql2[k] = wb[hf * 64u + 32u + i];
+          qhh[k] = wb[128u + hf * 32u + i];
         }
-        if (real) {
-          float* tt = terms + (b * R + row) * rs + blk * kNT;
-          if (sub == 0) tt[0] = wd * act_scale[b * KB + blk];
-          tt[1 + sub] = (float)acc;
+        for (uint32_t b = 0; b < nb; ++b) {
+          const int8_t* aq = act_q + (uint64_t)b * cols + blk * 256u;
+          int acc = 0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const uint32_t hf = k >> 2, i = sub + 8u * (k & 3), si = i / 16u;
+            const int q1 = ((ql1[k] & 15) | ((qhh[k] & 3) << 4)) - 32;
+            const int q2 = ((ql2[k] & 15) | (((qhh[k] >> 2) & 3) << 4)) - 32;
+            const int q3 = ((ql1[k] >> 4) | (((qhh[k] >> 4) & 3) << 4)) - 32;
+            const int q4 = ((ql2[k] >> 4) | (((qhh[k] >> 6) & 3) << 4)) - 32;
+            const int8_t* aa = aq + hf * 128u;
+            acc += sc[hf * 8u + si] * q1 * aa[i];
+            acc += sc[hf * 8u + si + 2u] * q2 * aa[i + 32u];
+            acc += sc[hf * 8u + si + 4u] * q3 * aa[i + 64u];
+            acc += sc[hf * 8u + si + 6u] * q4 * aa[i + 96u];
+          }
+          if (real) {
+            float* tt = terms + (b * R + row) * rs + blk * kNT;
+            if (sub == 0) tt[0] = wd * act_scale[b * KB + blk];
+            tt[1 + sub] = (float)acc;
+          }
         }
       }
     }
-  }
-  __syncthreads();
+    __syncthreads();
 
-  for (uint32_t t = tid; t < nb * nrows; t += kQThreads) {
-    const uint32_t b = t / nrows, row = t % nrows;
-    const float* tt = terms + (b * R + row) * rs;
-    float sum = 0.0f;
-    if constexpr (kQ45) {
-      for (uint32_t blk = 0; blk < KB; ++blk) {
-        sum = __builtin_fmaf(tt[blk * 4], tt[blk * 4 + 1], sum);
-        sum = __builtin_fmaf(tt[blk * 4 + 2], tt[blk * 4 + 3], sum);
+    for (uint32_t t = tid; t < nb * nrows; t += kQThreads) {
+      const uint32_t b = t / nrows, row = t % nrows;
+      const float* tt = terms + (b * R + row) * rs;
+      float sum = 0.0f;
+      if constexpr (kQ45) {
+        for (uint32_t blk = 0; blk < KB; ++blk) {
+          sum = __builtin_fmaf(tt[blk * 4], tt[blk * 4 + 1], sum);
+          sum = __builtin_fmaf(tt[blk * 4 + 2], tt[blk * 4 + 3], sum);
+        }
+      } else {
+        float ls[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (uint32_t blk = 0; blk < KB; ++blk)
+#pragma unroll
+          for (int l = 0; l < 8; ++l) ls[l] = __builtin_fmaf(tt[blk * 9], tt[blk * 9 + 1 + l], ls[l]);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) sum = sum + ls[l];
       }
-    } else {
-      float ls[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (uint32_t blk = 0; blk < KB; ++blk)
-#pragma unroll
-        for (int l = 0; l < 8; ++l) ls[l] = __builtin_fmaf(tt[blk * 9], tt[blk * 9 + 1 + l], ls[l]);
-#pragma unroll
-      for (int l = 0; l < 8; ++l) sum = sum + ls[l];
+      const uint32_t r = r0 + row;
+      const uint64_t o = (uint64_t)(b0 + b) * rows + r;
+      if (a.addend_mode == 1) sum = sum + addend[r];
+      else if (a.addend_mode == 2) sum = sum + addend[o];
+      out[o] = sum;
     }
-    const uint32_t r = r0 + row;
-    if (a.addend_mode == 1) sum = sum + addend[r];
-    else if (a.addend_mode == 2) sum = sum + addend[(uint64_t)b * rows + r];
-    out[(uint64_t)b * rows + r] = sum;
   }
-}
-
-size_t qkmatvec_lds_bytes(uint32_t fmt, uint32_t batch, uint32_t cols, uint32_t rows_per_tile) {
-  const uint32_t KB = cols / 256u, nt = fmt == 3 ? 9u : 4u;
-  return ((size_t)batch * cols + 15u) / 16u * 16u + (size_t)batch * KB * 4u +
-         (size_t)batch * (cols / 16u) * 4u + (size_t)batch * rows_per_tile * (KB * nt + 1u) * 4u;
-}
-
-size_t qmatvec_lds_bytes(uint32_t batch, uint32_t cols, uint32_t rows_per_tile) {
-  const uint32_t K = cols / 32u;
-  return ((size_t)batch * cols + 15u) / 16u * 16u + (size_t)batch * K * 8u +
-         (size_t)2u * batch * rows_per_tile * (K + 1u) * 4u;
 }
 
 hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream) {
-  const size_t lds = qmatvec_lds_bytes(a.batch, a.cols, a.rows_per_tile);
+  const size_t lds = qmatvec_lds_bytes(a.chunk, a.cols, a.rows_per_tile);
+  const dim3 grid(tiles, (a.batch + a.group_rows - 1) / a.group_rows);
   if (fmt == 0)
-    hipLaunchKernelGGL(qmatvec_kernel<0>, dim3(tiles), dim3(kQThreads), lds, stream, a);
+    hipLaunchKernelGGL(qmatvec_kernel<0>, grid, dim3(kQThreads), lds, stream, a);
   else if (fmt == 1)
-    hipLaunchKernelGGL(qmatvec_kernel<1>, dim3(tiles), dim3(kQThreads), lds, stream, a);
+    hipLaunchKernelGGL(qmatvec_kernel<1>, grid, dim3(kQThreads), lds, stream, a);
   else if (fmt == 2)
-    hipLaunchKernelGGL(qkmatvec_kernel<2>, dim3(tiles), dim3(kQThreads),
-                       qkmatvec_lds_bytes(2, a.batch, a.cols, a.rows_per_tile), stream, a);
+    hipLaunchKernelGGL(qkmatvec_kernel<2>, grid, dim3(kQThreads),
+                       qkmatvec_lds_bytes(2, a.chunk, a.cols, a.rows_per_tile), stream, a);
   else if (fmt == 3)
-    hipLaunchKernelGGL(qkmatvec_kernel<3>, dim3(tiles), dim3(kQThreads),
-                       qkmatvec_lds_bytes(3, a.batch, a.cols, a.rows_per_tile), stream, a);
+    hipLaunchKernelGGL(qkmatvec_kernel<3>, grid, dim3(kQThreads),
+                       qkmatvec_lds_bytes(3, a.chunk, a.cols, a.rows_per_tile), stream, a);
   else if (fmt == 4)
-    hipLaunchKernelGGL(qkmatvec_kernel<4>, dim3(tiles), dim3(kQThreads),
-                       qkmatvec_lds_bytes(4, a.batch, a.cols, a.rows_per_tile), stream, a);
+    hipLaunchKernelGGL(qkmatvec_kernel<4>, grid, dim3(kQThreads),
+                       qkmatvec_lds_bytes(4, a.chunk, a.cols, a.rows_per_tile), stream, a);
   else if (fmt == 5)
-    hipLaunchKernelGGL(qmatvec_kernel<5>, dim3(tiles), dim3(kQThreads), lds, stream, a);
+    hipLaunchKernelGGL(qmatvec_kernel<5>, grid, dim3(kQThreads), lds, stream, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

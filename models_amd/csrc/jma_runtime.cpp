@@ -737,10 +737,7 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(!mats.empty(), JMODELS_ATTN_INVALID_SHAPE, "no matrices");
   // Q4_0 / Q8_0 / Q5_0 take Q8_0 activations (32-element blocks), the K-quants Q8_K (256): one
   // call shares one activation format, as backend-native's grouped calls require (RS:1196-1204).
-  auto is_kquant = [](uint32_t f) {
-    return f == JMODELS_ATTN_WEIGHTS_Q4_K || f == JMODELS_ATTN_WEIGHTS_Q5_K || f == JMODELS_ATTN_WEIGHTS_Q6_K;
-  };
-  const bool kq = is_kquant(mats[0].format);
+  const bool kq = jma::qmat_kquant(mats[0].format);
   const uint32_t elems = kq ? 256u : 32u;
   require(batch > 0 && cols > 0 && cols % elems == 0, JMODELS_ATTN_INVALID_SHAPE,
           "batch_size and cols must be > 0 and cols a multiple of " + std::to_string(elems));
@@ -749,24 +746,13 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(((uintptr_t)input & 15u) == 0, JMODELS_ATTN_INVALID_SHAPE,
           "input must be 16-byte aligned");
   const uint32_t K = cols / elems;
-  // GGUF block sizes (RS:87-92).
-  auto block_bytes = [](uint32_t f) -> uint64_t {
-    switch (f) {
-      case JMODELS_ATTN_WEIGHTS_Q4_0: return 18u;
-      case JMODELS_ATTN_WEIGHTS_Q8_0: return 34u;
-      case JMODELS_ATTN_WEIGHTS_Q4_K: return 144u;
-      case JMODELS_ATTN_WEIGHTS_Q6_K: return 210u;
-      case JMODELS_ATTN_WEIGHTS_Q5_K: return 176u;
-      default: return 22u;  // Q5_0
-    }
-  };
   uint64_t total_rows = 0;
   for (size_t i = 0; i < mats.size(); ++i) {
     const QuantMatrix& m = mats[i];
     const std::string at = " (matrix " + std::to_string(i) + ")";
     require(m.format <= JMODELS_ATTN_WEIGHTS_Q5_0, JMODELS_ATTN_INVALID_SHAPE,
             "unknown weight format " + std::to_string(m.format) + at);
-    require(is_kquant(m.format) == kq, JMODELS_ATTN_INVALID_SHAPE,
+    require(jma::qmat_kquant(m.format) == kq, JMODELS_ATTN_INVALID_SHAPE,
             "one call mixes 32-element block formats (Q4_0/Q8_0/Q5_0) with K-quants "
             "(Q4_K/Q5_K/Q6_K)" + at);
     require(m.weights != nullptr, JMODELS_ATTN_NULL_POINTER, "null weights" + at);
@@ -774,7 +760,7 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
     require(((uintptr_t)m.weights & 1u) == 0, JMODELS_ATTN_INVALID_SHAPE,
             "weights must be 2-byte aligned" + at);
     require(addend_mode == 0 || m.addend != nullptr, JMODELS_ATTN_NULL_POINTER, "null addend" + at);
-    const uint64_t need = (uint64_t)m.rows * K * block_bytes(m.format);
+    const uint64_t need = (uint64_t)m.rows * K * jma::qmat_block_bytes(m.format);
     require(m.bytes >= need, JMODELS_ATTN_BUFFER_TOO_SMALL,
             "weights hold " + std::to_string(m.bytes) + " bytes, need " + std::to_string(need) + at);
     total_rows += m.rows;
@@ -785,52 +771,43 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(output_elements >= (uint64_t)batch * total_rows, JMODELS_ATTN_BUFFER_TOO_SMALL,
           "output holds " + std::to_string(output_elements) + " elements, needs " +
               std::to_string((uint64_t)batch * total_rows));
-  // Up to 512 (row, block) terms per workgroup for the 32-element formats (two per thread, all
-  // loaded at once), 64 for the K-quants (eight threads each); activation rows per launch as LDS
-  // allows (at most 8, within 64 KB).
-  constexpr size_t kLds = 64u * 1024u;
-  auto lds = [&](uint32_t nb, uint32_t t) {
-    size_t m = 0;
-    for (const QuantMatrix& q : mats)
-      m = std::max(m, kq ? jma::qkmatvec_lds_bytes(q.format, nb, cols, t)
-                         : jma::qmatvec_lds_bytes(nb, cols, t));
-    return m;
-  };
-  uint32_t tile = std::max<uint32_t>(1u, std::min<uint32_t>(64u, (kq ? 64u : 512u) / K));
-  while (tile > 1 && lds(1, tile) > kLds) tile /= 2;
-  require(lds(1, tile) <= kLds, JMODELS_ATTN_INVALID_SHAPE,
+  // One launch per weight format: every matrix of that format, every activation row (the
+  // workgroups of grid row y take activation rows y * group_rows ..., in passes of `chunk` rows
+  // through LDS, so a weight tile is read from memory once per workgroup, not once per pass).
+  std::vector<uint32_t> fmts;
+  for (const QuantMatrix& m : mats) fmts.push_back(m.format);
+  const jma::QMatPlan qp = jma::plan_qmat(fmts.data(), (uint32_t)fmts.size(), cols);
+  require(qp.rows_per_tile > 0, JMODELS_ATTN_INVALID_SHAPE,
           "cols too large for the device projection: " + std::to_string(cols));
-  uint32_t chunk = 8;
-  while (chunk > 1 && lds(chunk, tile) > kLds) --chunk;
   set_device(ctx);
-  for (uint32_t b0 = 0; b0 < batch; b0 += chunk) {
-    const uint32_t nb = std::min(chunk, batch - b0);
-    for (uint32_t fmt = 0; fmt <= JMODELS_ATTN_WEIGHTS_Q5_0; ++fmt) {
-      jma::QMatArgs a{};
-      a.x = input + (uint64_t)b0 * cols;
-      a.batch = nb;
-      a.cols = cols;
-      a.blocks = K;
-      a.rows_per_tile = tile;
-      a.addend_mode = addend_mode;
-      uint32_t tiles = 0;
-      uint64_t out_off = 0;
-      for (const QuantMatrix& m : mats) {
-        if (m.format == fmt) {
-          jma::QMatrix& q = a.m[a.count++];
-          q.w = (const uint8_t*)m.weights;
-          q.out = output + out_off + (uint64_t)b0 * m.rows;
-          q.addend = addend_mode == JMODELS_ATTN_ADDEND_RESIDUAL ? m.addend + (uint64_t)b0 * m.rows
-                                                                 : m.addend;
-          q.rows = m.rows;
-          q.tile0 = tiles;
-          tiles += (m.rows + tile - 1) / tile;
-        }
-        out_off += (uint64_t)batch * m.rows;
+  for (uint32_t fmt = 0; fmt <= JMODELS_ATTN_WEIGHTS_Q5_0; ++fmt) {
+    jma::QMatArgs a{};
+    a.x = input;
+    a.batch = batch;
+    a.cols = cols;
+    a.blocks = K;
+    a.rows_per_tile = qp.rows_per_tile;
+    a.chunk = qp.chunk;
+    a.addend_mode = addend_mode;
+    uint32_t tiles = 0;
+    uint64_t out_off = 0;
+    for (const QuantMatrix& m : mats) {
+      if (m.format == fmt) {
+        jma::QMatrix& q = a.m[a.count++];
+        q.w = (const uint8_t*)m.weights;
+        q.out = output + out_off;
+        q.addend = m.addend;
+        q.rows = m.rows;
+        q.tile0 = tiles;
+        tiles += (m.rows + qp.rows_per_tile - 1) / qp.rows_per_tile;
       }
-      if (a.count == 0) continue;
-      hip_check(jma::launch_qmatvec(a, fmt, tiles, ctx->stream), "quantized matmul launch");
+      out_off += (uint64_t)batch * m.rows;
     }
+    if (a.count == 0) continue;
+    a.group_rows = jma::qmat_group_rows(batch, qp.chunk, tiles);
+    require((batch + a.group_rows - 1) / a.group_rows <= 65535u, JMODELS_ATTN_INVALID_SHAPE,
+            "batch_size too large for one projection launch: " + std::to_string(batch));
+    hip_check(jma::launch_qmatvec(a, fmt, tiles, ctx->stream), "quantized matmul launch");
   }
 }
 

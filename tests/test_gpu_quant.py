@@ -251,6 +251,90 @@ def test_prefill_sized_grouped_projection_with_addends(hip, mode):
             d.free()
 
 
+@pytest.mark.parametrize("case", ["q5_0-q8_0-q4_0 bias x300", "q8_0 wo residual x64",
+                                  "q4_k-q5_k-q6_k residual x40", "q4_0 graph x96"])
+def test_prefill_sized_projections(hip, case):
+    """Prefill-sized batches in one launch per format: the workgroups of grid row y take 8-row
+    passes of their activation rows through LDS while the weight tile stays resident (read once
+    per workgroup). Grouped calls with biases or residuals (in place for the output projection),
+    mixed 32-element formats, a K-quant mix, and a captured graph replayed three times; every
+    output bit-exact against the oracle."""
+    kq = case.startswith("q4_k")
+    if case.startswith("q5_0"):
+        fmts, rows, batch, cols, mode = [A.WEIGHTS_Q5_0, A.WEIGHTS_Q8_0, A.WEIGHTS_Q4_0], [896, 128, 128], 300, 896, A.ADDEND_BIAS
+    elif case.startswith("q8_0"):
+        fmts, rows, batch, cols, mode = [A.WEIGHTS_Q8_0], [896], 64, 896, A.ADDEND_RESIDUAL
+    elif kq:
+        fmts, rows, batch, cols, mode = [A.WEIGHTS_Q4_K, A.WEIGHTS_Q5_K, A.WEIGHTS_Q6_K], [1536, 256, 256], 40, 1536, A.ADDEND_RESIDUAL
+    else:
+        fmts, rows, batch, cols, mode = [A.WEIGHTS_Q4_0] * 3, [2048, 512, 512], 96, 2048, A.ADDEND_NONE
+    ws = [(_kquant_weights if kq else _weights)(f, r, cols, f"pf/{case}/{i}")
+          for i, (f, r) in enumerate(zip(fmts, rows))]
+    x = synth.normal(11, f"pf/{case}/x", (batch, cols))
+    wants = [oracle.quantized_matmul(f, w, x, batch, r, cols) for f, w, r in zip(fmts, ws, rows)]
+    dws = [rt.DeviceArray.from_host(w) for w in ws]
+    dx = rt.DeviceArray.from_host(x)
+    extra = []
+    try:
+        if mode == A.ADDEND_RESIDUAL and len(fmts) == 1:
+            # x_res += wo . attn, the residual being the output itself
+            resid = synth.normal(11, f"pf/{case}/res", (batch, rows[0]))
+            dres = rt.DeviceArray.from_host(resid)
+            extra.append(dres)
+            hip.quantized_matmul_device(fmts[0], dws[0].ptr, ws[0].size, dx.ptr, x.size, dres.ptr,
+                                        dres.count, batch, rows[0], cols, dres.ptr, mode)
+            hip.synchronize()
+            _exact(dres.download().reshape(batch, rows[0]), (resid + wants[0]).astype(np.float32),
+                   f"{case}: residual in place")
+            _say(f"{case}: bit-exact")
+            return
+        adds = None
+        if mode == A.ADDEND_BIAS:
+            adds = [synth.normal(11, f"pf/{case}/b{i}", (r,)) for i, r in enumerate(rows)]
+        elif mode == A.ADDEND_RESIDUAL:
+            adds = [synth.normal(11, f"pf/{case}/r{i}", (batch, r)) for i, r in enumerate(rows)]
+        dadds = [rt.DeviceArray.from_host(a) for a in adds] if adds else []
+        extra += dadds
+        dout = rt.DeviceArray(batch * sum(rows))
+        extra.append(dout)
+
+        def call():
+            hip.quantized_grouped_matmul_device(fmts, [d.ptr for d in dws], [w.size for w in ws], rows,
+                                                dx.ptr, x.size, dout.ptr, dout.count, batch, cols,
+                                                [d.ptr for d in dadds] if adds else None, mode)
+
+        def check(what):
+            got, off = dout.download(), 0
+            for i, r in enumerate(rows):
+                want = wants[i]
+                if mode == A.ADDEND_BIAS:
+                    want = want + adds[i][None, :]
+                elif mode == A.ADDEND_RESIDUAL:
+                    want = want + adds[i]
+                _exact(got[off:off + batch * r].reshape(batch, r), want.astype(np.float32),
+                       f"{case} {what} matrix {i}")
+                off += batch * r
+
+        if case.endswith("graph x96"):
+            g = rt.Graph(hip.stream(), call)
+            try:
+                for rep in range(3):
+                    dout.zero()
+                    g.launch()
+                    rt.device_synchronize()
+                    check(f"replay {rep}")
+            finally:
+                g.destroy()
+        else:
+            call()
+            hip.synchronize()
+            check("eager")
+        _say(f"{case}: bit-exact")
+    finally:
+        for d in dws + [dx] + extra:
+            d.free()
+
+
 def test_grouped_qkv_mixed_formats_bias_and_residual(hip):
     """One grouped call for a Llama-3.2-1B layer's Q (2048 rows, Q8_0), K and V (512 rows each,
     Q4_0) over 2048 inputs, outputs q|k|v contiguous; with per-row biases (addOptionalBias); and

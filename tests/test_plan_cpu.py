@@ -28,3 +28,22 @@ def test_decode_plans_stay_in_bounds(tmp_path):
     assert run.stdout.strip().endswith("ok"), run.stdout
     assert "C5 global d256 4/1 @32767" in run.stdout and "separate" in run.stdout
     assert "K layout: bijective" in run.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_projection_launches_stay_in_bounds(tmp_path):
+    """tests/qmat_check.cpp: the quantized-projection launches of decode- and prefill-sized
+    grouped calls (biases, residuals, mixed formats, the 200-row grouped shape, 2048-row prefill
+    batches, 16 matrices, rows of 14336 inputs) planned with the runtime's planner, every
+    workgroup's weight, activation, LDS, output and addend index walked under ASan/UBSan, every
+    output written exactly once."""
+    exe = tmp_path / "qmat_check"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
+           "-fno-sanitize-recover=all", "-I", os.path.join(ROOT, "models_amd", "csrc"),
+           os.path.join(ROOT, "tests", "qmat_check.cpp"), "-o", str(exe)]
+    build = subprocess.run(cmd, capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.strip().endswith("ok"), run.stdout
+    assert "grouped 2048 rows, biases" in run.stdout
