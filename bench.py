@@ -678,6 +678,8 @@ def run_proj(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
                                                 rows, dx.ptr, batch * cols, dqkv.ptr, dqkv.count,
                                                 batch, cols)
 
+        qkv_prefill()  # eager first: sizes the activation scratch outside the capture
+        hip.synchronize()
         graph = rt.Graph(stream, qkv_prefill)
         graph.launch()
         hip.synchronize()

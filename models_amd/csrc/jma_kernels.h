@@ -189,5 +189,12 @@ struct QMatArgs {
 // the launch. tiles = sum of ceil(rows / rows_per_tile); the grid is tiles x ceil(batch /
 // group_rows).
 hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream);
+// Prefill-sized batches of the 32-element block formats (fmt 0, 1, 5): the activations quantized
+// once to q (int8 [batch][cols]) and scales ([batch][cols / 32]), then the register-tiled
+// product; tiles = sum of ceil(rows / kQGemmTile), grid tiles x ceil(batch / kQGemmTile).
+hipError_t launch_q8_0_quant(const float* x, uint32_t batch, uint32_t cols, int8_t* q,
+                             float* scales, hipStream_t stream);
+hipError_t launch_qgemm(const QMatArgs& a, uint32_t fmt, uint32_t tiles, const int8_t* aq,
+                        const float* as, hipStream_t stream);
 
 }  // namespace jma

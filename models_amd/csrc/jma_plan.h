@@ -244,6 +244,13 @@ constexpr uint64_t kQMatLds = 64u * 1024u;   // dynamic LDS a projection workgro
 constexpr uint32_t kQMatMaxChunk = 8;        // activation rows per pass
 constexpr uint32_t kQMatTargetBlocks = 1024;  // workgroups a projection launch aims for
 
+// Batches of at least kQGemmMinBatch activation rows run the 32-element block formats as a
+// register-tiled product (qgemm_kernel): tiles of kQGemmTile weight rows x kQGemmTile activation
+// rows, kQGemmKc blocks staged per step.
+constexpr uint32_t kQGemmMinBatch = 16;
+constexpr uint32_t kQGemmTile = 64;
+constexpr uint32_t kQGemmKc = 4;
+
 struct QMatPlan {
   uint32_t rows_per_tile = 0, chunk = 0;  // 0: cols too large for one workgroup's LDS
 };

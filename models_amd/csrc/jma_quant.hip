@@ -95,6 +95,41 @@ struct QBlock {
   }
 };
 
+// Q8_0 quantization of one eighth of a 32-element activation block (quantizeInputs,
+// NativeKernelLibraryTest.java:998-1017): the four consecutive lanes of a quad each take eight
+// elements and meet for the block maximum and the element sum through DPP quad exchanges. The
+// block's absolute maximum (NaN skipped) gives inverse = 127 / absmax, each element the nearest
+// integer of x * inverse (the reference's 1.5 * 2^23 addition), the scale the f16-rounded
+// absmax / 127. All four lanes of a quad must call it together.
+__device__ __forceinline__ void q8_0_eighth(const float* xs, uint2& packed, float& scale, int& sum) {
+  const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+  const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  float am = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(xv[i]));  // a NaN element is skipped
+  am = fmaxf(am, __int_as_float(dpp_int<kQuadXor1>(__float_as_int(am))));
+  am = fmaxf(am, __int_as_float(dpp_int<kQuadXor2>(__float_as_int(am))));
+  const float inverse = am == 0.0f ? 0.0f : 127.0f / am;
+  uint32_t pk[2] = {0u, 0u};
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float scaled;
+    {
+#pragma clang fp contract(off)
+      scaled = xv[i] * inverse;
+    }
+    const int q = nearest_int(scaled);
+    s += (int)(int8_t)q;
+    pk[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+  }
+  packed = make_uint2(pk[0], pk[1]);
+  s += dpp_int<kQuadXor1>(s);
+  s += dpp_int<kQuadXor2>(s);
+  sum = s;
+  scale = (float)(_Float16)(am / 127.0f);
+}
+
 }  // namespace
 
 template <int FMT>
@@ -137,33 +172,13 @@ __global__ __launch_bounds__(kQThreads) void qmatvec_kernel(const QMatArgs a) {
     // Q8_0 activations: four threads per 32-element block, eight elements each.
     for (uint32_t t = tid; t < nb * K * 4u; t += kQThreads) {
       const uint32_t b = t / (K * 4u), rem = t % (K * 4u), blk = rem >> 2, qtr = rem & 3u;
-      const float* xs = xb + (uint64_t)b * cols + blk * 32u + qtr * 8u;
-      const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
-      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      float am = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(xv[i]));  // a NaN element is skipped
-      am = fmaxf(am, __int_as_float(dpp_int<kQuadXor1>(__float_as_int(am))));
-      am = fmaxf(am, __int_as_float(dpp_int<kQuadXor2>(__float_as_int(am))));
-      const float inverse = am == 0.0f ? 0.0f : 127.0f / am;
-      uint32_t packed[2] = {0u, 0u};
-      int s = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float scaled;
-        {
-#pragma clang fp contract(off)
-          scaled = xv[i] * inverse;
-        }
-        const int q = nearest_int(scaled);
-        s += (int)(int8_t)q;
-        packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
-      }
-      *(uint2*)(act_q + (uint64_t)b * cols + blk * 32u + qtr * 8u) = make_uint2(packed[0], packed[1]);
-      s += dpp_int<kQuadXor1>(s);
-      s += dpp_int<kQuadXor2>(s);
+      uint2 packed;
+      float scale;
+      int s;
+      q8_0_eighth(xb + (uint64_t)b * cols + blk * 32u + qtr * 8u, packed, scale, s);
+      *(uint2*)(act_q + (uint64_t)b * cols + blk * 32u + qtr * 8u) = packed;
       if (qtr == 0) {
-        act_scale[b * K + blk] = (float)(_Float16)(am / 127.0f);
+        act_scale[b * K + blk] = scale;
         act_sum[b * K + blk] = s;
       }
     }
@@ -432,6 +447,213 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
       out[o] = sum;
     }
   }
+}
+
+// ---------------------------------------------------------------- prefill-sized batches (GEMM)
+//
+// For batches of kQGemmMinBatch activation rows and more, the 32-element block formats (Q4_0,
+// Q8_0, Q5_0) run as a register-tiled matrix product: the activations are quantized to Q8_0 once
+// (q8_0_quant_kernel, into scratch), then each workgroup computes a tile of kQGemmTile weight
+// rows x kQGemmTile activation rows, every thread a 4 x 4 block of outputs. The weight and
+// activation blocks of kQGemmKc consecutive 32-element blocks at a time are staged in LDS as
+// signed int8 (the weight nibbles with their offset applied, so the integer dot needs no
+// correction term) with their f32 scales; each output is the reference's in-order chain of
+// fma(weightScale * activationScale, integer block dot, sum) over the blocks, so the results are
+// the same bits as the matrix-vector kernel's.
+
+// Q8_0 activations [batch][cols] -> int8 [batch][cols] and f32 scales [batch][cols / 32]; four
+// threads per block.
+__global__ __launch_bounds__(kQThreads) void q8_0_quant_kernel(const float* x, uint32_t batch,
+                                                               uint32_t cols, int8_t* q,
+                                                               float* scales) {
+  const uint32_t K = cols / 32u;
+  const uint64_t units = (uint64_t)batch * K * 4u;
+  const uint64_t t = (uint64_t)blockIdx.x * kQThreads + threadIdx.x;
+  // The grid covers whole quads (units is a multiple of 4), so the four lanes of a quad are
+  // active together for the DPP exchanges.
+  if (t >= units) return;
+  const uint64_t b = t / (K * 4u);
+  const uint32_t rem = (uint32_t)(t % (K * 4u)), blk = rem >> 2, qtr = rem & 3u;
+  uint2 packed;
+  float scale;
+  int s;
+  q8_0_eighth(x + b * cols + blk * 32u + qtr * 8u, packed, scale, s);
+  *(uint2*)(q + b * cols + blk * 32u + qtr * 8u) = packed;
+  if (qtr == 0) scales[b * K + blk] = scale;
+}
+
+namespace {
+
+// Each byte of x (below 128) minus the byte `off` (at most 128), as signed bytes: with bit 7 set
+// first no byte's subtraction borrows from the next.
+__device__ __forceinline__ uint32_t bytes_minus(uint32_t x, uint32_t off4) {
+  return ((x | 0x80808080u) - off4) ^ 0x80808080u;
+}
+
+// A weight block as 32 signed int8 (8 words, element order) and its f32 scale.
+template <int FMT>
+__device__ __forceinline__ void gemm_weight_block(const uint16_t* rec, uint32_t (&wd)[8], float& scale) {
+  QBlock<FMT> blk;
+  blk.load(rec);
+  scale = f16_bits_to_float(blk.h[0]);
+  if constexpr (FMT == 1) {
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) wd[j] = blk.word(j);
+  } else if constexpr (FMT == 0) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t w = blk.word(j);
+      wd[j] = bytes_minus(w & 0x0F0F0F0Fu, 0x08080808u);
+      wd[4 + j] = bytes_minus((w >> 4) & 0x0F0F0F0Fu, 0x08080808u);
+    }
+  } else {
+    const uint32_t high = blk.word(0);
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t w = blk.h[3 + 2 * j] | (blk.h[4 + 2 * j] << 16);
+      wd[j] = bytes_minus((w & 0x0F0F0F0Fu) | fifth_bits((high >> (4 * j)) & 15u), 0x10101010u);
+      wd[4 + j] = bytes_minus(((w >> 4) & 0x0F0F0F0Fu) | fifth_bits((high >> (16 + 4 * j)) & 15u),
+                              0x10101010u);
+    }
+  }
+}
+
+}  // namespace
+
+template <int FMT>
+__global__ __launch_bounds__(kQThreads, 2) void qgemm_kernel(const QMatArgs a, const int8_t* aq,
+                                                             const float* as) {
+  constexpr uint32_t T = kQGemmTile, KC = kQGemmKc, kRow = KC * 32u + 16u;  // bytes per LDS row
+  __shared__ __attribute__((aligned(16))) int8_t s_w[T * kRow];
+  __shared__ __attribute__((aligned(16))) int8_t s_a[T * kRow];
+  __shared__ float s_ws[T][KC];
+  __shared__ float s_as[T][KC];
+  const uint32_t K = a.blocks, cols = a.cols, batch = a.batch;
+  uint32_t mi = 0;
+  for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
+  const uint8_t* w = a.m[mi].w;
+  float* out = a.m[mi].out;
+  const float* addend = a.m[mi].addend;
+  const uint32_t rows = a.m[mi].rows;
+  const uint32_t r0 = (blockIdx.x - a.m[mi].tile0) * T, b0 = blockIdx.y * T;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t ti = tid / 16u, tj = tid % 16u;  // outputs: weight rows 4 ti.., activation rows 4 tj..
+  constexpr uint32_t kRecHalves = QBlock<FMT>::kHalves;
+  // Staging unit of this thread: one block (row su / KC, block su % KC of the chunk) of the
+  // weight tile and one of the activation tile.
+  const uint32_t su_row = tid / KC, su_k = tid % KC;
+  static_assert(T * KC == kQThreads, "one staged block per thread and tile");
+  const bool w_ok = r0 + su_row < rows, a_ok = b0 + su_row < batch;
+  const uint16_t* w_rec = (const uint16_t*)(w + ((uint64_t)min(r0 + su_row, rows - 1) * K) * (2u * kRecHalves));
+  const int8_t* a_row = aq + (uint64_t)min(b0 + su_row, batch - 1) * cols;
+  const float* as_row = as + (uint64_t)min(b0 + su_row, batch - 1) * K;
+
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+
+  for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+    {
+      const uint32_t k = k0 + su_k;
+      uint32_t wd[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      float wsc = 0.0f;
+      uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0;
+      float asc = 0.0f;
+      if (k < K) {
+        if (w_ok) gemm_weight_block<FMT>(w_rec + (uint64_t)k * kRecHalves, wd, wsc);
+        if (a_ok) {
+          a0 = *(const uint4*)(a_row + k * 32u);
+          a1 = *(const uint4*)(a_row + k * 32u + 16u);
+          asc = as_row[k];
+        }
+      }
+      uint4* dw = (uint4*)(s_w + su_row * kRow + su_k * 32u);
+      dw[0] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+      dw[1] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+      uint4* da = (uint4*)(s_a + su_row * kRow + su_k * 32u);
+      da[0] = a0;
+      da[1] = a1;
+      s_ws[su_row][su_k] = wsc;
+      s_as[su_row][su_k] = asc;
+    }
+    __syncthreads();
+    const uint32_t kn = min(KC, K - k0);
+    for (uint32_t kb = 0; kb < kn; ++kb) {
+      uint4 wv[4][2], av[4][2];
+      float wsc[4], asc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4* pw = (const uint4*)(s_w + (4u * ti + i) * kRow + kb * 32u);
+        wv[i][0] = pw[0];
+        wv[i][1] = pw[1];
+        wsc[i] = s_ws[4u * ti + i][kb];
+        const uint4* pa = (const uint4*)(s_a + (4u * tj + i) * kRow + kb * 32u);
+        av[i][0] = pa[0];
+        av[i][1] = pa[1];
+        asc[i] = s_as[4u * tj + i][kb];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          int d = 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            d = __builtin_amdgcn_sdot4((int)wv[i][h].x, (int)av[j][h].x, d, false);
+            d = __builtin_amdgcn_sdot4((int)wv[i][h].y, (int)av[j][h].y, d, false);
+            d = __builtin_amdgcn_sdot4((int)wv[i][h].z, (int)av[j][h].z, d, false);
+            d = __builtin_amdgcn_sdot4((int)wv[i][h].w, (int)av[j][h].w, d, false);
+          }
+          float sc;
+          {
+#pragma clang fp contract(off)
+            sc = wsc[i] * asc[j];
+          }
+          acc[i][j] = __builtin_fmaf(sc, (float)d, acc[i][j]);
+        }
+    }
+    __syncthreads();  // the next chunk overwrites the stages
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t b = b0 + 4u * tj + j;
+    if (b >= batch) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = r0 + 4u * ti + i;
+      if (r >= rows) continue;
+      const uint64_t o = (uint64_t)b * rows + r;
+      float v = acc[i][j];
+      if (a.addend_mode == 1) v = v + addend[r];
+      else if (a.addend_mode == 2) v = v + addend[o];
+      out[o] = v;
+    }
+  }
+}
+
+hipError_t launch_q8_0_quant(const float* x, uint32_t batch, uint32_t cols, int8_t* q,
+                             float* scales, hipStream_t stream) {
+  const uint64_t units = (uint64_t)batch * (cols / 32u) * 4u;
+  const uint32_t blocks = (uint32_t)((units + kQThreads - 1) / kQThreads);
+  hipLaunchKernelGGL(q8_0_quant_kernel, dim3(blocks), dim3(kQThreads), 0, stream, x, batch, cols,
+                     q, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_qgemm(const QMatArgs& a, uint32_t fmt, uint32_t tiles, const int8_t* aq,
+                        const float* as, hipStream_t stream) {
+  const dim3 grid(tiles, (a.batch + kQGemmTile - 1) / kQGemmTile);
+  if (fmt == 0)
+    hipLaunchKernelGGL(qgemm_kernel<0>, grid, dim3(kQThreads), 0, stream, a, aq, as);
+  else if (fmt == 1)
+    hipLaunchKernelGGL(qgemm_kernel<1>, grid, dim3(kQThreads), 0, stream, a, aq, as);
+  else if (fmt == 5)
+    hipLaunchKernelGGL(qgemm_kernel<5>, grid, dim3(kQThreads), 0, stream, a, aq, as);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_qmatvec(const QMatArgs& a, uint32_t fmt, uint32_t tiles, hipStream_t stream) {

@@ -126,6 +126,7 @@ struct jmodels_attn_context {
   hipStream_t stream = nullptr;
   int* d_err = nullptr;
   DeviceBuffer part_acc, part_ml, part_f, counters, pf_part, pf_tickets, qrot, stage_q, stage_k, stage_v, stage_out;
+  DeviceBuffer qact;                // Q8_0 activations of prefill-sized projections
   int decode_target_blocks = 512;   // workgroups a decode launch aims for (two per CU)
   int tiles_per_wave = 1;           // minimum tiles each decode wave streams
   int min_split_tiles = 0;          // minimum tiles per decode split; 0: waves x tiles_per_wave
@@ -771,6 +772,46 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(output_elements >= (uint64_t)batch * total_rows, JMODELS_ATTN_BUFFER_TOO_SMALL,
           "output holds " + std::to_string(output_elements) + " elements, needs " +
               std::to_string((uint64_t)batch * total_rows));
+  // Prefill-sized batches of the 32-element block formats: the activations are quantized once
+  // into the context's scratch, then one register-tiled product launch per format.
+  if (!kq && batch >= jma::kQGemmMinBatch) {
+    const uint64_t q_bytes = ((uint64_t)batch * cols + 255u) & ~(uint64_t)255u;
+    ctx->qact.reserve(q_bytes + (uint64_t)batch * K * sizeof(float), ctx->stream,
+                      "projection activations");
+    int8_t* aq = (int8_t*)ctx->qact.ptr;
+    float* as = (float*)((char*)ctx->qact.ptr + q_bytes);
+    set_device(ctx);
+    hip_check(jma::launch_q8_0_quant(input, batch, cols, aq, as, ctx->stream),
+              "activation quantization launch");
+    for (uint32_t fmt = 0; fmt <= JMODELS_ATTN_WEIGHTS_Q5_0; ++fmt) {
+      jma::QMatArgs a{};
+      a.x = input;
+      a.batch = batch;
+      a.cols = cols;
+      a.blocks = K;
+      a.rows_per_tile = jma::kQGemmTile;
+      a.addend_mode = addend_mode;
+      uint32_t tiles = 0;
+      uint64_t out_off = 0;
+      for (const QuantMatrix& m : mats) {
+        if (m.format == fmt) {
+          jma::QMatrix& q = a.m[a.count++];
+          q.w = (const uint8_t*)m.weights;
+          q.out = output + out_off;
+          q.addend = m.addend;
+          q.rows = m.rows;
+          q.tile0 = tiles;
+          tiles += (m.rows + jma::kQGemmTile - 1) / jma::kQGemmTile;
+        }
+        out_off += (uint64_t)batch * m.rows;
+      }
+      if (a.count == 0) continue;
+      require((batch + jma::kQGemmTile - 1) / jma::kQGemmTile <= 65535u, JMODELS_ATTN_INVALID_SHAPE,
+              "batch_size too large for one projection launch: " + std::to_string(batch));
+      hip_check(jma::launch_qgemm(a, fmt, tiles, aq, as, ctx->stream), "quantized matmul launch");
+    }
+    return;
+  }
   // One launch per weight format: every matrix of that format, every activation row (the
   // workgroups of grid row y take activation rows y * group_rows ..., in passes of `chunk` rows
   // through LDS, so a weight tile is read from memory once per workgroup, not once per pass).
@@ -887,7 +928,7 @@ int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_f, &ctx->counters, &ctx->pf_part, &ctx->pf_tickets, &ctx->qrot, &ctx->stage_q,
-                            &ctx->stage_k, &ctx->stage_v, &ctx->stage_out})
+                            &ctx->stage_k, &ctx->stage_v, &ctx->stage_out, &ctx->qact})
       b->release();
     (void)hipFree(ctx->d_err);
     (void)hipStreamDestroy(ctx->stream);

@@ -36,8 +36,102 @@ struct Call {
   uint32_t batch, cols, addend_mode;
 };
 
+// The register-tiled product (qgemm_kernel) of the 32-element block formats at batches of
+// kQGemmMinBatch rows and more: the Q8_0 activation scratch [batch][cols] int8 + [batch][K] f32,
+// each workgroup's staged weight and activation blocks (one per thread and chunk, rows clamped to
+// the last valid one and skipped past it), its LDS rows, and every output it writes.
+void walk_gemm(const Call& c) {
+  const uint32_t n = (uint32_t)c.formats.size();
+  const uint32_t K = c.cols / 32, T = jma::kQGemmTile, KC = jma::kQGemmKc, kRow = KC * 32 + 16;
+  std::vector<uint8_t*> w(n);
+  std::vector<float*> add(n, nullptr);
+  uint64_t total_rows = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    w[i] = new uint8_t[(uint64_t)c.rows[i] * K * jma::qmat_block_bytes(c.formats[i])];
+    if (c.addend_mode == 1) add[i] = new float[c.rows[i]];
+    if (c.addend_mode == 2) add[i] = new float[(uint64_t)c.batch * c.rows[i]];
+    total_rows += c.rows[i];
+  }
+  int8_t* aq = new int8_t[(uint64_t)c.batch * c.cols];
+  float* as = new float[(uint64_t)c.batch * K];
+  std::vector<uint8_t> written(c.batch * total_rows, 0);
+  int8_t* lds = new int8_t[T * kRow];
+  volatile int sink = 0;
+  for (uint32_t fmt = 0; fmt <= 5; ++fmt) {
+    struct M { uint32_t idx, tile0; uint64_t out_off; };
+    std::vector<M> ms;
+    uint32_t tiles = 0;
+    uint64_t out_off = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+      if (c.formats[i] == fmt) {
+        ms.push_back({i, tiles, out_off});
+        tiles += (c.rows[i] + T - 1) / T;
+      }
+      out_off += (uint64_t)c.batch * c.rows[i];
+    }
+    if (ms.empty()) continue;
+    const uint32_t bb = jma::qmat_block_bytes(fmt);
+    const uint32_t gy = (c.batch + T - 1) / T;
+    expect(gy <= 65535u, c.name + ": gemm grid rows");
+    for (uint32_t bx = 0; bx < tiles; ++bx) {
+      uint32_t mi = 0;
+      for (uint32_t i = 1; i < ms.size(); ++i) mi = bx >= ms[i].tile0 ? i : mi;
+      const uint32_t idx = ms[mi].idx, rows = c.rows[idx];
+      const uint32_t r0 = (bx - ms[mi].tile0) * T;
+      expect(r0 < rows, c.name + ": gemm tile past its matrix");
+      for (uint32_t by = 0; by < gy; ++by) {
+        const uint32_t b0 = by * T;
+        for (uint32_t tid = 0; tid < 256; ++tid) {
+          const uint32_t su_row = tid / KC, su_k = tid % KC;
+          const bool w_ok = r0 + su_row < rows, a_ok = b0 + su_row < c.batch;
+          const uint64_t wrow = std::min(r0 + su_row, rows - 1), arow = std::min(b0 + su_row, c.batch - 1);
+          for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+            const uint32_t k = k0 + su_k;
+            if (k < K && w_ok) sink = sink + w[idx][(wrow * K + k) * bb] + w[idx][(wrow * K + k) * bb + bb - 1];
+            if (k < K && a_ok) sink = sink + aq[arow * c.cols + k * 32] + aq[arow * c.cols + k * 32 + 31] + (int)as[arow * K + k];
+            lds[su_row * kRow + su_k * 32] = 0;
+            lds[su_row * kRow + su_k * 32 + 31] = 0;
+          }
+          const uint32_t ti = tid / 16, tj = tid % 16;
+          for (uint32_t i = 0; i < 4; ++i) sink = sink + lds[(4 * ti + i) * kRow + (KC - 1) * 32 + 31] + lds[(4 * tj + i) * kRow];
+          for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t b = b0 + 4 * tj + j;
+            if (b >= c.batch) continue;
+            for (uint32_t i = 0; i < 4; ++i) {
+              const uint32_t r = r0 + 4 * ti + i;
+              if (r >= rows) continue;
+              const uint64_t o = (uint64_t)b * rows + r;
+              if (c.addend_mode == 1) sink = sink + (int)add[idx][r];
+              if (c.addend_mode == 2) sink = sink + (int)add[idx][o];
+              written[ms[mi].out_off + o]++;
+            }
+          }
+        }
+      }
+    }
+  }
+  for (uint64_t i = 0; i < written.size(); ++i)
+    if (written[i] != 1) {
+      expect(false, c.name + ": gemm output " + std::to_string(i) + " written " +
+                        std::to_string(written[i]) + " times");
+      break;
+    }
+  printf("%s: batch %u cols %u, register-tiled product\n", c.name.c_str(), c.batch, c.cols);
+  for (uint32_t i = 0; i < n; ++i) {
+    delete[] w[i];
+    delete[] add[i];
+  }
+  delete[] aq;
+  delete[] as;
+  delete[] lds;
+}
+
 void walk(const Call& c) {
   const uint32_t n = (uint32_t)c.formats.size();
+  if (!jma::qmat_kquant(c.formats[0]) && c.batch >= jma::kQGemmMinBatch) {
+    walk_gemm(c);
+    return;
+  }
   const jma::QMatPlan qp = jma::plan_qmat(c.formats.data(), n, c.cols);
   expect(qp.rows_per_tile > 0 && qp.chunk >= 1 && qp.chunk <= jma::kQMatMaxChunk,
          c.name + ": plan");
@@ -173,6 +267,9 @@ int main() {
       {"sixteen matrices", std::vector<uint32_t>(16, 0), std::vector<uint32_t>(16, 100), 33, 512, 1},
       {"batch 8", {0, 1}, {3072, 3}, 8, 2048, 0},
       {"batch 9", {0, 1}, {3072, 3}, 9, 2048, 0},
+      {"batch 16 (product)", {5, 1}, {17, 65}, 16, 2080, 2},
+      {"batch 15 (passes)", {5, 1}, {17, 65}, 15, 2080, 2},
+      {"ragged product 100 x 200", {0, 5}, {200, 7}, 100, 96, 1},
   };
   for (const Call& c : calls) walk(c);
   if (failures) {
