@@ -130,6 +130,61 @@ __device__ __forceinline__ void q8_0_eighth(const float* xs, uint2& packed, floa
   scale = (float)(_Float16)(am / 127.0f);
 }
 
+// Q8_K quantization of one thirty-second of a 256-element activation block (eight elements;
+// quantize_q8_k_batch, backend-native/src/main/rust/model-kernels/src/lib.rs:3906-3952): the 32
+// consecutive lanes of the block find the element of largest magnitude (the first on ties, NaN
+// skipped) with shuffles; inverse = -127 / that element, each element min(nearest(inverse * x),
+// 127). sum16: the 16-element sum of this lane's pair (valid on even parts); scale: 1 / inverse
+// (0 for an all-zero block). All 32 lanes of a block must call it together.
+__device__ __forceinline__ void q8_k_part(const float* xs, uint32_t part, uint2& packed, int& sum16,
+                                          float& scale) {
+  const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+  const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  float best = 0.0f, bval = 0.0f;
+  uint32_t bidx = 0xFFFFFFFFu;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float m = fabsf(xv[i]);
+    if (m > best) {  // strict: the first of equal magnitudes; a NaN compares false
+      best = m;
+      bval = xv[i];
+      bidx = part * 8u + i;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) {
+    const float ob = __shfl_xor(best, o, 32), ov = __shfl_xor(bval, o, 32);
+    const uint32_t oi = __shfl_xor(bidx, o, 32);
+    if (ob > best || (ob == best && oi < bidx)) {
+      best = ob;
+      bval = ov;
+      bidx = oi;
+    }
+  }
+  int s = 0;
+  if (best == 0.0f) {
+    packed = make_uint2(0u, 0u);
+  } else {
+    const float inverse = -127.0f / bval;
+    uint32_t pk[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float scaled;
+      {
+#pragma clang fp contract(off)
+        scaled = inverse * xv[i];
+      }
+      const int q = min(nearest_int(scaled), 127);
+      s += (int)(int8_t)q;
+      pk[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+    }
+    packed = make_uint2(pk[0], pk[1]);
+  }
+  s += __shfl_xor(s, 1, 32);  // two threads make one 16-element sum
+  sum16 = s;
+  scale = best == 0.0f ? 0.0f : 1.0f / (-127.0f / bval);
+}
+
 }  // namespace
 
 template <int FMT>
@@ -278,53 +333,13 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
     // Q8_K activations: 32 threads per block, eight consecutive elements each.
     for (uint32_t t = tid; t < nb * KB * 32u; t += kQThreads) {
       const uint32_t b = t / (KB * 32u), blk = (t / 32u) % KB, part = t & 31u;
-      const float* xs = xb + (uint64_t)b * cols + blk * 256u + part * 8u;
-      const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
-      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      float best = 0.0f, bval = 0.0f;
-      uint32_t bidx = 0xFFFFFFFFu;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float m = fabsf(xv[i]);
-        if (m > best) {  // strict: the first of equal magnitudes; a NaN compares false
-          best = m;
-          bval = xv[i];
-          bidx = part * 8u + i;
-        }
-      }
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) {
-        const float ob = __shfl_xor(best, o, 32), ov = __shfl_xor(bval, o, 32);
-        const uint32_t oi = __shfl_xor(bidx, o, 32);
-        if (ob > best || (ob == best && oi < bidx)) {
-          best = ob;
-          bval = ov;
-          bidx = oi;
-        }
-      }
-      int8_t* qd = act_q + (uint64_t)b * cols + blk * 256u + part * 8u;
-      int s = 0;
-      if (best == 0.0f) {
-        *(uint2*)qd = make_uint2(0u, 0u);
-      } else {
-        const float inverse = -127.0f / bval;
-        uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float scaled;
-          {
-#pragma clang fp contract(off)
-            scaled = inverse * xv[i];
-          }
-          const int q = min(nearest_int(scaled), 127);
-          s += (int)(int8_t)q;
-          packed[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
-        }
-        *(uint2*)qd = make_uint2(packed[0], packed[1]);
-      }
-      s += __shfl_xor(s, 1, 32);  // two threads make one 16-element sum
+      uint2 packed;
+      int s;
+      float scale;
+      q8_k_part(xb + (uint64_t)b * cols + blk * 256u + part * 8u, part, packed, s, scale);
+      *(uint2*)(act_q + (uint64_t)b * cols + blk * 256u + part * 8u) = packed;
       if ((part & 1u) == 0) act_sum[b * (cols / 16u) + blk * 16u + part / 2u] = s;
-      if (part == 0) act_scale[b * KB + blk] = best == 0.0f ? 0.0f : 1.0f / (-127.0f / bval);
+      if (part == 0) act_scale[b * KB + blk] = scale;
     }
     __syncthreads();
 
@@ -631,6 +646,229 @@ __global__ __launch_bounds__(kQThreads, 2) void qgemm_kernel(const QMatArgs a, c
       out[o] = v;
     }
   }
+}
+
+// Q8_K activations [batch][cols] -> int8 [batch][cols], f32 scales [batch][cols / 256] and int
+// 16-element sums [batch][cols / 16]; 32 threads per block.
+__global__ __launch_bounds__(kQThreads) void q8_k_quant_kernel(const float* x, uint32_t batch,
+                                                               uint32_t cols, int8_t* q,
+                                                               float* scales, int* sums) {
+  const uint32_t KB = cols / 256u;
+  const uint64_t units = (uint64_t)batch * KB * 32u;
+  const uint64_t t = (uint64_t)blockIdx.x * kQThreads + threadIdx.x;
+  if (t >= units) return;  // whole blocks: units is a multiple of 32
+  const uint64_t b = t / (KB * 32u);
+  const uint32_t blk = (uint32_t)((t / 32u) % KB), part = (uint32_t)(t & 31u);
+  uint2 packed;
+  int s;
+  float scale;
+  q8_k_part(x + b * cols + blk * 256u + part * 8u, part, packed, s, scale);
+  *(uint2*)(q + b * cols + blk * 256u + part * 8u) = packed;
+  if ((part & 1u) == 0) sums[b * (cols / 16u) + blk * 16u + part / 2u] = s;
+  if (part == 0) scales[b * KB + blk] = scale;
+}
+
+// The register-tiled product of Q4_K (FMT 2) and Q5_K (FMT 4) weights on Q8_K activations, with
+// the float order of dot_q4_k_q8_k_row_scalar / dot_q5_k_q8_k_row_scalar (RS:3410-3518): per
+// 256-element block the integer sums qsum = sum over groups of scale_g * dot_g and msum = sum of
+// min_g * (the group's two 16-element activation sums), then sum = fma(d * as, qsum, sum) and
+// sum = fma(-(dmin * as), msum, sum). Tiles of kQGemmTile x kQGemmTile outputs, 4 x 4 per thread,
+// one 256-element block staged per step: the quants as bytes (0..31), each row's 6-bit scales and
+// mins, d and dmin; the activations' bytes, scale and per-group sums.
+template <int FMT>
+__global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, const int8_t* aq,
+                                                              const float* as, const int* asum) {
+  constexpr uint32_t T = kQGemmTile, kRow = 256u + 16u, kBB = FMT == 2 ? 144u : 176u;
+  __shared__ __attribute__((aligned(16))) int8_t s_w[T * kRow];
+  __shared__ __attribute__((aligned(16))) int8_t s_a[T * kRow];
+  __shared__ __attribute__((aligned(16))) int s_sc[T][8];
+  __shared__ __attribute__((aligned(16))) int s_mn[T][8];
+  __shared__ __attribute__((aligned(16))) int s_gs[T][8];
+  __shared__ float s_d[T], s_dm[T], s_as[T];
+  const uint32_t KB = a.blocks, cols = a.cols, batch = a.batch;
+  uint32_t mi = 0;
+  for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
+  const uint8_t* w = a.m[mi].w;
+  float* out = a.m[mi].out;
+  const float* addend = a.m[mi].addend;
+  const uint32_t rows = a.m[mi].rows;
+  const uint32_t r0 = (blockIdx.x - a.m[mi].tile0) * T, b0 = blockIdx.y * T;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t ti = tid / 16u, tj = tid % 16u;
+  // Staging: row tid / 4, part tid % 4 (groups 2 part and 2 part + 1: 64 elements).
+  const uint32_t su_row = tid / 4u, part = tid % 4u;
+  const bool w_ok = r0 + su_row < rows, a_ok = b0 + su_row < batch;
+  const uint8_t* w_row = w + (uint64_t)min(r0 + su_row, rows - 1) * KB * kBB;
+  const uint64_t arow = min(b0 + su_row, batch - 1);
+
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+
+  for (uint32_t kb = 0; kb < KB; ++kb) {
+    {
+      uint32_t q[16];  // 64 quant bytes: group 2 part, then 2 part + 1
+#pragma unroll
+      for (int i = 0; i < 16; ++i) q[i] = 0u;
+      if (w_ok) {
+        const uint16_t* h = (const uint16_t*)(w_row + (uint64_t)kb * kBB);
+        const uint16_t* qs = h + (FMT == 4 ? 24 : 8) + part * 16;  // 32 bytes of nibbles
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t x = (uint32_t)qs[2 * i] | ((uint32_t)qs[2 * i + 1] << 16);
+          q[i] = x & 0x0F0F0F0Fu;
+          q[8 + i] = (x >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (FMT == 4) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const uint32_t qh = (uint32_t)h[8 + 2 * i] | ((uint32_t)h[9 + 2 * i] << 16);
+            q[i] |= ((qh >> (2 * part)) & 0x01010101u) << 4;
+            q[8 + i] |= ((qh >> (2 * part + 1)) & 0x01010101u) << 4;
+          }
+        }
+        if (part == 0) {
+          s_d[su_row] = f16_bits_to_float(h[0]);
+          s_dm[su_row] = f16_bits_to_float(h[1]);
+          uint32_t scb[12];
+#pragma unroll
+          for (int i = 0; i < 6; ++i) {
+            scb[2 * i] = h[2 + i] & 0xFFu;
+            scb[2 * i + 1] = h[2 + i] >> 8;
+          }
+#pragma unroll
+          for (int g = 0; g < 8; ++g) {
+            s_sc[su_row][g] = g < 4 ? (int)(scb[g] & 63u) : (int)((scb[g + 4] & 15u) | ((scb[g - 4] >> 6) << 4));
+            s_mn[su_row][g] = g < 4 ? (int)(scb[g + 4] & 63u) : (int)((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4));
+          }
+        }
+      } else if (part == 0) {
+        s_d[su_row] = 0.0f;
+        s_dm[su_row] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s_sc[su_row][g] = s_mn[su_row][g] = 0;
+      }
+      uint4* dw = (uint4*)(s_w + su_row * kRow + part * 64u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dw[i] = make_uint4(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
+      uint4 av[4] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u),
+                     make_uint4(0u, 0u, 0u, 0u)};
+      int4 sm = make_int4(0, 0, 0, 0);
+      float asc = 0.0f;
+      if (a_ok) {
+        const uint4* pa = (const uint4*)(aq + arow * cols + kb * 256u + part * 64u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) av[i] = pa[i];
+        sm = *(const int4*)(asum + arow * (cols / 16u) + kb * 16u + part * 4u);
+        asc = as[arow * KB + kb];
+      }
+      uint4* da = (uint4*)(s_a + su_row * kRow + part * 64u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) da[i] = av[i];
+      s_gs[su_row][2 * part] = sm.x + sm.y;
+      s_gs[su_row][2 * part + 1] = sm.z + sm.w;
+      if (part == 0) s_as[su_row] = asc;
+    }
+    __syncthreads();
+    int qsum[4][4], msum[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qsum[i][j] = msum[i][j] = 0;
+    for (int g = 0; g < 8; ++g) {
+      uint4 wv[4][2], avv[4][2];
+      int sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4* pw = (const uint4*)(s_w + (4u * ti + i) * kRow + g * 32u);
+        wv[i][0] = pw[0];
+        wv[i][1] = pw[1];
+        sc[i] = s_sc[4u * ti + i][g];
+        const uint4* pa = (const uint4*)(s_a + (4u * tj + i) * kRow + g * 32u);
+        avv[i][0] = pa[0];
+        avv[i][1] = pa[1];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          int d = 0;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            d = __builtin_amdgcn_sdot4((int)wv[i][hh].x, (int)avv[j][hh].x, d, false);
+            d = __builtin_amdgcn_sdot4((int)wv[i][hh].y, (int)avv[j][hh].y, d, false);
+            d = __builtin_amdgcn_sdot4((int)wv[i][hh].z, (int)avv[j][hh].z, d, false);
+            d = __builtin_amdgcn_sdot4((int)wv[i][hh].w, (int)avv[j][hh].w, d, false);
+          }
+          qsum[i][j] += sc[i] * d;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int4 m0 = *(const int4*)&s_mn[4u * ti + i][0], m1 = *(const int4*)&s_mn[4u * ti + i][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int4 g0 = *(const int4*)&s_gs[4u * tj + j][0], g1 = *(const int4*)&s_gs[4u * tj + j][4];
+        msum[i][j] = m0.x * g0.x + m0.y * g0.y + m0.z * g0.z + m0.w * g0.w + m1.x * g1.x +
+                     m1.y * g1.y + m1.z * g1.z + m1.w * g1.w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float wd = s_d[4u * ti + i], wdm = s_dm[4u * ti + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float asj = s_as[4u * tj + j];
+        float d, dm;
+        {
+#pragma clang fp contract(off)
+          d = wd * asj;
+          dm = wdm * asj;
+        }
+        acc[i][j] = __builtin_fmaf(d, (float)qsum[i][j], acc[i][j]);
+        acc[i][j] = __builtin_fmaf(-dm, (float)msum[i][j], acc[i][j]);
+      }
+    }
+    __syncthreads();  // the next block overwrites the stages
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t b = b0 + 4u * tj + j;
+    if (b >= batch) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = r0 + 4u * ti + i;
+      if (r >= rows) continue;
+      const uint64_t o = (uint64_t)b * rows + r;
+      float v = acc[i][j];
+      if (a.addend_mode == 1) v = v + addend[r];
+      else if (a.addend_mode == 2) v = v + addend[o];
+      out[o] = v;
+    }
+  }
+}
+
+hipError_t launch_q8_k_quant(const float* x, uint32_t batch, uint32_t cols, int8_t* q,
+                             float* scales, int* sums, hipStream_t stream) {
+  const uint64_t units = (uint64_t)batch * (cols / 256u) * 32u;
+  const uint32_t blocks = (uint32_t)((units + kQThreads - 1) / kQThreads);
+  hipLaunchKernelGGL(q8_k_quant_kernel, dim3(blocks), dim3(kQThreads), 0, stream, x, batch, cols,
+                     q, scales, sums);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkgemm(const QMatArgs& a, uint32_t fmt, uint32_t tiles, const int8_t* aq,
+                         const float* as, const int* asum, hipStream_t stream) {
+  const dim3 grid(tiles, (a.batch + kQGemmTile - 1) / kQGemmTile);
+  if (fmt == 2)
+    hipLaunchKernelGGL(qkgemm_kernel<2>, grid, dim3(kQThreads), 0, stream, a, aq, as, asum);
+  else if (fmt == 4)
+    hipLaunchKernelGGL(qkgemm_kernel<4>, grid, dim3(kQThreads), 0, stream, a, aq, as, asum);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_q8_0_quant(const float* x, uint32_t batch, uint32_t cols, int8_t* q,

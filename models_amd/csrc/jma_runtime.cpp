@@ -772,62 +772,55 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(output_elements >= (uint64_t)batch * total_rows, JMODELS_ATTN_BUFFER_TOO_SMALL,
           "output holds " + std::to_string(output_elements) + " elements, needs " +
               std::to_string((uint64_t)batch * total_rows));
-  // Prefill-sized batches of the 32-element block formats: the activations are quantized once
-  // into the context's scratch, then one register-tiled product launch per format.
-  if (!kq && batch >= jma::kQGemmMinBatch) {
-    const uint64_t q_bytes = ((uint64_t)batch * cols + 255u) & ~(uint64_t)255u;
-    ctx->qact.reserve(q_bytes + (uint64_t)batch * K * sizeof(float), ctx->stream,
-                      "projection activations");
-    int8_t* aq = (int8_t*)ctx->qact.ptr;
-    float* as = (float*)((char*)ctx->qact.ptr + q_bytes);
-    set_device(ctx);
-    hip_check(jma::launch_q8_0_quant(input, batch, cols, aq, as, ctx->stream),
-              "activation quantization launch");
-    for (uint32_t fmt = 0; fmt <= JMODELS_ATTN_WEIGHTS_Q5_0; ++fmt) {
-      jma::QMatArgs a{};
-      a.x = input;
-      a.batch = batch;
-      a.cols = cols;
-      a.blocks = K;
-      a.rows_per_tile = jma::kQGemmTile;
-      a.addend_mode = addend_mode;
-      uint32_t tiles = 0;
-      uint64_t out_off = 0;
-      for (const QuantMatrix& m : mats) {
-        if (m.format == fmt) {
-          jma::QMatrix& q = a.m[a.count++];
-          q.w = (const uint8_t*)m.weights;
-          q.out = output + out_off;
-          q.addend = m.addend;
-          q.rows = m.rows;
-          q.tile0 = tiles;
-          tiles += (m.rows + jma::kQGemmTile - 1) / jma::kQGemmTile;
-        }
-        out_off += (uint64_t)batch * m.rows;
-      }
-      if (a.count == 0) continue;
-      require((batch + jma::kQGemmTile - 1) / jma::kQGemmTile <= 65535u, JMODELS_ATTN_INVALID_SHAPE,
-              "batch_size too large for one projection launch: " + std::to_string(batch));
-      hip_check(jma::launch_qgemm(a, fmt, tiles, aq, as, ctx->stream), "quantized matmul launch");
-    }
-    return;
-  }
-  // One launch per weight format: every matrix of that format, every activation row (the
-  // workgroups of grid row y take activation rows y * group_rows ..., in passes of `chunk` rows
-  // through LDS, so a weight tile is read from memory once per workgroup, not once per pass).
-  std::vector<uint32_t> fmts;
-  for (const QuantMatrix& m : mats) fmts.push_back(m.format);
-  const jma::QMatPlan qp = jma::plan_qmat(fmts.data(), (uint32_t)fmts.size(), cols);
-  require(qp.rows_per_tile > 0, JMODELS_ATTN_INVALID_SHAPE,
-          "cols too large for the device projection: " + std::to_string(cols));
+  // Launches, one per weight format of the call. Prefill-sized batches of the formats with a
+  // register-tiled product (Q4_0, Q8_0, Q5_0, Q4_K, Q5_K) quantize the activations once into the
+  // context's scratch (Q8_0 or Q8_K, whichever the call's formats take) and run the product;
+  // other formats and smaller batches run the matrix-vector kernel, whose workgroups take 8-row
+  // passes of their activation rows through LDS (a weight tile read from memory once per
+  // workgroup, not once per pass).
+  auto gemm_format = [&](uint32_t f) {
+    return batch >= jma::kQGemmMinBatch && f != JMODELS_ATTN_WEIGHTS_Q6_K;
+  };
+  int8_t* aq = nullptr;
+  float* as = nullptr;
+  int* asum = nullptr;
   set_device(ctx);
+  bool need_gemm = false;
+  std::vector<uint32_t> pass_fmts;
+  for (const QuantMatrix& m : mats) {
+    if (gemm_format(m.format)) need_gemm = true;
+    else pass_fmts.push_back(m.format);
+  }
+  if (need_gemm) {
+    const uint64_t q_bytes = ((uint64_t)batch * cols + 255u) & ~(uint64_t)255u;
+    const uint64_t s_bytes = ((uint64_t)batch * K * sizeof(float) + 255u) & ~(uint64_t)255u;
+    const uint64_t sum_bytes = kq ? (uint64_t)batch * (cols / 16u) * sizeof(int) : 0u;
+    ctx->qact.reserve(q_bytes + s_bytes + sum_bytes, ctx->stream, "projection activations");
+    aq = (int8_t*)ctx->qact.ptr;
+    as = (float*)((char*)ctx->qact.ptr + q_bytes);
+    asum = kq ? (int*)((char*)ctx->qact.ptr + q_bytes + s_bytes) : nullptr;
+    if (kq)
+      hip_check(jma::launch_q8_k_quant(input, batch, cols, aq, as, asum, ctx->stream),
+                "activation quantization launch");
+    else
+      hip_check(jma::launch_q8_0_quant(input, batch, cols, aq, as, ctx->stream),
+                "activation quantization launch");
+  }
+  jma::QMatPlan qp;
+  if (!pass_fmts.empty()) {
+    qp = jma::plan_qmat(pass_fmts.data(), (uint32_t)pass_fmts.size(), cols);
+    require(qp.rows_per_tile > 0, JMODELS_ATTN_INVALID_SHAPE,
+            "cols too large for the device projection: " + std::to_string(cols));
+  }
   for (uint32_t fmt = 0; fmt <= JMODELS_ATTN_WEIGHTS_Q5_0; ++fmt) {
+    const bool gemm = gemm_format(fmt);
+    const uint32_t R = gemm ? jma::kQGemmTile : qp.rows_per_tile;
     jma::QMatArgs a{};
     a.x = input;
     a.batch = batch;
     a.cols = cols;
     a.blocks = K;
-    a.rows_per_tile = qp.rows_per_tile;
+    a.rows_per_tile = R;
     a.chunk = qp.chunk;
     a.addend_mode = addend_mode;
     uint32_t tiles = 0;
@@ -840,15 +833,24 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
         q.addend = m.addend;
         q.rows = m.rows;
         q.tile0 = tiles;
-        tiles += (m.rows + qp.rows_per_tile - 1) / qp.rows_per_tile;
+        tiles += (m.rows + R - 1) / R;
       }
       out_off += (uint64_t)batch * m.rows;
     }
     if (a.count == 0) continue;
-    a.group_rows = jma::qmat_group_rows(batch, qp.chunk, tiles);
-    require((batch + a.group_rows - 1) / a.group_rows <= 65535u, JMODELS_ATTN_INVALID_SHAPE,
-            "batch_size too large for one projection launch: " + std::to_string(batch));
-    hip_check(jma::launch_qmatvec(a, fmt, tiles, ctx->stream), "quantized matmul launch");
+    if (gemm) {
+      require((batch + jma::kQGemmTile - 1) / jma::kQGemmTile <= 65535u, JMODELS_ATTN_INVALID_SHAPE,
+              "batch_size too large for one projection launch: " + std::to_string(batch));
+      if (kq)
+        hip_check(jma::launch_qkgemm(a, fmt, tiles, aq, as, asum, ctx->stream), "quantized matmul launch");
+      else
+        hip_check(jma::launch_qgemm(a, fmt, tiles, aq, as, ctx->stream), "quantized matmul launch");
+    } else {
+      a.group_rows = jma::qmat_group_rows(batch, qp.chunk, tiles);
+      require((batch + a.group_rows - 1) / a.group_rows <= 65535u, JMODELS_ATTN_INVALID_SHAPE,
+              "batch_size too large for one projection launch: " + std::to_string(batch));
+      hip_check(jma::launch_qmatvec(a, fmt, tiles, ctx->stream), "quantized matmul launch");
+    }
   }
 }
 

@@ -102,11 +102,13 @@ def test_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
 
 @pytest.mark.parametrize("fmt", [A.WEIGHTS_Q4_K, A.WEIGHTS_Q5_K, A.WEIGHTS_Q6_K])
 @pytest.mark.parametrize("batch,rows,cols", [(1, 1, 256), (1, 3072, 2048), (3, 17, 4096),
-                                             (9, 100, 512), (1, 64, 14336)])
+                                             (9, 100, 512), (1, 64, 14336), (16, 65, 512),
+                                             (17, 130, 1024), (300, 96, 2048), (70, 3, 14336)])
 def test_kquant_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
     """Q4_K, Q5_K and Q6_K with Q8_K activations: the device repeats backend-native's scalar row
     kernels' float order (the integer parts are exact in any order), so the outputs are the
-    oracle's bits; batches over 8 run in chunks."""
+    oracle's bits; batches of 16 rows and more run Q4_K and Q5_K as the register-tiled product
+    (ragged tile edges in both dimensions included), Q6_K in 8-row passes."""
     w = _kquant_weights(fmt, rows, cols, f"kq/{fmt}/{rows}/{cols}")
     x = synth.normal(11, f"kq/x/{batch}/{cols}", (batch, cols)) * 1.5
     got = hip.quantized_matmul(fmt, w, x, batch, rows, cols)

@@ -46,4 +46,4 @@ def test_projection_launches_stay_in_bounds(tmp_path):
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert run.returncode == 0, run.stdout + run.stderr
     assert run.stdout.strip().endswith("ok"), run.stdout
-    assert "grouped 2048 rows, biases" in run.stdout
+    assert "grouped 2048 rows, biases" in run.stdout and "product" in run.stdout
