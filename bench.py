@@ -665,16 +665,20 @@ def run_proj(hip, A, rt, synth, reps: int = 20, per_graph: int = 32):
         for d in dws + [dwo, dx, dqkv, dres]:
             d.free()
     # Prefill-sized: C3's Llama-3.2-3B Q (3072 rows), K and V (1024 each) over 3072 inputs for
-    # the 2048-row prompt, one grouped call (one launch per format), events around 3 replays.
+    # the 2048-row prompt, one grouped call (one launch per format; q4_k_m: Q and K in Q4_K, V in
+    # Q6_K, as Q4_K_M files store them), events around 3 replays.
     cols, rows, batch = 3072, [3072, 1024, 1024], 2048
     dx = rt.DeviceArray.from_host(synth.normal(9, "bench/proj/xp", (batch, cols)))
     dqkv = rt.DeviceArray(batch * sum(rows))
-    for name, fmt in (("q4_0", A.WEIGHTS_Q4_0), ("q8_0", A.WEIGHTS_Q8_0), ("q4_k", A.WEIGHTS_Q4_K)):
-        ws = [_gguf_weights(synth, fmt, r, cols, f"bench/projp/{name}/{i}") for i, r in enumerate(rows)]
+    q4k, q6k = A.WEIGHTS_Q4_K, A.WEIGHTS_Q6_K
+    for name, fmts in (("q4_0", [A.WEIGHTS_Q4_0] * 3), ("q8_0", [A.WEIGHTS_Q8_0] * 3),
+                       ("q4_k", [q4k] * 3), ("q4_k_m", [q4k, q4k, q6k]), ("q6_k", [q6k] * 3)):
+        ws = [_gguf_weights(synth, f, r, cols, f"bench/projp/{name}/{i}")
+              for i, (f, r) in enumerate(zip(fmts, rows))]
         dws = [rt.DeviceArray.from_host(w) for w in ws]
 
         def qkv_prefill():
-            hip.quantized_grouped_matmul_device([fmt] * 3, [d.ptr for d in dws], [w.size for w in ws],
+            hip.quantized_grouped_matmul_device(fmts, [d.ptr for d in dws], [w.size for w in ws],
                                                 rows, dx.ptr, batch * cols, dqkv.ptr, dqkv.count,
                                                 batch, cols)
 

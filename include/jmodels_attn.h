@@ -351,11 +351,10 @@ JMODELS_ATTN_API int32_t jmodels_attn_prefill_device(jmodels_attn_context* ctx, 
  * K-quant kernels to 2e-3 of the Java path). One call takes either 32-element block formats or
  * K-quants, not both (their activation formats differ).
  *
- * Batches of 16 activation rows and more run every format but Q6_K as a register-tiled matrix
- * product on activations quantized once into the context's scratch (the same bits as the
- * matrix-vector path); such a call made while the stream is captured returns NOT_CAPTURABLE when
- * that scratch must grow first (make the call once outside the capture). Smaller batches, and
- * Q6_K matrices, use no scratch memory.
+ * Batches of 16 activation rows and more run as a register-tiled matrix product on activations
+ * quantized once into the context's scratch (the same bits as the matrix-vector path); such a
+ * call made while the stream is captured returns NOT_CAPTURABLE when that scratch must grow first
+ * (make the call once outside the capture). Smaller batches use no scratch memory.
  *
  * Device pointers, asynchronous on the context stream. weights:
  * [rows][cols / 32 or cols / 256] blocks, 2-byte aligned; input [batch][cols] f32, 16-byte

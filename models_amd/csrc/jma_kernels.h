@@ -196,8 +196,8 @@ hipError_t launch_q8_0_quant(const float* x, uint32_t batch, uint32_t cols, int8
                              float* scales, hipStream_t stream);
 hipError_t launch_qgemm(const QMatArgs& a, uint32_t fmt, uint32_t tiles, const int8_t* aq,
                         const float* as, hipStream_t stream);
-// The same for Q4_K (fmt 2) and Q5_K (fmt 4) on Q8_K activations: q int8 [batch][cols], scales
-// [batch][cols / 256], sums int [batch][cols / 16].
+// The same for Q4_K (fmt 2), Q6_K (fmt 3) and Q5_K (fmt 4) on Q8_K activations: q int8
+// [batch][cols], scales [batch][cols / 256], sums int [batch][cols / 16] (Q6_K reads no sums).
 hipError_t launch_q8_k_quant(const float* x, uint32_t batch, uint32_t cols, int8_t* q,
                              float* scales, int* sums, hipStream_t stream);
 hipError_t launch_qkgemm(const QMatArgs& a, uint32_t fmt, uint32_t tiles, const int8_t* aq,

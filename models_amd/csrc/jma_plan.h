@@ -244,9 +244,9 @@ constexpr uint64_t kQMatLds = 64u * 1024u;   // dynamic LDS a projection workgro
 constexpr uint32_t kQMatMaxChunk = 8;        // activation rows per pass
 constexpr uint32_t kQMatTargetBlocks = 1024;  // workgroups a projection launch aims for
 
-// Batches of at least kQGemmMinBatch activation rows run every format but Q6_K as a register-tiled
-// product (qgemm_kernel, qkgemm_kernel): tiles of kQGemmTile weight rows x kQGemmTile activation
-// rows, kQGemmKc 32-element blocks (or one 256-element block) staged per step.
+// Batches of at least kQGemmMinBatch activation rows run as a register-tiled product
+// (qgemm_kernel, qkgemm_kernel, q6gemm_kernel): tiles of kQGemmTile weight rows x kQGemmTile
+// activation rows, kQGemmKc 32-element blocks (or one 256-element block) staged per step.
 constexpr uint32_t kQGemmMinBatch = 16;
 constexpr uint32_t kQGemmTile = 64;
 constexpr uint32_t kQGemmKc = 4;

@@ -25,6 +25,7 @@ namespace jma {
 namespace {
 
 constexpr uint32_t kQThreads = 256;
+typedef short short2_t __attribute__((ext_vector_type(2)));
 
 template <int kCtrl>
 __device__ __forceinline__ int dpp_int(int x) {
@@ -850,6 +851,186 @@ __global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, 
   }
 }
 
+// The register-tiled product of Q6_K weights on Q8_K activations, with the float order of
+// dot_q6_k_q8_k_row_scalar (RS:3519-3577): per 256-element block eight integer lane sums (lane l
+// takes the elements whose index within their 32-element run is l, l + 8, l + 16 or l + 24, in
+// both 128-element halves), then lane_l = fma(d * as, isum_l, lane_l) for l = 0..7; after the last
+// block the eight lanes are added in order to 0. One block per step: each weight quant is staged
+// with its 16-element sub-block scale applied (16 bits: scale x (quant - 32)) and each activation
+// as 16 bits, both in lane-major order (int16 index 32 l + 16 half + 4 run + i / 8 for element
+// 128 half + 32 run + i), so a lane's integer sum is 16 v_dot2_i32_i16 over 64 contiguous bytes;
+// integer sums are exact in any order. Tiles of kQGemmTile x kQGemmTile outputs, 4 x 4 per thread,
+// each output with its eight lane chains.
+__global__ __launch_bounds__(kQThreads, 2) void q6gemm_kernel(const QMatArgs a, const int8_t* aq,
+                                                              const float* as) {
+  constexpr uint32_t T = kQGemmTile, kRow = 256u + 8u, kBB = 210u;  // int16 per staged row
+  __shared__ __attribute__((aligned(16))) int16_t s_w[T * kRow];
+  __shared__ __attribute__((aligned(16))) int16_t s_a[T * kRow];
+  __shared__ float s_d[T], s_as[T];
+  const uint32_t KB = a.blocks, cols = a.cols, batch = a.batch;
+  uint32_t mi = 0;
+  for (uint32_t i = 1; i < a.count; ++i) mi = blockIdx.x >= a.m[i].tile0 ? i : mi;
+  const uint8_t* w = a.m[mi].w;
+  float* out = a.m[mi].out;
+  const float* addend = a.m[mi].addend;
+  const uint32_t rows = a.m[mi].rows;
+  const uint32_t r0 = (blockIdx.x - a.m[mi].tile0) * T, b0 = blockIdx.y * T;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t ti = tid / 16u, tj = tid % 16u;
+  // Staging: row tid / 4, part tid % 4 = 128-element half (part / 2) and elements i0 .. i0 + 15 of
+  // its four 32-element runs (i0 = 16 (part % 2)), which land in dword (8 half + 2 run + part % 2)
+  // of each lane's 16.
+  const uint32_t su_row = tid / 4u, part = tid % 4u, half = part >> 1, i0 = (part & 1u) * 16u;
+  const bool w_ok = r0 + su_row < rows, a_ok = b0 + su_row < batch;
+  const uint8_t* w_row = w + (uint64_t)min(r0 + su_row, rows - 1) * KB * kBB;
+  const uint64_t arow = min(b0 + su_row, batch - 1);
+  uint32_t* const sw_row = (uint32_t*)(s_w + su_row * kRow) + 8u * half + (part & 1u);
+  uint32_t* const sa_row = (uint32_t*)(s_a + su_row * kRow) + 8u * half + (part & 1u);
+
+  float acc[4][4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) acc[i][j][l] = 0.0f;
+
+  // 16 bytes at a 2-byte aligned address, as four words.
+  auto load16 = [](const uint8_t* p, uint32_t (&x)[4]) {
+    const uint16_t* h = (const uint16_t*)p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
+  };
+  // Byte t of four words.
+  auto byte_of = [](const uint32_t (&x)[4], int t) -> uint32_t { return (x[t >> 2] >> (8 * (t & 3))) & 0xFFu; };
+
+  for (uint32_t kb = 0; kb < KB; ++kb) {
+    {
+      // Weights: ql bytes i0.. of both 32-byte runs of this half, qh bytes i0.., the four
+      // sub-block scales of runs 0..3 (scale index 8 half + i0 / 16 + 2 run), d.
+      uint32_t la[4] = {0u, 0u, 0u, 0u}, lb[4] = {0u, 0u, 0u, 0u}, hb[4] = {0u, 0u, 0u, 0u};
+      int sc[4] = {0, 0, 0, 0};
+      if (w_ok) {
+        const uint8_t* blk = w_row + (uint64_t)kb * kBB;
+        load16(blk + 64u * half + i0, la);
+        load16(blk + 64u * half + 32u + i0, lb);
+        load16(blk + 128u + 32u * half + i0, hb);
+        const uint16_t* sch = (const uint16_t*)(blk + 192u + 8u * half);  // scales 8 half .. + 7
+        uint32_t s8[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s8[i] = sch[i];
+#pragma unroll
+        for (int run = 0; run < 4; ++run) {
+          // scale byte i0 / 16 + 2 run: word run, low byte when i0 = 0, high byte otherwise
+          const uint32_t b = (s8[run] >> (i0 == 0u ? 0 : 8)) & 0xFFu;
+          sc[run] = (int)(int8_t)b;
+        }
+        if (part == 0) s_d[su_row] = f16_bits_to_float(((const uint16_t*)blk)[104]);
+      } else if (part == 0) {
+        s_d[su_row] = 0.0f;
+      }
+      // Element i0 + t of run `run`: the low nibble of la (runs 0, 2: low / high nibble) or lb
+      // (runs 1, 3), the high bits 2 run of hb; elements t and t + 8 share a lane and fill its
+      // dword's low and high halves.
+#pragma unroll
+      for (int run = 0; run < 4; ++run) {
+        const uint32_t(&lo)[4] = (run & 1) ? lb : la;
+        const int shift = (run >> 1) * 4;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          int v[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int t = l + 8 * e;
+            const int q = (int)(((byte_of(lo, t) >> shift) & 15u) | (((byte_of(hb, t) >> (2 * run)) & 3u) << 4)) - 32;
+            v[e] = w_ok ? sc[run] * q : 0;
+          }
+          sw_row[16 * l + 2 * run] = ((uint32_t)v[0] & 0xFFFFu) | ((uint32_t)v[1] << 16);
+        }
+      }
+      // Activations: bytes i0 .. i0 + 15 of each 32-element run of this half.
+      uint4 av[4] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u),
+                     make_uint4(0u, 0u, 0u, 0u)};
+      float asc = 0.0f;
+      if (a_ok) {
+        const int8_t* pa = aq + arow * cols + kb * 256u + 128u * half + i0;
+#pragma unroll
+        for (int run = 0; run < 4; ++run) av[run] = *(const uint4*)(pa + 32u * run);
+        asc = as[arow * KB + kb];
+      }
+#pragma unroll
+      for (int run = 0; run < 4; ++run) {
+        const uint32_t x[4] = {av[run].x, av[run].y, av[run].z, av[run].w};
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const int v0 = (int)(int8_t)byte_of(x, l), v1 = (int)(int8_t)byte_of(x, l + 8);
+          sa_row[16 * l + 2 * run] = ((uint32_t)v0 & 0xFFFFu) | ((uint32_t)v1 << 16);
+        }
+      }
+      if (part == 0) s_as[su_row] = asc;
+    }
+    __syncthreads();
+    float dd[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma clang fp contract(off)
+        dd[i][j] = s_d[4u * ti + i] * s_as[4u * tj + j];
+      }
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      int isum[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) isum[i][j] = 0;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {  // lane l's 16 dwords, four at a time
+        uint4 wv[4], avv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wv[i] = *(const uint4*)(s_w + (4u * ti + i) * kRow + 32u * l + 8u * qd);
+          avv[i] = *(const uint4*)(s_a + (4u * tj + i) * kRow + 32u * l + 8u * qd);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            int d = isum[i][j];
+            d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].x), __builtin_bit_cast(short2_t, avv[j].x), d, false);
+            d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].y), __builtin_bit_cast(short2_t, avv[j].y), d, false);
+            d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].z), __builtin_bit_cast(short2_t, avv[j].z), d, false);
+            d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].w), __builtin_bit_cast(short2_t, avv[j].w), d, false);
+            isum[i][j] = d;
+          }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j][l] = __builtin_fmaf(dd[i][j], (float)isum[i][j], acc[i][j][l]);
+    }
+    __syncthreads();  // the next block overwrites the stages
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t b = b0 + 4u * tj + j;
+    if (b >= batch) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = r0 + 4u * ti + i;
+      if (r >= rows) continue;
+      const uint64_t o = (uint64_t)b * rows + r;
+      float v = 0.0f;
+#pragma unroll
+      for (int l = 0; l < 8; ++l) v = v + acc[i][j][l];
+      if (a.addend_mode == 1) v = v + addend[r];
+      else if (a.addend_mode == 2) v = v + addend[o];
+      out[o] = v;
+    }
+  }
+}
+
 hipError_t launch_q8_k_quant(const float* x, uint32_t batch, uint32_t cols, int8_t* q,
                              float* scales, int* sums, hipStream_t stream) {
   const uint64_t units = (uint64_t)batch * (cols / 256u) * 32u;
@@ -866,6 +1047,8 @@ hipError_t launch_qkgemm(const QMatArgs& a, uint32_t fmt, uint32_t tiles, const 
     hipLaunchKernelGGL(qkgemm_kernel<2>, grid, dim3(kQThreads), 0, stream, a, aq, as, asum);
   else if (fmt == 4)
     hipLaunchKernelGGL(qkgemm_kernel<4>, grid, dim3(kQThreads), 0, stream, a, aq, as, asum);
+  else if (fmt == 3)
+    hipLaunchKernelGGL(q6gemm_kernel, grid, dim3(kQThreads), 0, stream, a, aq, as);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

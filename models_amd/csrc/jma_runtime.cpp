@@ -772,15 +772,12 @@ void quantized_matmul_impl(jmodels_attn_context* ctx, const std::vector<QuantMat
   require(output_elements >= (uint64_t)batch * total_rows, JMODELS_ATTN_BUFFER_TOO_SMALL,
           "output holds " + std::to_string(output_elements) + " elements, needs " +
               std::to_string((uint64_t)batch * total_rows));
-  // Launches, one per weight format of the call. Prefill-sized batches of the formats with a
-  // register-tiled product (Q4_0, Q8_0, Q5_0, Q4_K, Q5_K) quantize the activations once into the
-  // context's scratch (Q8_0 or Q8_K, whichever the call's formats take) and run the product;
-  // other formats and smaller batches run the matrix-vector kernel, whose workgroups take 8-row
-  // passes of their activation rows through LDS (a weight tile read from memory once per
+  // Launches, one per weight format of the call. Prefill-sized batches quantize the activations
+  // once into the context's scratch (Q8_0 or Q8_K, whichever the call's formats take) and run the
+  // register-tiled product; smaller batches run the matrix-vector kernel, whose workgroups take
+  // 8-row passes of their activation rows through LDS (a weight tile read from memory once per
   // workgroup, not once per pass).
-  auto gemm_format = [&](uint32_t f) {
-    return batch >= jma::kQGemmMinBatch && f != JMODELS_ATTN_WEIGHTS_Q6_K;
-  };
+  auto gemm_format = [&](uint32_t) { return batch >= jma::kQGemmMinBatch; };
   int8_t* aq = nullptr;
   float* as = nullptr;
   int* asum = nullptr;

@@ -2,9 +2,9 @@
 // with g++ and AddressSanitizer / UndefinedBehaviorSanitizer by tests/test_plan_cpu.py.
 //
 // For each call below it routes every weight format the way quantized_matmul_impl does and plans
-// its launch with the runtime's own planner (jma_plan.h): prefill-sized batches of the formats
-// with a register-tiled product (qgemm_kernel, qkgemm_kernel) take tiles of kQGemmTile rows x
-// kQGemmTile activation rows over activations quantized once into scratch; the others run the
+// its launch with the runtime's own planner (jma_plan.h): prefill-sized batches run the
+// register-tiled product (qgemm_kernel, qkgemm_kernel, q6gemm_kernel) in tiles of kQGemmTile rows
+// x kQGemmTile activation rows over activations quantized once into scratch; the others run the
 // matrix-vector kernels (plan_qmat, qmat_group_rows), whose workgroups take `chunk` activation
 // rows per pass. It then walks every workgroup (x, y) of every launch the way the kernels index
 // memory: the matrix a workgroup serves (the last with tile0 <= x), its weight blocks, the
@@ -40,7 +40,7 @@ struct Call {
 };
 
 // The routing of quantized_matmul_impl.
-bool gemm_format(uint32_t fmt, uint32_t batch) { return batch >= jma::kQGemmMinBatch && fmt != 3; }
+bool gemm_format(uint32_t, uint32_t batch) { return batch >= jma::kQGemmMinBatch; }
 
 struct Buffers {
   std::vector<uint8_t*> w;
@@ -73,6 +73,8 @@ std::vector<M> table(const Call& c, uint32_t fmt, uint32_t R, uint32_t& tiles) {
 
 // qgemm_kernel / qkgemm_kernel: each thread stages one weight block and one activation block per
 // step (rows clamped to the last valid one and skipped past it), every thread writes 4 x 4 outputs.
+// q6gemm_kernel (Q6_K): four threads per row each stage a quarter of the 210-byte block and of the
+// 256 activation bytes into lane-major int16 stages.
 void walk_gemm(const Call& c, uint32_t fmt, Buffers& B) {
   const bool kq = jma::qmat_kquant(fmt);
   const uint32_t T = jma::kQGemmTile, KB = c.cols / jma::qmat_block_elems(fmt);
@@ -85,6 +87,8 @@ void walk_gemm(const Call& c, uint32_t fmt, Buffers& B) {
   const uint32_t gy = (c.batch + T - 1) / T;
   expect(gy <= 65535u, c.name + ": product grid rows");
   int8_t* lds = new int8_t[T * kRow];
+  constexpr uint32_t kRow6 = 256u + 8u;  // q6gemm_kernel's int16 per staged row
+  int16_t* lds16 = new int16_t[T * kRow6];
   for (uint32_t bx = 0; bx < tiles; ++bx) {
     uint32_t mi = 0;
     for (uint32_t i = 1; i < ms.size(); ++i) mi = bx >= ms[i].tile0 ? i : mi;
@@ -97,7 +101,36 @@ void walk_gemm(const Call& c, uint32_t fmt, Buffers& B) {
         const uint32_t su_row = tid / per, su = tid % per;
         const bool w_ok = r0 + su_row < rows, a_ok = b0 + su_row < c.batch;
         const uint64_t wrow = std::min(r0 + su_row, rows - 1), arow = std::min(b0 + su_row, c.batch - 1);
-        for (uint32_t k0 = 0; k0 < KB; k0 += KC) {
+        if (fmt == 3) {  // q6gemm_kernel: int16 stages of kRow6 halves per row
+          const uint32_t half = su >> 1, i0 = (su & 1u) * 16u;
+          for (uint32_t k = 0; k < KB; ++k) {
+            const uint64_t blk = (wrow * KB + k) * bb;
+            if (w_ok) {
+              for (uint32_t off : {64u * half + i0, 64u * half + 32u + i0, 128u + 32u * half + i0})
+                sink = sink + B.w[idx][blk + off] + B.w[idx][blk + off + 15u];
+              sink = sink + B.w[idx][blk + 192u + 8u * half] + B.w[idx][blk + 192u + 8u * half + 7u];
+              if (su == 0) sink = sink + B.w[idx][blk + 208u] + B.w[idx][blk + 209u];
+            }
+            if (a_ok) {
+              for (uint32_t run = 0; run < 4; ++run) {
+                const uint64_t a0 = arow * c.cols + k * 256u + 128u * half + i0 + 32u * run;
+                sink = sink + B.aq[a0] + B.aq[a0 + 15u];
+              }
+              sink = sink + B.as[arow * KB + k];
+            }
+            for (uint32_t l = 0; l < 8; ++l)
+              for (uint32_t run = 0; run < 4; ++run) {
+                const uint32_t dw = su_row * (kRow6 / 2u) + 8u * half + (su & 1u) + 16u * l + 2u * run;
+                lds16[2 * dw] = 0;
+                lds16[2 * dw + 1] = 0;
+              }
+          }
+          const uint32_t ti = tid / 16, tj = tid % 16;
+          for (uint32_t i = 0; i < 4; ++i)
+            for (uint32_t l = 0; l < 8; ++l)
+              sink = sink + lds16[(4 * ti + i) * kRow6 + 32u * l + 31u] + lds16[(4 * tj + i) * kRow6 + 32u * l];
+        }
+        for (uint32_t k0 = 0; fmt != 3 && k0 < KB; k0 += KC) {
           const uint32_t k = kq ? k0 : k0 + su;
           if (k < KB && w_ok) sink = sink + B.w[idx][(wrow * KB + k) * bb] + B.w[idx][(wrow * KB + k) * bb + bb - 1];
           if (k < KB && a_ok) {
@@ -110,7 +143,7 @@ void walk_gemm(const Call& c, uint32_t fmt, Buffers& B) {
           lds[l0 + (kq ? 63u : 31u)] = 0;
         }
         const uint32_t ti = tid / 16, tj = tid % 16;
-        for (uint32_t i = 0; i < 4; ++i)
+        for (uint32_t i = 0; fmt != 3 && i < 4; ++i)
           sink = sink + lds[(4 * ti + i) * kRow + (kq ? 255u : (KC - 1) * 32u + 31u)] + lds[(4 * tj + i) * kRow];
         for (uint32_t j = 0; j < 4; ++j) {
           const uint32_t b = b0 + 4 * tj + j;
@@ -128,6 +161,7 @@ void walk_gemm(const Call& c, uint32_t fmt, Buffers& B) {
     }
   }
   delete[] lds;
+  delete[] lds16;
 }
 
 // qmatvec_kernel / qkmatvec_kernel: the tile's weight units, the activation rows of each pass,
@@ -276,6 +310,8 @@ int main() {
       {"batch 15 (passes)", {5, 1}, {17, 65}, 15, 2080, 2},
       {"ragged product 100 x 200", {0, 5}, {200, 7}, 100, 96, 1},
       {"K-quant product 17 x 65 rows", {4, 2}, {17, 65}, 17, 512, 2},
+      {"Q6_K product 33 x 70 rows", {3, 2, 3}, {70, 33, 1}, 33, 768, 1},
+      {"wide row Q6_K product", {3}, {65}, 20, 14336, 2},
   };
   for (const Call& c : calls) walk(c);
   if (failures) {

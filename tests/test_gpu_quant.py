@@ -107,13 +107,37 @@ def test_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
 def test_kquant_random_shapes_bit_exact(hip, fmt, batch, rows, cols):
     """Q4_K, Q5_K and Q6_K with Q8_K activations: the device repeats backend-native's scalar row
     kernels' float order (the integer parts are exact in any order), so the outputs are the
-    oracle's bits; batches of 16 rows and more run Q4_K and Q5_K as the register-tiled product
-    (ragged tile edges in both dimensions included), Q6_K in 8-row passes."""
+    oracle's bits; batches of 16 rows and more run as the register-tiled product (ragged tile
+    edges in both dimensions included), smaller ones in the matrix-vector kernel."""
     w = _kquant_weights(fmt, rows, cols, f"kq/{fmt}/{rows}/{cols}")
     x = synth.normal(11, f"kq/x/{batch}/{cols}", (batch, cols)) * 1.5
     got = hip.quantized_matmul(fmt, w, x, batch, rows, cols)
     want = oracle.quantized_matmul(fmt, w, x, batch, rows, cols)
     _exact(got, want, f"fmt {fmt} {batch}x{rows}x{cols}")
+
+
+@pytest.mark.parametrize("batch", [5, 32])
+def test_q6_k_extreme_quants_and_scales(hip, batch):
+    """Q6_K at the ends of its ranges: quants 0 and 63 (-32 and 31 after the offset), sub-block
+    scales -128 and 127, activations quantized to +-127, and d = 1; the product stages
+    scale x quant as 16 bits, and every output must still be the oracle's bits (matrix-vector
+    kernel at batch 5, register-tiled product at 32)."""
+    rows, cols = 70, 512
+    raw = np.zeros((rows, cols // 256, 210), np.uint8)
+    for r in range(rows):
+        for b in range(cols // 256):
+            pat = (r + 3 * b) % 4
+            raw[r, b, 0:128] = [0x00, 0xFF, 0x0F, 0xF0][pat]      # low nibbles
+            raw[r, b, 128:192] = [0x00, 0xFF, 0x55, 0xAA][pat]    # high bits
+            raw[r, b, 192:208] = np.array([-128, 127] * 8, np.int8).view(np.uint8) if pat % 2 else \
+                np.array([127, -128] * 8, np.int8).view(np.uint8)
+            raw[r, b, 208:210] = np.array([1.0], np.float16).view(np.uint8)
+    w = raw.reshape(-1)
+    x = np.where(synth.normal(11, f"q6x/{batch}", (batch, cols)) > 0, 1.0, -1.0).astype(np.float32) * 3.0
+    got = hip.quantized_matmul(A.WEIGHTS_Q6_K, w, x, batch, rows, cols)
+    want = oracle.quantized_matmul(A.WEIGHTS_Q6_K, w, x, batch, rows, cols)
+    assert np.max(np.abs(want)) > 1e5  # the extremes are reached
+    _exact(got, want, f"q6_k extremes batch {batch}")
 
 
 def test_kquant_activation_edge_cases_and_grouped_q4_k_m(hip):
@@ -256,11 +280,10 @@ def test_prefill_sized_grouped_projection_with_addends(hip, mode):
 @pytest.mark.parametrize("case", ["q5_0-q8_0-q4_0 bias x300", "q8_0 wo residual x64",
                                   "q4_k-q5_k-q6_k residual x40", "q4_0 graph x96"])
 def test_prefill_sized_projections(hip, case):
-    """Prefill-sized batches in one launch per format: the workgroups of grid row y take 8-row
-    passes of their activation rows through LDS while the weight tile stays resident (read once
-    per workgroup). Grouped calls with biases or residuals (in place for the output projection),
-    mixed 32-element formats, a K-quant mix, and a captured graph replayed three times; every
-    output bit-exact against the oracle."""
+    """Prefill-sized batches in one launch per format (the register-tiled product on activations
+    quantized once). Grouped calls with biases or residuals (in place for the output projection),
+    mixed 32-element formats, a K-quant mix with Q6_K, and a captured graph replayed three times;
+    every output bit-exact against the oracle."""
     kq = case.startswith("q4_k")
     if case.startswith("q5_0"):
         fmts, rows, batch, cols, mode = [A.WEIGHTS_Q5_0, A.WEIGHTS_Q8_0, A.WEIGHTS_Q4_0], [896, 128, 128], 300, 896, A.ADDEND_BIAS
