@@ -888,8 +888,9 @@ def main() -> int:
     proj = None
     if not args.no_proj:
         proj = run_proj(hip, A, rt, synth)
-        log("projections (us, GB/s of weights): " + ", ".join(
-            f"{k} {v['us']:.2f} {v['gbs']:.0f}" for k, v in proj.items()))
+        log("projections (us, then GB/s of weights at decode or integer TOPS at prefill size): " +
+            ", ".join(f"{k} {v['us']:.2f} " + (f"{v['gbs']:.0f}" if "gbs" in v else f"{v['tops']:.1f}")
+                      for k, v in proj.items()))
     hip.close()
 
     value = c2["algo_bytes"] / c2["elapsed"] / 1e9

@@ -130,7 +130,43 @@ struct PrefillPlan {
   uint32_t row_blocks = 0, split_blocks = 0, pairs = 0;
   size_t part_bytes = 0;
 };
-PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t cus);
+
+// Stripes (32-column query groups) and kv groups of one prefill_kernel workgroup at head dim d.
+constexpr int prefill_stripes(int d) { return d >= 256 ? 2 : 4; }
+constexpr int kPrefillKvGroups = 2;
+
+inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t cus) {
+  if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return PrefillPlan{};
+  const uint32_t S = (uint32_t)prefill_stripes(dk);
+  PrefillPlan p;
+  const uint32_t rows_per_block = S * a.rows_per_stripe;
+  p.row_blocks = (a.n + rows_per_block - 1) / rows_per_block;
+  const uint64_t per_block = (uint64_t)a.head_groups * a.num_kv_heads;  // workgroups per row block
+  auto tiles_of = [&](uint32_t rb) {  // kv tiles row block rb sees
+    const uint32_t r0 = rb * rows_per_block, r1 = std::min(r0 + rows_per_block, a.n) - 1;
+    const uint32_t w = a.window, p0 = a.start + r0;
+    const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
+    return (a.start + r1) / 32 + 1 - first / 32;
+  };
+  uint32_t min_tiles = (uint32_t)std::max(split_tiles, 2);
+  if (split_tiles < 0) {
+    // Automatic: a block is split when it holds more than 1.5x the tiles the average compute unit
+    // runs, and at least 48 (the exchange of the halves' partials, through device-coherent
+    // memory, costs about as much as 12 tiles): otherwise the longest blocks set the duration.
+    uint64_t total = 0;
+    for (uint32_t rb = 0; rb < p.row_blocks; ++rb) total += tiles_of(rb);
+    const uint64_t per_cu = total * per_block / std::max<uint32_t>(cus, 1);
+    min_tiles = (uint32_t)std::max<uint64_t>(48, per_cu * 3 / 2 + 1);
+  }
+  if (split_tiles < 0 || split_tiles >= 2) {
+    // Split the longest blocks, from the last one down.
+    while (p.split_blocks < p.row_blocks && tiles_of(p.row_blocks - 1 - p.split_blocks) >= min_tiles)
+      ++p.split_blocks;
+  }
+  p.pairs = p.split_blocks * (uint32_t)per_block;
+  p.part_bytes = (size_t)p.pairs * 2 * (S * ((dk / 8) * 64 + 32) + S * kPrefillKvGroups) * 16;
+  return p;
+}
 
 // Fixed device scratch of the allocation-free decode entry point: one file-scope array per GPU
 // (in jma_kernels.hip), split into the regions a decode launch may need. Every call on a GPU
@@ -151,10 +187,19 @@ hipError_t fixed_scratch(int device, hipStream_t stream, FixedScratch* out);
 // Restores the exchange regions of `device`'s array (after a reducer gave up waiting).
 hipError_t fixed_scratch_reset(const FixedScratch& s, hipStream_t stream);
 
-bool decode_supported(bool f16, int dk, int dv);
-bool prefill_supported(int dk, int dv);
+inline bool decode_supported(bool f16, int dk, int dv) {
+  if (dk != dv) return false;
+  if (f16) return dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
+  return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
+}
+inline bool prefill_supported(int dk, int dv) {
+  return dk == dv && (dk == 32 || dk == 64 || dk == 128 || dk == 256);
+}
 // Shapes of the d-sliced prefill kernel: f32 caches at head dims 32-512, f16 caches at 512.
-bool prefill_slice_supported(bool f16, int dk, int dv);
+inline bool prefill_slice_supported(bool f16, int dk, int dv) {
+  if (dk != dv) return false;
+  return f16 ? dk == 512 : (dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512);
+}
 
 hipError_t launch_append(const AppendArgs& a, bool f16, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStream_t stream);

@@ -1560,11 +1560,6 @@ hipError_t fixed_scratch(int device, hipStream_t stream, FixedScratch* out) {
   return hipSuccess;
 }
 
-bool decode_supported(bool f16, int dk, int dv) {
-  if (dk != dv) return false;
-  if (f16) return dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
-  return dk == 16 || dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512;
-}
 
 template <typename KV, bool kSimple, bool kNT, bool kPack>
 static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream) {
@@ -1699,7 +1694,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // Stripes (32-column query groups) and kv groups of one workgroup per head dimension.
-template <int D> struct Shape { static constexpr int S = D >= 256 ? 2 : 4, Q = 2; };
+template <int D> struct Shape { static constexpr int S = prefill_stripes(D), Q = kPrefillKvGroups; };
 
 }  // namespace pf
 
@@ -2641,52 +2636,6 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
   }
 }
 
-bool prefill_supported(int dk, int dv) {
-  return dk == dv && (dk == 32 || dk == 64 || dk == 128 || dk == 256);
-}
-
-template <int D>
-PrefillPlan plan_prefill_t(const PrefillArgs& a, int split_tiles, uint32_t cus) {
-  constexpr int S = pf::Shape<D>::S;
-  PrefillPlan p;
-  const uint32_t rows_per_block = S * a.rows_per_stripe;
-  p.row_blocks = (a.n + rows_per_block - 1) / rows_per_block;
-  const uint64_t per_block = (uint64_t)a.head_groups * a.num_kv_heads;  // workgroups per row block
-  auto tiles_of = [&](uint32_t rb) {  // kv tiles row block rb sees
-    const uint32_t r0 = rb * rows_per_block, r1 = std::min(r0 + rows_per_block, a.n) - 1;
-    const uint32_t w = a.window, p0 = a.start + r0;
-    const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
-    return (a.start + r1) / 32 + 1 - first / 32;
-  };
-  uint32_t min_tiles = (uint32_t)std::max(split_tiles, 2);
-  if (split_tiles < 0) {
-    // Automatic: a block is split when it holds more than 1.5x the tiles the average compute unit
-    // runs, and at least 48 (the exchange of the halves' partials, through device-coherent
-    // memory, costs about as much as 12 tiles): otherwise the longest blocks set the duration.
-    uint64_t total = 0;
-    for (uint32_t rb = 0; rb < p.row_blocks; ++rb) total += tiles_of(rb);
-    const uint64_t per_cu = total * per_block / std::max<uint32_t>(cus, 1);
-    min_tiles = (uint32_t)std::max<uint64_t>(48, per_cu * 3 / 2 + 1);
-  }
-  if (split_tiles < 0 || split_tiles >= 2) {
-    // Split the longest blocks, from the last one down.
-    while (p.split_blocks < p.row_blocks && tiles_of(p.row_blocks - 1 - p.split_blocks) >= min_tiles)
-      ++p.split_blocks;
-  }
-  p.pairs = p.split_blocks * (uint32_t)per_block;
-  p.part_bytes = (size_t)p.pairs * 2 * (S * ((D / 8) * 64 + 32) + S * pf::Shape<D>::Q) * 16;
-  return p;
-}
-
-PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, uint32_t cus) {
-  switch (dk) {
-    case 32: return plan_prefill_t<32>(a, split_tiles, cus);
-    case 64: return plan_prefill_t<64>(a, split_tiles, cus);
-    case 128: return plan_prefill_t<128>(a, split_tiles, cus);
-    case 256: return plan_prefill_t<256>(a, split_tiles, cus);
-    default: return PrefillPlan{};
-  }
-}
 
 template <int D>
 hipError_t launch_prefill_t(PrefillArgs a, hipStream_t stream) {
@@ -2715,10 +2664,6 @@ hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stre
   }
 }
 
-bool prefill_slice_supported(bool f16, int dk, int dv) {
-  if (dk != dv) return false;
-  return f16 ? dk == 512 : (dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512);
-}
 
 template <typename KV, int D, int W>
 hipError_t launch_prefill_slice_t(const PrefillArgs& a, hipStream_t stream) {

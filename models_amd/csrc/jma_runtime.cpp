@@ -113,6 +113,30 @@ void reserve_filled(DeviceBuffer& buf, size_t need, int byte, hipStream_t stream
   hip_check(hipStreamSynchronize(stream), "fill scratch");
 }
 
+// IEEE binary16 bits -> float, exactly (subnormals normalised, NaN payloads kept as the compiler's
+// own half-to-float conversion keeps them), for reading an f16 cache back on the host.
+float f16_bits_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
+  if (exp == 0x1Fu) {
+    bits = sign | 0x7F800000u | (man << 13);
+  } else if (exp != 0) {
+    bits = sign | ((exp + 112u) << 23) | (man << 13);
+  } else if (man == 0) {
+    bits = sign;
+  } else {
+    exp = 113u;
+    while ((man & 0x400u) == 0) {
+      man <<= 1;
+      --exp;
+    }
+    bits = sign | (exp << 23) | ((man & 0x3FFu) << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
 int env_int(const char* name, int fallback) {
   const char* v = std::getenv(name);
   if (!v || !*v) return fallback;
@@ -1318,9 +1342,9 @@ int32_t jmodels_attn_kv_read(jmodels_attn_context* ctx, const jmodels_attn_kv* k
     hip_check(hipMemcpy(hv.data(), vbase, hv.size(), hipMemcpyDeviceToHost), "read V");
     auto widen = [&](const unsigned char* src, uint64_t index) -> float {
       if (kv->f16()) {
-        _Float16 h;
+        uint16_t h;
         memcpy(&h, src + index * 2, 2);
-        return (float)h;
+        return f16_bits_to_float(h);
       }
       float f;
       memcpy(&f, src + index * 4, 4);
