@@ -993,8 +993,11 @@ def main() -> int:
         result["projections"] = {
             "workload": "Llama-3.2-1B layer at decode (batch 1): grouped Q/K/V projection (2048 -> "
                         "2048 + 512 + 512) and output projection 2048 x 2048 plus residual, GGUF "
-                        "Q4_0 / Q8_0 / Q4_K / Q6_K weights, activations quantized (Q8_0 or Q8_K) "
-                        "in the launch",
+                        "Q4_0 / Q8_0 / Q5_0 / Q4_K / Q5_K / Q6_K weights, activations quantized "
+                        "(Q8_0 or Q8_K) in the launch (us, GB/s of weights); qkv_prefill2048_*: "
+                        "C3's grouped Q/K/V (3072 -> 3072 + 1024 + 1024) over its 2048-row prompt, "
+                        "activations quantized once, then the register-tiled product (us, integer "
+                        "TOPS); q4_k_m: Q and K in Q4_K, V in Q6_K",
             **proj,
         }
     if not args.no_cpu:
