@@ -33,6 +33,28 @@ __device__ __forceinline__ int dpp_int(int x) {
 }
 constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
 constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+// Once the quads of 8 consecutive lanes hold equal values, row_half_mirror (lane 7 - i within
+// each half row) pairs quad 0 with quad 1 as i ^ 4 would; once those 8-lane groups are equal,
+// row_mirror (lane 15 - i within each row of 16) pairs them as i ^ 8 would.
+constexpr int kHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// A value of the other row of 16 lanes in a 32-lane group (the lane 16 away): v_permlane16_swap
+// with both operands x leaves rows {0, 0, 2, 2} and {1, 1, 3, 3} of x in its two results, so a
+// lane of row 0 finds its partner in the second and a lane of row 1 in the first. Symmetric
+// combinations of the two results give both partners the same bits without choosing.
+__device__ __forceinline__ void rows16(uint32_t x, uint32_t& r0, uint32_t& r1) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  r0 = r[0];
+  r1 = r[1];
+}
+
+// Sum over the 8 consecutive lanes of a group (exact in integers, so the pairing order is free).
+__device__ __forceinline__ int sum8(int x) {
+  x += dpp_int<kQuadXor1>(x);
+  x += dpp_int<kQuadXor2>(x);
+  return x + dpp_int<kHalfMirror>(x);
+}
 
 // ggmlNearestInt (NativeKernelLibraryTest.java:1019-1022): x + 1.5 * 2^23 rounds x to an integer
 // (nearest, ties to even) in the low mantissa bits.
@@ -152,15 +174,35 @@ __device__ __forceinline__ void q8_k_part(const float* xs, uint32_t part, uint2&
       bidx = part * 8u + i;
     }
   }
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float ob = __shfl_xor(best, o, 32), ov = __shfl_xor(bval, o, 32);
-    const uint32_t oi = __shfl_xor(bidx, o, 32);
+  // The block maximum over its 32 lanes under the total order (magnitude, then the lower index
+  // first): the same winner whatever the pairing, so DPP exchanges within rows of 16, then the
+  // two rows of the group through v_permlane16_swap.
+  auto take = [&](float ob, float ov, uint32_t oi) {
     if (ob > best || (ob == best && oi < bidx)) {
       best = ob;
       bval = ov;
       bidx = oi;
     }
+  };
+  auto step = [&](auto ctrl) {
+    constexpr int c = decltype(ctrl)::value;
+    take(__int_as_float(dpp_int<c>(__float_as_int(best))), __int_as_float(dpp_int<c>(__float_as_int(bval))),
+         (uint32_t)dpp_int<c>((int)bidx));
+  };
+  step(std::integral_constant<int, kQuadXor1>{});
+  step(std::integral_constant<int, kQuadXor2>{});
+  step(std::integral_constant<int, kHalfMirror>{});
+  step(std::integral_constant<int, kRowMirror>{});
+  {
+    uint32_t b0, b1, v0, v1, i0, i1;
+    rows16(__float_as_uint(best), b0, b1);
+    rows16(__float_as_uint(bval), v0, v1);
+    rows16(bidx, i0, i1);
+    const float fb0 = __uint_as_float(b0), fb1 = __uint_as_float(b1);
+    const bool second = fb1 > fb0 || (fb1 == fb0 && i1 < i0);
+    best = second ? fb1 : fb0;
+    bval = __uint_as_float(second ? v1 : v0);
+    bidx = second ? i1 : i0;
   }
   int s = 0;
   if (best == 0.0f) {
@@ -181,7 +223,7 @@ __device__ __forceinline__ void q8_k_part(const float* xs, uint32_t part, uint2&
     }
     packed = make_uint2(pk[0], pk[1]);
   }
-  s += __shfl_xor(s, 1, 32);  // two threads make one 16-element sum
+  s += dpp_int<kQuadXor1>(s);  // two threads make one 16-element sum
   sum16 = s;
   scale = best == 0.0f ? 0.0f : 1.0f / (-127.0f / bval);
 }
@@ -384,13 +426,7 @@ __global__ __launch_bounds__(kQThreads) void qkmatvec_kernel(const QMatArgs a) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) dot = __builtin_amdgcn_sdot4((int)nib[i], aq[i], dot, false);
           const int* s16 = act_sum + b * (cols / 16u) + blk * 16u;
-          int qs = sc * dot, ms = mn * (s16[2 * g] + s16[2 * g + 1]);
-          qs += __shfl_xor(qs, 1, 8);
-          qs += __shfl_xor(qs, 2, 8);
-          qs += __shfl_xor(qs, 4, 8);
-          ms += __shfl_xor(ms, 1, 8);
-          ms += __shfl_xor(ms, 2, 8);
-          ms += __shfl_xor(ms, 4, 8);
+          const int qs = sum8(sc * dot), ms = sum8(mn * (s16[2 * g] + s16[2 * g + 1]));
           if (real && sub == 0) {
             const float as = act_scale[b * KB + blk];
             float* tt = terms + (b * R + row) * rs + blk * kNT;
