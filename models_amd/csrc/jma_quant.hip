@@ -542,11 +542,9 @@ __device__ __forceinline__ uint32_t bytes_minus(uint32_t x, uint32_t off4) {
   return ((x | 0x80808080u) - off4) ^ 0x80808080u;
 }
 
-// A weight block as 32 signed int8 (8 words, element order) and its f32 scale.
+// A loaded weight block as 32 signed int8 (8 words, element order) and its f32 scale.
 template <int FMT>
-__device__ __forceinline__ void gemm_weight_block(const uint16_t* rec, uint32_t (&wd)[8], float& scale) {
-  QBlock<FMT> blk;
-  blk.load(rec);
+__device__ __forceinline__ void gemm_weight_unpack(const QBlock<FMT>& blk, uint32_t (&wd)[8], float& scale) {
   scale = f16_bits_to_float(blk.h[0]);
   if constexpr (FMT == 1) {
 #pragma unroll
@@ -606,31 +604,46 @@ __global__ __launch_bounds__(kQThreads, 2) void qgemm_kernel(const QMatArgs a, c
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
 
+  // This thread's staging unit of one k-step, as loaded (the weight block still packed). The
+  // next step's unit is loaded while the current one is computed, so each step's global loads are
+  // in flight during the previous step's dot products instead of ahead of its own.
+  struct Stage {
+    QBlock<FMT> wb;
+    uint4 a0, a1;
+    float asc;
+    bool w_valid;
+  };
+  auto load_stage = [&](uint32_t k0, Stage& st) {
+    const uint32_t k = k0 + su_k;
+    st.a0 = make_uint4(0u, 0u, 0u, 0u);
+    st.a1 = st.a0;
+    st.asc = 0.0f;
+    st.w_valid = k < K && w_ok;
+    if (st.w_valid) st.wb.load(w_rec + (uint64_t)k * kRecHalves);
+    if (k < K && a_ok) {
+      st.a0 = *(const uint4*)(a_row + k * 32u);
+      st.a1 = *(const uint4*)(a_row + k * 32u + 16u);
+      st.asc = as_row[k];
+    }
+  };
+  Stage st;
+  load_stage(0, st);
   for (uint32_t k0 = 0; k0 < K; k0 += KC) {
     {
-      const uint32_t k = k0 + su_k;
       uint32_t wd[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
       float wsc = 0.0f;
-      uint4 a0 = make_uint4(0u, 0u, 0u, 0u), a1 = a0;
-      float asc = 0.0f;
-      if (k < K) {
-        if (w_ok) gemm_weight_block<FMT>(w_rec + (uint64_t)k * kRecHalves, wd, wsc);
-        if (a_ok) {
-          a0 = *(const uint4*)(a_row + k * 32u);
-          a1 = *(const uint4*)(a_row + k * 32u + 16u);
-          asc = as_row[k];
-        }
-      }
+      if (st.w_valid) gemm_weight_unpack<FMT>(st.wb, wd, wsc);
       uint4* dw = (uint4*)(s_w + su_row * kRow + su_k * 32u);
       dw[0] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
       dw[1] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
       uint4* da = (uint4*)(s_a + su_row * kRow + su_k * 32u);
-      da[0] = a0;
-      da[1] = a1;
+      da[0] = st.a0;
+      da[1] = st.a1;
       s_ws[su_row][su_k] = wsc;
-      s_as[su_row][su_k] = asc;
+      s_as[su_row][su_k] = st.asc;
     }
     __syncthreads();
+    if (k0 + KC < K) load_stage(k0 + KC, st);
     const uint32_t kn = min(KC, K - k0);
     for (uint32_t kb = 0; kb < kn; ++kb) {
       uint4 wv[4][2], av[4][2];
@@ -650,14 +663,17 @@ __global__ __launch_bounds__(kQThreads, 2) void qgemm_kernel(const QMatArgs a, c
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          int d = 0;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            d = __builtin_amdgcn_sdot4((int)wv[i][h].x, (int)av[j][h].x, d, false);
-            d = __builtin_amdgcn_sdot4((int)wv[i][h].y, (int)av[j][h].y, d, false);
-            d = __builtin_amdgcn_sdot4((int)wv[i][h].z, (int)av[j][h].z, d, false);
-            d = __builtin_amdgcn_sdot4((int)wv[i][h].w, (int)av[j][h].w, d, false);
-          }
+          // The block's first dot in the three-operand form with an inline zero accumulator:
+          // the accumulating form the compiler picks would need a register cleared first.
+          int d;
+          asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(d) : "v"((int)wv[i][0].x), "v"((int)av[j][0].x));
+          d = __builtin_amdgcn_sdot4((int)wv[i][0].y, (int)av[j][0].y, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][0].z, (int)av[j][0].z, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][0].w, (int)av[j][0].w, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].x, (int)av[j][1].x, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].y, (int)av[j][1].y, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].z, (int)av[j][1].z, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].w, (int)av[j][1].w, d, false);
           float sc;
           {
 #pragma clang fp contract(off)
