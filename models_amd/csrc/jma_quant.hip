@@ -727,7 +727,10 @@ __global__ __launch_bounds__(kQThreads) void q8_k_quant_kernel(const float* x, u
 // min_g * (the group's two 16-element activation sums), then sum = fma(d * as, qsum, sum) and
 // sum = fma(-(dmin * as), msum, sum). Tiles of kQGemmTile x kQGemmTile outputs, 4 x 4 per thread,
 // one 256-element block staged per step: the quants as bytes (0..31), each row's 6-bit scales and
-// mins, d and dmin; the activations' bytes, scale and per-group sums.
+// mins, d and dmin; the activations' bytes, scale and per-group sums. The integer arithmetic is
+// exact in narrow forms: a group's dot is at most 32 x 31 x 128 in magnitude, so scale_g * dot_g
+// is a 24-bit multiply-add, and mins (0..63) and group sums (at most 32 x 128) are 16-bit, so msum
+// is four v_dot2_i32_i16.
 template <int FMT>
 __global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, const int8_t* aq,
                                                               const float* as, const int* asum) {
@@ -735,8 +738,8 @@ __global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, 
   __shared__ __attribute__((aligned(16))) int8_t s_w[T * kRow];
   __shared__ __attribute__((aligned(16))) int8_t s_a[T * kRow];
   __shared__ __attribute__((aligned(16))) int s_sc[T][8];
-  __shared__ __attribute__((aligned(16))) int s_mn[T][8];
-  __shared__ __attribute__((aligned(16))) int s_gs[T][8];
+  __shared__ __attribute__((aligned(16))) int16_t s_mn[T][8];
+  __shared__ __attribute__((aligned(16))) int16_t s_gs[T][8];
   __shared__ float s_d[T], s_dm[T], s_as[T];
   const uint32_t KB = a.blocks, cols = a.cols, batch = a.batch;
   uint32_t mi = 0;
@@ -794,14 +797,17 @@ __global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, 
 #pragma unroll
           for (int g = 0; g < 8; ++g) {
             s_sc[su_row][g] = g < 4 ? (int)(scb[g] & 63u) : (int)((scb[g + 4] & 15u) | ((scb[g - 4] >> 6) << 4));
-            s_mn[su_row][g] = g < 4 ? (int)(scb[g + 4] & 63u) : (int)((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4));
+            s_mn[su_row][g] = (int16_t)(g < 4 ? (scb[g + 4] & 63u) : ((scb[g + 4] >> 4) | ((scb[g] >> 6) << 4)));
           }
         }
       } else if (part == 0) {
         s_d[su_row] = 0.0f;
         s_dm[su_row] = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 8; ++g) s_sc[su_row][g] = s_mn[su_row][g] = 0;
+        for (int g = 0; g < 8; ++g) {
+          s_sc[su_row][g] = 0;
+          s_mn[su_row][g] = 0;
+        }
       }
       uint4* dw = (uint4*)(s_w + su_row * kRow + part * 64u);
 #pragma unroll
@@ -820,8 +826,8 @@ __global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, 
       uint4* da = (uint4*)(s_a + su_row * kRow + part * 64u);
 #pragma unroll
       for (int i = 0; i < 4; ++i) da[i] = av[i];
-      s_gs[su_row][2 * part] = sm.x + sm.y;
-      s_gs[su_row][2 * part + 1] = sm.z + sm.w;
+      s_gs[su_row][2 * part] = (int16_t)(sm.x + sm.y);
+      s_gs[su_row][2 * part + 1] = (int16_t)(sm.z + sm.w);
       if (part == 0) s_as[su_row] = asc;
     }
     __syncthreads();
@@ -847,25 +853,28 @@ __global__ __launch_bounds__(kQThreads, 2) void qkgemm_kernel(const QMatArgs a, 
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          int d = 0;
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            d = __builtin_amdgcn_sdot4((int)wv[i][hh].x, (int)avv[j][hh].x, d, false);
-            d = __builtin_amdgcn_sdot4((int)wv[i][hh].y, (int)avv[j][hh].y, d, false);
-            d = __builtin_amdgcn_sdot4((int)wv[i][hh].z, (int)avv[j][hh].z, d, false);
-            d = __builtin_amdgcn_sdot4((int)wv[i][hh].w, (int)avv[j][hh].w, d, false);
-          }
-          qsum[i][j] += sc[i] * d;
+          int d;  // first dot in the zero-accumulator form: no register to clear
+          asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(d) : "v"((int)wv[i][0].x), "v"((int)avv[j][0].x));
+          d = __builtin_amdgcn_sdot4((int)wv[i][0].y, (int)avv[j][0].y, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][0].z, (int)avv[j][0].z, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][0].w, (int)avv[j][0].w, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].x, (int)avv[j][1].x, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].y, (int)avv[j][1].y, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].z, (int)avv[j][1].z, d, false);
+          d = __builtin_amdgcn_sdot4((int)wv[i][1].w, (int)avv[j][1].w, d, false);
+          qsum[i][j] += __mul24(sc[i], d);
         }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int4 m0 = *(const int4*)&s_mn[4u * ti + i][0], m1 = *(const int4*)&s_mn[4u * ti + i][4];
+      const uint4 m = *(const uint4*)&s_mn[4u * ti + i][0];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int4 g0 = *(const int4*)&s_gs[4u * tj + j][0], g1 = *(const int4*)&s_gs[4u * tj + j][4];
-        msum[i][j] = m0.x * g0.x + m0.y * g0.y + m0.z * g0.z + m0.w * g0.w + m1.x * g1.x +
-                     m1.y * g1.y + m1.z * g1.z + m1.w * g1.w;
+        const uint4 gs = *(const uint4*)&s_gs[4u * tj + j][0];
+        int t = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, m.x), __builtin_bit_cast(short2_t, gs.x), 0, false);
+        t = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, m.y), __builtin_bit_cast(short2_t, gs.y), t, false);
+        t = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, m.z), __builtin_bit_cast(short2_t, gs.z), t, false);
+        msum[i][j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, m.w), __builtin_bit_cast(short2_t, gs.w), t, false);
       }
     }
 #pragma unroll
@@ -1034,10 +1043,6 @@ __global__ __launch_bounds__(kQThreads, 2) void q6gemm_kernel(const QMatArgs a, 
     for (int l = 0; l < 8; ++l) {
       int isum[4][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) isum[i][j] = 0;
-#pragma unroll
       for (int qd = 0; qd < 4; ++qd) {  // lane l's 16 dwords, four at a time
         uint4 wv[4], avv[4];
 #pragma unroll
@@ -1049,8 +1054,11 @@ __global__ __launch_bounds__(kQThreads, 2) void q6gemm_kernel(const QMatArgs a, 
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            int d = isum[i][j];
-            d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].x), __builtin_bit_cast(short2_t, avv[j].x), d, false);
+            int d;
+            if (qd == 0)  // the lane's first dot in the zero-accumulator form: no register to clear
+              asm("v_dot2_i32_i16 %0, %1, %2, 0" : "=v"(d) : "v"(wv[i].x), "v"(avv[j].x));
+            else
+              d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].x), __builtin_bit_cast(short2_t, avv[j].x), isum[i][j], false);
             d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].y), __builtin_bit_cast(short2_t, avv[j].y), d, false);
             d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].z), __builtin_bit_cast(short2_t, avv[j].z), d, false);
             d = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, wv[i].w), __builtin_bit_cast(short2_t, avv[j].w), d, false);
