@@ -34,6 +34,11 @@ HIPCC_FLAGS = [
     # the decode kernel's seven leading scalar arguments arrive in SGPRs at wave start (kernels
     # whose first argument is a struct preload nothing)
     "-mllvm", "-amdgpu-kernarg-preload-count=7",
+    # matrix-op results and accumulators in ordinary vector registers: the accumulation registers
+    # then hold only what a kernel pins there (the d-512 prefill's q operands) or what exceeds 256
+    # vector registers, instead of every matrix result plus copies (several decode and prefill
+    # instances stop spilling)
+    "-mllvm", "--amdgpu-mfma-vgpr-form=true",
     "-Wall",
     "-Wno-unused-result",
 ]

@@ -195,7 +195,8 @@ inline bool decode_supported(bool f16, int dk, int dv) {
 inline bool prefill_supported(int dk, int dv) {
   return dk == dv && (dk == 32 || dk == 64 || dk == 128 || dk == 256);
 }
-// Shapes of the d-sliced prefill kernel: f32 caches at head dims 32-512, f16 caches at 512.
+// Shapes of the sliced prefills: f32 caches at head dims 32-512 (d-sliced, kernel 3b), f16
+// caches at 512 (stripe pairs, kernel 3c).
 inline bool prefill_slice_supported(bool f16, int dk, int dv) {
   if (dk != dv) return false;
   return f16 ? dk == 512 : (dk == 32 || dk == 64 || dk == 128 || dk == 256 || dk == 512);
@@ -205,7 +206,8 @@ hipError_t launch_append(const AppendArgs& a, bool f16, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool f16, int dk, int dv, hipStream_t stream);
 hipError_t launch_reduce(const DecodeArgs& a, int dv, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stream);
-// rows_per_stripe x heads_per_stripe columns per workgroup, row_blocks = stripes; no split.
+// rows_per_stripe x heads_per_stripe columns per stripe, row_blocks = stripes; one stripe per
+// workgroup (f32) or two (f16); no split.
 hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, hipStream_t stream);
 
 // ---------------------------------------------------------------- block-quantized projections

@@ -3,7 +3,8 @@
 //   kernel 1  rope_append_kernel   RoPE on q and k, K/V store into the HBM-resident cache
 //   kernel 2  decode_kernel        split-K flash-decoding on MFMA, GQA heads share K/V loads
 //   kernel 3  prefill_kernel       causal / sliding-window prefill, f16 MFMA, LDS K/V tiles
-//   kernel 3b prefill_slice_kernel the same for f32 caches and head dim 512, head-dim slices
+//   kernel 3b prefill_slice_kernel the same for f32 caches, head-dim slices
+//   kernel 3c prefill_pair_kernel  the same for f16 caches at head dim 512, stripe pairs
 //   kernel 4  reduce_kernel        cross-split log-sum-exp reduction
 //
 // Reference semantics (paths under backend-java/src/main/java/com/integrallis/models/backend/
@@ -2357,11 +2358,9 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
 
 // ================================================================ kernel 3b: d-sliced prefill
 
-// Causal / sliding-window prefill for the shapes the f16 kernel above cannot hold in registers:
-// f32 caches (head dims 32..512, on the f32 matrix ops, so scores and weighted sums keep f32
-// products as the reference's do) and f16 caches at head dim 512 (Gemma 4 full layers). A
-// workgroup is one stripe of 32 (query row, query head) columns of one kv head, as in the f16
-// kernel, and its W waves cut the head dimension into W slices of DS = D / W: wave w forms the
+// Causal / sliding-window prefill for f32 caches (head dims 32..512, on the f32 matrix ops, so
+// scores and weighted sums keep f32 products as the reference's do). A workgroup is one stripe
+// of 32 (query row, query head) columns of one kv head, as in the f16 kernel, and its W waves cut the head dimension into W slices of DS = D / W: wave w forms the
 // partial scores of each kv tile over its DS dims of q and K, the waves add their partial tiles
 // through LDS in wave order (so every wave holds the same scores, bit for bit), each runs the
 // same online softmax, and wave w accumulates output dims w*DS .. (w+1)*DS - 1 from the same
@@ -2376,19 +2375,16 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
 //    8m + 4 + t. PV: op u (u < 16) takes the lane's own probability u (slot 8(u/4) + 4h + u%4)
 //    as its B operand and V^T at the same slots as A, four consecutive slots per float4 load of
 //    an f32 V block.
-//  f16, v_mfma_f32_32x32x16_f16: as in the f16 kernel (K rows in swap34 order, so the rounded
-//    probabilities are ready PV operands against perm32-ordered V blocks); q and p are rounded
-//    to f16 there too.
 template <typename KV, int D, int W>
 __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs a) {
   using namespace pf;
-  constexpr bool kF16 = std::is_same<KV, _Float16>::value;
+  static_assert(std::is_same<KV, float>::value, "f32 caches (f16 at head dim 512: kernel 3c)");
   constexpr int DS = D / W;                      // dims of this wave's slice
   constexpr int kNb = DS / 32;                   // 32-row blocks of its O^T slice
   static_assert(D % W == 0 && DS % 32 == 0, "head-dim slices of 32-row blocks");
-  constexpr int kKq = kF16 ? DS / 16 : DS / 8;   // K (and q) operand registers per tile
-  constexpr int kVq = kF16 ? 2 * kNb : 4 * kNb;  // V operand registers per tile
-  using Op = typename std::conditional<kF16, half8_t, float4_t>::type;
+  constexpr int kKq = DS / 8;                    // K (and q) operand registers per tile
+  constexpr int kVq = 4 * kNb;                   // V operand registers per tile
+  using Op = float4_t;
   struct Ops {
     Op k[kKq];
     Op v[kVq];
@@ -2434,74 +2430,38 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
     const uint64_t slot0 = a.kv.ring ? (32u * t) % a.kv.cap : 32u * t;
     const KV* const kt = kb + slot0 * D;
     const KV* const vt = vb + slot0 * D;
-    if constexpr (kF16) {
-      // K panels of 32 slots x 32 dims (k_index); row swap34(j).
-      const uint32_t kr = swap34(j);
+    // K panels of 16 slots x 16 dims (k_index): slot j, dims 8m + 4h .. +3.
 #pragma unroll
-      for (int i = 0; i < kKq; ++i) {
-        const uint32_t e = 16 * (w * kKq + i) + 8 * h;
-        op.k[i] = *(const half8_t*)(kt + (e / 32) * 1024 + kr * 32 + e % 32);
-      }
-      // V blocks [32 slots, perm32][D]: row dv, halves 8(2b + h) .. +7.
-#pragma unroll
-      for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          op.v[2 * nb + b] = *(const half8_t*)(vt + (uint64_t)(32 * (w * kNb + nb) + j) * 32 + 8 * (2 * b + h));
-    } else {
-      // K panels of 16 slots x 16 dims (k_index): slot j, dims 8m + 4h .. +3.
-#pragma unroll
-      for (int i = 0; i < kKq; ++i) {
-        const uint32_t m = w * kKq + i;
-        op.k[i] = *(const float4_t*)(kt + (uint64_t)(16 * (j / 16)) * D + (m / 2) * 256 +
-                                     (j % 16) * 16 + 8 * (m % 2) + 4 * h);
-      }
-      // V blocks [16 slots][D]: row dv, slots 8c + 4h .. +3 (block c / 2).
-#pragma unroll
-      for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          op.v[4 * nb + c] = *(const float4_t*)(vt + (uint64_t)(c / 2) * 16 * D +
-                                                (uint64_t)(32 * (w * kNb + nb) + j) * 16 +
-                                                8 * (c % 2) + 4 * h);
+    for (int i = 0; i < kKq; ++i) {
+      const uint32_t m = w * kKq + i;
+      op.k[i] = *(const float4_t*)(kt + (uint64_t)(16 * (j / 16)) * D + (m / 2) * 256 +
+                                   (j % 16) * 16 + 8 * (m % 2) + 4 * h);
     }
+    // V blocks [16 slots][D]: row dv, slots 8c + 4h .. +3 (block c / 2).
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        op.v[4 * nb + c] = *(const float4_t*)(vt + (uint64_t)(c / 2) * 16 * D +
+                                              (uint64_t)(32 * (w * kNb + nb) + j) * 16 +
+                                              8 * (c % 2) + 4 * h);
   };
   // Tile slot of result element e in lane half h.
-  auto slot_of_e = [&](int e) JMA_INL -> uint32_t {
-    return kF16 ? score_slot(e, h) : (uint32_t)(8 * (e >> 2) + 4 * h + (e & 3));
-  };
+  auto slot_of_e = [&](int e) JMA_INL -> uint32_t { return (uint32_t)(8 * (e >> 2) + 4 * h + (e & 3)); };
 
   Ops cur, nxt;
   if (t0 < t1) load(t0, cur);
 
-  // q operands of this wave's slice, scaled by scale * log2(e). f16: a scaled element beyond the
-  // f16 range (where the reference's f32 scores stay finite) is reported like a non-finite score.
+  // q operands of this wave's slice, scaled by scale * log2(e).
   Op qf[kKq];
   {
     const float* const qrow = a.q + ((uint64_t)crow * a.num_heads + head) * D;
     const float qs = col_ok ? a.qscale : 0.0f;
-    if constexpr (kF16) {
-      float qmax = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kKq; ++i) {
-        const uint32_t e = 16 * (w * kKq + i) + 8 * h;
-        const float4_t x0 = *(const float4_t*)(qrow + e);
-        const float4_t x1 = *(const float4_t*)(qrow + e + 4);
+    for (int i = 0; i < kKq; ++i) {
+      const float4_t x = *(const float4_t*)(qrow + 8 * (w * kKq + i) + 4 * h);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          qmax = fmaxf(qmax, fmaxf(fabsf(x0[t] * qs), fabsf(x1[t] * qs)));
-          qf[i][t] = (_Float16)(x0[t] * qs);
-          qf[i][4 + t] = (_Float16)(x1[t] * qs);
-        }
-      }
-      if (__ballot(col_ok && !(qmax < 65520.0f)) != 0 && lane == 0) atomicOr(a.err, 1);
-    } else {
-#pragma unroll
-      for (int i = 0; i < kKq; ++i) {
-        const float4_t x = *(const float4_t*)(qrow + 8 * (w * kKq + i) + 4 * h);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) qf[i][t] = x[t] * qs;
-      }
+      for (int t = 0; t < 4; ++t) qf[i][t] = x[t] * qs;
     }
   }
 
@@ -2517,15 +2477,10 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
     float16_t s;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = 0.0f;
-    if constexpr (kF16) {
 #pragma unroll
-      for (int i = 0; i < kKq; ++i) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(op.k[i], qf[i], s, 0, 0, 0);
-    } else {
+    for (int i = 0; i < kKq; ++i)
 #pragma unroll
-      for (int i = 0; i < kKq; ++i)
-#pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) s = __builtin_amdgcn_mfma_f32_32x32x2f32(op.k[i][t4], qf[i][t4], s, 0, 0, 0);
-    }
+      for (int t4 = 0; t4 < 4; ++t4) s = __builtin_amdgcn_mfma_f32_32x32x2f32(op.k[i][t4], qf[i][t4], s, 0, 0, 0);
     // Every wave adds the W partial tiles in wave order.
     if constexpr (W > 1) {
       float4_t(*const xb)[4][64] = s_x[t & 1];
@@ -2574,42 +2529,23 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
 #pragma unroll
       for (int i = 0; i < kVq; ++i)
 #pragma unroll
-        for (int x = 0; x < (kF16 ? 8 : 4); ++x) {
-          const uint32_t sl = kF16 ? score_slot(8 * (i & 1) + x, h) : (uint32_t)(8 * (i & 3) + 4 * h + x);
-          const uint32_t p = p0 + sl;
+        for (int x = 0; x < 4; ++x) {
+          const uint32_t p = p0 + (uint32_t)(8 * (i & 3) + 4 * h + x);
           if (p < s_first || p > s_last) v.v[i][x] = 0;
         }
     }
-    if constexpr (kF16) {
-      half8_t pf[2];
+    float p[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(s[e] - mu);
-      const half2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const half2_t pr = {pf[i >> 2][2 * (i & 3)], pf[i >> 2][2 * (i & 3) + 1]};
-        if (i & 1) lb = __builtin_amdgcn_fdot2(pr, one, lb, false);
-        else l = __builtin_amdgcn_fdot2(pr, one, l, false);
-      }
-#pragma unroll
-      for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(v.v[2 * nb + b], pf[b], o[nb], 0, 0, 0);
-    } else {
-      float p[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        p[e] = __builtin_amdgcn_exp2f(s[e] - mu);
-        if (e & 1) lb += p[e];
-        else l += p[e];
-      }
-#pragma unroll
-      for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-          o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.v[4 * nb + (u >> 2)][u & 3], p[u], o[nb], 0, 0, 0);
+    for (int e = 0; e < 16; ++e) {
+      p[e] = __builtin_amdgcn_exp2f(s[e] - mu);
+      if (e & 1) lb += p[e];
+      else l += p[e];
     }
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.v[4 * nb + (u >> 2)][u & 3], p[u], o[nb], 0, 0, 0);
   };
 
   // Two tiles per iteration, so the two operand sets stay distinct registers.
@@ -2636,6 +2572,328 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
   }
 }
 
+
+// ================================================================ kernel 3c: paired-stripe prefill
+
+// Causal / sliding-window prefill for f16 caches at head dim 512 (Gemma 4 full layers). A
+// workgroup is two adjacent stripes of 32 (query row, query head) columns of one kv head, and its
+// four waves are (stripe s, head-dim half hf): wave (s, hf) forms stripe s's partial scores over
+// dims 256hf .. 256hf+255, the two waves of a stripe add their partial tiles through LDS (a + b
+// is the same float either way, so both hold the same scores bit for bit) and run the same
+// select-masked online softmax as kernel 3b, and wave (s, hf) accumulates output dims 256hf ..
+// 256hf+255 of its stripe. K and V tiles are staged in LDS once for both stripes (kernel 3b read
+// each tile into registers once per stripe, and per-CU load issue bounded it), by direct-to-LDS
+// loads in kernel 3's layout and swizzles; K and V each alternate between two stage arrays.
+//
+// Per tile t: QK^T over the wave's half (16 matrix ops, K operands read eight ahead), partial
+// tile to LDS, wait for V(t), barrier A; K(t+2) into K(t)'s array; add the partner's partial,
+// read the first eight V operands (their latency passes under the softmax), mask, softmax; PV
+// (16 matrix ops); wait for K(t+1), barrier B; V(t+2) into V(t)'s array. So each tile is
+// loaded about one and a half tiles ahead of use. The pair's tile range is the union of its
+// stripes' (adjacent rows, so at most one tile more than either); a tile a stripe does not see is
+// masked to -inf entirely and adds nothing. Past the pair's last tile the loads repeat that
+// tile, so every wave issues the same loads each step and the load counters count the same.
+//
+// V rows at positions a stripe does not see are fed to its PV product as loaded (probability 0)
+// in the fast pass; a non-finite value there makes the column's state non-finite, and the
+// workgroup then runs again in a robust pass that zeroes those operand elements (as the main
+// prefill kernel does). The q operands live in the accumulation registers (the matrix ops read
+// them there), leaving the vector registers to O^T, the scores and the operands.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) {
+  using namespace pf;
+  static_assert(D == 512, "paired stripes at head dim 512");
+  constexpr int kHalf = D / 2;      // dims of a wave
+  constexpr int kKq = kHalf / 16;   // QK^T k-steps of a wave
+  constexpr int kNb = kHalf / 32;   // 32-row blocks of its O^T
+  constexpr int kT = 32 * D;        // halves of one K (or V^T) tile
+  constexpr int kChunks = D / 16;   // 1 KB chunks per tile
+  constexpr int kCPW = kChunks / 4; // chunks of each tile one wave loads
+  __shared__ __attribute__((aligned(16))) _Float16 ka[kT];
+  __shared__ __attribute__((aligned(16))) _Float16 kb2[kT];
+  __shared__ __attribute__((aligned(16))) _Float16 va[kT];
+  __shared__ __attribute__((aligned(16))) _Float16 vb2[kT];
+  __shared__ float4_t s_x[2][2][4][64];  // partial scores [stripe][half][float4 chunk][lane]
+
+  const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int st = w & 1, hf = w >> 1;
+  // Kv heads vary fastest (consecutive workgroups on different XCDs); pairs run last-first
+  // (longest causal ranges first).
+  const uint32_t pairs = (a.row_blocks + 1) / 2;
+  const uint32_t kvh = blockIdx.x % a.num_kv_heads;
+  const uint32_t rest = blockIdx.x / a.num_kv_heads;
+  const uint32_t hz = rest % a.head_groups;
+  const uint32_t pr = pairs - 1 - rest / a.head_groups;
+  const uint32_t stripe = 2 * pr + st;
+  const bool stripe_ok = stripe < a.row_blocks;
+  const uint32_t R = a.rows_per_stripe, Gz = a.heads_per_stripe;
+  // An absent second stripe (odd stripe count) aliases the first and stores nothing.
+  const uint32_t row0 = min(stripe, a.row_blocks - 1) * R;
+  const uint32_t row_last = min(row0 + R - 1, a.n - 1);
+  const uint32_t cr = min((uint32_t)j / Gz, R - 1);
+  const uint32_t hz_head = hz * Gz + (uint32_t)j % Gz;
+  const bool col_ok = stripe_ok && (uint32_t)j < R * Gz && row0 + cr < a.n && hz_head < a.group;
+  const uint32_t crow = min(row0 + cr, a.n - 1);
+  const uint32_t head = kvh * a.group + min(hz_head, a.group - 1);
+  const uint32_t cpos = a.start + crow;
+  const uint32_t cfirst = first_visible(cpos, a.window);
+  // Positions some column of the stripe sees, [s_first, s_last], and those every column sees,
+  // [all_first, all_last] (first_visible does not decrease with the position).
+  const uint32_t s_first = first_visible(a.start + row0, a.window);
+  const uint32_t s_last = a.start + row_last;
+  const uint32_t all_first = first_visible(s_last, a.window);
+  const uint32_t all_last = a.start + row0;
+  // The pair's tiles (the same for every wave).
+  const uint32_t p_row0 = 2 * pr * R;
+  const uint32_t p_last = min(p_row0 + 2 * R - 1, a.n - 1);
+  const uint32_t t0 = first_visible(a.start + p_row0, a.window) / 32;
+  const uint32_t t1 = (a.start + p_last) / 32 + 1;
+
+  const _Float16* const kbase = (const _Float16*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
+                                (uint64_t)kvh * a.kv.cap * D;
+  const _Float16* const vbase = (const _Float16*)a.kv.v + a.seq * a.kv.seq_stride_v + a.kv.layer_off_v +
+                                (uint64_t)kvh * a.kv.cap * D;
+  // Byte offsets inside a tile of the 16 bytes this lane stages per chunk (chunk c = w + 4i: K row
+  // c, V^T rows 16c .. 16c+15), with kernel 3's swizzles applied on the global side.
+  uint32_t koff[kCPW], voff[kCPW];
+#pragma unroll
+  for (int i = 0; i < kCPW; ++i) {
+    const uint32_t c = (uint32_t)w + 4u * i;
+    const uint32_t cc = (uint32_t)lane ^ swz_k<D>(c);
+    koff[i] = 2 * ((cc / 4) * (32 * 32) + c * 32 + 8 * (cc % 4));
+    const uint32_t rv = c * 16 + lane / 4;
+    voff[i] = 2 * (rv * 32 + 8 * ((lane % 4) ^ swz_v(rv)));
+  }
+  // Tile t's K (or V) into the given stage array (t clamped to the pair's last tile; a ring's
+  // physical capacity is a multiple of 32 and holds the pair's visible range).
+  auto tile_bytes = [&](uint32_t t) JMA_INL {
+    const uint32_t tt = min(t, t1 - 1);
+    return (a.kv.ring ? (32u * tt) % a.kv.cap : 32u * tt) * (2u * D);
+  };
+  auto issue_k = [&](uint32_t t, _Float16* kd) JMA_INL {
+    const uint32_t off = tile_bytes(t);
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) dma16(kbase, kd + 512 * (w + 4 * i), koff[i], off);
+  };
+  auto issue_v = [&](uint32_t t, _Float16* vd) JMA_INL {
+    const uint32_t off = tile_bytes(t);
+#pragma unroll
+    for (int i = 0; i < kCPW; ++i) dma16(vbase, vd + 512 * (w + 4 * i), voff[i], off);
+  };
+  // Waits until at most n of this wave's loads are in flight (and its LDS operations are done),
+  // then barrier.
+  auto wait_barrier = [](auto outstanding) JMA_INL {
+    constexpr int n = decltype(outstanding)::value;
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  issue_k(t0, ka);
+  issue_v(t0, va);
+  issue_k(t0 + 1, kb2);
+  issue_v(t0 + 1, vb2);
+
+  // q operands of this wave's half, scaled by scale * log2(e) and rounded to f16; a scaled element
+  // beyond the f16 range (where the reference's f32 scores stay finite) is reported like a
+  // non-finite score.
+  half8_t qf[kKq];
+  {
+    const float* const qrow = a.q + ((uint64_t)crow * a.num_heads + head) * D;
+    const float qs = col_ok ? a.qscale : 0.0f;
+    float qmax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kKq; ++i) {
+      const uint32_t e = 16 * (hf * kKq + i) + 8 * h;
+      const float4_t x0 = *(const float4_t*)(qrow + e);
+      const float4_t x1 = *(const float4_t*)(qrow + e + 4);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        qmax = fmaxf(qmax, fmaxf(fabsf(x0[t] * qs), fabsf(x1[t] * qs)));
+        qf[i][t] = (_Float16)(x0[t] * qs);
+        qf[i][4 + t] = (_Float16)(x1[t] * qs);
+      }
+    }
+    if (__ballot(col_ok && !(qmax < 65520.0f)) != 0 && lane == 0) atomicOr(a.err, 1);
+    // The q operands stay in the accumulation registers (matrix ops read them there), leaving
+    // the vector registers to O^T, the scores and the tile operands.
+#pragma unroll
+    for (int i = 0; i < kKq; ++i) asm("" : "+a"(qf[i]));
+  }
+
+  float16_t o[kNb];
+  float m, l, lb;
+  const uint32_t kr = swap34(j);
+  float4_t(*const x_own)[64] = s_x[st][hf];
+  float4_t(*const x_other)[64] = s_x[st][1 - hf];
+
+  // One tile. The fast pass (robust false) feeds V operands as loaded; the robust pass zeroes the
+  // elements of positions the stripe does not see (see the end of the kernel).
+  auto tile = [&](uint32_t t, _Float16* kd, _Float16* vd, auto robust) JMA_INL {
+    // This wave's partial scores over its half, K operands read eight k-steps ahead of the
+    // matrix ops that use them (one wave per SIMD: nothing else hides the LDS latency).
+    float16_t sc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+    auto kread = [&](int i) JMA_INL {
+      const int ks = hf * kKq + i;
+      return *(const half8_t*)(kd + kr * D + 8 * ((2 * ks + h) ^ swz_k<D>(kr)));
+    };
+    half8_t kf[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kf[i] = kread(i);
+#pragma unroll
+    for (int i = 0; i < kKq; ++i) {
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i % 8], qf[i], sc, 0, 0, 0);
+      if (i + 8 < kKq) kf[i % 8] = kread(i + 8);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x_own[c][lane] = float4_t{sc[4 * c], sc[4 * c + 1], sc[4 * c + 2], sc[4 * c + 3]};
+    // V(t) staged: after it this wave issued K(t+1) and V(t+1). Past this barrier every wave is
+    // done with K(t), whose array takes K(t+2).
+    wait_barrier(std::integral_constant<int, 2 * kCPW>{});
+    issue_k(t + 2, kd);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4_t x = x_other[c][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[4 * c + i] += x[i];
+    }
+    // V operands (2 per 32-row block of O^T): the first eight are read now, so their LDS latency
+    // passes under the softmax, the rest eight ahead of the matrix ops that use them.
+    auto vaddr = [&](int u) JMA_INL {
+      const uint32_t vr = 32 * (hf * kNb + u / 2) + j;
+      return (const uint4*)(vd + vr * 32 + 8 * ((2 * (u & 1) + h) ^ swz_v(vr)));
+    };
+    uint4 vraw[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) vraw[u] = *vaddr(u);
+    // Masks: positions outside [first, position] of a column are -inf (after the products, so a
+    // non-finite key there never reaches a result).
+    const uint32_t p0 = 32 * t;
+    if (!(p0 >= all_first && p0 + 31 <= all_last)) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t p = p0 + score_slot(e, h);
+        sc[e] = p >= cfirst && p <= cpos ? sc[e] : -INFINITY;
+      }
+    }
+    // Online softmax: the reference maximum m moves only when a tile's maximum exceeds it by
+    // more than 8 (log2 units), so exponentials stay <= 256 and most tiles skip the rescale.
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+    tmax = half_max(tmax);
+    const bool up = tmax > m + 8.0f;
+    if (__ballot(up) != 0) {
+      const float alpha = !up ? 1.0f : (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - tmax));
+      m = up ? tmax : m;
+      l *= alpha;
+      lb *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb) o[nb] *= alpha;
+    }
+    const float mu = m == -INFINITY ? 0.0f : m;
+    half8_t pf[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) pf[e >> 3][e & 7] = (_Float16)__builtin_amdgcn_exp2f(sc[e] - mu);
+    const half2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const half2_t pr2 = {pf[i >> 2][2 * (i & 3)], pf[i >> 2][2 * (i & 3) + 1]};
+      if (i & 1) lb = __builtin_amdgcn_fdot2(pr2, one, lb, false);
+      else l = __builtin_amdgcn_fdot2(pr2, one, l, false);
+    }
+    // Robust pass: element e of V operand b holds position p0 + score_slot(8b + e, h), and the
+    // masks clear the elements of positions the stripe does not see at its edge tiles.
+    uint32_t vm[2][4];
+    if constexpr (decltype(robust)::value) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t q0 = p0 + score_slot(8 * b + 2 * d, h), q1 = p0 + score_slot(8 * b + 2 * d + 1, h);
+          vm[b][d] = (q0 < s_first || q0 > s_last ? 0u : 0xFFFFu) | (q1 < s_first || q1 > s_last ? 0u : 0xFFFF0000u);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2 * kNb; ++u) {
+      uint4 x = vraw[u % 8];
+      if constexpr (decltype(robust)::value) {
+        x.x &= vm[u & 1][0];
+        x.y &= vm[u & 1][1];
+        x.z &= vm[u & 1][2];
+        x.w &= vm[u & 1][3];
+      }
+      o[u / 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, x), pf[u & 1], o[u / 2], 0, 0, 0);
+      if (u + 8 < 2 * kNb) vraw[u % 8] = *vaddr(u + 8);
+    }
+    // K(t+1) staged (after it this wave issued V(t+1) and K(t+2)); every wave is past V(t) and
+    // the partial tiles, which V(t+2) and the next partials overwrite.
+    wait_barrier(std::integral_constant<int, 2 * kCPW>{});
+    issue_v(t + 2, vd);
+  };
+  // One pass over the pair's tiles (K(t0), V(t0), K(t0+1), V(t0+1) already on their way).
+  auto run = [&](auto robust) JMA_INL {
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[nb][e] = 0.0f;
+    m = -INFINITY;
+    l = 0.0f;
+    lb = 0.0f;
+    // K(t0) staged (V(t0), K(t0+1), V(t0+1) may still be in flight).
+    wait_barrier(std::integral_constant<int, 3 * kCPW>{});
+    for (uint32_t t = t0; t < t1; t += 2) {
+      tile(t, ka, va, robust);
+      if (t + 1 >= t1) break;
+      tile(t + 1, kb2, vb2, robust);
+    }
+    // The repeated loads of the last steps land, and every wave is past its last LDS reads,
+    // before the arrays are loaded again or the workgroup's LDS is released.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  };
+  // V rows at positions no column of a stripe sees may hold anything (a discarded tail, an old
+  // ring slot, a value that overflowed f16). Their probabilities are 0, but 0 * inf is NaN, so a
+  // non-finite value there turns the column's state non-finite, where the reference never reads
+  // that position. A workgroup with a valid column whose state is not finite after the fast pass
+  // runs its pair again in the robust pass; a state still non-finite then is the reference's too.
+  __shared__ uint32_t s_rerun;
+  if (threadIdx.x == 0) s_rerun = 0u;
+  run(std::false_type{});
+  {
+    float osum = 0.0f;
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) osum += o[nb][e];
+    const bool bad = col_ok && !(l + lb < INFINITY && m < INFINITY && fabsf(osum) < INFINITY);
+    if (__ballot(bad) != 0 && lane == 0) s_rerun = 1u;
+  }
+  __syncthreads();
+  if (s_rerun != 0u) {
+    issue_k(t0, ka);
+    issue_v(t0, va);
+    issue_k(t0 + 1, kb2);
+    issue_v(t0 + 1, vb2);
+    run(std::true_type{});
+  }
+
+  const float L = half_sum(l + lb);
+  const bool bad = col_ok && !(L > 0.0f && L < INFINITY);
+  if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  if (col_ok) {
+    float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *(float4_t*)(orow + 32 * (hf * kNb + nb) + 8 * c) =
+            float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]} * inv;
+  }
+}
 
 template <int D>
 hipError_t launch_prefill_t(PrefillArgs a, hipStream_t stream) {
@@ -2683,7 +2941,14 @@ hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, 
       a.row_blocks != (a.n + a.rows_per_stripe - 1) / a.rows_per_stripe ||
       a.head_groups != (a.group + a.heads_per_stripe - 1) / a.heads_per_stripe)
     return hipErrorInvalidValue;
-  if (f16) return launch_prefill_slice_t<_Float16, 512, 4>(a, stream);
+  if (f16) {
+    // Stripe pairs (kernel 3c); 32-bit tile byte offsets.
+    const uint64_t blocks = (uint64_t)(a.row_blocks + 1) / 2 * a.head_groups * a.num_kv_heads;
+    if (blocks == 0) return hipSuccess;
+    if (blocks > 0x7fffffffu || (uint64_t)a.kv.cap * 512 * 2 > 0x7fffffffu) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((prefill_pair_kernel<512>), dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
   switch (dk) {
     case 32: return launch_prefill_slice_t<float, 32, 1>(a, stream);
     case 64: return launch_prefill_slice_t<float, 64, 2>(a, stream);

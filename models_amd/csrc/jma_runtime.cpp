@@ -588,8 +588,8 @@ void check_decode_shape(const jmodels_attn_kv* kv, const LayerCall& lc) {
 }
 
 // Which kernel runs a causal block of rows: the f16 MFMA prefill (f16 caches, head dims 32-256),
-// the d-sliced prefill (f32 caches at 32-512, f16 at 512), else the split-K decode kernel over
-// chunks of listed rows.
+// the sliced prefills (f32 caches at 32-512: head-dim slices; f16 at 512: stripe pairs), else
+// the split-K decode kernel over chunks of listed rows.
 enum class PrefillPath { kF16, kSlice, kDecodeRows };
 
 PrefillPath prefill_path(const jmodels_attn_kv* kv, const LayerCall& lc) {
