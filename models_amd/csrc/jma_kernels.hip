@@ -1597,10 +1597,6 @@ static hipError_t launch_decode_t(const DecodeArgs& a, int d, hipStream_t stream
         hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 128, kSimple, true, kNT, kPack>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
         break;
       }
-      if (a.slices == 2) {
-        hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 256, kSimple, true, kNT, kPack>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
-        break;
-      }
       // One tile buffer always: a tile is the whole register budget of a wave at this width.
       hipLaunchKernelGGL((decode_kernel<KV, 512, 512, 512, kSimple, true, kNT, kPack>), grid, block, 0, stream, kb, vb, start, window, tps, cap, ring, a);
       break;

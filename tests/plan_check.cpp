@@ -52,7 +52,7 @@ void check(const Case& c) {
                                    c.target, c.tiles_per_wave, c.unfused, c.min_split);
   const uint32_t blk = (uint32_t)v_block(c.f16);
   const uint32_t hgroups = p.hgroups;  // virtual head groups: head groups x column slices
-  if (p.slices != 1 && p.slices != 4 && !(p.slices == 2 && c.dk == 512)) die(c, "column slices");
+  if (p.slices != 1 && p.slices != 4) die(c, "column slices");
   if (hgroups != (c.group + kHeadSlots - 1) / kHeadSlots * p.slices) die(c, "head groups");
   if (p.slices > 1 && (c.dk < 256 || (c.dk == 256 && (p.separate || p.tiles_per_split > 4))))
     die(c, "column slices outside the sliced instances (fused d 256 one tile per wave, d 512)");
@@ -259,7 +259,7 @@ int main() {
     cases.push_back({"Gemma-4 full d512 8/1 @" + std::to_string(p) + " (wide)", {p}, 0, 1, 8, 512, 512, true, 512, 1, false, 0});
   cases.push_back({"Gemma-4 full d512 ragged 3 rows x 2 groups (wide)", {20000, 5000, 12000}, 0, 1, 20, 512, 512, true, 512, 1, false, 0});
   cases.push_back({"d512 ragged 3 rows x 2 groups, target 8192 (wide, sliced)", {9000, 5000, 7000}, 0, 1, 20, 512, 512, true, 8192, 1, false, 0});
-  cases.push_back({"d512 one row @16000 (wide, 2 slices)", {16000}, 0, 1, 8, 512, 512, true, 512, 1, false, 0});
+  cases.push_back({"d512 one row @16000 (wide, unsliced)", {16000}, 0, 1, 8, 512, 512, true, 512, 1, false, 0});
   cases.push_back({"d512 ragged 9000/5000/7000 x 2 groups", {9000, 5000, 7000}, 0, 1, 20, 512, 512, true, 512, 1, false, 0});
   cases.push_back({"d512 ragged 9000/5000/7000 x 2 groups, f32", {9000, 5000, 7000}, 0, 1, 20, 512, 512, false, 512, 1, false, 0});
   cases.push_back({"d512 one row @16000, f32", {16000}, 0, 1, 8, 512, 512, false, 512, 1, false, 0});

@@ -1083,19 +1083,20 @@ D512_SLICED_CASES = {
     # name: (query heads, row lengths, workgroup target); the plan each gets (tests/plan_check.cpp
     # prints them) follows the name
     "one row @4096: wide, 4 slices": (8, [4096], None),
-    "one row @16000: wide, 2 slices": (8, [16000], None),
+    "one row @16000: wide, unsliced": (8, [16000], None),
     "three ragged rows, two head groups, target 8192: wide, 4 slices": (20, [9000, 5000, 7000], "8192"),
-    "three ragged rows, two head groups: fused, 2 slices": (20, [9000, 5000, 7000], None),
+    "three ragged rows, two head groups: fused, unsliced": (20, [9000, 5000, 7000], None),
 }
 
 
 @pytest.mark.parametrize("half", [True, False])
 @pytest.mark.parametrize("case", list(D512_SLICED_CASES))
 def test_wide_sliced_d512_decode_matches_oracle(monkeypatch, half, case):
-    """Head dim 512 plans with column slices: four (short plans) or two (long ones, where four
-    would exceed the workgroup target) workgroups per (head group, split), each forming all of
-    q.K and its share of the V columns. Wide plans write the slices' columns into one part_acc
-    item that reduce_kernel combines; fused plans reduce each slice through the split exchange.
+    """Head dim 512 plans with and without column slices: four workgroups per (head group,
+    split) in short plans, each forming all of q.K and its share of the V columns, none in long
+    ones (where four would exceed the workgroup target). Wide plans write the slices' columns
+    into one part_acc item that reduce_kernel combines; fused plans reduce each slice through the
+    split exchange.
     One row (8 Q / 1 KV heads: the uniform, single-group instance) and three ragged rows of
     20 Q / 1 KV heads (two head groups, unequal split counts, row starts in virtual items: the
     listed-rows instance); the new token appended by the decode kernel; against the oracle over
