@@ -2763,7 +2763,7 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     };
     uint4 vraw[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) vraw[u] = *vaddr(u);
+    for (int k = 0; k < 8; ++k) vraw[k] = *vaddr(2 * (k % kNb) + k / kNb);
     // Masks: positions outside [first, position] of a column are -inf (after the products, so a
     // non-finite key there never reaches a result).
     const uint32_t p0 = 32 * t;
@@ -2812,9 +2812,12 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
           vm[b][d] = (q0 < s_first || q0 > s_last ? 0u : 0xFFFFu) | (q1 < s_first || q1 > s_last ? 0u : 0xFFFF0000u);
         }
     }
+    // Operand u = 2 nb + b; the ops run b-major (every block's b = 0 op, then every b = 1 op), so
+    // the two ops into one accumulator are eight apart and never wait on each other.
 #pragma unroll
-    for (int u = 0; u < 2 * kNb; ++u) {
-      uint4 x = vraw[u % 8];
+    for (int k = 0; k < 2 * kNb; ++k) {
+      const int u = 2 * (k % kNb) + k / kNb;
+      uint4 x = vraw[k % 8];
       if constexpr (decltype(robust)::value) {
         x.x &= vm[u & 1][0];
         x.y &= vm[u & 1][1];
@@ -2822,7 +2825,7 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
         x.w &= vm[u & 1][3];
       }
       o[u / 2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, x), pf[u & 1], o[u / 2], 0, 0, 0);
-      if (u + 8 < 2 * kNb) vraw[u % 8] = *vaddr(u + 8);
+      if (k + 8 < 2 * kNb) vraw[k % 8] = *vaddr(2 * ((k + 8) % kNb) + (k + 8) / kNb);
     }
     // K(t+1) staged (after it this wave issued V(t+1) and K(t+2)); every wave is past V(t) and
     // the partial tiles, which V(t+2) and the next partials overwrite.
