@@ -268,10 +268,11 @@ JMODELS_ATTN_API int32_t jmodels_attn_decode(jmodels_attn_context* ctx, jmodels_
 /* Causal prefill of n consecutive tokens of one sequence at start .. start+n-1
  * (prepareBatchedAttention + computeBatchedAttention, BJ/llama/LlamaForwardPass.java:1479-1541):
  * RoPE + append every row (one kernel-1 launch), then jmodels_attn_attend_causal: f16 caches at
- * head dims 32-256 run the MFMA kernel (kernel 3) with f16 queries; f32 caches at 32-512, and
- * f16 caches at 512, run the d-sliced prefill kernel (kernel 3b: the waves of a workgroup split
- * the head dimension and add their partial score tiles through LDS); other shapes run the decode
- * kernel over chunks of the rows. */
+ * head dims 32-256 run the MFMA kernel (kernel 3) with f16 queries; f32 caches at 32-512 run the
+ * d-sliced prefill kernel (kernel 3b: the waves of a workgroup split the head dimension and add
+ * their partial score tiles through LDS); f16 caches at 512 run the paired-stripe kernel (kernel
+ * 3c: two stripes share each LDS-staged tile, each split over two waves); other shapes run the
+ * decode kernel over chunks of the rows. */
 JMODELS_ATTN_API int32_t jmodels_attn_prefill(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
                              const jmodels_attn_layer* layer, uint32_t sequence, uint32_t start,
                              uint32_t n, const float* q, uint64_t q_elements, const float* k,

@@ -1,5 +1,6 @@
-"""GPU parity of the d-sliced prefill kernel (prefill_slice_kernel): f32 caches at head dims
-32-512 and f16 caches at head dim 512, against the oracle's prefill (computeBatchedAttention,
+"""GPU parity of the sliced prefill kernels: prefill_slice_kernel (f32 caches at head dims
+32-512) and prefill_pair_kernel (f16 caches at head dim 512: two stripes per workgroup, odd stripe
+counts leaving the last pair half empty), against the oracle's prefill (computeBatchedAttention,
 backend-java llama/LlamaForwardPass.java:1515-1541) on identical seeded inputs.
 
 Bars: attention outputs within max-abs 1e-3 with f32 KV and normwise relative 2e-2 per (row, head)
@@ -81,7 +82,8 @@ def test_f32_prefill_matches_oracle(hip, d, window):
 @pytest.mark.parametrize("window", [0, 200])
 def test_f16_d512_prefill_matches_oracle(hip, hq, hkv, window):
     """f16 caches at head dim 512 (Gemma 4 full layers): 8 or 16 query heads on 1 or 2 kv heads
-    (8 rows x 4 heads or 4 rows x 8 heads per stripe) and group 1 (32 rows per stripe)."""
+    (8 rows x 4 heads or 4 rows x 8 heads per stripe) and group 1 (32 rows per stripe); the
+    first chunk's 130 rows make an odd stripe count (33, or 5 at group 1)."""
     err = _chunked_case(hip, True, 512, hq, hkv, 130, 350, window, 1e6, 32)
     _say(f"f16 d 512 {hq}/{hkv} window {window} normwise rel err {err:.2e}")
 
