@@ -1395,22 +1395,33 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   const uint32_t sl = lane / kQ, q = lane % kQ;
   const uint32_t e = chunk * kOut + 4 * q;
   const uint32_t el = e < DV ? e : DV - 4;  // lanes past the head load a valid quad
-  const float* acc = (const float*)g_acc;
-  const float* mlp = (const float*)g_ml;
+  // Buffer loads with 32-bit byte offsets (the runtime keeps both buffers under 2 GiB). A split
+  // past ns is addressed past the record count, where a buffer load returns zeros: every load is
+  // issued unconditionally, with no per-split branch (whose join made the compiler wait for the
+  // first loads before issuing the rest, two memory round trips instead of one).
+  const __amdgpu_buffer_rsrc_t rs_acc = part_rsrc(const_cast<float*>((const float*)g_acc));
+  const __amdgpu_buffer_rsrc_t rs_ml = part_rsrc(const_cast<float*>((const float*)g_ml));
+  constexpr uint32_t kSkip = 0xFFFFFF00u;
 
   float2 ml[kMl];
 #pragma unroll
   for (uint32_t i = 0; i < kMl; ++i) {
     const uint32_t sp = tid + 64 * kWaves * i;
-    ml[i] = sp < ns ? *(const float2*)(mlp + sep_ml_float(base + sp, c16)) : float2{-INFINITY, 0.0f};
+    const uint32_t off = sp < ns ? (uint32_t)(sep_ml_float(base + sp, c16) * 4) : kSkip;
+    const float2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs_ml, off, 0, 0);
+    ml[i] = float2{sp < ns ? v[0] : -INFINITY, v[1]};
   }
   float4_t xv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const uint32_t sp = (i * kWaves + wave) * kSL + sl;
-    xv[i] = sp < ns ? *(const float4_t*)(acc + sep_acc_float(base + sp, c16, DV, el))
-                    : float4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t off = sp < ns ? (uint32_t)(sep_acc_float(base + sp, c16, DV, el) * 4) : kSkip;
+    xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_acc, off, 0, 0);
   }
+  // The output pointer is not preloaded: its argument load is issued here, behind the partial
+  // loads, so that it completes under their latency instead of after the last barrier.
+  float* out_p = a.out;
+  asm volatile("" : "+s"(out_p));
 
   float mt = -INFINITY;
 #pragma unroll
@@ -1464,7 +1475,7 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
     xt += s_x[i][q];
   }
   if (!(lt > 0.0f) && q == 0 && chunk == 0) atomicOr(a.err, 1);  // all -inf, NaN or +inf
-  if (e < DV) *(float4_t*)(a.out + ((uint64_t)row * p_heads + head) * DV + e) = xt * __builtin_amdgcn_rcpf(lt);
+  if (e < DV) *(float4_t*)(out_p + ((uint64_t)row * p_heads + head) * DV + e) = xt * __builtin_amdgcn_rcpf(lt);
 }
 
 // Workgroups of 16 outputs when 64-output ones would leave most compute units idle (few rows

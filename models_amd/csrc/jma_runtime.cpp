@@ -489,6 +489,9 @@ void run_attend_rows(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, const
   if (fixed) check_fixed_fit(plan, *fixed);
   if (plan.separate) {
     const size_t acc_b = plan.acc_bytes, ml_b = plan.ml_bytes;
+    // reduce_kernel addresses the partials with 32-bit byte offsets.
+    require(acc_b <= 0x7FFFFFF0u && ml_b <= 0x7FFFFFF0u, JMODELS_ATTN_INVALID_SHAPE,
+            "decode plan needs more than 2 GiB of split partials (lower JMA_DECODE_TARGET_BLOCKS)");
     if (fixed) {
       a.part_acc = fixed->part_acc;
       a.part_ml = fixed->part_ml;
