@@ -1349,20 +1349,21 @@ __device__ __forceinline__ float wave_sum64(float x) {
   return wave_sum_groups(x);
 }
 
-// One workgroup of kWaves = 16 waves per (row, query head, 64-element chunk of the head's
-// output): out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to
-// kMaxWideSplits. (Four waves, each taking 16 splits per lane, measured slower on a 256-split C5
-// global layer: 14.1 against 12.2 us per layer-step; sixteen waves issue the loads in parallel.)
-// Lane (s, q) of wave w takes output quad q of the chunk for splits
+// One workgroup of kWaves waves per (row, query head, chunk of 4 kQ outputs of the head):
+// out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the row's splits, up to kMaxNs
+// (at most kMaxWideSplits). With 16 outputs per workgroup: 16 waves for more than 256 splits,
+// else 4, or 1 for up to 64, each lane taking at most four splits (four waves taking 16 splits
+// per lane with 64 outputs measured slower, 14.1 against 12.2 us per C5 global layer-step).
+// With kQ = 16, lane (s, q) of wave w takes output quad q of the chunk for splits
 // (kWaves i + w) * 4 + s, so every load instruction moves 16 bytes per lane (four splits'
-// 256-byte rows, 1 KB), and thread t loads split t's (m, l) (and t + 64 kWaves, ... at 4 waves);
+// 256-byte rows, 1 KB); with kQ = 4, 16 split lanes per wave; thread t loads split t's (m, l);
 // all loads are issued before any is used (one memory round trip). The workgroup agrees on M
 // through DPP and row-swap exchanges and LDS, takes the weights 2^(m_s - M) from the (m, l) staged
 // in LDS, sums each lane's splits in order, then the four split lanes in a fixed tree and the
 // waves in wave order: the same result on every run for a plan. The leading scalar arguments
 // (the partial buffers, the uniform split count, the head counts) arrive preloaded in SGPRs, so
 // the loads need no kernel-argument load first; the row tables are read only for listed rows.
-template <int DV, int kWaves, int kQ>
+template <int DV, int kWaves, int kQ, int kMaxNs = kMaxWideSplits>
 __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc, const float* p_ml,
                                                              uint32_t p_ns, uint32_t p_heads,
                                                              uint32_t p_group, const DecodeArgs a) {
@@ -1370,9 +1371,11 @@ __global__ __launch_bounds__(64 * kWaves) void reduce_kernel(const float* p_acc,
   constexpr uint32_t kOut = 4 * kQ;                          // outputs per workgroup
   constexpr uint32_t kChunks = (DV + kOut - 1) / kOut;
   constexpr uint32_t kSL = 64 / kQ;                          // split lanes of a quad per wave
-  constexpr int kPer = kMaxWideSplits / (kWaves * kSL);      // splits one lane sums at most
-  constexpr uint32_t kMl = kMaxWideSplits / (64 * kWaves);  // (m, l) words one thread loads
-  __shared__ float2 s_ml[kMaxWideSplits];
+  constexpr int kPer = kMaxNs / (kWaves * kSL);              // splits one lane sums at most
+  constexpr uint32_t kMl = kMaxNs / (64 * kWaves);           // (m, l) words one thread loads
+  static_assert(kPer >= 1 && kMl >= 1 && kPer * kWaves * kSL == kMaxNs && kMl * 64 * kWaves == kMaxNs,
+                "the lanes cover kMaxNs splits exactly");
+  __shared__ float2 s_ml[kMaxNs];
   __shared__ float s_m[kWaves], s_l[kWaves];
   __shared__ float4_t s_x[kWaves][kQ];
   JMA_GLOBAL const float* g_acc = (JMA_GLOBAL const float*)p_acc;
@@ -1485,8 +1488,17 @@ static void launch_reduce_t(const DecodeArgs& a, hipStream_t stream) {
   const uint32_t wide_groups = a.rows.count * a.num_heads * ((DV + 63) / 64);
   if (wide_groups < 128 && DV >= 16) {
     const dim3 grid(a.rows.count * a.num_heads * ((DV + 15) / 16));
-    hipLaunchKernelGGL((reduce_kernel<DV, 16, 4>), grid, dim3(1024), 0, stream, a.part_acc, a.part_ml,
-                       a.ns_uniform, a.num_heads, a.group, a);
+    // As few waves as cover the splits with four loads per lane: fewer waves to start and to
+    // synchronise (one row at 32 704 positions, 256 splits: 22.6 -> 21.8 us per d-512 layer-step).
+    if (a.max_splits <= 64)
+      hipLaunchKernelGGL((reduce_kernel<DV, 1, 4, 64>), grid, dim3(64), 0, stream, a.part_acc,
+                         a.part_ml, a.ns_uniform, a.num_heads, a.group, a);
+    else if (a.max_splits <= 256)
+      hipLaunchKernelGGL((reduce_kernel<DV, 4, 4, 256>), grid, dim3(256), 0, stream, a.part_acc,
+                         a.part_ml, a.ns_uniform, a.num_heads, a.group, a);
+    else
+      hipLaunchKernelGGL((reduce_kernel<DV, 16, 4>), grid, dim3(1024), 0, stream, a.part_acc, a.part_ml,
+                         a.ns_uniform, a.num_heads, a.group, a);
   } else {
     hipLaunchKernelGGL((reduce_kernel<DV, 16, 16>), dim3(wide_groups), dim3(1024), 0, stream, a.part_acc,
                        a.part_ml, a.ns_uniform, a.num_heads, a.group, a);

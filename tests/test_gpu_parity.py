@@ -1079,6 +1079,55 @@ def test_wide_split_decode_matches_oracle(hip, half, d):
         rope.close()
 
 
+REDUCE_SHAPE_CASES = {
+    # name: (query heads, row length, minimum tiles per split, workgroup target); one f16 row of
+    # head dim 128 on one KV head, planned wide so that reduce_kernel combines its splits
+    "64 splits: one-wave workgroups": (4, 8191, "4", None),
+    "128 splits: four-wave workgroups": (4, 8191, "2", None),
+    "256 splits: four-wave workgroups": (4, 8191, "1", None),
+    "512 splits: sixteen-wave workgroups": (4, 16383, "1", None),
+    "64 query heads, 64 splits: 64-output workgroups": (64, 8191, "4", "4096"),
+}
+
+
+@pytest.mark.parametrize("case", list(REDUCE_SHAPE_CASES))
+def test_reduce_workgroup_shapes_match_oracle(monkeypatch, case):
+    """reduce_kernel's workgroup shapes, each chosen by the split count and the output count of a
+    wide plan: one wave for up to 64 splits, four for up to 256 and sixteen beyond (16 outputs per
+    workgroup), or 64 outputs per workgroup when there are enough of them. The split size is
+    forced through JMA_DECODE_MIN_SPLIT_TILES; the result is checked against the oracle's GQA over
+    the read-back cache, and a repeated call must give the same bits."""
+    d, hkv, theta = 128, 1, 1e6
+    scale = A.default_scale(d)
+    hq, L, tiles, target = REDUCE_SHAPE_CASES[case]
+    monkeypatch.setenv("JMA_DECODE_MIN_SPLIT_TILES", tiles)
+    if target:
+        monkeypatch.setenv("JMA_DECODE_TARGET_BLOCKS", target)
+    lib = A.HipAttentionLibrary(0)
+    try:
+        rope = lib.rotary_table(d, theta, 1.0, max_positions=L + 1)
+        kv = lib.kv_cache(1, L + 1, hkv, d, d, half_precision=True)
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        tag = f"rshape/{case}"
+        kv.append(layer, np.arange(L), np.zeros((L, hq * d), np.float32),
+                  normal(19, f"{tag}/k", (L, hkv * d)), normal(19, f"{tag}/v", (L, hkv * d)))
+        qn = normal(19, f"{tag}/qn", (1, hq * d))
+        kn = normal(19, f"{tag}/kn", (1, hkv * d))
+        vn = normal(19, f"{tag}/vn", (1, hkv * d))
+        got = kv.decode(layer, [L], qn, kn, vn).reshape(1, -1)
+        again = kv.decode(layer, [L], qn, kn, vn).reshape(1, -1)
+        np.testing.assert_array_equal(again, got)  # deterministic, the same row rewritten
+        keys, values = kv.read(0, 0, L + 1)
+        q_rot = rope_rows(qn, [L], hq, d, d, theta, True, check_against_oracle=False)
+        want = oracle.gqa_rows(q_rot[0], keys, values, hq, hkv, d, d, scale)
+        err = assert_f16_close(got[0], want, f"reduce shape {case}", head_dim=d)
+        _say(f"reduce shape {case} err {err:.2e}")
+        kv.close()
+        rope.close()
+    finally:
+        lib.close()
+
+
 D512_SLICED_CASES = {
     # name: (query heads, row lengths, workgroup target); the plan each gets (tests/plan_check.cpp
     # prints them) follows the name
