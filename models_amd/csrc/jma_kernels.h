@@ -5,6 +5,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <functional>
+#include <vector>
+
 #include "jma_plan.h"
 
 namespace jma {
@@ -115,7 +118,10 @@ struct PrefillArgs {
   // The split_blocks longest row blocks (they run first) have their kv range cut in two halves,
   // each a workgroup; the later of the two to arrive (ticket) merges them. part: [pair][half]
   // [stripe][D / 8 chunks x 64 lanes + 32 columns] float4 words, every word 0xFFFFFFFF (not
-  // written) between launches; tickets: [pair], zero between launches.
+  // written) between launches; tickets: [pair], zero between launches. The f16 head-dim-512
+  // prefill (kernel 3c) splits stripe pairs the same way (split_blocks pairs, planned by
+  // plan_prefill_pairs): part [split pair][half][wave][kPairPartWords][64 lanes] float4 words
+  // with no initial value; tickets zero between launches.
   uint32_t split_blocks;
   float* part;
   uint32_t* tickets;
@@ -165,6 +171,83 @@ inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, u
   }
   p.pairs = p.split_blocks * (uint32_t)per_block;
   p.part_bytes = (size_t)p.pairs * 2 * (S * ((dk / 8) * 64 + 32) + S * kPrefillKvGroups) * 16;
+  return p;
+}
+
+// Stripe-pair splits of kernel 3c. A pair costs its kv tiles (each ~1.7 us on one compute unit,
+// which holds one such workgroup) plus ~1.5 tiles of prologue and epilogue, and the later half
+// of a split pair ~0.9 tiles more for the merge. The longest pairs run first, split pairs as two
+// workgroups of half the tiles. split_tiles >= 2 splits the trailing pairs of at least that many
+// tiles; 0 or 1 never splits; -1 (automatic) replays the dispatch (each workgroup to the compute
+// unit that frees first, in launch order) for up to 33 choices of how many trailing pairs to
+// split and takes the shortest, when the launch holds at most 4 workgroups per compute unit
+// (beyond that the dispatch already balances the pairs).
+constexpr uint32_t kPairPartWords = 33;  // float4 words per lane of a half's state: O^T (8 blocks x 4) and (m, l, lb)
+struct PairPlan {
+  uint32_t split_pairs = 0;
+  size_t part_bytes = 0, ticket_bytes = 0;
+};
+
+inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32_t cus) {
+  PairPlan p;
+  const uint32_t pairs = (a.row_blocks + 1) / 2;
+  const uint32_t per = a.head_groups * a.num_kv_heads;  // workgroups per pair
+  if (pairs == 0 || per == 0 || split_tiles == 0 || split_tiles == 1) return p;
+  const uint32_t R = a.rows_per_stripe;
+  auto tiles_of = [&](uint32_t pr) -> uint32_t {  // kv tiles of pair pr (the kernel's t1 - t0)
+    const uint32_t r0 = 2 * pr * R, r1 = std::min(r0 + 2 * R, a.n) - 1;
+    const uint32_t w = a.window, p0 = a.start + r0;
+    const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
+    return (a.start + r1) / 32 + 1 - first / 32;
+  };
+  // Trailing pairs with at least `min_tiles` tiles (all of them have two or more).
+  auto trailing = [&](uint32_t min_tiles) {
+    uint32_t n = 0;
+    while (n < pairs && tiles_of(pairs - 1 - n) >= std::max<uint32_t>(min_tiles, 2)) ++n;
+    return n;
+  };
+  uint32_t sp = 0;
+  if (split_tiles >= 2) {
+    sp = trailing((uint32_t)split_tiles);
+  } else if ((uint64_t)pairs * per <= 4ull * std::max<uint32_t>(cus, 1)) {
+    const uint32_t slots = std::max<uint32_t>(cus, 1);
+    std::vector<double> free_at(slots);
+    auto makespan = [&](uint32_t nsplit) {  // in tiles
+      std::fill(free_at.begin(), free_at.end(), 0.0);
+      std::make_heap(free_at.begin(), free_at.end(), std::greater<double>());
+      double end = 0.0;
+      auto run = [&](double cost) {
+        std::pop_heap(free_at.begin(), free_at.end(), std::greater<double>());
+        free_at.back() += cost;
+        end = std::max(end, free_at.back());
+        std::push_heap(free_at.begin(), free_at.end(), std::greater<double>());
+      };
+      for (uint32_t i = 0; i < nsplit; ++i) {
+        const uint32_t t = tiles_of(pairs - 1 - i);
+        for (uint32_t k = 0; k < per; ++k) run(1.5 + t / 2);
+        for (uint32_t k = 0; k < per; ++k) run(1.5 + (t - t / 2) + 0.9);
+      }
+      for (uint32_t i = nsplit; i < pairs; ++i)
+        for (uint32_t k = 0; k < per; ++k) run(1.5 + tiles_of(pairs - 1 - i));
+      return end;
+    };
+    double best = makespan(0);
+    const uint32_t most = trailing(2);
+    uint32_t last = 0;
+    for (uint32_t k = 1; k <= 32; ++k) {
+      const uint32_t n = (uint32_t)(((uint64_t)most * k + 31) / 32);
+      if (n == last) continue;
+      last = n;
+      const double e = makespan(n);
+      if (e < best - 1e-9) {
+        best = e;
+        sp = n;
+      }
+    }
+  }
+  p.split_pairs = sp;
+  p.part_bytes = (size_t)sp * per * 2 * 4 * kPairPartWords * 64 * 16;
+  p.ticket_bytes = (size_t)sp * per * sizeof(uint32_t);
   return p;
 }
 

@@ -2618,6 +2618,14 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
 // workgroup then runs again in a robust pass that zeroes those operand elements (as the main
 // prefill kernel does). The q operands live in the accumulation registers (the matrix ops read
 // them there), leaving the vector registers to O^T, the scores and the operands.
+//
+// One workgroup per compute unit (the four stage arrays take 128 KB of LDS), and a pair's cost
+// grows with its row, so the longest pairs would set the duration: the split_blocks longest
+// pairs (planned by plan_prefill_pairs) run first as two workgroups each, one per half of the
+// pair's kv tiles. Both store their state (O^T, m, l per lane) device-coherent and take a ticket;
+// the later one loads the other's state, merges the two online-softmax states (the same products
+// and one sum whichever half merges, so the result does not depend on the arrival order), resets
+// the ticket and stores the output.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) {
   using namespace pf;
@@ -2638,12 +2646,17 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int st = w & 1, hf = w >> 1;
   // Kv heads vary fastest (consecutive workgroups on different XCDs); pairs run last-first
-  // (longest causal ranges first).
+  // (longest causal ranges first): items 0 .. 2 split_blocks - 1 are the halves of the split
+  // pairs, the rest one pair each.
   const uint32_t pairs = (a.row_blocks + 1) / 2;
   const uint32_t kvh = blockIdx.x % a.num_kv_heads;
   const uint32_t rest = blockIdx.x / a.num_kv_heads;
   const uint32_t hz = rest % a.head_groups;
-  const uint32_t pr = pairs - 1 - rest / a.head_groups;
+  const uint32_t item = rest / a.head_groups, sp = a.split_blocks;
+  const bool split = item < 2 * sp;
+  const uint32_t half = split ? item & 1u : 0u;
+  const uint32_t pr = pairs - 1 - (split ? item / 2 : item - sp);
+  const uint32_t sidx = ((split ? item / 2 : 0u) * a.head_groups + hz) * a.num_kv_heads + kvh;
   const uint32_t stripe = 2 * pr + st;
   const bool stripe_ok = stripe < a.row_blocks;
   const uint32_t R = a.rows_per_stripe, Gz = a.heads_per_stripe;
@@ -2668,6 +2681,11 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
   const uint32_t p_last = min(p_row0 + 2 * R - 1, a.n - 1);
   const uint32_t t0 = first_visible(a.start + p_row0, a.window) / 32;
   const uint32_t t1 = (a.start + p_last) / 32 + 1;
+  // This workgroup's tiles [tb, te): all of the pair's, or one half (a split pair has at least
+  // two tiles).
+  const uint32_t tm = t0 + (t1 - t0) / 2;
+  const uint32_t tb = split && half != 0u ? tm : t0;
+  const uint32_t te = split && half == 0u ? tm : t1;
 
   const _Float16* const kbase = (const _Float16*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
                                 (uint64_t)kvh * a.kv.cap * D;
@@ -2684,10 +2702,10 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     const uint32_t rv = c * 16 + lane / 4;
     voff[i] = 2 * (rv * 32 + 8 * ((lane % 4) ^ swz_v(rv)));
   }
-  // Tile t's K (or V) into the given stage array (t clamped to the pair's last tile; a ring's
-  // physical capacity is a multiple of 32 and holds the pair's visible range).
+  // Tile t's K (or V) into the given stage array (t clamped to the workgroup's last tile; a
+  // ring's physical capacity is a multiple of 32 and holds the pair's visible range).
   auto tile_bytes = [&](uint32_t t) JMA_INL {
-    const uint32_t tt = min(t, t1 - 1);
+    const uint32_t tt = min(t, te - 1);
     return (a.kv.ring ? (32u * tt) % a.kv.cap : 32u * tt) * (2u * D);
   };
   auto issue_k = [&](uint32_t t, _Float16* kd) JMA_INL {
@@ -2708,10 +2726,10 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
 
-  issue_k(t0, ka);
-  issue_v(t0, va);
-  issue_k(t0 + 1, kb2);
-  issue_v(t0 + 1, vb2);
+  issue_k(tb, ka);
+  issue_v(tb, va);
+  issue_k(tb + 1, kb2);
+  issue_v(tb + 1, vb2);
 
   // q operands of this wave's half, scaled by scale * log2(e) and rounded to f16; a scaled element
   // beyond the f16 range (where the reference's f32 scores stay finite) is reported like a
@@ -2855,7 +2873,7 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     wait_barrier(std::integral_constant<int, 2 * kCPW>{});
     issue_v(t + 2, vd);
   };
-  // One pass over the pair's tiles (K(t0), V(t0), K(t0+1), V(t0+1) already on their way).
+  // One pass over the workgroup's tiles (K(tb), V(tb), K(tb+1), V(tb+1) already on their way).
   auto run = [&](auto robust) JMA_INL {
 #pragma unroll
     for (int nb = 0; nb < kNb; ++nb)
@@ -2864,11 +2882,11 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     m = -INFINITY;
     l = 0.0f;
     lb = 0.0f;
-    // K(t0) staged (V(t0), K(t0+1), V(t0+1) may still be in flight).
+    // K(tb) staged (V(tb), K(tb+1), V(tb+1) may still be in flight).
     wait_barrier(std::integral_constant<int, 3 * kCPW>{});
-    for (uint32_t t = t0; t < t1; t += 2) {
+    for (uint32_t t = tb; t < te; t += 2) {
       tile(t, ka, va, robust);
-      if (t + 1 >= t1) break;
+      if (t + 1 >= te) break;
       tile(t + 1, kb2, vb2, robust);
     }
     // The repeated loads of the last steps land, and every wave is past its last LDS reads,
@@ -2895,11 +2913,62 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
   }
   __syncthreads();
   if (s_rerun != 0u) {
-    issue_k(t0, ka);
-    issue_v(t0, va);
-    issue_k(t0 + 1, kb2);
-    issue_v(t0 + 1, vb2);
+    issue_k(tb, ka);
+    issue_v(tb, va);
+    issue_k(tb + 1, kb2);
+    issue_v(tb + 1, vb2);
     run(std::true_type{});
+  }
+
+  if (split) {
+    static_assert(kPairPartWords == 4 * kNb + 1, "a half's state: O^T's float4 words, then (m, l, lb)");
+    // Word k of lane `lane` of wave w of a half's state: [sidx][half][w][k][lane] float4 words;
+    // the descriptor's record count is the launch's state bytes (the host keeps them < 2 GiB).
+    const uint32_t state_bytes = sp * a.head_groups * a.num_kv_heads * 2u * 4u * kPairPartWords * 64u * 16u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, state_bytes, 0x00020000);
+    auto word = [&](uint32_t hh, int k) JMA_INL {
+      return (uint32_t)((((sidx * 2 + hh) * 4 + (uint32_t)w) * kPairPartWords + (uint32_t)k) * 64 + lane) * 16u;
+    };
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        store_part(rs, word(half, 4 * nb + c), float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]});
+    store_part(rs, word(half, 4 * kNb), float4_t{m, l, lb, 0.0f});
+    // The stores are acknowledged (visible device-wide) before the ticket is taken.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ uint32_t s_tk;
+    if (threadIdx.x == 0)
+      s_tk = __hip_atomic_fetch_add(&a.tickets[sidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_tk == 0u) return;  // the other half merges
+    if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[sidx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float16_t ox[kNb];
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float4_t x = load_part(rs, word(1u - half, 4 * nb + c));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ox[nb][4 * c + i] = x[i];
+      }
+    const float4_t mx = load_part(rs, word(1u - half, 4 * kNb));
+    {
+      // Each half's terms are rounded products (no fused multiply-add) and the sum is
+      // commutative, so either half merging gives the same bits.
+#pragma clang fp contract(off)
+      const float M = fmaxf(m, mx[0]);
+      const float aw = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+      const float ax = mx[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mx[0] - M);
+      l = l * aw + mx[1] * ax;
+      lb = lb * aw + mx[2] * ax;
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[nb][e] = o[nb][e] * aw + ox[nb][e] * ax;
+      m = M;
+    }
   }
 
   const float L = half_sum(l + lb);
@@ -2964,13 +3033,27 @@ hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, 
       a.head_groups != (a.group + a.heads_per_stripe - 1) / a.heads_per_stripe)
     return hipErrorInvalidValue;
   if (f16) {
-    // Stripe pairs (kernel 3c); 32-bit tile byte offsets.
-    const uint64_t blocks = (uint64_t)(a.row_blocks + 1) / 2 * a.head_groups * a.num_kv_heads;
+    // Stripe pairs (kernel 3c), split_blocks of them as two workgroups; 32-bit tile byte offsets.
+    const uint32_t pairs = (a.row_blocks + 1) / 2;
+    const uint64_t blocks = ((uint64_t)pairs + a.split_blocks) * a.head_groups * a.num_kv_heads;
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffu || (uint64_t)a.kv.cap * 512 * 2 > 0x7fffffffu) return hipErrorInvalidValue;
+    if (a.split_blocks > 0) {
+      // Every split pair (the trailing ones) has at least two kv tiles; the halves' states fit
+      // 32-bit byte offsets.
+      const uint32_t pr = pairs - a.split_blocks, R = a.rows_per_stripe;
+      const uint32_t r0 = 2 * pr * R, r1 = std::min(r0 + 2 * R, a.n) - 1;
+      const uint32_t t0 = first_visible(a.start + r0, a.window) / 32, t1 = (a.start + r1) / 32 + 1;
+      const uint64_t part_b = (uint64_t)a.split_blocks * a.head_groups * a.num_kv_heads * 2 * 4 *
+                              kPairPartWords * 64 * 16;
+      if (a.split_blocks > pairs || a.part == nullptr || a.tickets == nullptr || t1 - t0 < 2 ||
+          part_b > 0x7FFFFFF0u)
+        return hipErrorInvalidValue;
+    }
     hipLaunchKernelGGL((prefill_pair_kernel<512>), dim3((uint32_t)blocks), dim3(256), 0, stream, a);
     return hipGetLastError();
   }
+  if (a.split_blocks != 0) return hipErrorInvalidValue;  // f32 stripes are not split
   switch (dk) {
     case 32: return launch_prefill_slice_t<float, 32, 1>(a, stream);
     case 64: return launch_prefill_slice_t<float, 64, 2>(a, stream);

@@ -151,6 +151,16 @@ struct jmodels_attn_context {
   int* d_err = nullptr;
   DeviceBuffer part_acc, part_ml, part_f, counters, pf_part, pf_tickets, qrot, stage_q, stage_k, stage_v, stage_out;
   DeviceBuffer qact;                // Q8_0 activations of prefill-sized projections
+  DeviceBuffer pp_part, pp_tickets; // split stripe pairs of the head-dim-512 f16 prefill
+  // Recent pair-split plans (their replayed dispatch takes up to ~1 ms of host time): the
+  // layers of one prefill chunk share a plan. Key: n, start, window, rows per stripe,
+  // workgroups per pair, split_tiles, compute units.
+  struct PairMemo {
+    uint64_t key[4] = {~0ull, ~0ull, ~0ull, ~0ull};
+    uint32_t split_pairs = 0;
+  };
+  PairMemo pair_memo[8];
+  uint32_t pair_memo_next = 0;
   int decode_target_blocks = 512;   // workgroups a decode launch aims for (two per CU)
   int tiles_per_wave = 1;           // minimum tiles each decode wave streams
   int min_split_tiles = 0;          // minimum tiles per decode split; 0: waves x tiles_per_wave
@@ -631,6 +641,40 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.rows_per_stripe = 32 / a.heads_per_stripe;
     a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
     a.row_blocks = (n + a.rows_per_stripe - 1) / a.rows_per_stripe;
+    if (kv->f16()) {
+      const uint64_t key[4] = {(uint64_t)n << 32 | start, (uint64_t)lc.window << 32 | a.rows_per_stripe,
+                               (uint64_t)a.head_groups * lc.hkv << 32 | (uint32_t)ctx->prefill_split_tiles,
+                               ctx->cus};
+      uint32_t split = 0;
+      bool hit = false;
+      for (const auto& e : ctx->pair_memo)
+        if (std::equal(key, key + 4, e.key)) {
+          split = e.split_pairs;
+          hit = true;
+          break;
+        }
+      if (!hit) {
+        split = jma::plan_prefill_pairs(a, ctx->prefill_split_tiles, ctx->cus).split_pairs;
+        auto& e = ctx->pair_memo[ctx->pair_memo_next++ % 8];
+        std::copy(key, key + 4, e.key);
+        e.split_pairs = split;
+      }
+      if (split > 0) {
+        const size_t per = (size_t)a.head_groups * lc.hkv;
+        const size_t part_b = (size_t)split * per * 2 * 4 * jma::kPairPartWords * 64 * 16;
+        // The kernel addresses the halves' states with 32-bit byte offsets.
+        require(part_b <= 0x7FFFFFF0u, JMODELS_ATTN_INVALID_SHAPE,
+                "prefill pair split needs more than 2 GiB of partial states");
+        // No initial value for the states; tickets start at zero and the merging workgroups
+        // restore them, so they are zeroed only when (re)allocated.
+        ctx->pp_part.reserve(part_b, ctx->stream, "prefill pair split");
+        reserve_filled(ctx->pp_tickets, (size_t)split * per * sizeof(uint32_t), 0, ctx->stream,
+                       "prefill pair split");
+        a.split_blocks = split;
+        a.part = (float*)ctx->pp_part.ptr;
+        a.tickets = (uint32_t*)ctx->pp_tickets.ptr;
+      }
+    }
     hip_check(jma::launch_prefill_slice(a, kv->f16(), (int)lc.dk, (int)lc.dv, ctx->stream),
               "prefill launch");
     return;
@@ -723,7 +767,7 @@ int32_t collect_errors(jmodels_attn_context* ctx) {
       // A reducer gave up waiting: tickets and partial words may be left set; clear them.
       for (DeviceBuffer* b : {&ctx->part_f, &ctx->pf_part})
         if (b->ptr) hip_check(hipMemset(b->ptr, 0xFF, b->bytes), "reset partials");
-      for (DeviceBuffer* b : {&ctx->counters, &ctx->pf_tickets})
+      for (DeviceBuffer* b : {&ctx->counters, &ctx->pf_tickets, &ctx->pp_tickets})
         if (b->ptr) hip_check(hipMemset(b->ptr, 0, b->bytes), "reset tickets");
       hip_check(jma::fixed_scratch_reset(ctx->fixed, ctx->stream), "reset fixed scratch");
       fail(JMODELS_ATTN_DEVICE_ERROR, "cross-split reduction timed out waiting for a partial");
@@ -954,7 +998,8 @@ int32_t jmodels_attn_context_destroy(jmodels_attn_context* ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (DeviceBuffer* b : {&ctx->part_acc, &ctx->part_ml, &ctx->part_f, &ctx->counters, &ctx->pf_part, &ctx->pf_tickets, &ctx->qrot, &ctx->stage_q,
-                            &ctx->stage_k, &ctx->stage_v, &ctx->stage_out, &ctx->qact})
+                            &ctx->stage_k, &ctx->stage_v, &ctx->stage_out, &ctx->qact, &ctx->pp_part,
+                            &ctx->pp_tickets})
       b->release();
     (void)hipFree(ctx->d_err);
     (void)hipStreamDestroy(ctx->stream);

@@ -68,6 +68,8 @@ const char* hipGetErrorString(hipError_t error);
 // printed otherwise). hipsim_launch: runs `check(arg)` now, or records it into the stream's capture
 // so that every replay of the graph runs it; `drop(arg)` frees arg with the last graph using it.
 void hipsim_check_range(const void* p, size_t bytes, const char* what);
+// hipsim_fail: records (and prints) an error found by a launch stub's own check.
+void hipsim_fail(const char* what);
 hipError_t hipsim_launch(hipStream_t stream, const char* kernel, void (*check)(void*), void* arg,
                          void (*drop)(void*));
 long hipsim_errors(void);

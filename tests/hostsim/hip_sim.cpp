@@ -300,6 +300,11 @@ void hipsim_check_range(const void* p, size_t bytes, const char* what) {
   }
 }
 
+void hipsim_fail(const char* what) {
+  std::lock_guard<std::mutex> l(g_mu);
+  error("launch stub check failed: %s", what);
+}
+
 hipError_t hipsim_launch(hipStream_t s, const char* kernel, void (*check)(void*), void* arg,
                          void (*drop)(void*)) {
   Op op{Op::kKernel};

@@ -88,6 +88,37 @@ def test_f16_d512_prefill_matches_oracle(hip, hq, hkv, window):
     _say(f"f16 d 512 {hq}/{hkv} window {window} normwise rel err {err:.2e}")
 
 
+@pytest.mark.parametrize("split", ["2", "0"])
+@pytest.mark.parametrize("window", [0, 200])
+def test_f16_d512_prefill_split_pairs_match_oracle(monkeypatch, split, window):
+    """Stripe pairs cut in two halves of their kv tiles (JMA_PREFILL_SPLIT_TILES=2 splits every
+    pair of two or more tiles; 0 splits none): each half a workgroup, the later one merging the
+    two states. Both plans against the oracle; a repeated call gives the same bits whichever half
+    merges (attend_causal again inside the case)."""
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", split)
+    lib = A.HipAttentionLibrary(0)
+    try:
+        err = _chunked_case(lib, True, 512, 8, 1, 130, 350, window, 1e6, 35)
+        err2 = _chunked_case(lib, True, 512, 16, 2, 70, 200, window, 1e6, 36)
+    finally:
+        lib.close()
+    _say(f"f16 d 512 split tiles {split} window {window} normwise rel err {max(err, err2):.2e}")
+
+
+@pytest.mark.parametrize("which", ["k", "v"])
+@pytest.mark.parametrize("window", [0, 20])
+def test_f16_d512_split_pairs_ignore_rows_they_do_not_see(monkeypatch, which, window):
+    """The unseen-row case above with every stripe pair split: the infinite row sits in the
+    second half's tile, whose state goes non-finite in the fast pass and is recomputed in the
+    robust pass before the merge."""
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
+    lib = A.HipAttentionLibrary(0)
+    try:
+        test_slice_prefill_ignores_rows_it_does_not_see(lib, True, 512, which, window)
+    finally:
+        lib.close()
+
+
 def test_c1_qwen3_prefill_f32(hip):
     """C1's shape: 16 Q heads, 8 KV heads, d 128, NeoX theta 1e6, f32 KV, the 512-row prompt as
     one chunk, every row against the oracle."""
