@@ -5,9 +5,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <functional>
-#include <vector>
-
 #include "jma_plan.h"
 
 namespace jma {
@@ -174,15 +171,18 @@ inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, u
   return p;
 }
 
-// Stripe-pair splits of kernel 3c. A pair costs its kv tiles (each ~1.7 us on one compute unit,
-// which holds one such workgroup) plus ~1.5 tiles of prologue and epilogue, and the later half
-// of a split pair ~0.9 tiles more for the merge. The longest pairs run first, split pairs as two
-// workgroups of half the tiles. split_tiles >= 2 splits the trailing pairs of at least that many
-// tiles; 0 or 1 never splits; -1 (automatic) replays the dispatch (each workgroup to the compute
-// unit that frees first, in launch order) for up to 33 choices of how many trailing pairs to
-// split and takes the shortest, when the launch holds at most 4 workgroups per compute unit
-// (beyond that the dispatch already balances the pairs).
+// Stripe-pair splits of kernel 3c: one workgroup per compute unit (the stage arrays take 128 KB
+// of LDS) and a pair's cost grows with its row, so without splits the longest pairs set the
+// duration. split_tiles >= 2 splits the trailing (longest) pairs of at least that many kv tiles;
+// 0 or 1 never splits; -1 (automatic) splits every pair of 8 or more tiles when the pairs'
+// workgroups fit on the compute units at once (with more, the dispatch already fills the units
+// that short pairs free). Measured on the Gemma 4 full-layer prefill (S 2048, 256 pairs of 1-64
+// tiles): 115 us unsplit; every pair of at least 2 tiles split 97-98 us, of 8 94.7, of 16 98.3,
+// of 48 96.3, of 64 113. A half's state exchange costs ~9 us of the 97 (timing-only copy without
+// it: 88), the rest of the gap to perfect balance is the extra prologues and the shared K/V
+// traffic of a fully occupied device.
 constexpr uint32_t kPairPartWords = 33;  // float4 words per lane of a half's state: O^T (8 blocks x 4) and (m, l, lb)
+constexpr uint32_t kPairAutoSplitTiles = 8;
 struct PairPlan {
   uint32_t split_pairs = 0;
   size_t part_bytes = 0, ticket_bytes = 0;
@@ -193,6 +193,8 @@ inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32
   const uint32_t pairs = (a.row_blocks + 1) / 2;
   const uint32_t per = a.head_groups * a.num_kv_heads;  // workgroups per pair
   if (pairs == 0 || per == 0 || split_tiles == 0 || split_tiles == 1) return p;
+  if (split_tiles < 0 && (uint64_t)pairs * per > std::max<uint32_t>(cus, 1)) return p;
+  const uint32_t min_tiles = split_tiles >= 2 ? (uint32_t)split_tiles : kPairAutoSplitTiles;
   const uint32_t R = a.rows_per_stripe;
   auto tiles_of = [&](uint32_t pr) -> uint32_t {  // kv tiles of pair pr (the kernel's t1 - t0)
     const uint32_t r0 = 2 * pr * R, r1 = std::min(r0 + 2 * R, a.n) - 1;
@@ -200,51 +202,9 @@ inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32
     const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
     return (a.start + r1) / 32 + 1 - first / 32;
   };
-  // Trailing pairs with at least `min_tiles` tiles (all of them have two or more).
-  auto trailing = [&](uint32_t min_tiles) {
-    uint32_t n = 0;
-    while (n < pairs && tiles_of(pairs - 1 - n) >= std::max<uint32_t>(min_tiles, 2)) ++n;
-    return n;
-  };
+  // The trailing pairs with at least min_tiles (>= 2) tiles.
   uint32_t sp = 0;
-  if (split_tiles >= 2) {
-    sp = trailing((uint32_t)split_tiles);
-  } else if ((uint64_t)pairs * per <= 4ull * std::max<uint32_t>(cus, 1)) {
-    const uint32_t slots = std::max<uint32_t>(cus, 1);
-    std::vector<double> free_at(slots);
-    auto makespan = [&](uint32_t nsplit) {  // in tiles
-      std::fill(free_at.begin(), free_at.end(), 0.0);
-      std::make_heap(free_at.begin(), free_at.end(), std::greater<double>());
-      double end = 0.0;
-      auto run = [&](double cost) {
-        std::pop_heap(free_at.begin(), free_at.end(), std::greater<double>());
-        free_at.back() += cost;
-        end = std::max(end, free_at.back());
-        std::push_heap(free_at.begin(), free_at.end(), std::greater<double>());
-      };
-      for (uint32_t i = 0; i < nsplit; ++i) {
-        const uint32_t t = tiles_of(pairs - 1 - i);
-        for (uint32_t k = 0; k < per; ++k) run(1.5 + t / 2);
-        for (uint32_t k = 0; k < per; ++k) run(1.5 + (t - t / 2) + 0.9);
-      }
-      for (uint32_t i = nsplit; i < pairs; ++i)
-        for (uint32_t k = 0; k < per; ++k) run(1.5 + tiles_of(pairs - 1 - i));
-      return end;
-    };
-    double best = makespan(0);
-    const uint32_t most = trailing(2);
-    uint32_t last = 0;
-    for (uint32_t k = 1; k <= 32; ++k) {
-      const uint32_t n = (uint32_t)(((uint64_t)most * k + 31) / 32);
-      if (n == last) continue;
-      last = n;
-      const double e = makespan(n);
-      if (e < best - 1e-9) {
-        best = e;
-        sp = n;
-      }
-    }
-  }
+  while (sp < pairs && tiles_of(pairs - 1 - sp) >= std::max<uint32_t>(min_tiles, 2)) ++sp;
   p.split_pairs = sp;
   p.part_bytes = (size_t)sp * per * 2 * 4 * kPairPartWords * 64 * 16;
   p.ticket_bytes = (size_t)sp * per * sizeof(uint32_t);

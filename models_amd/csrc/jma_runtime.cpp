@@ -152,15 +152,6 @@ struct jmodels_attn_context {
   DeviceBuffer part_acc, part_ml, part_f, counters, pf_part, pf_tickets, qrot, stage_q, stage_k, stage_v, stage_out;
   DeviceBuffer qact;                // Q8_0 activations of prefill-sized projections
   DeviceBuffer pp_part, pp_tickets; // split stripe pairs of the head-dim-512 f16 prefill
-  // Recent pair-split plans (their replayed dispatch takes up to ~1 ms of host time): the
-  // layers of one prefill chunk share a plan. Key: n, start, window, rows per stripe,
-  // workgroups per pair, split_tiles, compute units.
-  struct PairMemo {
-    uint64_t key[4] = {~0ull, ~0ull, ~0ull, ~0ull};
-    uint32_t split_pairs = 0;
-  };
-  PairMemo pair_memo[8];
-  uint32_t pair_memo_next = 0;
   int decode_target_blocks = 512;   // workgroups a decode launch aims for (two per CU)
   int tiles_per_wave = 1;           // minimum tiles each decode wave streams
   int min_split_tiles = 0;          // minimum tiles per decode split; 0: waves x tiles_per_wave
@@ -642,23 +633,7 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
     a.row_blocks = (n + a.rows_per_stripe - 1) / a.rows_per_stripe;
     if (kv->f16()) {
-      const uint64_t key[4] = {(uint64_t)n << 32 | start, (uint64_t)lc.window << 32 | a.rows_per_stripe,
-                               (uint64_t)a.head_groups * lc.hkv << 32 | (uint32_t)ctx->prefill_split_tiles,
-                               ctx->cus};
-      uint32_t split = 0;
-      bool hit = false;
-      for (const auto& e : ctx->pair_memo)
-        if (std::equal(key, key + 4, e.key)) {
-          split = e.split_pairs;
-          hit = true;
-          break;
-        }
-      if (!hit) {
-        split = jma::plan_prefill_pairs(a, ctx->prefill_split_tiles, ctx->cus).split_pairs;
-        auto& e = ctx->pair_memo[ctx->pair_memo_next++ % 8];
-        std::copy(key, key + 4, e.key);
-        e.split_pairs = split;
-      }
+      const uint32_t split = jma::plan_prefill_pairs(a, ctx->prefill_split_tiles, ctx->cus).split_pairs;
       if (split > 0) {
         const size_t per = (size_t)a.head_groups * lc.hkv;
         const size_t part_b = (size_t)split * per * 2 * 4 * jma::kPairPartWords * 64 * 16;
