@@ -183,6 +183,7 @@ inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, u
 // traffic of a fully occupied device.
 constexpr uint32_t kPairPartWords = 33;  // float4 words per lane of a half's state: O^T (8 blocks x 4) and (m, l, lb)
 constexpr uint32_t kPairAutoSplitTiles = 8;
+constexpr uint32_t kPairLead = 2;  // tiles by which a split pair's first half is the shorter
 struct PairPlan {
   uint32_t split_pairs = 0;
   size_t part_bytes = 0, ticket_bytes = 0;

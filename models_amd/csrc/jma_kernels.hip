@@ -2682,8 +2682,9 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
   const uint32_t t0 = first_visible(a.start + p_row0, a.window) / 32;
   const uint32_t t1 = (a.start + p_last) / 32 + 1;
   // This workgroup's tiles [tb, te): all of the pair's, or one half (a split pair has at least
-  // two tiles).
-  const uint32_t tm = t0 + (t1 - t0) / 2;
+  // two tiles). The first half is kPairLead tiles shorter (at least one tile), so it usually
+  // stores its state while the second still computes, and the second merges without storing.
+  const uint32_t tm = t0 + max(1u, (t1 - t0 - min(t1 - t0, kPairLead)) / 2);
   const uint32_t tb = split && half != 0u ? tm : t0;
   const uint32_t te = split && half == 0u ? tm : t1;
 
@@ -2929,20 +2930,27 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     auto word = [&](uint32_t hh, int k) JMA_INL {
       return (uint32_t)((((sidx * 2 + hh) * 4 + (uint32_t)w) * kPairPartWords + (uint32_t)k) * 64 + lane) * 16u;
     };
-#pragma unroll
-    for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        store_part(rs, word(half, 4 * nb + c), float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]});
-    store_part(rs, word(half, 4 * kNb), float4_t{m, l, lb, 0.0f});
-    // The stores are acknowledged (visible device-wide) before the ticket is taken.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // The ticket counts stored states. A half that finds the other's state stored merges at once
+    // (its own never leaves the registers); otherwise it stores its state and takes a ticket, and
+    // the one that then finds the count at 1 merges: exactly one half merges either way.
     __shared__ uint32_t s_tk;
-    if (threadIdx.x == 0)
-      s_tk = __hip_atomic_fetch_add(&a.tickets[sidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) s_tk = __hip_atomic_load(&a.tickets[sidx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (s_tk == 0u) return;  // the other half merges
+    if (s_tk == 0u) {
+#pragma unroll
+      for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          store_part(rs, word(half, 4 * nb + c), float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]});
+      store_part(rs, word(half, 4 * kNb), float4_t{m, l, lb, 0.0f});
+      // The stores are acknowledged (visible device-wide) before the ticket is taken.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (threadIdx.x == 0)
+        s_tk = __hip_atomic_fetch_add(&a.tickets[sidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (s_tk == 0u) return;  // the other half merges
+    }
     if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[sidx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float16_t ox[kNb];
 #pragma unroll
