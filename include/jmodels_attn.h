@@ -202,8 +202,9 @@ typedef struct jmodels_attn_layer_spec {
  * calls use the layer's own dimensions (jmodels_attn_layer.num_heads must be a multiple of that
  * layer's num_kv_heads). Decode supports key_length == value_length in {32, 64, 128, 256, 512}
  * (f16) or {16, ..., 512} (f32). Prefill of f16 caches runs the MFMA kernel at key lengths
- * 32-256 and the d-sliced prefill kernel at 512; f32 caches run the d-sliced kernel (32-512);
- * other supported decode shapes run the decode kernel over chunks of the prefill's rows. */
+ * 32-256 and the paired-stripe prefill kernel at 512; f32 caches run the d-sliced kernel
+ * (32-512); other supported decode shapes run the decode kernel over chunks of the prefill's
+ * rows. */
 JMODELS_ATTN_API int32_t jmodels_attn_kv_create_layered(jmodels_attn_context* ctx, uint32_t sequences,
                                        uint32_t num_layers, uint32_t max_seq_len,
                                        const jmodels_attn_layer_spec* specs, uint32_t dtype,
@@ -271,8 +272,9 @@ JMODELS_ATTN_API int32_t jmodels_attn_decode(jmodels_attn_context* ctx, jmodels_
  * head dims 32-256 run the MFMA kernel (kernel 3) with f16 queries; f32 caches at 32-512 run the
  * d-sliced prefill kernel (kernel 3b: the waves of a workgroup split the head dimension and add
  * their partial score tiles through LDS); f16 caches at 512 run the paired-stripe kernel (kernel
- * 3c: two stripes share each LDS-staged tile, each split over two waves); other shapes run the
- * decode kernel over chunks of the rows. */
+ * 3c: two stripes share each LDS-staged tile, each split over two waves; when the pairs fit the
+ * compute units at once, the longer pairs run as two workgroups over halves of their tiles,
+ * merged by the later one); other shapes run the decode kernel over chunks of the rows. */
 JMODELS_ATTN_API int32_t jmodels_attn_prefill(jmodels_attn_context* ctx, jmodels_attn_kv* kv,
                              const jmodels_attn_layer* layer, uint32_t sequence, uint32_t start,
                              uint32_t n, const float* q, uint64_t q_elements, const float* k,
