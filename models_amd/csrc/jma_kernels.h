@@ -183,22 +183,30 @@ inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, u
 // traffic of a fully occupied device.
 constexpr uint32_t kPairPartWords = 33;  // float4 words per lane of a half's state: O^T (8 blocks x 4) and (m, l, lb)
 constexpr uint32_t kPairAutoSplitTiles = 8;
-constexpr uint32_t kPairLead = 2;  // tiles by which a split pair's first half is the shorter
 struct PairPlan {
   uint32_t split_pairs = 0;
   size_t part_bytes = 0, ticket_bytes = 0;
 };
 
-inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32_t cus) {
+// Waves of a kernel 3b workgroup at head dim d, and the float4 words per lane of one wave's state
+// when its stripe is split (O^T slice, then m, l, lb).
+constexpr int slice_waves(int d) { return d <= 32 ? 1 : d == 64 ? 2 : d <= 256 ? 4 : 8; }
+constexpr uint32_t slice_state_words(int d) { return 4u * (uint32_t)(d / slice_waves(d) / 32) + 1u; }
+
+// The split plan of kernel 3c's stripe pairs (unit_rows = 2 rows_per_stripe) or of kernel 3b's
+// single stripes (unit_rows = rows_per_stripe), whose units run last-first: the trailing units
+// with enough kv tiles run as two workgroups each (same rule and measurements as above).
+inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32_t cus,
+                                   uint32_t unit_rows = 0, uint32_t state_bytes_per_half = 0) {
   PairPlan p;
-  const uint32_t pairs = (a.row_blocks + 1) / 2;
-  const uint32_t per = a.head_groups * a.num_kv_heads;  // workgroups per pair
+  const uint32_t R = unit_rows ? unit_rows : 2 * a.rows_per_stripe;
+  const uint32_t pairs = unit_rows ? a.row_blocks : (a.row_blocks + 1) / 2;
+  const uint32_t per = a.head_groups * a.num_kv_heads;  // workgroups per unit
   if (pairs == 0 || per == 0 || split_tiles == 0 || split_tiles == 1) return p;
   if (split_tiles < 0 && (uint64_t)pairs * per > std::max<uint32_t>(cus, 1)) return p;
   const uint32_t min_tiles = split_tiles >= 2 ? (uint32_t)split_tiles : kPairAutoSplitTiles;
-  const uint32_t R = a.rows_per_stripe;
-  auto tiles_of = [&](uint32_t pr) -> uint32_t {  // kv tiles of pair pr (the kernel's t1 - t0)
-    const uint32_t r0 = 2 * pr * R, r1 = std::min(r0 + 2 * R, a.n) - 1;
+  auto tiles_of = [&](uint32_t pr) -> uint32_t {  // kv tiles of unit pr (the kernel's t1 - t0)
+    const uint32_t r0 = pr * R, r1 = std::min(r0 + R, a.n) - 1;
     const uint32_t w = a.window, p0 = a.start + r0;
     const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
     return (a.start + r1) / 32 + 1 - first / 32;
@@ -207,7 +215,8 @@ inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32
   uint32_t sp = 0;
   while (sp < pairs && tiles_of(pairs - 1 - sp) >= std::max<uint32_t>(min_tiles, 2)) ++sp;
   p.split_pairs = sp;
-  p.part_bytes = (size_t)sp * per * 2 * 4 * kPairPartWords * 64 * 16;
+  p.part_bytes = (size_t)sp * per * 2 *
+                 (state_bytes_per_half ? state_bytes_per_half : 4 * kPairPartWords * 64 * 16);
   p.ticket_bytes = (size_t)sp * per * sizeof(uint32_t);
   return p;
 }

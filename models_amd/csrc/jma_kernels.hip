@@ -2394,6 +2394,71 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
 //    8m + 4 + t. PV: op u (u < 16) takes the lane's own probability u (slot 8(u/4) + 4h + u%4)
 //    as its B operand and V^T at the same slots as A, four consecutive slots per float4 load of
 //    an f32 V block.
+// A split stripe (kernel 3b) or stripe pair (kernel 3c) runs as two workgroups, one per half of
+// its kv tiles. Each ends with an online-softmax state per lane of each of its W waves (O^T,
+// m, l, lb), kept at [sidx][half][wave][4 kNb + 1 float4 words][64 lanes] in a.part, and
+// a.tickets[sidx] counts the states stored. A half that finds the other's state stored merges at
+// once (its own never leaves the registers); otherwise it stores its state (device-coherent,
+// acknowledged) and takes a ticket, and the one that then finds the count at 1 merges: exactly one
+// half merges either way, and it resets the ticket. The merge forms each half's rounded terms
+// o 2^(m_h - M) (no fused multiply-add) and adds them, which commutes, so the result does not
+// depend on which half merges. Returns whether this workgroup merged (o, m, l, lb then hold the
+// pair's state); the other returns false and stores nothing more.
+template <int W, int kNb>
+__device__ __forceinline__ bool merge_halves(const PrefillArgs& a, uint32_t sidx, uint32_t half, int w,
+                                             int lane, pf::float16_t (&o)[kNb], float& m, float& l, float& lb) {
+  constexpr uint32_t kWords = 4u * kNb + 1u;
+  // The descriptor's record count is the launch's state bytes (the host keeps them < 2 GiB).
+  const uint32_t state_bytes = a.split_blocks * a.head_groups * a.num_kv_heads * 2u * W * kWords * 64u * 16u;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, state_bytes, 0x00020000);
+  auto word = [&](uint32_t hh, uint32_t k) JMA_INL {
+    return (uint32_t)((((sidx * 2 + hh) * W + (uint32_t)w) * kWords + k) * 64 + (uint32_t)lane) * 16u;
+  };
+  __shared__ uint32_t s_tk;
+  if (threadIdx.x == 0) s_tk = __hip_atomic_load(&a.tickets[sidx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_tk == 0u) {
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        store_part(rs, word(half, 4 * nb + c), float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]});
+    store_part(rs, word(half, 4 * kNb), float4_t{m, l, lb, 0.0f});
+    // The stores are acknowledged (visible device-wide) before the ticket is taken.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_tk = __hip_atomic_fetch_add(&a.tickets[sidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_tk == 0u) return false;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[sidx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  pf::float16_t ox[kNb];
+#pragma unroll
+  for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4_t x = load_part(rs, word(1u - half, 4 * nb + c));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ox[nb][4 * c + i] = x[i];
+    }
+  const float4_t mx = load_part(rs, word(1u - half, 4 * kNb));
+  {
+#pragma clang fp contract(off)
+    const float M = fmaxf(m, mx[0]);
+    const float aw = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+    const float ax = mx[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mx[0] - M);
+    l = l * aw + mx[1] * ax;
+    lb = lb * aw + mx[2] * ax;
+#pragma unroll
+    for (int nb = 0; nb < kNb; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[nb][e] = o[nb][e] * aw + ox[nb][e] * ax;
+    m = M;
+  }
+  return true;
+}
+
 template <typename KV, int D, int W>
 __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs a) {
   using namespace pf;
@@ -2414,12 +2479,18 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
 
   const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  static_assert(W == slice_waves(D) && slice_state_words(D) == 4 * kNb + 1, "split state layout");
   // Kv heads vary fastest (consecutive workgroups on different XCDs, each XCD's L2 keeping few
-  // kv heads); stripes run last-first (longest causal ranges first).
+  // kv heads); stripes run last-first (longest causal ranges first): items 0 .. 2 split_blocks - 1
+  // are the halves of the split stripes (as kernel 3c splits its pairs), the rest one stripe each.
   const uint32_t kvh = blockIdx.x % a.num_kv_heads;
   const uint32_t rest = blockIdx.x / a.num_kv_heads;
   const uint32_t hz = rest % a.head_groups;
-  const uint32_t stripe = a.row_blocks - 1 - rest / a.head_groups;
+  const uint32_t item = rest / a.head_groups;
+  const SplitItem si = split_item(a.row_blocks, a.split_blocks, item);
+  const bool split = si.split;
+  const uint32_t half = si.half, stripe = si.unit;
+  const uint32_t sidx = ((split ? item / 2 : 0u) * a.head_groups + hz) * a.num_kv_heads + kvh;
   const uint32_t R = a.rows_per_stripe, Gz = a.heads_per_stripe;
   const uint32_t row0 = stripe * R;
   const uint32_t row_last = min(row0 + R - 1, a.n - 1);
@@ -2437,7 +2508,9 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
   const uint32_t s_last = a.start + row_last;
   const uint32_t all_first = first_visible(s_last, a.window);
   const uint32_t all_last = a.start + row0;
-  const uint32_t t0 = s_first / 32, t1 = s_last / 32 + 1;
+  // This workgroup's tiles [t0, t1): the stripe's, or one half of them.
+  uint32_t t0, t1;
+  split_range(s_first / 32, s_last / 32 + 1, si, t0, t1);
 
   const KV* const kb = (const KV*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
                        (uint64_t)kvh * a.kv.cap * D;
@@ -2576,6 +2649,8 @@ __global__ __launch_bounds__(64 * W) void prefill_slice_kernel(const PrefillArgs
     tile(t + 1, nxt);
   }
 
+  if (split && !merge_halves<W, kNb>(a, sidx, half, w, lane, o, m, l, lb)) return;  // the other merges
+
   const float L = half_sum(l + lb);
   const bool bad = col_ok && !(L > 0.0f && L < INFINITY);
   if (__ballot(bad) != 0 && lane == 0) atomicOr(a.err, 1);
@@ -2652,10 +2727,10 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
   const uint32_t kvh = blockIdx.x % a.num_kv_heads;
   const uint32_t rest = blockIdx.x / a.num_kv_heads;
   const uint32_t hz = rest % a.head_groups;
-  const uint32_t item = rest / a.head_groups, sp = a.split_blocks;
-  const bool split = item < 2 * sp;
-  const uint32_t half = split ? item & 1u : 0u;
-  const uint32_t pr = pairs - 1 - (split ? item / 2 : item - sp);
+  const uint32_t item = rest / a.head_groups;
+  const SplitItem si = split_item(pairs, a.split_blocks, item);
+  const bool split = si.split;
+  const uint32_t half = si.half, pr = si.unit;
   const uint32_t sidx = ((split ? item / 2 : 0u) * a.head_groups + hz) * a.num_kv_heads + kvh;
   const uint32_t stripe = 2 * pr + st;
   const bool stripe_ok = stripe < a.row_blocks;
@@ -2681,12 +2756,11 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
   const uint32_t p_last = min(p_row0 + 2 * R - 1, a.n - 1);
   const uint32_t t0 = first_visible(a.start + p_row0, a.window) / 32;
   const uint32_t t1 = (a.start + p_last) / 32 + 1;
-  // This workgroup's tiles [tb, te): all of the pair's, or one half (a split pair has at least
-  // two tiles). The first half is kPairLead tiles shorter (at least one tile), so it usually
-  // stores its state while the second still computes, and the second merges without storing.
-  const uint32_t tm = t0 + max(1u, (t1 - t0 - min(t1 - t0, kPairLead)) / 2);
-  const uint32_t tb = split && half != 0u ? tm : t0;
-  const uint32_t te = split && half == 0u ? tm : t1;
+  // This workgroup's tiles [tb, te): all of the pair's, or one half. The first half is shorter,
+  // so it usually stores its state while the second still computes, and the second merges
+  // without storing its own.
+  uint32_t tb, te;
+  split_range(t0, t1, si, tb, te);
 
   const _Float16* const kbase = (const _Float16*)a.kv.k + a.seq * a.kv.seq_stride_k + a.kv.layer_off_k +
                                 (uint64_t)kvh * a.kv.cap * D;
@@ -2921,63 +2995,8 @@ __global__ __launch_bounds__(256) void prefill_pair_kernel(const PrefillArgs a) 
     run(std::true_type{});
   }
 
-  if (split) {
-    static_assert(kPairPartWords == 4 * kNb + 1, "a half's state: O^T's float4 words, then (m, l, lb)");
-    // Word k of lane `lane` of wave w of a half's state: [sidx][half][w][k][lane] float4 words;
-    // the descriptor's record count is the launch's state bytes (the host keeps them < 2 GiB).
-    const uint32_t state_bytes = sp * a.head_groups * a.num_kv_heads * 2u * 4u * kPairPartWords * 64u * 16u;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, state_bytes, 0x00020000);
-    auto word = [&](uint32_t hh, int k) JMA_INL {
-      return (uint32_t)((((sidx * 2 + hh) * 4 + (uint32_t)w) * kPairPartWords + (uint32_t)k) * 64 + lane) * 16u;
-    };
-    // The ticket counts stored states. A half that finds the other's state stored merges at once
-    // (its own never leaves the registers); otherwise it stores its state and takes a ticket, and
-    // the one that then finds the count at 1 merges: exactly one half merges either way.
-    __shared__ uint32_t s_tk;
-    if (threadIdx.x == 0) s_tk = __hip_atomic_load(&a.tickets[sidx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_tk == 0u) {
-#pragma unroll
-      for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          store_part(rs, word(half, 4 * nb + c), float4_t{o[nb][4 * c], o[nb][4 * c + 1], o[nb][4 * c + 2], o[nb][4 * c + 3]});
-      store_part(rs, word(half, 4 * kNb), float4_t{m, l, lb, 0.0f});
-      // The stores are acknowledged (visible device-wide) before the ticket is taken.
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (threadIdx.x == 0)
-        s_tk = __hip_atomic_fetch_add(&a.tickets[sidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (s_tk == 0u) return;  // the other half merges
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[sidx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    float16_t ox[kNb];
-#pragma unroll
-    for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float4_t x = load_part(rs, word(1u - half, 4 * nb + c));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ox[nb][4 * c + i] = x[i];
-      }
-    const float4_t mx = load_part(rs, word(1u - half, 4 * kNb));
-    {
-      // Each half's terms are rounded products (no fused multiply-add) and the sum is
-      // commutative, so either half merging gives the same bits.
-#pragma clang fp contract(off)
-      const float M = fmaxf(m, mx[0]);
-      const float aw = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-      const float ax = mx[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mx[0] - M);
-      l = l * aw + mx[1] * ax;
-      lb = lb * aw + mx[2] * ax;
-#pragma unroll
-      for (int nb = 0; nb < kNb; ++nb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[nb][e] = o[nb][e] * aw + ox[nb][e] * ax;
-      m = M;
-    }
-  }
+  static_assert(kPairPartWords == 4 * kNb + 1, "a half's state: O^T's float4 words, then (m, l, lb)");
+  if (split && !merge_halves<4, kNb>(a, sidx, half, w, lane, o, m, l, lb)) return;  // the other merges
 
   const float L = half_sum(l + lb);
   const bool bad = col_ok && !(L > 0.0f && L < INFINITY);
@@ -3024,7 +3043,8 @@ hipError_t launch_prefill(const PrefillArgs& a, int dk, int dv, hipStream_t stre
 
 template <typename KV, int D, int W>
 hipError_t launch_prefill_slice_t(const PrefillArgs& a, hipStream_t stream) {
-  const uint64_t blocks = (uint64_t)a.row_blocks * a.head_groups * a.num_kv_heads;
+  // One workgroup per stripe, two per split stripe.
+  const uint64_t blocks = split_items(a.row_blocks, a.split_blocks) * a.head_groups * a.num_kv_heads;
   if (blocks == 0) return hipSuccess;
   if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_slice_kernel<KV, D, W>), dim3((uint32_t)blocks), dim3(64 * W), 0,
@@ -3043,7 +3063,7 @@ hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, 
   if (f16) {
     // Stripe pairs (kernel 3c), split_blocks of them as two workgroups; 32-bit tile byte offsets.
     const uint32_t pairs = (a.row_blocks + 1) / 2;
-    const uint64_t blocks = ((uint64_t)pairs + a.split_blocks) * a.head_groups * a.num_kv_heads;
+    const uint64_t blocks = split_items(pairs, a.split_blocks) * a.head_groups * a.num_kv_heads;
     if (blocks == 0) return hipSuccess;
     if (blocks > 0x7fffffffu || (uint64_t)a.kv.cap * 512 * 2 > 0x7fffffffu) return hipErrorInvalidValue;
     if (a.split_blocks > 0) {
@@ -3061,7 +3081,18 @@ hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, 
     hipLaunchKernelGGL((prefill_pair_kernel<512>), dim3((uint32_t)blocks), dim3(256), 0, stream, a);
     return hipGetLastError();
   }
-  if (a.split_blocks != 0) return hipErrorInvalidValue;  // f32 stripes are not split
+  if (a.split_blocks > 0) {
+    // Split stripes (the trailing ones) have at least two kv tiles; the halves' states fit 32-bit
+    // byte offsets.
+    const uint32_t st = a.row_blocks - a.split_blocks, R = a.rows_per_stripe;
+    const uint32_t r0 = st * R, r1 = std::min(r0 + R, a.n) - 1;
+    const uint32_t t0 = first_visible(a.start + r0, a.window) / 32, t1 = (a.start + r1) / 32 + 1;
+    const uint64_t part_b = (uint64_t)a.split_blocks * a.head_groups * a.num_kv_heads * 2 *
+                            slice_waves(dk) * slice_state_words(dk) * 64 * 16;
+    if (a.split_blocks > a.row_blocks || a.part == nullptr || a.tickets == nullptr || t1 - t0 < 2 ||
+        part_b > 0x7FFFFFF0u)
+      return hipErrorInvalidValue;
+  }
   switch (dk) {
     case 32: return launch_prefill_slice_t<float, 32, 1>(a, stream);
     case 64: return launch_prefill_slice_t<float, 64, 2>(a, stream);

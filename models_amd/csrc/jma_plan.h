@@ -206,6 +206,39 @@ inline DecodePlan plan_decode(uint32_t count, const uint32_t* positions, uint32_
   return p;
 }
 
+// ---------------------------------------------------------------- split prefill units
+//
+// Work items of a prefill launch whose units (kernel 3b's stripes, kernel 3c's stripe pairs) run
+// last-first (the longest causal ranges first), the trailing split_units of them as two items each
+// (they come first), one per half of the unit's kv tiles [t0, t1); the first half is kPairLead
+// tiles shorter (at least one tile; a split unit has two or more). Shared by the kernels, their
+// launches (grid size) and a CPU check that every unit's tiles are covered exactly once.
+constexpr uint32_t kPairLead = 2;  // tiles by which a split unit's first half is the shorter
+
+struct SplitItem {
+  uint32_t unit, half;
+  bool split;
+};
+JMA_HD uint64_t split_items(uint32_t units, uint32_t split_units) {
+  return (uint64_t)units + split_units;
+}
+JMA_HD SplitItem split_item(uint32_t units, uint32_t split_units, uint32_t item) {
+  SplitItem r;
+  r.split = item < 2 * split_units;
+  r.half = r.split ? item & 1u : 0u;
+  r.unit = units - 1 - (r.split ? item / 2 : item - split_units);
+  return r;
+}
+// The item's tiles [tb, te) of its unit's [t0, t1).
+JMA_HD void split_range(uint32_t t0, uint32_t t1, const SplitItem& it, uint32_t& tb, uint32_t& te) {
+  const uint32_t n = t1 - t0;
+  const uint32_t lead = n < kPairLead ? n : kPairLead;
+  const uint32_t first = (n - lead) / 2 > 1u ? (n - lead) / 2 : 1u;
+  const uint32_t tm = t0 + first;
+  tb = it.split && it.half != 0u ? tm : t0;
+  te = it.split && it.half == 0u ? tm : t1;
+}
+
 // ---------------------------------------------------------------- quantized projections
 //
 // Launch planning of the block-quantized projections (jma_quant.hip), shared by the runtime and a

@@ -632,11 +632,17 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.rows_per_stripe = 32 / a.heads_per_stripe;
     a.head_groups = (lc.group + a.heads_per_stripe - 1) / a.heads_per_stripe;
     a.row_blocks = (n + a.rows_per_stripe - 1) / a.rows_per_stripe;
-    if (kv->f16()) {
-      const uint32_t split = jma::plan_prefill_pairs(a, ctx->prefill_split_tiles, ctx->cus).split_pairs;
+    {
+      // Split stripe pairs (f16, kernel 3c) or stripes (f32, kernel 3b).
+      const uint32_t half_bytes =
+          kv->f16() ? 4u * jma::kPairPartWords * 64u * 16u
+                    : (uint32_t)jma::slice_waves((int)lc.dk) * jma::slice_state_words((int)lc.dk) * 64u * 16u;
+      const jma::PairPlan pp = jma::plan_prefill_pairs(a, ctx->prefill_split_tiles, ctx->cus,
+                                                       kv->f16() ? 0u : a.rows_per_stripe, half_bytes);
+      const uint32_t split = pp.split_pairs;
       if (split > 0) {
         const size_t per = (size_t)a.head_groups * lc.hkv;
-        const size_t part_b = (size_t)split * per * 2 * 4 * jma::kPairPartWords * 64 * 16;
+        const size_t part_b = pp.part_bytes;
         // The kernel addresses the halves' states with 32-bit byte offsets.
         require(part_b <= 0x7FFFFFF0u, JMODELS_ATTN_INVALID_SHAPE,
                 "prefill pair split needs more than 2 GiB of partial states");

@@ -187,9 +187,9 @@ hipError_t launch_prefill_slice(const PrefillArgs& a, bool f16, int dk, int dv, 
   one.seq0 = a.seq;
   add_cache(l, a.kv, one, a.num_kv_heads, dk, dv, f16 ? 2 : 4);
   if (a.split_blocks > 0) {
-    if (!f16) hipsim_fail("f32 prefill stripes planned with splits");
     const size_t splits = (size_t)a.split_blocks * a.head_groups * a.num_kv_heads;
-    add(l, a.part, splits * 2 * 4 * kPairPartWords * 64 * 16, "pair split states");
+    const size_t half = f16 ? 4 * kPairPartWords * 64 * 16 : (size_t)slice_waves(dk) * slice_state_words(dk) * 64 * 16;
+    add(l, a.part, splits * 2 * half, "split states");
     add(l, a.tickets, splits * 4, "pair split tickets");
   }
   return submit(stream, "prefill_slice_kernel", l);

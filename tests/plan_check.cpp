@@ -19,6 +19,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -224,7 +225,38 @@ void check_k_layout(uint32_t dk, bool f16, uint32_t cap) {
 
 }  // namespace
 
+// Split prefill units (kernels 3b and 3c): the launch's items cover every unit's kv tiles exactly
+// once, a split unit's two halves nonempty and adjacent.
+void check_split_items(uint32_t units, uint32_t split_units, uint32_t (*tiles)(uint32_t)) {
+  std::vector<std::vector<std::pair<uint32_t, uint32_t>>> seen(units);
+  const uint64_t n = jma::split_items(units, split_units);
+  for (uint32_t item = 0; item < n; ++item) {
+    const jma::SplitItem it = jma::split_item(units, split_units, item);
+    if (it.unit >= units) k_fail("split item maps past the units");
+    const uint32_t t1 = tiles(it.unit) + 3, t0 = 3;
+    if (it.split && t1 - t0 < 2) k_fail("split unit with fewer than two tiles");
+    uint32_t tb, te;
+    jma::split_range(t0, t1, it, tb, te);
+    if (!(t0 <= tb && tb < te && te <= t1)) k_fail("empty or out-of-range split half");
+    seen[it.unit].push_back({tb, te});
+  }
+  for (uint32_t u = 0; u < units; ++u) {
+    const bool split = u + split_units >= units;
+    auto& r = seen[u];
+    std::sort(r.begin(), r.end());
+    const uint32_t t1 = tiles(u) + 3;
+    if (r.size() != (split ? 2u : 1u) || r.front().first != 3 || r.back().second != t1 ||
+        (split && r[0].second != r[1].first))
+      k_fail("unit " + std::to_string(u) + " not covered exactly once");
+  }
+}
+
 int main() {
+  for (uint32_t units : {1u, 2u, 7u, 64u, 256u, 257u})
+    for (uint32_t frac : {0u, 1u, 2u, 4u})
+      check_split_items(units, frac == 0 ? 0 : (units * frac + 3) / 4,
+                        [](uint32_t u) -> uint32_t { return 2 + u / 3; });
+  printf("split prefill items: every unit covered once\n");
   std::vector<Case> cases;
   // BASELINE configs at their configured sizes (one decode row per launch unless listed).
   cases.push_back({"C1 f32 d128 16/8 @512", {512}, 0, 8, 2, 128, 128, false, 512, 1, false, 0});

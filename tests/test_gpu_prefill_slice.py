@@ -4,7 +4,8 @@ counts leaving the last pair half empty), against the oracle's prefill (computeB
 backend-java llama/LlamaForwardPass.java:1515-1541) on identical seeded inputs.
 
 Bars: attention outputs within max-abs 1e-3 with f32 KV and normwise relative 2e-2 per (row, head)
-with f16 KV; the stored K/V rows bit-exact. The cases cover chunked prefill (a chunk start > 0
+with f16 KV; the stored K/V rows bit-exact. The cases cover split stripes and stripe pairs (two
+workgroups per stripe over halves of its kv tiles, merged), chunked prefill (a chunk start > 0
 attends to cached rows), sliding windows, GQA groups that leave padding columns in a stripe
 (group 3: 10 rows x 3 heads of 32 columns), ragged tails, non-finite cache contents at positions a
 row does not see, a NaN query (status NON_FINITE), and C1's shape (Qwen3-0.6B, 512 rows, f32)."""
@@ -103,6 +104,35 @@ def test_f16_d512_prefill_split_pairs_match_oracle(monkeypatch, split, window):
     finally:
         lib.close()
     _say(f"f16 d 512 split tiles {split} window {window} normwise rel err {max(err, err2):.2e}")
+
+
+@pytest.mark.parametrize("d", [32, 128, 512])
+@pytest.mark.parametrize("window", [0, 100])
+def test_f32_prefill_split_stripes_match_oracle(monkeypatch, d, window):
+    """f32 stripes cut in two halves of their kv tiles (JMA_PREFILL_SPLIT_TILES=2: every stripe of
+    two or more tiles), the later half merging the two states: 1, 4 and 8 waves per workgroup
+    against the oracle, and the same bits on a repeated call."""
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
+    lib = A.HipAttentionLibrary(0)
+    try:
+        n2 = 229 if d < 512 else 131
+        err = _chunked_case(lib, False, d, 12, 4, 70, n2, window, 1e4, 37)
+    finally:
+        lib.close()
+    _say(f"f32 d {d} split stripes window {window} max abs err {err:.2e}")
+
+
+@pytest.mark.parametrize("half,d", [(False, 64), (False, 256), (True, 512)])
+@pytest.mark.parametrize("which", ["k", "v"])
+def test_split_prefill_ignores_rows_it_does_not_see(monkeypatch, half, d, which):
+    """The unseen-row case above with every stripe (f32) or stripe pair (f16) split, windowed: the
+    infinite rows sit in tiles of both halves."""
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
+    lib = A.HipAttentionLibrary(0)
+    try:
+        test_slice_prefill_ignores_rows_it_does_not_see(lib, half, d, which, 20)
+    finally:
+        lib.close()
 
 
 @pytest.mark.parametrize("which", ["k", "v"])

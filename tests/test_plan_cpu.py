@@ -4,7 +4,8 @@ configured sizes, including C5's global layers with the wide split plan and its 
 ring layers) and extreme tuning settings with the runtime's own planner, then walks every
 workgroup's partial-buffer, counter and tile indexing with the kernels' own index functions. It
 also checks the K tile layout (k_index is a bijection, and the decode and prefill K loads address
-the elements it places there, each decode operand load one contiguous 1 KB run)."""
+the elements it places there, each decode operand load one contiguous 1 KB run), and that a split
+prefill launch's work items cover every stripe's (or stripe pair's) kv tiles exactly once."""
 
 import os
 import shutil
@@ -28,6 +29,7 @@ def test_decode_plans_stay_in_bounds(tmp_path):
     assert run.stdout.strip().endswith("ok"), run.stdout
     assert "C5 global d256 4/1 @32767" in run.stdout and "separate" in run.stdout
     assert "K layout: bijective" in run.stdout
+    assert "split prefill items: every unit covered once" in run.stdout
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
