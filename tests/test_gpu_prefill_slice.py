@@ -149,6 +149,60 @@ def test_f16_d512_split_pairs_ignore_rows_they_do_not_see(monkeypatch, which, wi
         lib.close()
 
 
+@pytest.mark.parametrize("half,d,hq,hkv", [(True, 512, 8, 1), (False, 128, 16, 8)])
+def test_split_prefill_graph_replays_match_eager(monkeypatch, half, d, hq, hkv):
+    """Split stripes (f32) and stripe pairs (f16 at 512) from a captured graph: attend_causal on
+    device buffers, captured once its scratch exists, replayed three times with an eager call of
+    another split shape (same ticket and state buffers) between replays; every replay gives the
+    eager call's bits, so the merging halves leave every ticket at zero for the next launch."""
+    import importlib
+    rt = importlib.import_module("models_amd.hip_runtime")
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
+    lib = A.HipAttentionLibrary(0)
+    theta, n, n2 = 1e6, 300, 180
+    tag = f"psl-graph/{int(half)}/{d}"
+    rope = lib.rotary_table(d, theta, 1.0, max_positions=n + 1)
+    kv = lib.kv_cache(1, n + 32, hkv, d, d, half_precision=half)
+    bufs, graph = [], None
+    try:
+        layer = A.AttentionLayer(0, hq, neox=True, rope=rope)
+        q = normal(38, tag + "q", (n, hq * d))
+        kv.append(layer, list(range(n)), q, normal(38, tag + "k", (n, hkv * d)),
+                  normal(38, tag + "v", (n, hkv * d)))
+        q_rot = rope_rows(q, range(n), hq, d, d, theta, True, check_against_oracle=False)
+        dq = rt.DeviceArray.from_host(np.ascontiguousarray(q_rot, np.float32))
+        dout = rt.DeviceArray(n * hq * d)
+        dout2 = rt.DeviceArray(n2 * hq * d)
+        bufs += [dq, dout, dout2]
+
+        def call():
+            kv.attend_causal_device(layer, 0, 0, n, dq.ptr, n * hq * d, dout.ptr, n * hq * d)
+
+        def other():  # rows 0 .. n2-1: another split plan on the same scratch
+            kv.attend_causal_device(layer, 0, 0, n2, dq.ptr, n2 * hq * d, dout2.ptr, n2 * hq * d)
+
+        call()
+        lib.synchronize()
+        eager = dout.download()
+        assert np.all(np.isfinite(eager))
+        graph = rt.Graph(lib.stream(), call)
+        for replay in range(3):
+            dout.zero()
+            graph.launch()
+            lib.synchronize()
+            np.testing.assert_array_equal(dout.download(), eager, err_msg=f"replay {replay}")
+            other()
+            lib.synchronize()
+    finally:
+        if graph is not None:
+            graph.destroy()
+        for b in bufs:
+            b.free()
+        kv.close()
+        rope.close()
+        lib.close()
+
+
 def test_c1_qwen3_prefill_f32(hip):
     """C1's shape: 16 Q heads, 8 KV heads, d 128, NeoX theta 1e6, f32 KV, the 512-row prompt as
     one chunk, every row against the oracle."""
