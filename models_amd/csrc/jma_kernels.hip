@@ -1720,81 +1720,45 @@ template <int D> struct Shape { static constexpr int S = prefill_stripes(D), Q =
 
 // Finish of one half of a split row block. Each wave holds kCQ finished O^T chunks of its stripe
 // (chunks c0 .. c0 + kCQ - 1, unnormalised: weighted by 2^(m_r - M) over the kv groups) and its
-// columns' (M, L). The first half to arrive stores them as plain words ((M, L) once per stripe,
-// by the stripe's wave of kv group 0), waits for the stores, sets its wave's flag word and exits.
-// The second polls the one or two flags its wave needs (one word each: bulk polling of the data
-// words would load the whole partial per round), loads the other half's words until none reads
-// kClear (they already hold data once the flag is set), combines the halves in half order,
-// (O0 e0 + O1 e1) / (L0 e0 + L1 e1) with e_h = 2^(M_h - max), stores the output and clears the
-// words and flags, so the result does not depend on which half merges. The merge decision is
-// uniform over the workgroup.
+// columns' (M, L). a.tickets[pair] counts the halves' stored states. A half that finds the other's
+// state stored merges at once; otherwise it stores its words ((M, L) once per stripe, by the
+// stripe's wave of kv group 0; device-coherent, acknowledged) and takes a ticket, and the one that
+// then finds the count at 1 merges: exactly one half merges, with no wait, and resets the ticket.
+// The merge combines the halves in half order, (O0 e0 + O1 e1) / (L0 e0 + L1 e1) with
+// e_h = 2^(M_h - max), so the result does not depend on which half merges. Every wave of the
+// workgroup calls this (the decisions are uniform).
 template <int D, int S, int kWaves, int kCQ>
 __device__ __forceinline__ void split_exchange(const PrefillArgs& a, uint32_t pair, uint32_t half,
-                                               bool merger, int s, int wave, uint32_t c0,
-                                               bool post_ml, int lane, int j, int h, bool col_ok,
-                                               uint32_t crow, uint32_t head, float m, float l,
-                                               const float4_t (&v)[kCQ]) {
+                                               int s, uint32_t c0, bool post_ml, int lane, int j, int h,
+                                               bool col_ok, uint32_t crow, uint32_t head, float m,
+                                               float l, const float4_t (&v)[kCQ]) {
   constexpr int kC = D / 8;  // float4 chunks of O^T per lane and stripe
   const __amdgpu_buffer_rsrc_t rs = part_rsrc(a.part);
   auto base = [&](uint32_t hf) JMA_INL {
     return (uint32_t)((((uint64_t)pair * 2 + hf) * S + s) * (kC * 64 + 32) * 16);
   };
-  // Flag words follow the partials of every pair: [pair][half][wave], 16 bytes each.
-  const uint64_t pairs = (uint64_t)a.split_blocks * a.head_groups * a.num_kv_heads;
-  auto flag = [&](uint32_t hf, int w) JMA_INL {
-    return (uint32_t)(pairs * 2 * S * (kC * 64 + 32) * 16 + (((uint64_t)pair * 2 + hf) * kWaves + w) * 16);
-  };
-  if (!merger) {
+  __shared__ uint32_t s_tk;
+  if (threadIdx.x == 0) s_tk = __hip_atomic_load(&a.tickets[pair], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_tk == 0u) {
     const uint32_t b = base(half);
 #pragma unroll
-    for (int i = 0; i < kCQ; ++i)
-      store_part(rs, b + ((c0 + i) * 64 + lane) * 16,
-                 float4_t{canon(v[i][0]), canon(v[i][1]), canon(v[i][2]), canon(v[i][3])});
-    if (post_ml && h == 0) {
-      const float cl = __uint_as_float(kClear);
-      store_part(rs, b + (kC * 64 + j) * 16, float4_t{canon(m), canon(l), cl, cl});
-    }
+    for (int i = 0; i < kCQ; ++i) store_part(rs, b + ((c0 + i) * 64 + lane) * 16, v[i]);
+    if (post_ml && h == 0) store_part(rs, b + (kC * 64 + j) * 16, float4_t{m, l, 0.0f, 0.0f});
+    // The stores are acknowledged (visible device-wide) before the ticket is taken.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (lane == 0) store_part(rs, flag(half, wave), float4_t{0.f, 0.f, 0.f, 0.f});
-    return;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_tk = __hip_atomic_fetch_add(&a.tickets[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_tk == 0u) return;  // the other half merges
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&a.tickets[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(&a.tickets[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t ob = base(1 - half);
-  bool timed_out = false;
-  {
-    const uint32_t f_own = flag(1 - half, wave), f_ml = flag(1 - half, s);  // wave s posts (M, L)
-    float4_t f1 = load_part(rs, f_own), f0 = load_part(rs, f_ml);
-    for (uint32_t spin = 0; !(written(f1) && written(f0)); ++spin) {
-      if (spin == kSpinLimit) {
-        timed_out = true;
-        break;
-      }
-      poll_barrier();
-      f1 = load_part(rs, f_own);
-      f0 = load_part(rs, f_ml);
-    }
-  }
   float4_t x[kCQ];
 #pragma unroll
   for (int i = 0; i < kCQ; ++i) x[i] = load_part(rs, ob + ((c0 + i) * 64 + lane) * 16);
-  float4_t mlv = load_part(rs, ob + (kC * 64 + j) * 16);
-  auto ml_ready = [&]() JMA_INL { return written(float4_t{mlv[0], mlv[1], mlv[0], mlv[1]}); };
-  for (uint32_t spin = 0; !timed_out; ++spin) {
-    bool ready = ml_ready();
-#pragma unroll
-    for (int i = 0; i < kCQ; ++i) ready &= written(x[i]);
-    if (ready) break;
-    if (spin == kSpinLimit) {
-      timed_out = true;
-      break;
-    }
-    poll_barrier();
-    if (!ml_ready()) mlv = load_part(rs, ob + (kC * 64 + j) * 16);
-#pragma unroll
-    for (int i = 0; i < kCQ; ++i)
-      if (!written(x[i])) x[i] = load_part(rs, ob + ((c0 + i) * 64 + lane) * 16);
-  }
+  const float4_t mlv = load_part(rs, ob + (kC * 64 + j) * 16);
   const float m0 = half == 0 ? m : mlv[0], l0 = half == 0 ? l : mlv[1];
   const float m1 = half == 0 ? mlv[0] : m, l1 = half == 0 ? mlv[1] : l;
   const float M = fmaxf(m0, m1);
@@ -1812,13 +1776,7 @@ __device__ __forceinline__ void split_exchange(const PrefillArgs& a, uint32_t pa
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = fmaf(v1[e], e1, v0[e] * e0) * inv;
     if (col_ok) *(float4_t*)(orow + 32 * (c >> 2) + 8 * (c & 3)) = r;
-    store_part(rs, ob + (c * 64 + lane) * 16, clear4());
   }
-  // Every wave of the stripe has read the (M, L) word and the flags before they are cleared.
-  __syncthreads();
-  if (post_ml && h == 0) store_part(rs, ob + (kC * 64 + j) * 16, clear4());
-  if (lane == 0) store_part(rs, flag(1 - half, wave), clear4());
-  if (timed_out && lane == 0) atomicOr(a.err, 2);
 }
 
 // Workgroup = (kv head, head group, block of S stripes). A stripe is R query rows x Gz query heads
@@ -1878,12 +1836,8 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   const uint32_t rank = split ? rest / a.head_groups / 2 : a.split_blocks + rest / a.head_groups;
   const uint32_t rb = a.row_blocks - 1 - rank;
   const uint32_t pair = (rank * a.head_groups + hz) * a.num_kv_heads + kvh;
-  __shared__ uint32_t s_ticket;
   __shared__ uint32_t s_rerun;  // set when the block needs the robust pass
   if (threadIdx.x == 0) s_rerun = 0u;
-  uint32_t ticket = 0;  // arrival order of this half of a split pair, taken first
-  if (split && threadIdx.x == 0)
-    ticket = __hip_atomic_fetch_add(&a.tickets[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lane = threadIdx.x & 63, j = lane & 31, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int s = wave % S, q = wave / S;
@@ -1908,9 +1862,14 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   // stripe sees.
   const uint32_t bt0 = first_visible(a.start + b_row0, a.window) / 32;
   const uint32_t bt1 = (a.start + b_row1) / 32 + 1;
-  const uint32_t tmid = bt0 + (bt1 - bt0 + 1) / 2;
-  const uint32_t t0 = split && half == 1 ? tmid : bt0;
-  const uint32_t t1 = split && half == 0 ? tmid : bt1;
+  // The first half is a little shorter (split_range), so it usually stores its state while the
+  // second still computes, and the second merges without storing its own.
+  SplitItem si;
+  si.split = split;
+  si.half = half;
+  si.unit = rb;
+  uint32_t t0, t1;
+  split_range(bt0, bt1, si, t0, t1);
   const uint32_t steps = (t1 - t0 + Q - 1) / Q;
   const uint32_t w_last = a.start + row_last;
   const uint32_t w_first_early = first_visible(a.start + row0, a.window);
@@ -2283,7 +2242,6 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
   // chunks wave r finishes; then it combines its own chunks (from registers) with the Q - 1
   // posted ones, in kv-group order, weighted by exp2(m_r - M) / L.
   l = half_sum(l + lb);
-  if (split && threadIdx.x == 0) s_ticket = ticket;
   constexpr int kCQ = kC / Q;  // chunks one wave finishes
   // Posted chunks of stripe s: [source group][destination slot][kCQ][64 lanes] float4, in lx for
   // even stripes and ly for odd ones (each holds Q * (Q - 1) * kCQ KB <= one LDS array).
@@ -2363,8 +2321,8 @@ __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void prefill_kernel(const
     }
   });
   if (split) {
-    split_exchange<D, S, kWaves, kCQ>(a, pair, half, s_ticket != 0, s, wave, (uint32_t)q * kCQ,
-                                      q == 0, lane, j, h, col_ok, crow, head, M, L, fin);
+    split_exchange<D, S, kWaves, kCQ>(a, pair, half, s, (uint32_t)q * kCQ, q == 0, lane, j, h,
+                                      col_ok, crow, head, M, L, fin);
     return;
   }
   float* const orow = a.out + ((uint64_t)crow * a.num_heads + head) * D + 4 * h;

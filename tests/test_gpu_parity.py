@@ -453,8 +453,8 @@ def test_prefill_chunked_and_windowed_matches_oracle(hip):
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
 def test_prefill_split_blocks_match_oracle(monkeypatch, d):
-    """Row blocks whose kv range is split between two workgroups (the second to arrive merges the
-    halves through not-written words) against the oracle, for every split threshold
+    """Row blocks whose kv range is split between two workgroups (the later to finish merges the
+    two states, the other's stored device-coherent) against the oracle, for every split threshold
     (JMA_PREFILL_SPLIT_TILES: 0 never splits, 2 splits every block of two or more kv tiles, 32 the
     longest, -1 splits while the grid underfills the device), causal and windowed, a chunk start,
     a group of 3 (ragged stripes) and ragged tails."""
