@@ -113,12 +113,11 @@ struct PrefillArgs {
   uint32_t head_groups;       // ceil(group / heads_per_stripe)
   uint32_t row_blocks;        // set by plan_prefill
   // The split_blocks longest row blocks (they run first) have their kv range cut in two halves,
-  // each a workgroup; the later of the two to arrive (ticket) merges them. part: [pair][half]
-  // [stripe][D / 8 chunks x 64 lanes + 32 columns] float4 words, every word 0xFFFFFFFF (not
-  // written) between launches; tickets: [pair], zero between launches. The f16 head-dim-512
-  // prefill (kernel 3c) splits stripe pairs the same way (split_blocks pairs, planned by
-  // plan_prefill_pairs): part [split pair][half][wave][kPairPartWords][64 lanes] float4 words
-  // with no initial value; tickets zero between launches.
+  // each a workgroup; the later of the two to finish merges them (the tickets count stored
+  // states). part: [pair][half][stripe][D / 8 chunks x 64 lanes + 32 columns] float4 words, no
+  // initial value; tickets: [pair], zero between launches. The sliced prefills split their units
+  // the same way (kernel 3b's stripes, kernel 3c's stripe pairs; planned by plan_prefill_pairs):
+  // part [split unit][half][wave][4 kNb + 1][64 lanes] float4 words.
   uint32_t split_blocks;
   float* part;
   uint32_t* tickets;

@@ -681,8 +681,9 @@ void attend_causal_impl(jmodels_attn_context* ctx, const jmodels_attn_kv* kv, co
     a.row_blocks = plan.row_blocks;
     a.split_blocks = plan.split_blocks;
     if (plan.pairs > 0) {
-      // Tickets start at zero and partial words not-written; the merging workgroups restore both.
-      reserve_filled(ctx->pf_part, plan.part_bytes, 0xFF, ctx->stream, "prefill split exchange");
+      // No initial value for the halves' states; tickets start at zero and the merging
+      // workgroups restore them, so they are zeroed only when (re)allocated.
+      ctx->pf_part.reserve(plan.part_bytes, ctx->stream, "prefill split exchange");
       reserve_filled(ctx->pf_tickets, (size_t)plan.pairs * sizeof(uint32_t), 0, ctx->stream,
                      "prefill split exchange");
       a.part = (float*)ctx->pf_part.ptr;
@@ -746,7 +747,7 @@ int32_t collect_errors(jmodels_attn_context* ctx) {
     hip_check(hipMemcpy(ctx->d_err, &zero, sizeof(int), hipMemcpyHostToDevice), "reset error word");
     if (err & 2) {
       // A reducer gave up waiting: tickets and partial words may be left set; clear them.
-      for (DeviceBuffer* b : {&ctx->part_f, &ctx->pf_part})
+      for (DeviceBuffer* b : {&ctx->part_f})
         if (b->ptr) hip_check(hipMemset(b->ptr, 0xFF, b->bytes), "reset partials");
       for (DeviceBuffer* b : {&ctx->counters, &ctx->pf_tickets, &ctx->pp_tickets})
         if (b->ptr) hip_check(hipMemset(b->ptr, 0, b->bytes), "reset tickets");
