@@ -181,10 +181,11 @@ inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, u
 // 0 or 1 never splits; -1 (automatic) splits every pair of 8 or more tiles when the pairs'
 // workgroups fit on the compute units at once (with more, the dispatch already fills the units
 // that short pairs free). Measured on the Gemma 4 full-layer prefill (S 2048, 256 pairs of 1-64
-// tiles): 115 us unsplit; every pair of at least 2 tiles split 97-98 us, of 8 94.7, of 16 98.3,
-// of 48 96.3, of 64 113. A half's state exchange costs ~9 us of the 97 (timing-only copy without
-// it: 88), the rest of the gap to perfect balance is the extra prologues and the shared K/V
-// traffic of a fully occupied device.
+// tiles): 115 us unsplit; every pair of at least 2 tiles split 94.8-95.2 us, of 8 93.4-94.0, of
+// 16 97.9, of 48 93.8-95.4, of 64 113. The state exchange costs ~6 us (a timing-only copy
+// without it: 88 us with every pair split); the rest of the gap to perfect balance is the extra
+// prologues and the shared K/V traffic of a fully occupied device. The same rule on kernel 3b's
+// stripes: the C1-shaped f32 prefill (256 stripes of 1-16 tiles) 38 -> 31 us.
 constexpr uint32_t kPairPartWords = 33;  // float4 words per lane of a half's state: O^T (8 blocks x 4) and (m, l, lb)
 constexpr uint32_t kPairAutoSplitTiles = 8;
 struct PairPlan {
@@ -215,7 +216,7 @@ inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32
     const uint32_t first = (w == 0 || p0 + 1 <= w) ? 0u : p0 + 1 - w;
     return (a.start + r1) / 32 + 1 - first / 32;
   };
-  // The trailing pairs with at least min_tiles (>= 2) tiles.
+  // The trailing units with at least min_tiles (>= 2) tiles.
   uint32_t sp = 0;
   while (sp < pairs && tiles_of(pairs - 1 - sp) >= std::max<uint32_t>(min_tiles, 2)) ++sp;
   p.split_pairs = sp;
