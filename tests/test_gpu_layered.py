@@ -290,3 +290,16 @@ def test_gemma4_layered_cache_attention(hip, half):
         kv.close()
         for x in norms + ropes:
             x.close()
+
+
+@pytest.mark.parametrize("half", [True, False])
+def test_gemma4_layered_cache_attention_every_unit_split(monkeypatch, half):
+    """The Gemma-4-shaped case above with every prefill row block, stripe and stripe pair of two
+    or more kv tiles split into two workgroups (JMA_PREFILL_SPLIT_TILES=2), including the sliding
+    layer's ring (the halves' tiles wrap around its 356 slots)."""
+    monkeypatch.setenv("JMA_PREFILL_SPLIT_TILES", "2")
+    lib = A.HipAttentionLibrary(0)
+    try:
+        test_gemma4_layered_cache_attention(lib, half)
+    finally:
+        lib.close()
