@@ -180,7 +180,7 @@ inline PrefillPlan plan_prefill(const PrefillArgs& a, int dk, int split_tiles, u
 // duration. split_tiles >= 2 splits the trailing (longest) pairs of at least that many kv tiles;
 // 0 or 1 never splits; -1 (automatic) splits every pair of 8 or more tiles when the pairs'
 // workgroups fit on the compute units at once (with more, the dispatch already fills the units
-// that short pairs free). Measured on the Gemma 4 full-layer prefill (S 2048, 256 pairs of 1-64
+// that short pairs free; kernel 3b then splits its stripes of 32 or more tiles, below). Measured on the Gemma 4 full-layer prefill (S 2048, 256 pairs of 1-64
 // tiles): 115 us unsplit; every pair of at least 2 tiles split 94.8-95.2 us, of 8 93.4-94.0, of
 // 16 97.9, of 48 93.8-95.4, of 64 113. The state exchange costs ~6 us (a timing-only copy
 // without it: 88 us with every pair split); the rest of the gap to perfect balance is the extra
@@ -208,8 +208,16 @@ inline PairPlan plan_prefill_pairs(const PrefillArgs& a, int split_tiles, uint32
   const uint32_t pairs = unit_rows ? a.row_blocks : (a.row_blocks + 1) / 2;
   const uint32_t per = a.head_groups * a.num_kv_heads;  // workgroups per unit
   if (pairs == 0 || per == 0 || split_tiles == 0 || split_tiles == 1) return p;
-  if (split_tiles < 0 && (uint64_t)pairs * per > std::max<uint32_t>(cus, 1)) return p;
-  const uint32_t min_tiles = split_tiles >= 2 ? (uint32_t)split_tiles : kPairAutoSplitTiles;
+  uint32_t min_tiles = split_tiles >= 2 ? (uint32_t)split_tiles : kPairAutoSplitTiles;
+  if (split_tiles < 0 && (uint64_t)pairs * per > std::max<uint32_t>(cus, 1)) {
+    // More units than compute units. Kernel 3c (one workgroup per compute unit) measured slower
+    // with any split (Gemma 4 full layer at S 4096: 254 us unsplit, 268-309 split; 16 Q / 2 KV
+    // heads at S 2048: 143 us against 143-189); kernel 3b's stripes (several workgroups per
+    // compute unit) still gain from splitting their longest (C3's shape in f32, 1640 stripes of
+    // 1-64 tiles: 351-353 us unsplit, 337 splitting 32+ tiles, 340 48+, 349 16+).
+    if (unit_rows == 0) return p;
+    min_tiles = 32;
+  }
   auto tiles_of = [&](uint32_t pr) -> uint32_t {  // kv tiles of unit pr (the kernel's t1 - t0)
     const uint32_t r0 = pr * R, r1 = std::min(r0 + R, a.n) - 1;
     const uint32_t w = a.window, p0 = a.start + r0;
